@@ -1,0 +1,416 @@
+"""Benchmark of the MI355X attention hot path (one GPU).
+
+Default workload (the headline line): BASELINE config 4 — ragged paged
+decode at the Qwen3-8B attention shape (32 q / 8 kv heads, head_dim 128,
+bf16), batch 256, kv lengths ~ U[128, 4096], page_size 16, seeded random
+page table, split-KV. One step = one sgl_paged_decode call (the decode
+kernel plus its split merge) over the whole batch, inputs resident in HBM.
+
+The other configs are reported under "extra" (and as their own lines with
+--workload): cfg1 small decode, cfg2 prefill with prefix hits, cfg3 fused
+RoPE + qk-norm + KV store, cfg5 mixed 48-layer step replayed as a hipGraph.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload cfgN]
+                       [--no-extra] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO))
+
+METRIC = "paged decode attn GB/s & prefill TFLOP/s (% MI355X peak), 1 GPU"
+HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, AMD published
+BF16_PEAK_TFLOPS = 2500.0    # MI355X dense bf16 MFMA, AMD published
+PROFILE_TRAFFIC = REPO / "profiles" / "traffic.json"
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="cfg4",
+                    choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5"])
+    ap.add_argument("--no-extra", action="store_true", help="headline workload only")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    ap.add_argument("--cfg5-layers", type=int, default=48)
+    return ap.parse_args()
+
+
+# ------------------------------------------------------------------ helpers
+
+class Timer:
+    """Times K launches of fn: wall clock around the loop (synchronized) and
+    HIP events recorded on the stream the kernels run on."""
+
+    def __init__(self, torch):
+        self.torch = torch
+
+    def run(self, fn, steps, warmup):
+        torch = self.torch
+        stream = torch.cuda.current_stream()
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+               for _ in range(steps)]
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for a, b in evs:
+            a.record(stream)
+            fn()
+            b.record(stream)
+        torch.cuda.synchronize()
+        wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+        ev_ms = float(np.mean([a.elapsed_time(b) for a, b in evs]))
+        return wall_ms, ev_ms
+
+
+def load_traffic(key):
+    try:
+        return json.loads(PROFILE_TRAFFIC.read_text()).get(key)
+    except (OSError, ValueError):
+        return None
+
+
+# ------------------------------------------------------------------ workloads
+
+def setup_decode(torch, capi, wl, w, dev, seed=0):
+    b, s = w.batch, w.shape
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    hq, hkv, D = s.num_qo_heads, s.num_kv_heads, s.head_dim
+    kc = torch.randn((b.num_slots, hkv, D), device=dev, generator=g).to(torch.bfloat16)
+    vc = torch.randn((b.num_slots, hkv, D), device=dev, generator=g).to(torch.bfloat16)
+    qkv = torch.randn((b.batch_size, s.qkv_width), device=dev, generator=g).to(torch.bfloat16)
+    q = qkv[:, :hq * D].view(-1, hq, D)
+    o = torch.empty((b.batch_size, hq, D), device=dev, dtype=torch.bfloat16)
+    plan = capi.decode_plan(b.kv_indptr, hq, hkv, D)
+    ws = torch.empty(max(plan.workspace_bytes, 16), dtype=torch.uint8, device=dev)
+    idx = torch.from_numpy(b.indices).to(dev)
+    kvp = torch.from_numpy(b.kv_indptr).to(dev)
+    scale = 1.0 / math.sqrt(D)
+
+    def step():
+        capi.paged_decode(plan, q, kc, vc, idx, kvp, o, ws, scale)
+
+    nbytes = wl.attention_bytes(s, b.qo_lens, b.kv_lens, b.page_size)
+    flops = wl.attention_flops(s, b.qo_lens, b.kv_lens, causal=False)
+    return step, nbytes, flops, dict(q=q, kc=kc, vc=vc, plan=plan)
+
+
+def setup_prefill(torch, capi, wl, w, dev, seed=0):
+    b, s = w.batch, w.shape
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    hq, hkv, D = s.num_qo_heads, s.num_kv_heads, s.head_dim
+    rows = int(b.qo_indptr[-1])
+    kc = torch.randn((b.num_slots, hkv, D), device=dev, generator=g).to(torch.bfloat16)
+    vc = torch.randn((b.num_slots, hkv, D), device=dev, generator=g).to(torch.bfloat16)
+    qkv = torch.randn((rows, s.qkv_width), device=dev, generator=g).to(torch.bfloat16)
+    q = qkv[:, :hq * D].view(-1, hq, D)
+    o = torch.empty((rows, hq, D), device=dev, dtype=torch.bfloat16)
+    idx = torch.from_numpy(b.indices).to(dev)
+    qop = torch.from_numpy(b.qo_indptr).to(dev)
+    kvp = torch.from_numpy(b.kv_indptr).to(dev)
+    scale = 1.0 / math.sqrt(D)
+    max_qo = int(b.qo_lens.max())
+
+    def step():
+        capi.paged_prefill(q, kc, vc, idx, qop, kvp, max_qo, o, scale)
+
+    nbytes = wl.attention_bytes(s, b.qo_lens, b.kv_lens, b.page_size)
+    flops = wl.attention_flops(s, b.qo_lens, b.kv_lens, causal=True)
+    return step, nbytes, flops
+
+
+def setup_fused(torch, capi, wl, w, dev, seed=0):
+    b, s = w.batch, w.shape
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    hq, hkv, D = s.num_qo_heads, s.num_kv_heads, s.head_dim
+    T = int(b.qo_indptr[-1])
+    qkv = torch.randn((T, s.qkv_width), device=dev, generator=g).to(torch.bfloat16)
+    slots = T
+    kc = torch.empty((slots, hkv, D), device=dev, dtype=torch.bfloat16)
+    vc = torch.empty_like(kc)
+    qw = (torch.rand(D, device=dev, generator=g) + 0.5).to(torch.bfloat16)
+    kw = (torch.rand(D, device=dev, generator=g) + 0.5).to(torch.bfloat16)
+    cos, sin = capi.rope_cos_sin_cache(w.extra["max_pos"], D, w.extra["theta"], dev)
+    pos = torch.from_numpy(b.positions).to(dev)
+    loc = torch.from_numpy(b.out_loc).to(dev)
+    eps = w.extra["eps"]
+    # The pass is in place; repeated steps re-normalise already-normalised
+    # rows, which costs the same bytes and keeps values finite.
+
+    def step():
+        capi.fused_qknorm_rope_store(qkv, kc, vc, qw, kw, cos, sin, pos, loc, hq, hkv, D, eps)
+
+    return step, wl.fused_store_bytes(s, T)
+
+
+def setup_mixed(torch, capi, wl, w, dev, layers, seed=0):
+    """Config 5: per layer, decode of the 64 qo=1 requests plus prefill of the
+    2048-token chunk, each layer on its own slice of a [2, L, slots, Hkv, D]
+    pool; the whole 48-layer step captured once and replayed as a hipGraph."""
+    b, s = w.batch, w.shape
+    hq, hkv, D = s.num_qo_heads, s.num_kv_heads, s.head_dim
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    slots = b.num_slots
+    pool = torch.empty((2, layers, slots, hkv, D), device=dev, dtype=torch.bfloat16)
+    for l in range(layers):
+        pool[0, l].normal_(generator=g)
+        pool[1, l].normal_(generator=g)
+    rows = int(b.qo_indptr[-1])
+    qkv = torch.randn((rows, s.qkv_width), device=dev, generator=g).to(torch.bfloat16)
+    q = qkv[:, :hq * D].view(-1, hq, D)
+    o = torch.empty((rows, hq, D), device=dev, dtype=torch.bfloat16)
+    qo = b.qo_lens
+    dec = np.nonzero(qo == 1)[0]
+    pre = np.nonzero(qo > 1)[0]
+    kvl = b.kv_lens
+
+    def sub(reqs):
+        ip = np.concatenate([[0], np.cumsum(kvl[reqs])]).astype(np.int32)
+        idx = np.concatenate([b.indices[b.kv_indptr[r]:b.kv_indptr[r + 1]] for r in reqs])
+        return ip, idx.astype(np.int32)
+
+    d_ip, d_idx = sub(dec)
+    p_ip, p_idx = sub(pre)
+    p_qo = np.concatenate([[b.qo_indptr[pre[0]]], b.qo_indptr[pre + 1]]).astype(np.int32)
+    plan = capi.decode_plan(d_ip, hq, hkv, D)
+    ws = torch.empty(max(plan.workspace_bytes, 16), dtype=torch.uint8, device=dev)
+    t = lambda a: torch.from_numpy(a).to(dev)
+    d_ip_t, d_idx_t, d_q_t = t(d_ip), t(d_idx), t(b.qo_indptr[dec].astype(np.int32))
+    p_ip_t, p_idx_t, p_qo_t = t(p_ip), t(p_idx), t(p_qo)
+    max_qo = int(qo[pre].max())
+    scale = 1.0 / math.sqrt(D)
+
+    def layer_pass():
+        for l in range(layers):
+            kc, vc = pool[0, l], pool[1, l]
+            capi.paged_decode(plan, q, kc, vc, d_idx_t, d_ip_t, o, ws, scale, d_q_t)
+            capi.paged_prefill(q, kc, vc, p_idx_t, p_qo_t, p_ip_t, max_qo, o, scale)
+
+    layer_pass()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    cap = torch.cuda.Stream()
+    cap.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(cap):
+        layer_pass()  # warm the capture stream
+    torch.cuda.current_stream().wait_stream(cap)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph):
+        layer_pass()
+    torch.cuda.synchronize()
+
+    dec_bytes = wl.attention_bytes(s, qo[dec], kvl[dec], b.page_size) * layers
+    pre_flops = wl.attention_flops(s, qo[pre], kvl[pre], causal=True) * layers
+    pre_bytes = wl.attention_bytes(s, qo[pre], kvl[pre], b.page_size) * layers
+    return graph.replay, dec_bytes, pre_flops, pre_bytes, (graph, pool)
+
+
+# ------------------------------------------------------------------ CPU baseline
+
+def cpu_baseline_decode(wl, w, budget_s=12.0):
+    """The CPU oracle (C, OpenMP) on a bounded sample of the same workload:
+    the first requests of the batch, repeated until ~budget_s of CPU work."""
+    from oracle import oracle as orc
+    b, s = w.batch, w.shape
+    rng = np.random.default_rng(1)
+    n = min(16, b.batch_size)
+    lens = b.kv_lens[:n]
+    ip = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    slots = int(ip[-1])
+    idx = rng.permutation(slots).astype(np.int32)
+    hkv, hq, D = s.num_kv_heads, s.num_qo_heads, s.head_dim
+    kc = orc.f32_to_bf16(rng.standard_normal((slots, hkv, D), dtype=np.float32))
+    vc = orc.f32_to_bf16(rng.standard_normal((slots, hkv, D), dtype=np.float32))
+    q = orc.f32_to_bf16(rng.standard_normal((n, hq, D), dtype=np.float32))
+    scale = 1.0 / math.sqrt(D)
+    orc.decode(q, kc, vc, idx, ip, scale)  # warm
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        orc.decode(q, kc, vc, idx, ip, scale)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or reps >= 1000:
+            break
+    nbytes = wl.attention_bytes(s, np.ones(n, np.int64), lens, b.page_size)
+    return {"value": round(nbytes * reps / el / 1e9, 3), "unit": "GB/s",
+            "cores": orc.threads(), "kind": "port",
+            "sample": f"oracle_decode on the first {n} requests of {w.name} "
+                      f"(sum kv {slots} tokens), {reps} repetitions in {el:.1f} s"}
+
+
+def cpu_baseline_prefill(wl, w, budget_s=10.0):
+    from oracle import oracle as orc
+    b, s = w.batch, w.shape
+    rng = np.random.default_rng(2)
+    n = min(2, b.batch_size)
+    qo, kv = b.qo_lens[:n], b.kv_lens[:n]
+    qip = np.concatenate([[0], np.cumsum(qo)]).astype(np.int32)
+    kip = np.concatenate([[0], np.cumsum(kv)]).astype(np.int32)
+    slots = int(kip[-1])
+    idx = rng.permutation(slots).astype(np.int32)
+    hkv, hq, D = s.num_kv_heads, s.num_qo_heads, s.head_dim
+    kc = orc.f32_to_bf16(rng.standard_normal((slots, hkv, D), dtype=np.float32))
+    vc = orc.f32_to_bf16(rng.standard_normal((slots, hkv, D), dtype=np.float32))
+    q = orc.f32_to_bf16(rng.standard_normal((int(qip[-1]), hq, D), dtype=np.float32))
+    scale = 1.0 / math.sqrt(D)
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        orc.prefill(q, kc, vc, idx, qip, kip, scale)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or reps >= 1000:
+            break
+    flops = wl.attention_flops(s, qo, kv, causal=True)
+    return {"value": round(flops * reps / el / 1e12, 5), "unit": "TFLOP/s",
+            "cores": orc.threads(), "kind": "port",
+            "sample": f"oracle_prefill on {n} requests of {w.name}, {reps} reps in {el:.1f} s"}
+
+
+# ------------------------------------------------------------------ main
+
+def roofline_hbm(nbytes, kernel_ms, traffic_key):
+    achieved = nbytes / (kernel_ms * 1e-3) / 1e9
+    return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": load_traffic(traffic_key)}
+
+
+def roofline_mfma(flops, kernel_ms, traffic_key):
+    achieved = flops / (kernel_ms * 1e-3) / 1e12
+    return {"bound": "mfma", "achieved": round(achieved, 2), "peak": BF16_PEAK_TFLOPS,
+            "unit": "TFLOP/s", "frac": round(achieved / BF16_PEAK_TFLOPS, 4),
+            "traffic": load_traffic(traffic_key)}
+
+
+def run_workload(name, torch, capi, wl, dev, steps, warmup, cfg5_layers):
+    timer = Timer(torch)
+    if name in ("cfg1", "cfg4"):
+        w = wl.cfg1_decode_small() if name == "cfg1" else wl.cfg4_decode_large()
+        step, nbytes, flops, _ = setup_decode(torch, capi, wl, w, dev)
+        wall, ev = timer.run(step, steps, warmup)
+        rec = {"workload": w.name, "ms_per_step": wall, "kernel_ms": ev, "bytes": nbytes,
+               "GB/s": nbytes / (wall * 1e-3) / 1e9,
+               "roofline": roofline_hbm(nbytes, ev, "paged_decode_" + name)}
+        return w, rec
+    if name == "cfg2":
+        w = wl.cfg2_prefill_prefix()
+        step, nbytes, flops = setup_prefill(torch, capi, wl, w, dev)
+        wall, ev = timer.run(step, steps, warmup)
+        rec = {"workload": w.name, "ms_per_step": wall, "kernel_ms": ev, "flops": flops,
+               "bytes": nbytes, "TFLOP/s": flops / (wall * 1e-3) / 1e12,
+               "GB/s": nbytes / (wall * 1e-3) / 1e9,
+               "roofline": roofline_mfma(flops, ev, "paged_prefill_cfg2"),
+               "roofline_hbm": roofline_hbm(nbytes, ev, None)}
+        return w, rec
+    if name == "cfg3":
+        w = wl.cfg3_fused_store()
+        step, nbytes = setup_fused(torch, capi, wl, w, dev)
+        wall, ev = timer.run(step, steps, warmup)
+        rec = {"workload": w.name, "ms_per_step": wall, "kernel_ms": ev, "bytes": nbytes,
+               "GB/s": nbytes / (wall * 1e-3) / 1e9,
+               "roofline": roofline_hbm(nbytes, ev, "fused_qknorm_rope_store_cfg3")}
+        return w, rec
+    if name == "cfg5":
+        w = wl.cfg5_mixed(layers=cfg5_layers)
+        step, dec_bytes, pre_flops, pre_bytes, keep = setup_mixed(torch, capi, wl, w, dev,
+                                                                  cfg5_layers)
+        wall, ev = timer.run(step, max(2, steps // 4), max(1, warmup // 2))
+        t_roof = dec_bytes / (HBM_PEAK_GBS * 1e9) + pre_flops / (BF16_PEAK_TFLOPS * 1e12)
+        rec = {"workload": w.name, "layers": cfg5_layers, "ms_per_step": wall, "graph_ms": ev,
+               "decode_bytes": dec_bytes, "prefill_flops": pre_flops,
+               "t_roofline_ms": t_roof * 1e3, "roofline_frac": t_roof * 1e3 / ev}
+        del keep
+        return w, rec
+    raise ValueError(name)
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the attention hot "
+              "path is single-GPU in this build — run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import __graft_entry__ as entry
+    pkg = entry.load_package()
+    capi, wl = pkg.capi, pkg.workloads
+    capi.lib()
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP GPU", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    w, head = run_workload(args.workload, torch, capi, wl, dev, args.steps, args.warmup,
+                           args.cfg5_layers)
+    extra = {}
+    if not args.no_extra:
+        for name in ("cfg1", "cfg2", "cfg3", "cfg4", "cfg5"):
+            if name == args.workload:
+                continue
+            try:
+                _, rec = run_workload(name, torch, capi, wl, dev, args.steps, args.warmup,
+                                      args.cfg5_layers)
+                extra[name] = rec
+            except Exception as e:  # report, keep the headline line
+                extra[name] = {"error": repr(e)}
+            torch.cuda.empty_cache()
+            print(f"[bench] {name}: {json.dumps(extra[name])}", file=sys.stderr, flush=True)
+
+    cpu = None
+    if not args.no_cpu:
+        if args.workload in ("cfg1", "cfg4"):
+            cpu = cpu_baseline_decode(wl, w)
+        elif args.workload == "cfg2":
+            cpu = cpu_baseline_prefill(wl, w)
+
+    if "GB/s" in head and args.workload != "cfg2":
+        value, unit = head["GB/s"], "GB/s"
+    elif args.workload == "cfg2":
+        value, unit = head["TFLOP/s"], "TFLOP/s"
+    else:
+        value, unit = head["decode_bytes"] / (head["ms_per_step"] * 1e-3) / 1e9, "GB/s"
+    s = w.shape
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": unit,
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["ms_per_step"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: seeded N(0,1) bf16 Q/K/V, seeded random page permutation",
+        "config": {"workload": head["workload"], "batch": w.batch.batch_size,
+                   "num_qo_heads": s.num_qo_heads, "num_kv_heads": s.num_kv_heads,
+                   "head_dim": s.head_dim, "page_size": w.batch.page_size,
+                   "sum_kv": int(w.batch.kv_lens.sum()), "parallelism": "single GPU"},
+        "roofline": head.get("roofline"),
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,243 @@
+/*
+ * sgl_attn.h — C ABI of the MI355X (gfx950) attention hot path.
+ *
+ * Every entry point takes plain device pointers, element counts and
+ * strides (in elements), a hipStream_t passed as `void*`, and returns an
+ * int status: 0 on success, a negative SGL_ERR_* code for an argument the
+ * call rejects before launching anything, or a positive hipError_t when the
+ * HIP runtime refuses the launch. No entry point allocates device memory;
+ * workspaces are passed in by the caller. The pool layout is the
+ * reference's MHAKVCache: one layer's K (or V) cache is [slots, Hkv, D]
+ * bf16, token-granular (a "page" of page_size P is P consecutive slots).
+ *
+ * Each declaration names the reference interface (allen-shaw/sglang.cpp,
+ * file:line) it replaces.
+ */
+#ifndef SGL_ATTN_H_
+#define SGL_ATTN_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SGL_OK 0
+#define SGL_ERR_INVALID_ARG (-1)  /* null pointer, bad size, bad stride */
+#define SGL_ERR_UNSUPPORTED (-2)  /* head_dim / group size / dtype not built */
+#define SGL_ERR_CAPACITY (-3)     /* workspace or plan capacity exceeded */
+#define SGL_ERR_ALIGNMENT (-4)    /* pointer / stride misaligned for vector path */
+
+#define SGL_INDEX_I32 0
+#define SGL_INDEX_I64 1
+
+/* Human-readable text for a status code (static storage). */
+const char* sgl_status_string(int status);
+
+/* Library version, to check that the loaded .so matches this header. */
+int sgl_abi_version(void);
+#define SGL_ABI_VERSION 1
+
+/* ------------------------------------------------------------------ */
+/* KV-cache store                                                      */
+/* ------------------------------------------------------------------ */
+
+/*
+ * k_cache[out_loc[t], :] = k[t, :] and v_cache[out_loc[t], :] = v[t, :]
+ * for t < num_tokens, copying elems_per_token 2-byte elements (bf16 or
+ * fp16: the copy is bitwise). k/v rows are strided by k_stride_token /
+ * v_stride_token elements (the narrow views of a qkv row); cache rows are
+ * contiguous, elems_per_token apart. out_loc is int32 (index_dtype
+ * SGL_INDEX_I32) or int64 (SGL_INDEX_I64).
+ * Replaces: MHAKVCache::store_kv + store_kv_cache_kernel
+ *           (src/kvcache/mha_kvcache.cu:111-155, :13-41).
+ */
+int sgl_store_kv(void* k_cache, void* v_cache, const void* k, const void* v,
+                 const void* out_loc, int index_dtype, int64_t num_tokens,
+                 int64_t elems_per_token, int64_t k_stride_token,
+                 int64_t v_stride_token, void* stream);
+
+/* ------------------------------------------------------------------ */
+/* Page-table / token-pool plumbing                                    */
+/* ------------------------------------------------------------------ */
+
+/*
+ * indices[kv_indptr[r] + p] = page_table[table_indices[r] * stride + p]
+ * for p < kv_indptr[r+1]-kv_indptr[r] (0 where p >= cols); rows whose
+ * table index is outside [0, rows) are left untouched.
+ * Replaces: build_decode_indices_kernel (src/attention/flashinfer_backend.cu:43-70).
+ */
+int sgl_build_decode_indices(const int32_t* page_table, int64_t rows,
+                             int64_t stride, int64_t cols,
+                             const int32_t* table_indices,
+                             const int32_t* kv_indptr, int32_t* indices,
+                             int batch_size, void* stream);
+
+/*
+ * Prefill metadata gather: indices = cat_r(page_table[table_indices[r], :kv_len_r]),
+ * with kv_indptr the prefix sum of kv_len. Device-side replacement of the
+ * torch::cat over page-table slices.
+ * Replaces: prefill branch of FlashInferBackend::prepare_metadata
+ *           (src/attention/flashinfer_backend.cu:466-484).
+ */
+int sgl_build_prefill_indices(const int32_t* page_table, int64_t rows,
+                              int64_t stride, int64_t cols,
+                              const int32_t* table_indices,
+                              const int32_t* kv_indptr, int32_t* indices,
+                              int batch_size, void* stream);
+
+/*
+ * pool[req_indices[i] * stride + positions[i]] = tokens[i]; entries with an
+ * out-of-range row or column are skipped.
+ * Replaces: write_token_pool (src/kernels/token_pool.cu:53-93, kernel :10-29).
+ */
+int sgl_write_token_pool(int32_t* pool, int64_t rows, int64_t stride,
+                         int64_t cols, const int32_t* req_indices,
+                         const int32_t* positions, const int32_t* tokens,
+                         int64_t count, void* stream);
+
+/*
+ * out[i] = table[req_indices[i] * stride + positions[i]] (0 when out of range).
+ * Replaces: gather_int32_2d (src/kernels/token_pool.cu:95-133, kernel :31-49).
+ */
+int sgl_gather_int32_2d(const int32_t* table, int64_t rows, int64_t stride,
+                        int64_t cols, const int32_t* req_indices,
+                        const int32_t* positions, int32_t* out, int64_t count,
+                        void* stream);
+
+/* ------------------------------------------------------------------ */
+/* RoPE and q/k RMSNorm                                                */
+/* ------------------------------------------------------------------ */
+
+/*
+ * cos[p, i] = cos(p * inv_freq[i]), sin likewise, for p < max_pos,
+ * i < rotary_dim/2, inv_freq[i] = 1 / base^(2i / rotary_dim), fp32.
+ * Replaces: RotaryEmbedding ctor cache build (src/layers/rotary_embedding.cu:75-94).
+ */
+int sgl_rope_cos_sin_cache(float* cos_cache, float* sin_cache, int64_t max_pos,
+                           int rotary_dim, float base, void* stream);
+
+/*
+ * In-place per-(token, head) RMSNorm of q [tokens, q_heads, d] and
+ * k [tokens, k_heads, d] (strided views, last dim contiguous):
+ * x <- bf16(x * rsqrt(mean(x^2) + eps) * w), fp32 accumulation.
+ * Pass k = NULL / k_heads = 0 to normalise q only.
+ * Replaces: fused_qk_rmsnorm_inplace_3d_strided (src/layers/normalization.cu:318-384)
+ *           and RMSNorm::forward_inplace_3d_strided (:271-316).
+ */
+int sgl_qk_rmsnorm(void* q, void* k, const void* q_weight,
+                   const void* k_weight, int64_t tokens, int64_t q_heads,
+                   int64_t k_heads, int64_t d, int64_t q_stride_token,
+                   int64_t q_stride_head, int64_t k_stride_token,
+                   int64_t k_stride_head, float eps, void* stream);
+
+/*
+ * In-place NeoX (rotate-half) RoPE of q [nnz, q_heads, head_dim] and
+ * k [nnz, kv_heads, head_dim] at positions[t] (int32), using fp32 cos/sin
+ * caches of width cos_width (rotary_dim/2 or rotary_dim). Elements at
+ * index >= rotary_dim pass through.
+ * Replaces: RotaryEmbedding::forward_inplace (src/layers/rotary_embedding.cu:96-178;
+ *           formula :50-66).
+ */
+int sgl_rope(void* q, void* k, const float* cos_cache, const float* sin_cache,
+             const int32_t* positions, int64_t nnz, int64_t q_heads,
+             int64_t kv_heads, int64_t rotary_dim, int64_t head_dim,
+             int64_t cos_width, int64_t q_stride_token, int64_t q_stride_head,
+             int64_t k_stride_token, int64_t k_stride_head, void* stream);
+
+/*
+ * One pass over the qkv activation [T, (Hq + 2 Hkv) * D] (row stride
+ * qkv_stride_token): per token, q/k heads are RMS-normalised (weights
+ * q_weight / k_weight, skipped when NULL), rounded to bf16, rotated by
+ * RoPE at positions[t] (full rotary, half-width fp32 cos/sin cache
+ * [max_pos, D/2]), rounded to bf16 and written back in place; the rotated
+ * k row and the raw v row are also written to k_cache / v_cache at slot
+ * out_loc[t] (int32). Bitwise the same as running sgl_qk_rmsnorm, then
+ * sgl_rope, then sgl_store_kv.
+ * Replaces the sequence AttentionLayer::forward -> qk-norm -> RoPE ->
+ * store_kv (src/layers/attention_layer.cc:27-47, flashinfer_backend.cu:530-532).
+ */
+int sgl_fused_qknorm_rope_store(void* qkv, int64_t qkv_stride_token,
+                                void* k_cache, void* v_cache,
+                                const void* q_weight, const void* k_weight,
+                                const float* cos_cache, const float* sin_cache,
+                                const int32_t* positions, const int32_t* out_loc,
+                                int64_t num_tokens, int num_qo_heads,
+                                int num_kv_heads, int head_dim, float eps,
+                                void* stream);
+
+/* ------------------------------------------------------------------ */
+/* Paged attention                                                     */
+/* ------------------------------------------------------------------ */
+
+/* Split-KV decode plan (host). */
+typedef struct {
+  int32_t kv_chunk_size;  /* tokens per split; multiple of 32 */
+  int32_t max_chunks;     /* grid extent along the split axis */
+  int32_t split_kv;       /* 1 when any request spans more than one chunk */
+  int32_t batch_size;
+  int32_t num_qo_heads;
+  int32_t head_dim;
+  int64_t workspace_bytes; /* float workspace the run needs */
+} sgl_decode_plan_t;
+
+/*
+ * Chooses the split size from the host copy of kv_indptr so the launch
+ * has enough work items to fill the GPU, and the workspace that size
+ * implies. Pass a kv_indptr with every request at its maximum length to
+ * build a plan that stays valid for any shorter batch (graph capture).
+ * Replaces: FlashInfer DecodePlan as called from
+ *           FlashInferBackend::initialize_decode_metadata_once
+ *           (src/attention/flashinfer_backend.cu:354-397).
+ */
+int sgl_decode_plan(const int32_t* kv_indptr_host, int batch_size,
+                    int num_qo_heads, int num_kv_heads, int head_dim,
+                    sgl_decode_plan_t* plan);
+
+/*
+ * Paged decode: for request r (rows q[q_row(r)], q_row(r) = r, or
+ * q_indptr[r] when q_indptr is non-NULL) and q head h,
+ * o[q_row, h] = softmax_j(q.K[indices[kv_indptr[r] + j], h / G] * sm_scale)
+ *               . V[indices[...], h / G]
+ * over j < kv_indptr[r+1] - kv_indptr[r]. G = Hq / Hkv. q is strided
+ * (q_stride_token, q_stride_head), o likewise; k_cache/v_cache are one
+ * layer's [slots, Hkv, D] (slot stride kv_stride_slot, head stride
+ * kv_stride_head). workspace holds split partials (plan->workspace_bytes).
+ * Replaces: BatchDecodeWithPagedKVCacheDispatched call in
+ *           FlashInferBackend::forward (src/attention/flashinfer_backend.cu:553-595).
+ */
+int sgl_paged_decode(const sgl_decode_plan_t* plan, const void* q,
+                     int64_t q_stride_token, int64_t q_stride_head,
+                     const void* k_cache, const void* v_cache,
+                     int64_t kv_stride_slot, int64_t kv_stride_head,
+                     const int32_t* indices, const int32_t* kv_indptr,
+                     const int32_t* q_indptr, int batch_size,
+                     int num_qo_heads, int num_kv_heads, int head_dim,
+                     float sm_scale, void* o, int64_t o_stride_token,
+                     int64_t o_stride_head, void* workspace,
+                     int64_t workspace_bytes, void* stream);
+
+/*
+ * Paged causal prefill over ragged requests: query i (0-based inside
+ * request r, qo_len = qo_indptr[r+1]-qo_indptr[r]) attends kv j with
+ * j <= i + kv_len - qo_len (bottom-right alignment), kv_len =
+ * kv_indptr[r+1]-kv_indptr[r], slots from indices[kv_indptr[r] + j].
+ * max_qo_len bounds qo_len over the batch (sizes the grid).
+ * Replaces: BatchPrefillWithPagedKVCacheDispatched<..., kCausal, ...> in
+ *           FlashInferBackend::forward (src/attention/flashinfer_backend.cu:596-679).
+ */
+int sgl_paged_prefill(const void* q, int64_t q_stride_token,
+                      int64_t q_stride_head, const void* k_cache,
+                      const void* v_cache, int64_t kv_stride_slot,
+                      int64_t kv_stride_head, const int32_t* indices,
+                      const int32_t* qo_indptr, const int32_t* kv_indptr,
+                      int batch_size, int max_qo_len, int num_qo_heads,
+                      int num_kv_heads, int head_dim, float sm_scale, void* o,
+                      int64_t o_stride_token, int64_t o_stride_head,
+                      void* stream);
+
+#ifdef __cplusplus
+}  /* extern "C" */
+#endif
+
+#endif  /* SGL_ATTN_H_ */

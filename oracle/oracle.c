@@ -1,0 +1,301 @@
+/*
+ * oracle.c — CPU restatement of the reference attention hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY. This file is the checker the parity tests and
+ * the bench's cpu_baseline leg compare the HIP library against. Nothing in
+ * the product (sglang.cpp_amd/) links, loads or calls it.
+ *
+ * Each function names the reference file:line it restates
+ * (allen-shaw/sglang.cpp). Attention outputs are fp32 (an fp32-softmax
+ * reference); the elementwise kernels reproduce the reference's bf16
+ * rounding points exactly. How each function is pinned (closed forms,
+ * library routines, invariants) is listed in DESIGN.md; none is left
+ * unpinned.
+ *
+ * Build: oracle/Makefile (gcc, OpenMP). Floating-point contraction is off so
+ * products and sums round exactly as written.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+/* ---------- bf16 ---------- */
+
+static inline float bf16_to_f32(uint16_t b) {
+  uint32_t u = (uint32_t)b << 16;
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+/* Round to nearest even, NaN kept quiet (what a bf16 cast does). */
+static inline uint16_t f32_to_bf16(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+int oracle_threads(void) {
+#ifdef _OPENMP
+  return omp_get_max_threads();
+#else
+  return 1;
+#endif
+}
+
+void oracle_set_threads(int n) {
+#ifdef _OPENMP
+  if (n > 0) omp_set_num_threads(n);
+#else
+  (void)n;
+#endif
+}
+
+void oracle_f32_to_bf16(const float* in, uint16_t* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = f32_to_bf16(in[i]);
+}
+
+/* ---------- KV store: src/kvcache/mha_kvcache.cu:13-41 ---------- */
+
+void oracle_store_kv(uint16_t* k_cache, uint16_t* v_cache, const uint16_t* k,
+                     const uint16_t* v, const int64_t* out_loc, int64_t num_tokens,
+                     int64_t elems, int64_t k_stride, int64_t v_stride) {
+  for (int64_t t = 0; t < num_tokens; ++t) {
+    const int64_t slot = out_loc[t];
+    memcpy(k_cache + slot * elems, k + t * k_stride, (size_t)elems * 2);
+    memcpy(v_cache + slot * elems, v + t * v_stride, (size_t)elems * 2);
+  }
+}
+
+/* ---------- decode indices: src/attention/flashinfer_backend.cu:43-70 ---------- */
+
+void oracle_build_indices(const int32_t* page_table, int64_t rows, int64_t stride,
+                          int64_t cols, const int32_t* table_indices,
+                          const int32_t* kv_indptr, int32_t* indices, int batch) {
+  for (int r = 0; r < batch; ++r) {
+    const int32_t row = table_indices[r];
+    const int32_t start = kv_indptr[r];
+    const int32_t len = kv_indptr[r + 1] - start;
+    if (row < 0 || row >= rows || len <= 0) continue;
+    for (int32_t p = 0; p < len; ++p)
+      indices[start + p] = p < cols ? page_table[(int64_t)row * stride + p] : 0;
+  }
+}
+
+/* ---------- token pool: src/kernels/token_pool.cu:10-49 ---------- */
+
+void oracle_write_token_pool(int32_t* pool, int64_t rows, int64_t stride, int64_t cols,
+                             const int32_t* req, const int32_t* pos, const int32_t* tok,
+                             int64_t count) {
+  for (int64_t i = 0; i < count; ++i) {
+    const int64_t r = req[i], p = pos[i];
+    if (r < 0 || r >= rows || p < 0 || p >= cols) continue;
+    pool[r * stride + p] = tok[i];
+  }
+}
+
+void oracle_gather_int32_2d(const int32_t* table, int64_t rows, int64_t stride, int64_t cols,
+                            const int32_t* req, const int32_t* pos, int32_t* out,
+                            int64_t count) {
+  for (int64_t i = 0; i < count; ++i) {
+    const int64_t r = req[i], p = pos[i];
+    out[i] = (r >= 0 && r < rows && p >= 0 && p < cols) ? table[r * stride + p] : 0;
+  }
+}
+
+/* ---------- page allocation -> page table: src/scheduler/prefill.cc:103-187 ----------
+ * Expands page starts (slot of a page's first token) into token slots and
+ * writes row table_idx, positions [first_page*P, last_page*P).           */
+void oracle_pages_to_tokens(const int32_t* page_starts, int64_t npages, int page_size,
+                            int32_t* tokens) {
+  for (int64_t p = 0; p < npages; ++p)
+    for (int i = 0; i < page_size; ++i) tokens[p * page_size + i] = page_starts[p] + i;
+}
+
+/* ---------- RoPE cache: src/layers/rotary_embedding.cu:75-94 ---------- */
+
+void oracle_cos_sin_cache(float* cos_cache, float* sin_cache, int64_t max_pos, int rotary_dim,
+                          float base) {
+  const int half = rotary_dim / 2;
+  for (int k = 0; k < half; ++k) {
+    const float expo = (float)(2 * k) / (float)rotary_dim;
+    const float inv_freq = 1.0f / powf(base, expo);
+    for (int64_t p = 0; p < max_pos; ++p) {
+      const float f = (float)p * inv_freq;
+      cos_cache[p * half + k] = cosf(f);
+      sin_cache[p * half + k] = sinf(f);
+    }
+  }
+}
+
+/* ---------- q/k RMSNorm: src/layers/normalization.cu:99-170 ---------- */
+
+static void rmsnorm_row(uint16_t* row, const uint16_t* w, int64_t d, float eps) {
+  float ss = 0.f;
+  for (int64_t i = 0; i < d; ++i) {
+    const float x = bf16_to_f32(row[i]);
+    ss += x * x;
+  }
+  const float scale = 1.0f / sqrtf(ss / (float)d + eps);
+  for (int64_t i = 0; i < d; ++i)
+    row[i] = f32_to_bf16((bf16_to_f32(row[i]) * scale) * bf16_to_f32(w[i]));
+}
+
+void oracle_qk_rmsnorm(uint16_t* q, uint16_t* k, const uint16_t* qw, const uint16_t* kw,
+                       int64_t tokens, int64_t qh, int64_t kh, int64_t d, int64_t q_st,
+                       int64_t q_sh, int64_t k_st, int64_t k_sh, float eps) {
+  for (int64_t t = 0; t < tokens; ++t) {
+    for (int64_t h = 0; h < qh; ++h) rmsnorm_row(q + t * q_st + h * q_sh, qw, d, eps);
+    if (k)
+      for (int64_t h = 0; h < kh; ++h) rmsnorm_row(k + t * k_st + h * k_sh, kw, d, eps);
+  }
+}
+
+/* ---------- RoPE: src/layers/rotary_embedding.cu:50-66 (NeoX rotate-half) ---------- */
+
+static void rope_row(uint16_t* row, const float* cos_row, const float* sin_row,
+                     int64_t rotary_dim, int64_t cos_width) {
+  const int64_t half = rotary_dim / 2;
+  float buf[4096];
+  for (int64_t i = 0; i < rotary_dim; ++i) {
+    const int first = i < half;
+    const int64_t pair = first ? i : i - half;
+    const int64_t other = first ? i + half : i - half;
+    const int64_t ci = cos_width == rotary_dim ? i : pair;
+    const float v = bf16_to_f32(row[i]);
+    const float o = bf16_to_f32(row[other]);
+    const float c = cos_row[ci], s = sin_row[ci];
+    buf[i] = first ? (v * c - o * s) : (v * c + o * s);
+  }
+  for (int64_t i = 0; i < rotary_dim; ++i) row[i] = f32_to_bf16(buf[i]);
+}
+
+int oracle_rope(uint16_t* q, uint16_t* k, const float* cos_cache, const float* sin_cache,
+                const int32_t* positions, int64_t nnz, int64_t qh, int64_t kh,
+                int64_t rotary_dim, int64_t cos_width, int64_t q_st, int64_t q_sh,
+                int64_t k_st, int64_t k_sh) {
+  if (rotary_dim > 4096) return -1;
+  for (int64_t t = 0; t < nnz; ++t) {
+    const int64_t p = positions[t];
+    const float* cr = cos_cache + p * cos_width;
+    const float* sr = sin_cache + p * cos_width;
+    for (int64_t h = 0; h < qh; ++h) rope_row(q + t * q_st + h * q_sh, cr, sr, rotary_dim, cos_width);
+    for (int64_t h = 0; h < kh; ++h) rope_row(k + t * k_st + h * k_sh, cr, sr, rotary_dim, cos_width);
+  }
+  return 0;
+}
+
+/* ---------- attention core (fp32 softmax) ----------
+ * o[h, :] = sum_j softmax_j(q[h].K[j] * sm_scale) V[j], over the visible j.
+ * The max-subtracted softmax of src/attention/flashinfer_backend.cu:553-679
+ * (FlashInfer's online softmax computes the same quantity).             */
+
+static void attend_row(const uint16_t* qrow, const uint16_t* k_cache, const uint16_t* v_cache,
+                       int64_t kv_ss, const int32_t* slots, int64_t nvis, int64_t D,
+                       float sm_scale, float* out, float* scores, float* qf) {
+  for (int64_t d = 0; d < D; ++d) qf[d] = bf16_to_f32(qrow[d]);
+  float mx = -INFINITY;
+  for (int64_t j = 0; j < nvis; ++j) {
+    const uint16_t* kr = k_cache + (int64_t)slots[j] * kv_ss;
+    float s = 0.f;
+    for (int64_t d = 0; d < D; ++d) s += qf[d] * bf16_to_f32(kr[d]);
+    s *= sm_scale;
+    scores[j] = s;
+    if (s > mx) mx = s;
+  }
+  float den = 0.f;
+  for (int64_t j = 0; j < nvis; ++j) {
+    scores[j] = expf(scores[j] - mx);
+    den += scores[j];
+  }
+  for (int64_t d = 0; d < D; ++d) out[d] = 0.f;
+  for (int64_t j = 0; j < nvis; ++j) {
+    const uint16_t* vr = v_cache + (int64_t)slots[j] * kv_ss;
+    const float p = scores[j] / den;
+    for (int64_t d = 0; d < D; ++d) out[d] += p * bf16_to_f32(vr[d]);
+  }
+}
+
+/* Decode: src/attention/flashinfer_backend.cu:553-595. out is fp32
+ * [rows, hq, D] contiguous; q row of request r is q_indptr ? q_indptr[r] : r.
+ * kv_ss / kv_sh: slot and head strides of one layer's cache (elements).  */
+void oracle_decode(const uint16_t* q, int64_t q_st, int64_t q_sh, const uint16_t* k_cache,
+                   const uint16_t* v_cache, int64_t kv_ss, int64_t kv_sh,
+                   const int32_t* indices, const int32_t* kv_indptr, const int32_t* q_indptr,
+                   int batch, int hq, int hkv, int D, float sm_scale, float* out) {
+  const int G = hq / hkv;
+#pragma omp parallel
+  {
+    int64_t maxlen = 0;
+    for (int r = 0; r < batch; ++r) {
+      const int64_t len = kv_indptr[r + 1] - kv_indptr[r];
+      if (len > maxlen) maxlen = len;
+    }
+    float* scores = (float*)malloc(sizeof(float) * (size_t)(maxlen + 1));
+    float* qf = (float*)malloc(sizeof(float) * (size_t)D);
+#pragma omp for schedule(dynamic)
+    for (int64_t rh = 0; rh < (int64_t)batch * hq; ++rh) {
+      const int r = (int)(rh / hq), h = (int)(rh % hq);
+      const int64_t row = q_indptr ? q_indptr[r] : r;
+      const int64_t beg = kv_indptr[r], len = kv_indptr[r + 1] - beg;
+      float* o = out + (row * hq + h) * D;
+      if (len <= 0) {
+        for (int d = 0; d < D; ++d) o[d] = 0.f;
+        continue;
+      }
+      const int64_t kvh = h / G;
+      attend_row(q + row * q_st + h * q_sh, k_cache + kvh * kv_sh, v_cache + kvh * kv_sh, kv_ss,
+                 indices + beg, len, D, sm_scale, o, scores, qf);
+    }
+    free(scores);
+    free(qf);
+  }
+}
+
+/* Causal prefill: src/attention/flashinfer_backend.cu:596-679 (kCausal):
+ * query i of request r sees kv j <= i + kv_len - qo_len. out fp32 [sum qo, hq, D]. */
+void oracle_prefill(const uint16_t* q, int64_t q_st, int64_t q_sh, const uint16_t* k_cache,
+                    const uint16_t* v_cache, int64_t kv_ss, int64_t kv_sh,
+                    const int32_t* indices, const int32_t* qo_indptr, const int32_t* kv_indptr,
+                    int batch, int hq, int hkv, int D, float sm_scale, float* out) {
+  const int G = hq / hkv;
+  int64_t total_rows = qo_indptr[batch];
+#pragma omp parallel
+  {
+    int64_t maxlen = 0;
+    for (int r = 0; r < batch; ++r) {
+      const int64_t len = kv_indptr[r + 1] - kv_indptr[r];
+      if (len > maxlen) maxlen = len;
+    }
+    float* scores = (float*)malloc(sizeof(float) * (size_t)(maxlen + 1));
+    float* qf = (float*)malloc(sizeof(float) * (size_t)D);
+#pragma omp for schedule(dynamic, 4)
+    for (int64_t th = 0; th < total_rows * hq; ++th) {
+      const int64_t row = th / hq;
+      const int h = (int)(th % hq);
+      int r = 0;
+      while (qo_indptr[r + 1] <= row) ++r;
+      const int64_t i = row - qo_indptr[r];
+      const int64_t qo_len = qo_indptr[r + 1] - qo_indptr[r];
+      const int64_t beg = kv_indptr[r], kv_len = kv_indptr[r + 1] - beg;
+      int64_t nvis = i + kv_len - qo_len + 1;
+      if (nvis > kv_len) nvis = kv_len;
+      float* o = out + (row * hq + h) * D;
+      if (nvis <= 0) {
+        for (int d = 0; d < D; ++d) o[d] = 0.f;
+        continue;
+      }
+      const int64_t kvh = h / G;
+      attend_row(q + row * q_st + h * q_sh, k_cache + kvh * kv_sh, v_cache + kvh * kv_sh, kv_ss,
+                 indices + beg, nvis, D, sm_scale, o, scores, qf);
+    }
+    free(scores);
+    free(qf);
+  }
+}

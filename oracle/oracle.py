@@ -1,0 +1,179 @@
+"""ctypes front end of the CPU oracle (oracle.c) — TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg use
+this module, always as the checker and never as the thing measured or
+shipped. Arrays are numpy; bf16 is carried as uint16 bit patterns.
+"""
+from __future__ import annotations
+
+import ctypes
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+ORACLE_DIR = Path(__file__).resolve().parent
+LIB_PATH = ORACLE_DIR / "liboracle.so"
+
+_lib = None
+
+
+def build() -> Path:
+    res = subprocess.run(["make", "-C", str(ORACLE_DIR), "-s"], capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"oracle build failed:\n{res.stdout}\n{res.stderr}")
+    return LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            build()
+        _lib = ctypes.CDLL(str(LIB_PATH))
+        _lib.oracle_threads.restype = ctypes.c_int
+    return _lib
+
+
+def _p(a: np.ndarray | None):
+    if a is None:
+        return None
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _row_stride(a: np.ndarray) -> int:
+    """Row stride in elements of a 2-D array whose rows are contiguous."""
+    assert a.ndim == 2
+    if a.size == 0:
+        return a.shape[1]
+    assert a.strides[1] == a.itemsize, "rows must be contiguous"
+    return a.strides[0] // a.itemsize
+
+
+I64 = ctypes.c_int64
+F32 = ctypes.c_float
+
+
+# ---------------------------------------------------------------- bf16 helpers
+
+def f32_to_bf16(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, dtype=np.uint16)
+    lib().oracle_f32_to_bf16(_p(x), _p(out), I64(x.size))
+    return out
+
+
+def bf16_to_f32(b: np.ndarray) -> np.ndarray:
+    return (np.asarray(b, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def threads() -> int:
+    return lib().oracle_threads()
+
+
+def set_threads(n: int) -> None:
+    lib().oracle_set_threads(ctypes.c_int(n))
+
+
+# ---------------------------------------------------------------- kernels
+
+def store_kv(k_cache, v_cache, k, v, out_loc) -> None:
+    """k_cache/v_cache: contiguous uint16 [slots, elems]; k/v: uint16 [T, >= elems]
+    row-strided views (e.g. slices of a qkv row); the first elems of each row are stored."""
+    out_loc = np.ascontiguousarray(out_loc, dtype=np.int64)
+    assert k_cache.flags["C_CONTIGUOUS"] and v_cache.flags["C_CONTIGUOUS"]
+    elems = k_cache.shape[1]
+    assert k.shape[1] >= elems and v.shape[1] >= elems
+    lib().oracle_store_kv(_p(k_cache), _p(v_cache), _p(k), _p(v), _p(out_loc), I64(len(out_loc)),
+                          I64(elems), I64(_row_stride(k)), I64(_row_stride(v)))
+
+
+def build_indices(page_table, table_indices, kv_indptr) -> np.ndarray:
+    pt = np.ascontiguousarray(page_table, dtype=np.int32)
+    ti = np.ascontiguousarray(table_indices, dtype=np.int32)
+    ip = np.ascontiguousarray(kv_indptr, dtype=np.int32)
+    out = np.zeros(int(ip[-1]) if len(ip) else 0, dtype=np.int32)
+    lib().oracle_build_indices(_p(pt), I64(pt.shape[0]), I64(pt.shape[1]), I64(pt.shape[1]),
+                               _p(ti), _p(ip), _p(out), ctypes.c_int(len(ti)))
+    return out
+
+
+def write_token_pool(pool, req, pos, tok) -> None:
+    req = np.ascontiguousarray(req, np.int32)
+    pos = np.ascontiguousarray(pos, np.int32)
+    tok = np.ascontiguousarray(tok, np.int32)
+    lib().oracle_write_token_pool(_p(pool), I64(pool.shape[0]), I64(pool.shape[1]),
+                                  I64(pool.shape[1]), _p(req), _p(pos), _p(tok), I64(len(tok)))
+
+
+def gather_int32_2d(table, req, pos) -> np.ndarray:
+    table = np.ascontiguousarray(table, np.int32)
+    req = np.ascontiguousarray(req, np.int32)
+    pos = np.ascontiguousarray(pos, np.int32)
+    out = np.empty(len(req), np.int32)
+    lib().oracle_gather_int32_2d(_p(table), I64(table.shape[0]), I64(table.shape[1]),
+                                 I64(table.shape[1]), _p(req), _p(pos), _p(out), I64(len(req)))
+    return out
+
+
+def pages_to_tokens(page_starts, page_size: int) -> np.ndarray:
+    ps = np.ascontiguousarray(page_starts, np.int32)
+    out = np.empty(len(ps) * page_size, np.int32)
+    lib().oracle_pages_to_tokens(_p(ps), I64(len(ps)), ctypes.c_int(page_size), _p(out))
+    return out
+
+
+def cos_sin_cache(max_pos: int, rotary_dim: int, base: float):
+    cos = np.empty((max_pos, rotary_dim // 2), np.float32)
+    sin = np.empty_like(cos)
+    lib().oracle_cos_sin_cache(_p(cos), _p(sin), I64(max_pos), ctypes.c_int(rotary_dim), F32(base))
+    return cos, sin
+
+
+def qk_rmsnorm(q, k, qw, kw, eps: float) -> None:
+    """In place on uint16 arrays q [T, Hq, D], k [T, Hk, D] (contiguous)."""
+    T, qh, d = q.shape
+    kh = 0 if k is None else k.shape[1]
+    lib().oracle_qk_rmsnorm(_p(q), _p(k), _p(qw), _p(kw), I64(T), I64(qh), I64(kh), I64(d),
+                            I64(qh * d), I64(d), I64(kh * d), I64(d), F32(eps))
+
+
+def rope(q, k, cos, sin, positions, rotary_dim: int | None = None) -> None:
+    T, qh, d = q.shape
+    kh = k.shape[1]
+    rd = d if rotary_dim is None else rotary_dim
+    pos = np.ascontiguousarray(positions, np.int32)
+    rc = lib().oracle_rope(_p(q), _p(k), _p(cos), _p(sin), _p(pos), I64(T), I64(qh), I64(kh),
+                           I64(rd), I64(cos.shape[1]), I64(qh * d), I64(d), I64(kh * d), I64(d))
+    assert rc == 0
+
+
+def decode(q, k_cache, v_cache, indices, kv_indptr, sm_scale: float, q_indptr=None) -> np.ndarray:
+    """q: uint16 [rows, Hq, D]; caches: uint16 [slots, Hkv, D]. Returns fp32 [rows, Hq, D]."""
+    rows, hq, D = q.shape
+    hkv = k_cache.shape[1]
+    B = len(kv_indptr) - 1
+    out = np.zeros((rows, hq, D), np.float32)
+    qi = None if q_indptr is None else np.ascontiguousarray(q_indptr, np.int32)
+    lib().oracle_decode(_p(np.ascontiguousarray(q)), I64(hq * D), I64(D),
+                        _p(k_cache), _p(v_cache), I64(hkv * D), I64(D),
+                        _p(np.ascontiguousarray(indices, np.int32)),
+                        _p(np.ascontiguousarray(kv_indptr, np.int32)), _p(qi), ctypes.c_int(B),
+                        ctypes.c_int(hq), ctypes.c_int(hkv), ctypes.c_int(D), F32(sm_scale),
+                        _p(out))
+    return out
+
+
+def prefill(q, k_cache, v_cache, indices, qo_indptr, kv_indptr, sm_scale: float) -> np.ndarray:
+    rows, hq, D = q.shape
+    hkv = k_cache.shape[1]
+    B = len(qo_indptr) - 1
+    out = np.zeros((rows, hq, D), np.float32)
+    lib().oracle_prefill(_p(np.ascontiguousarray(q)), I64(hq * D), I64(D),
+                         _p(k_cache), _p(v_cache), I64(hkv * D), I64(D),
+                         _p(np.ascontiguousarray(indices, np.int32)),
+                         _p(np.ascontiguousarray(qo_indptr, np.int32)),
+                         _p(np.ascontiguousarray(kv_indptr, np.int32)), ctypes.c_int(B),
+                         ctypes.c_int(hq), ctypes.c_int(hkv), ctypes.c_int(D), F32(sm_scale),
+                         _p(out))
+    return out

@@ -1,0 +1,340 @@
+"""ctypes binding of libsgl_attn.so (the C ABI in include/sgl_attn.h).
+
+Thin tensor-level wrappers used by the tests and the bench: each function
+checks shapes and dtypes the way the reference's TORCH_CHECKs do, passes
+raw device pointers, strides and the current HIP stream, and raises
+SglError on a non-zero status. There is no fallback: if the library is
+not built, or a call is made on a tensor that is not on a HIP device,
+the call raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+from pathlib import Path
+from typing import Optional, Sequence
+
+import torch
+
+PKG_DIR = Path(__file__).resolve().parent
+LIB_PATH = PKG_DIR / "libsgl_attn.so"
+HEADER_PATH = PKG_DIR.parent / "include" / "sgl_attn.h"
+
+SGL_INDEX_I32 = 0
+SGL_INDEX_I64 = 1
+ABI_VERSION = 1
+
+
+class SglError(RuntimeError):
+    def __init__(self, status: int, what: str):
+        self.status = status
+        super().__init__(f"{what} failed: status {status} ({status_string(status)})")
+
+
+class DecodePlan(ctypes.Structure):
+    _fields_ = [
+        ("kv_chunk_size", ctypes.c_int32),
+        ("max_chunks", ctypes.c_int32),
+        ("split_kv", ctypes.c_int32),
+        ("batch_size", ctypes.c_int32),
+        ("num_qo_heads", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("workspace_bytes", ctypes.c_int64),
+    ]
+
+
+_lib: Optional[ctypes.CDLL] = None
+
+_vp = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_i32 = ctypes.c_int
+_f32 = ctypes.c_float
+
+_SIGNATURES = {
+    "sgl_status_string": ([_i32], ctypes.c_char_p),
+    "sgl_abi_version": ([], _i32),
+    "sgl_store_kv": ([_vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i64, _vp], _i32),
+    "sgl_build_decode_indices": ([_vp, _i64, _i64, _i64, _vp, _vp, _vp, _i32, _vp], _i32),
+    "sgl_build_prefill_indices": ([_vp, _i64, _i64, _i64, _vp, _vp, _vp, _i32, _vp], _i32),
+    "sgl_write_token_pool": ([_vp, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _vp], _i32),
+    "sgl_gather_int32_2d": ([_vp, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _vp], _i32),
+    "sgl_rope_cos_sin_cache": ([_vp, _vp, _i64, _i32, _f32, _vp], _i32),
+    "sgl_qk_rmsnorm": ([_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                        _f32, _vp], _i32),
+    "sgl_rope": ([_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                  _i64, _i64, _vp], _i32),
+    "sgl_fused_qknorm_rope_store": ([_vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64,
+                                     _i32, _i32, _i32, _f32, _vp], _i32),
+    "sgl_decode_plan": ([_vp, _i32, _i32, _i32, _i32, ctypes.POINTER(DecodePlan)], _i32),
+    "sgl_paged_decode": ([ctypes.POINTER(DecodePlan), _vp, _i64, _i64, _vp, _vp, _i64, _i64,
+                          _vp, _vp, _vp, _i32, _i32, _i32, _i32, _f32, _vp, _i64, _i64, _vp,
+                          _i64, _vp], _i32),
+    "sgl_paged_prefill": ([_vp, _i64, _i64, _vp, _vp, _i64, _i64, _vp, _vp, _vp, _i32, _i32,
+                           _i32, _i32, _i32, _f32, _vp, _i64, _i64, _vp], _i32),
+}
+
+
+def lib() -> ctypes.CDLL:
+    """Load the library once. Raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build it with __graft_entry__.build() "
+                "(python sglang.cpp_amd/build.py)")
+        handle = ctypes.CDLL(str(LIB_PATH))
+        for name, (args, res) in _SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.argtypes = args
+            fn.restype = res
+        if handle.sgl_abi_version() != ABI_VERSION:
+            raise RuntimeError("libsgl_attn.so ABI version does not match capi.py")
+        _lib = handle
+    return _lib
+
+
+def exported_symbols() -> Sequence[str]:
+    return tuple(_SIGNATURES)
+
+
+def status_string(status: int) -> str:
+    try:
+        return lib().sgl_status_string(status).decode()
+    except Exception:  # library not loadable: still format the error
+        return "unknown"
+
+
+def _check(status: int, what: str) -> None:
+    if status != 0:
+        raise SglError(status, what)
+
+
+def _p(t: Optional[torch.Tensor]):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(dev: torch.device):
+    return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+
+def _need_gpu(*ts: Optional[torch.Tensor]) -> torch.device:
+    dev = None
+    for t in ts:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise ValueError("sgl_attn ops take HIP device tensors only")
+        dev = t.device if dev is None else dev
+        if t.device != dev:
+            raise ValueError("all tensors must be on the same device")
+    return dev
+
+
+# ---------------------------------------------------------------- KV store
+
+def store_kv(k_cache: torch.Tensor, v_cache: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+             out_loc: torch.Tensor) -> None:
+    """MHAKVCache::store_kv semantics (src/kvcache/mha_kvcache.cu:111-155).
+
+    k_cache/v_cache: one layer's [slots, Hkv, D]; k/v: [T, Hkv, D] or
+    [T, Hkv*D] views with a contiguous last dim; out_loc int32/int64 [T].
+    """
+    dev = _need_gpu(k_cache, v_cache, k, v, out_loc)
+    if k.dtype != v.dtype or k.dtype != k_cache.dtype or k.element_size() != 2:
+        raise ValueError("key, val and cache must share a 2-byte dtype (bf16/fp16)")
+    if k.stride(-1) != 1 or v.stride(-1) != 1:
+        raise ValueError("key and val last dimension must be contiguous")
+    if out_loc.dim() != 1:
+        raise ValueError("out_loc must be rank 1")
+    if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
+        raise ValueError("KV cache buffers must be contiguous")
+    elems = k_cache.shape[1:].numel()
+    T = k.shape[0]
+    if v.shape[0] != T or out_loc.shape[0] != T:
+        raise ValueError("key, val and out_loc token counts must match")
+    if k.shape[1:].numel() != elems or v.shape[1:].numel() != elems:
+        raise ValueError("key and val shape must match KV cache layout")
+    if out_loc.dtype == torch.int32:
+        idt = SGL_INDEX_I32
+    elif out_loc.dtype == torch.int64:
+        idt = SGL_INDEX_I64
+    else:
+        raise ValueError("out_loc must be int32 or int64")
+    _check(lib().sgl_store_kv(_p(k_cache), _p(v_cache), _p(k), _p(v), _p(out_loc), idt, T, elems,
+                              k.stride(0), v.stride(0), _stream(dev)), "sgl_store_kv")
+
+
+# ---------------------------------------------------------------- metadata
+
+def _table_args(t: torch.Tensor):
+    if t.dtype != torch.int32 or t.dim() != 2 or t.stride(1) != 1:
+        raise ValueError("page table / token pool must be a 2-D int32 tensor, unit column stride")
+    return t.shape[0], t.stride(0), t.shape[1]
+
+
+def build_decode_indices(page_table: torch.Tensor, table_indices: torch.Tensor,
+                         kv_indptr: torch.Tensor, indices: torch.Tensor) -> None:
+    dev = _need_gpu(page_table, table_indices, kv_indptr, indices)
+    rows, stride, cols = _table_args(page_table)
+    B = table_indices.shape[0]
+    _check(lib().sgl_build_decode_indices(_p(page_table), rows, stride, cols, _p(table_indices),
+                                          _p(kv_indptr), _p(indices), B, _stream(dev)),
+           "sgl_build_decode_indices")
+
+
+def build_prefill_indices(page_table: torch.Tensor, table_indices: torch.Tensor,
+                          kv_indptr: torch.Tensor, indices: torch.Tensor) -> None:
+    dev = _need_gpu(page_table, table_indices, kv_indptr, indices)
+    rows, stride, cols = _table_args(page_table)
+    B = table_indices.shape[0]
+    _check(lib().sgl_build_prefill_indices(_p(page_table), rows, stride, cols, _p(table_indices),
+                                           _p(kv_indptr), _p(indices), B, _stream(dev)),
+           "sgl_build_prefill_indices")
+
+
+def write_token_pool(pool: torch.Tensor, req_indices: torch.Tensor, positions: torch.Tensor,
+                     tokens: torch.Tensor) -> None:
+    """write_token_pool (src/kernels/token_pool.cu:53-93)."""
+    dev = _need_gpu(pool, req_indices, positions, tokens)
+    rows, stride, cols = _table_args(pool)
+    for t in (req_indices, positions, tokens):
+        if t.dtype != torch.int32 or t.dim() != 1:
+            raise ValueError("req_indices, positions and tokens must be 1-D int32")
+    if not (req_indices.numel() == positions.numel() == tokens.numel()):
+        raise ValueError("req_indices, positions and tokens must have the same length")
+    _check(lib().sgl_write_token_pool(_p(pool), rows, stride, cols, _p(req_indices),
+                                      _p(positions), _p(tokens), tokens.numel(), _stream(dev)),
+           "sgl_write_token_pool")
+
+
+def gather_int32_2d(table: torch.Tensor, req_indices: torch.Tensor,
+                    positions: torch.Tensor) -> torch.Tensor:
+    """gather_int32_2d (src/kernels/token_pool.cu:95-133)."""
+    dev = _need_gpu(table, req_indices, positions)
+    rows, stride, cols = _table_args(table)
+    if req_indices.numel() != positions.numel():
+        raise ValueError("req_indices and positions must have the same length")
+    out = torch.empty(req_indices.numel(), dtype=torch.int32, device=dev)
+    _check(lib().sgl_gather_int32_2d(_p(table), rows, stride, cols, _p(req_indices),
+                                     _p(positions), _p(out), out.numel(), _stream(dev)),
+           "sgl_gather_int32_2d")
+    return out
+
+
+# ---------------------------------------------------------------- RoPE / norm
+
+def rope_cos_sin_cache(max_pos: int, rotary_dim: int, base: float,
+                       device: torch.device) -> tuple[torch.Tensor, torch.Tensor]:
+    cos = torch.empty((max_pos, rotary_dim // 2), dtype=torch.float32, device=device)
+    sin = torch.empty_like(cos)
+    _check(lib().sgl_rope_cos_sin_cache(_p(cos), _p(sin), max_pos, rotary_dim, base,
+                                        _stream(cos.device)), "sgl_rope_cos_sin_cache")
+    return cos, sin
+
+
+def qk_rmsnorm(q: torch.Tensor, k: Optional[torch.Tensor], q_weight: torch.Tensor,
+               k_weight: Optional[torch.Tensor], eps: float) -> None:
+    """fused_qk_rmsnorm_inplace_3d_strided (src/layers/normalization.cu:318-384), in place."""
+    dev = _need_gpu(q, k, q_weight, k_weight)
+    if q.dim() != 3 or q.stride(2) != 1 or (k is not None and (k.dim() != 3 or k.stride(2) != 1)):
+        raise ValueError("q/k must be rank-3 with a contiguous last dimension")
+    if q.dtype != torch.bfloat16 or (k is not None and k.dtype != torch.bfloat16):
+        raise ValueError("q/k must be bf16")
+    d = q.shape[2]
+    kh = 0 if k is None else k.shape[1]
+    _check(lib().sgl_qk_rmsnorm(_p(q), _p(k), _p(q_weight), _p(k_weight), q.shape[0], q.shape[1],
+                                kh, d, q.stride(0), q.stride(1),
+                                0 if k is None else k.stride(0), 0 if k is None else k.stride(1),
+                                eps, _stream(dev)), "sgl_qk_rmsnorm")
+
+
+def rope(positions: torch.Tensor, q: torch.Tensor, k: torch.Tensor, cos_cache: torch.Tensor,
+         sin_cache: torch.Tensor, rotary_dim: Optional[int] = None) -> None:
+    """RotaryEmbedding::forward_inplace (src/layers/rotary_embedding.cu:96-178), in place."""
+    dev = _need_gpu(positions, q, k, cos_cache, sin_cache)
+    head_dim = q.shape[2]
+    rd = head_dim if rotary_dim is None else rotary_dim
+    if positions.dtype != torch.int32:
+        raise ValueError("positions must be int32")
+    _check(lib().sgl_rope(_p(q), _p(k), _p(cos_cache), _p(sin_cache), _p(positions),
+                          positions.shape[0], q.shape[1], k.shape[1], rd, head_dim,
+                          cos_cache.shape[1], q.stride(0), q.stride(1), k.stride(0), k.stride(1),
+                          _stream(dev)), "sgl_rope")
+
+
+def fused_qknorm_rope_store(qkv: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                            q_weight: Optional[torch.Tensor], k_weight: Optional[torch.Tensor],
+                            cos_cache: torch.Tensor, sin_cache: torch.Tensor,
+                            positions: torch.Tensor, out_loc: torch.Tensor, num_qo_heads: int,
+                            num_kv_heads: int, head_dim: int, eps: float) -> None:
+    dev = _need_gpu(qkv, k_cache, v_cache, q_weight, k_weight, cos_cache, sin_cache, positions,
+                    out_loc)
+    if qkv.dtype != torch.bfloat16 or qkv.dim() != 2 or qkv.stride(1) != 1:
+        raise ValueError("qkv must be a 2-D bf16 tensor with a contiguous last dimension")
+    if out_loc.dtype != torch.int32 or positions.dtype != torch.int32:
+        raise ValueError("positions and out_loc must be int32")
+    _check(lib().sgl_fused_qknorm_rope_store(
+        _p(qkv), qkv.stride(0), _p(k_cache), _p(v_cache), _p(q_weight), _p(k_weight),
+        _p(cos_cache), _p(sin_cache), _p(positions), _p(out_loc), qkv.shape[0], num_qo_heads,
+        num_kv_heads, head_dim, eps, _stream(dev)), "sgl_fused_qknorm_rope_store")
+
+
+# ---------------------------------------------------------------- attention
+
+def decode_plan(kv_indptr_host: Sequence[int], num_qo_heads: int, num_kv_heads: int,
+                head_dim: int) -> DecodePlan:
+    arr = (ctypes.c_int32 * len(kv_indptr_host))(*[int(x) for x in kv_indptr_host])
+    plan = DecodePlan()
+    _check(lib().sgl_decode_plan(ctypes.cast(arr, ctypes.c_void_p), len(kv_indptr_host) - 1,
+                                 num_qo_heads, num_kv_heads, head_dim, ctypes.byref(plan)),
+           "sgl_decode_plan")
+    return plan
+
+
+def _kv_strides(k_cache: torch.Tensor):
+    if k_cache.dim() != 3 or k_cache.stride(2) != 1:
+        raise ValueError("KV cache layer must be [slots, Hkv, D] with a contiguous last dim")
+    return k_cache.stride(0), k_cache.stride(1)
+
+
+def paged_decode(plan: DecodePlan, q: torch.Tensor, k_cache: torch.Tensor,
+                 v_cache: torch.Tensor, indices: torch.Tensor, kv_indptr: torch.Tensor,
+                 o: torch.Tensor, workspace: Optional[torch.Tensor],
+                 sm_scale: Optional[float] = None,
+                 q_indptr: Optional[torch.Tensor] = None) -> None:
+    dev = _need_gpu(q, k_cache, v_cache, indices, kv_indptr, o, workspace, q_indptr)
+    if q.dtype != torch.bfloat16 or k_cache.dtype != torch.bfloat16 or o.dtype != torch.bfloat16:
+        raise ValueError("decode supports bf16 q / KV / o only")
+    hq, D = q.shape[1], q.shape[2]
+    hkv = k_cache.shape[1]
+    ss, sh = _kv_strides(k_cache)
+    if v_cache.stride() != k_cache.stride():
+        raise ValueError("K and V caches must share strides")
+    B = kv_indptr.shape[0] - 1
+    scale = 1.0 / math.sqrt(D) if sm_scale is None else sm_scale
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    _check(lib().sgl_paged_decode(ctypes.byref(plan), _p(q), q.stride(0), q.stride(1),
+                                  _p(k_cache), _p(v_cache), ss, sh, _p(indices), _p(kv_indptr),
+                                  _p(q_indptr), B, hq, hkv, D, scale, _p(o), o.stride(0),
+                                  o.stride(1), _p(workspace), ws_bytes, _stream(dev)),
+           "sgl_paged_decode")
+
+
+def paged_prefill(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                  indices: torch.Tensor, qo_indptr: torch.Tensor, kv_indptr: torch.Tensor,
+                  max_qo_len: int, o: torch.Tensor, sm_scale: Optional[float] = None) -> None:
+    dev = _need_gpu(q, k_cache, v_cache, indices, qo_indptr, kv_indptr, o)
+    if q.dtype != torch.bfloat16 or k_cache.dtype != torch.bfloat16 or o.dtype != torch.bfloat16:
+        raise ValueError("prefill supports bf16 q / KV / o only")
+    hq, D = q.shape[1], q.shape[2]
+    hkv = k_cache.shape[1]
+    ss, sh = _kv_strides(k_cache)
+    if v_cache.stride() != k_cache.stride():
+        raise ValueError("K and V caches must share strides")
+    B = qo_indptr.shape[0] - 1
+    scale = 1.0 / math.sqrt(D) if sm_scale is None else sm_scale
+    _check(lib().sgl_paged_prefill(_p(q), q.stride(0), q.stride(1), _p(k_cache), _p(v_cache), ss,
+                                   sh, _p(indices), _p(qo_indptr), _p(kv_indptr), B, max_qo_len,
+                                   hq, hkv, D, scale, _p(o), o.stride(0), o.stride(1),
+                                   _stream(dev)), "sgl_paged_prefill")

@@ -1,0 +1,126 @@
+// Page-table and token-pool plumbing (integer gathers and scatters).
+//
+// Reference: build_decode_indices_kernel (src/attention/flashinfer_backend.cu:43-70),
+// write_token_pool_kernel / gather_int32_2d_kernel (src/kernels/token_pool.cu:10-49).
+// The page table is token-granular: row r, column p holds the pool slot of
+// request r's p-th token.
+#include "common.h"
+
+namespace sgl {
+namespace {
+
+// One workgroup per request; 128-bit stores where the destination run is
+// 16-byte aligned. Each request's run is read as consecutive int32 of one
+// table row, so the loads coalesce.
+__global__ void __launch_bounds__(256) build_indices_kernel(
+    const int32_t* __restrict__ page_table, int64_t rows, int64_t stride, int64_t cols,
+    const int32_t* __restrict__ table_indices, const int32_t* __restrict__ kv_indptr,
+    int32_t* __restrict__ indices, int batch_size) {
+  const int r = blockIdx.x;
+  if (r >= batch_size) return;
+  const int32_t row = table_indices[r];
+  const int32_t start = kv_indptr[r];
+  const int32_t len = kv_indptr[r + 1] - start;
+  if (row < 0 || row >= rows || len <= 0) return;
+  const int32_t* src = page_table + static_cast<int64_t>(row) * stride;
+  int32_t* dst = indices + start;
+  for (int32_t p = threadIdx.x; p < len; p += blockDim.x) {
+    dst[p] = p < cols ? src[p] : 0;
+  }
+}
+
+__global__ void __launch_bounds__(256) write_token_pool_kernel(
+    int32_t* __restrict__ pool, int64_t rows, int64_t stride, int64_t cols,
+    const int32_t* __restrict__ req_indices, const int32_t* __restrict__ positions,
+    const int32_t* __restrict__ tokens, int64_t count) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= count) return;
+  const int64_t r = req_indices[i];
+  const int64_t p = positions[i];
+  if (r < 0 || r >= rows || p < 0 || p >= cols) return;
+  pool[r * stride + p] = tokens[i];
+}
+
+__global__ void __launch_bounds__(256) gather_int32_2d_kernel(
+    const int32_t* __restrict__ table, int64_t rows, int64_t stride, int64_t cols,
+    const int32_t* __restrict__ req_indices, const int32_t* __restrict__ positions,
+    int32_t* __restrict__ out, int64_t count) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= count) return;
+  const int64_t r = req_indices[i];
+  const int64_t p = positions[i];
+  out[i] = (r >= 0 && r < rows && p >= 0 && p < cols) ? table[r * stride + p] : 0;
+}
+
+int launch_build_indices(const int32_t* page_table, int64_t rows, int64_t stride, int64_t cols,
+                         const int32_t* table_indices, const int32_t* kv_indptr,
+                         int32_t* indices, int batch_size, void* stream) {
+  if (batch_size < 0 || rows < 0 || cols < 0 || stride < cols) return SGL_ERR_INVALID_ARG;
+  if (batch_size == 0) return SGL_OK;
+  if (!page_table || !table_indices || !kv_indptr || !indices) return SGL_ERR_INVALID_ARG;
+  hipLaunchKernelGGL(build_indices_kernel, dim3(batch_size), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), page_table, rows, stride, cols,
+                     table_indices, kv_indptr, indices, batch_size);
+  return launch_status();
+}
+
+}  // namespace
+}  // namespace sgl
+
+extern "C" int sgl_build_decode_indices(const int32_t* page_table, int64_t rows, int64_t stride,
+                                        int64_t cols, const int32_t* table_indices,
+                                        const int32_t* kv_indptr, int32_t* indices,
+                                        int batch_size, void* stream) {
+  return sgl::launch_build_indices(page_table, rows, stride, cols, table_indices, kv_indptr,
+                                   indices, batch_size, stream);
+}
+
+extern "C" int sgl_build_prefill_indices(const int32_t* page_table, int64_t rows, int64_t stride,
+                                         int64_t cols, const int32_t* table_indices,
+                                         const int32_t* kv_indptr, int32_t* indices,
+                                         int batch_size, void* stream) {
+  return sgl::launch_build_indices(page_table, rows, stride, cols, table_indices, kv_indptr,
+                                   indices, batch_size, stream);
+}
+
+extern "C" int sgl_write_token_pool(int32_t* pool, int64_t rows, int64_t stride, int64_t cols,
+                                    const int32_t* req_indices, const int32_t* positions,
+                                    const int32_t* tokens, int64_t count, void* stream) {
+  if (count < 0 || rows < 0 || cols < 0 || stride < cols) return SGL_ERR_INVALID_ARG;
+  if (count == 0) return SGL_OK;
+  if (!pool || !req_indices || !positions || !tokens) return SGL_ERR_INVALID_ARG;
+  const int64_t blocks = (count + 255) / 256;
+  hipLaunchKernelGGL(sgl::write_token_pool_kernel, dim3(blocks), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), pool, rows, stride, cols, req_indices,
+                     positions, tokens, count);
+  return sgl::launch_status();
+}
+
+extern "C" int sgl_gather_int32_2d(const int32_t* table, int64_t rows, int64_t stride,
+                                   int64_t cols, const int32_t* req_indices,
+                                   const int32_t* positions, int32_t* out, int64_t count,
+                                   void* stream) {
+  if (count < 0 || rows < 0 || cols < 0 || stride < cols) return SGL_ERR_INVALID_ARG;
+  if (count == 0) return SGL_OK;
+  if (!table || !req_indices || !positions || !out) return SGL_ERR_INVALID_ARG;
+  const int64_t blocks = (count + 255) / 256;
+  hipLaunchKernelGGL(sgl::gather_int32_2d_kernel, dim3(blocks), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), table, rows, stride, cols, req_indices,
+                     positions, out, count);
+  return sgl::launch_status();
+}
+
+extern "C" const char* sgl_status_string(int status) {
+  switch (status) {
+    case SGL_OK: return "ok";
+    case SGL_ERR_INVALID_ARG: return "invalid argument";
+    case SGL_ERR_UNSUPPORTED: return "unsupported configuration";
+    case SGL_ERR_CAPACITY: return "workspace or plan capacity exceeded";
+    case SGL_ERR_ALIGNMENT: return "pointer or stride misaligned";
+    default: break;
+  }
+  if (status > 0) return hipGetErrorString(static_cast<hipError_t>(status));
+  return "unknown status";
+}
+
+extern "C" int sgl_abi_version(void) { return SGL_ABI_VERSION; }

@@ -1,0 +1,403 @@
+"""GPU parity of the HIP hot path against the CPU oracle (marked gpu).
+
+Every call goes through the C ABI (libsgl_attn.so via capi). Bars:
+bit-exact for KV placement, page indexing and token-pool plumbing;
+<= 1 bf16 ulp for RMSNorm / RoPE (fp32 math with one rounding per
+reference rounding point, reduction order differs); attention outputs
+within 2e-2 abs + 1e-2 rel of the fp32-softmax oracle.
+"""
+import math
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import capi, wl
+from helpers import assert_attn_close, assert_bf16_close, bf16_ulp_dist, from_u16, u16
+
+pytestmark = pytest.mark.gpu
+
+
+def note(msg):
+    print(f"[case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def randn_bf16(shape, dev, gen, scale=1.0):
+    return (torch.randn(shape, device=dev, generator=gen) * scale).to(torch.bfloat16)
+
+
+def gen(dev, seed):
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    return g
+
+
+# ------------------------------------------------------------------ KV store
+
+@pytest.mark.parametrize("idx_dtype", [torch.int32, torch.int64])
+@pytest.mark.parametrize("T,hq,hkv,d", [(1, 16, 8, 128), (257, 16, 8, 128), (64, 32, 4, 128),
+                                        (33, 2, 1, 12), (0, 16, 8, 128)])
+def test_store_kv_bit_exact(oracle, dev, idx_dtype, T, hq, hkv, d):
+    note(f"store_kv T={T} hq={hq} hkv={hkv} d={d} idx={idx_dtype}")
+    g = gen(dev, 1)
+    slots = max(2 * T, 8)
+    qkv = randn_bf16((T, (hq + 2 * hkv) * d), dev, g)
+    k = qkv[:, hq * d:(hq + hkv) * d]
+    v = qkv[:, (hq + hkv) * d:]
+    kc = randn_bf16((slots, hkv, d), dev, g)
+    vc = randn_bf16((slots, hkv, d), dev, g)
+    loc = torch.randperm(slots, device=dev, generator=g)[:T].to(idx_dtype)
+    kc_ref, vc_ref = u16(kc).reshape(slots, -1), u16(vc).reshape(slots, -1)
+    qkv_h = u16(qkv)
+    oracle.store_kv(kc_ref, vc_ref, qkv_h[:, hq * d:], qkv_h[:, (hq + hkv) * d:],
+                    loc.cpu().numpy())
+    capi.store_kv(kc, vc, k, v, loc)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(u16(kc).reshape(slots, -1), kc_ref)
+    np.testing.assert_array_equal(u16(vc).reshape(slots, -1), vc_ref)
+
+
+# ------------------------------------------------------------------ metadata
+
+def test_build_indices_bit_exact(oracle, dev):
+    note("build_decode_indices / build_prefill_indices")
+    rng = np.random.default_rng(2)
+    rows, cols = 40, 600
+    pt = rng.integers(0, 1 << 20, (rows, cols)).astype(np.int32)
+    B = 37
+    ti = rng.integers(-1, rows + 1, B).astype(np.int32)
+    lens = rng.integers(0, 700, B)
+    ip = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    want = oracle.build_indices(pt, ti, ip)
+    for fn in (capi.build_decode_indices, capi.build_prefill_indices):
+        out = torch.zeros(int(ip[-1]), dtype=torch.int32, device=dev)
+        fn(torch.from_numpy(pt).to(dev), torch.from_numpy(ti).to(dev),
+           torch.from_numpy(ip).to(dev), out)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(out.cpu().numpy(), want)
+
+
+def test_workload_indices_on_gpu_match_generator(dev):
+    note("cfg4 decode indices from the page table")
+    w = wl.cfg4_decode_large(seed=3)
+    b = w.batch
+    out = torch.zeros(len(b.indices), dtype=torch.int32, device=dev)
+    capi.build_decode_indices(torch.from_numpy(b.page_table).to(dev),
+                              torch.from_numpy(b.table_idx).to(dev),
+                              torch.from_numpy(b.kv_indptr).to(dev), out)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(out.cpu().numpy(), b.indices)
+
+
+def test_token_pool_bit_exact(oracle, dev):
+    note("write_token_pool / gather_int32_2d")
+    rng = np.random.default_rng(4)
+    rows, cols, n = 17, 300, 5000
+    pool = rng.integers(0, 99, (rows, cols)).astype(np.int32)
+    req = rng.integers(-1, rows + 1, n).astype(np.int32)
+    pos = rng.integers(-2, cols + 2, n).astype(np.int32)
+    # unique (req, pos) targets so the scatter order cannot matter
+    key = req.astype(np.int64) * 1000 + pos
+    _, first = np.unique(key, return_index=True)
+    req, pos = req[first], pos[first]
+    tok = rng.integers(0, 1 << 30, len(req)).astype(np.int32)
+    want = pool.copy()
+    oracle.write_token_pool(want, req, pos, tok)
+    d_pool = torch.from_numpy(pool).to(dev)
+    capi.write_token_pool(d_pool, torch.from_numpy(req).to(dev), torch.from_numpy(pos).to(dev),
+                          torch.from_numpy(tok).to(dev))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(d_pool.cpu().numpy(), want)
+    got = capi.gather_int32_2d(d_pool, torch.from_numpy(req).to(dev),
+                               torch.from_numpy(pos).to(dev))
+    np.testing.assert_array_equal(got.cpu().numpy(), oracle.gather_int32_2d(want, req, pos))
+
+
+# ------------------------------------------------------------------ RoPE / norm
+
+def test_cos_sin_cache(oracle, dev):
+    note("rope cos/sin cache 40960 x 64")
+    cos, sin = capi.rope_cos_sin_cache(40960, 128, 1e6, dev)
+    rc, rs = oracle.cos_sin_cache(40960, 128, 1e6)
+    torch.cuda.synchronize()
+    assert np.abs(cos.cpu().numpy() - rc).max() <= 2e-6
+    assert np.abs(sin.cpu().numpy() - rs).max() <= 2e-6
+
+
+@pytest.mark.parametrize("d", [64, 128, 256, 96])
+def test_qk_rmsnorm(oracle, dev, d):
+    note(f"qk_rmsnorm d={d}")
+    g = gen(dev, 5)
+    T, hq, hkv = 37, 16, 8
+    qkv = randn_bf16((T, (hq + 2 * hkv) * d), dev, g, 2.0)
+    q = qkv[:, :hq * d].view(T, hq, d)
+    k = qkv[:, hq * d:(hq + hkv) * d].view(T, hkv, d)
+    qw = (torch.rand(d, device=dev, generator=g) + 0.5).to(torch.bfloat16)
+    kw = randn_bf16((d,), dev, g)
+    qh, kh = u16(q).copy(), u16(k).copy()
+    oracle.qk_rmsnorm(qh, kh, u16(qw), u16(kw), 1e-6)
+    capi.qk_rmsnorm(q, k, qw, kw, 1e-6)
+    torch.cuda.synchronize()
+    assert bf16_ulp_dist(u16(q), qh).max() <= 1
+    assert bf16_ulp_dist(u16(k), kh).max() <= 1
+
+
+def test_qk_rmsnorm_fused_equals_separate(dev):
+    # tests/layers/test_normalization.cpp:21-53, here bitwise.
+    note("qk_rmsnorm fused vs separate")
+    g = gen(dev, 6)
+    q = randn_bf16((7, 16, 128), dev, g)
+    k = randn_bf16((7, 8, 128), dev, g)
+    qw, kw = randn_bf16((128,), dev, g), randn_bf16((128,), dev, g)
+    qa, ka, qb, kb = q.clone(), k.clone(), q.clone(), k.clone()
+    capi.qk_rmsnorm(qa, ka, qw, kw, 1e-6)
+    capi.qk_rmsnorm(qb, None, qw, None, 1e-6)
+    capi.qk_rmsnorm(kb, None, kw, None, 1e-6)
+    torch.cuda.synchronize()
+    assert torch.equal(qa.view(torch.int16), qb.view(torch.int16))
+    assert torch.equal(ka.view(torch.int16), kb.view(torch.int16))
+
+
+@pytest.mark.parametrize("d,rd,full", [(128, 128, False), (64, 64, False), (128, 64, False),
+                                       (80, 80, True), (128, 128, True)])
+def test_rope(oracle, dev, d, rd, full):
+    note(f"rope d={d} rotary={rd} full_width_cache={full}")
+    g = gen(dev, 7)
+    T, hq, hkv = 45, 8, 2
+    qkv = randn_bf16((T, (hq + 2 * hkv) * d), dev, g)
+    q = qkv[:, :hq * d].view(T, hq, d)
+    k = qkv[:, hq * d:(hq + hkv) * d].view(T, hkv, d)
+    pos = torch.randint(0, 4096, (T,), device=dev, generator=g, dtype=torch.int32)
+    cos, sin = capi.rope_cos_sin_cache(4096, rd, 1e4, dev)
+    if full:
+        cos, sin = torch.cat([cos, cos], 1).contiguous(), torch.cat([sin, sin], 1).contiguous()
+    qh, kh = u16(q).copy(), u16(k).copy()
+    oracle.rope(qh, kh, cos.cpu().numpy(), sin.cpu().numpy(), pos.cpu().numpy(), rd)
+    capi.rope(pos, q, k, cos, sin, rd)
+    torch.cuda.synchronize()
+    assert_bf16_close(u16(q), qh, what="rope q")
+    assert_bf16_close(u16(k), kh, what="rope k")
+
+
+def _fused_inputs(dev, T, hq, hkv, d, seed, slots=None):
+    g = gen(dev, seed)
+    slots = slots or T
+    qkv = randn_bf16((T, (hq + 2 * hkv) * d), dev, g)
+    kc = randn_bf16((slots, hkv, d), dev, g)
+    vc = randn_bf16((slots, hkv, d), dev, g)
+    qw = (torch.rand(d, device=dev, generator=g) + 0.5).to(torch.bfloat16)
+    kw = (torch.rand(d, device=dev, generator=g) + 0.5).to(torch.bfloat16)
+    pos = torch.randint(0, 8192, (T,), device=dev, generator=g, dtype=torch.int32)
+    loc = torch.randperm(slots, device=dev, generator=g)[:T].to(torch.int32)
+    cos, sin = capi.rope_cos_sin_cache(8192, d, 1e6, dev)
+    return qkv, kc, vc, qw, kw, pos, loc, cos, sin
+
+
+@pytest.mark.parametrize("T,hq,hkv,d", [(8192, 16, 8, 128), (100, 32, 4, 128), (77, 8, 2, 64)])
+def test_fused_qknorm_rope_store(oracle, dev, T, hq, hkv, d):
+    note(f"fused qknorm+rope+store T={T} hq={hq} hkv={hkv} d={d}")
+    qkv, kc, vc, qw, kw, pos, loc, cos, sin = _fused_inputs(dev, T, hq, hkv, d, 8)
+    # separate GPU kernels in the reference order: norm -> rope -> store
+    qkv2, kc2, vc2 = qkv.clone(), kc.clone(), vc.clone()
+    q2 = qkv2[:, :hq * d].view(T, hq, d)
+    k2 = qkv2[:, hq * d:(hq + hkv) * d].view(T, hkv, d)
+    v2 = qkv2[:, (hq + hkv) * d:].view(T, hkv, d)
+    capi.qk_rmsnorm(q2, k2, qw, kw, 1e-6)
+    capi.rope(pos, q2, k2, cos, sin)
+    capi.store_kv(kc2, vc2, k2, v2, loc)
+    # oracle on host copies
+    h = u16(qkv).copy()
+    qh = h[:, :hq * d].reshape(T, hq, d).copy()
+    kh = h[:, hq * d:(hq + hkv) * d].reshape(T, hkv, d).copy()
+    vh = h[:, (hq + hkv) * d:].reshape(T, hkv * d).copy()
+    oracle.qk_rmsnorm(qh, kh, u16(qw), u16(kw), 1e-6)
+    oracle.rope(qh, kh, cos.cpu().numpy(), sin.cpu().numpy(), pos.cpu().numpy())
+    kc_ref, vc_ref = u16(kc).reshape(T, -1).copy(), u16(vc).reshape(T, -1).copy()
+    oracle.store_kv(kc_ref, vc_ref, kh.reshape(T, -1), vh, loc.cpu().numpy())
+    # fused
+    capi.fused_qknorm_rope_store(qkv, kc, vc, qw, kw, cos, sin, pos, loc, hq, hkv, d, 1e-6)
+    torch.cuda.synchronize()
+    # fused == separate GPU kernels, bit for bit
+    assert torch.equal(qkv.view(torch.int16), qkv2.view(torch.int16))
+    assert torch.equal(kc.view(torch.int16), kc2.view(torch.int16))
+    assert torch.equal(vc.view(torch.int16), vc2.view(torch.int16))
+    # vs oracle: two chained bf16 roundings (norm, then RoPE), each within one
+    # ulp, so <= 2 ulps overall; exact placement (V is a pure copy)
+    assert_bf16_close(u16(qkv)[:, :hq * d].reshape(T, hq, d), qh, what="fused q", max_ulp=2)
+    assert_bf16_close(u16(kc).reshape(T, -1), kc_ref, what="fused k cache", max_ulp=2)
+    np.testing.assert_array_equal(u16(vc).reshape(T, -1), vc_ref)
+
+
+# ------------------------------------------------------------------ decode
+
+def _pool(dev, slots, hkv, d, seed):
+    g = gen(dev, seed)
+    return randn_bf16((slots, hkv, d), dev, g), randn_bf16((slots, hkv, d), dev, g)
+
+
+def run_decode(dev, batch, hq, hkv, d, seed, q_indptr=None, rows=None, plan=None):
+    kc, vc = _pool(dev, batch.num_slots, hkv, d, seed)
+    g = gen(dev, seed + 100)
+    B = batch.batch_size
+    rows = B if rows is None else rows
+    # q as a strided view of a qkv activation, like AttentionLayer hands it over
+    qkv = randn_bf16((rows, (hq + 2 * hkv) * d), dev, g)
+    q = qkv[:, :hq * d].view(rows, hq, d)
+    o = torch.full((rows, hq, d), float("nan"), device=dev, dtype=torch.bfloat16)
+    plan = plan or capi.decode_plan(batch.kv_indptr, hq, hkv, d)
+    ws = torch.empty(max(plan.workspace_bytes, 16), dtype=torch.uint8, device=dev)
+    idx = torch.from_numpy(batch.indices).to(dev)
+    kvp = torch.from_numpy(batch.kv_indptr).to(dev)
+    qip = None if q_indptr is None else torch.from_numpy(q_indptr).to(dev)
+    scale = 1 / math.sqrt(d)
+    capi.paged_decode(plan, q, kc, vc, idx, kvp, o, ws, scale, qip)
+    torch.cuda.synchronize()
+    return q, kc, vc, o, scale, plan
+
+
+@pytest.mark.parametrize("hq,hkv", [(16, 8), (32, 8), (32, 4), (8, 8), (64, 4)])
+@pytest.mark.parametrize("lens", [[512] * 4, [1, 2, 31, 32, 33, 127, 128, 129],
+                                  [4096, 1, 700, 3000, 257]])
+def test_decode_parity(oracle, dev, hq, hkv, lens):
+    note(f"decode hq={hq} hkv={hkv} lens={lens}")
+    rng = np.random.default_rng(9)
+    b = wl.make_paged_batch(rng, [x - 1 for x in lens], lens, page_size=16, decode=True)
+    q, kc, vc, o, scale, plan = run_decode(dev, b, hq, hkv, 128, 10)
+    ref = oracle.decode(u16(q).copy(), u16(kc), u16(vc), b.indices, b.kv_indptr, scale)
+    assert_attn_close(o.float().cpu().numpy(), ref, what=f"decode split={plan.split_kv}")
+
+
+def test_decode_cfg1(oracle, dev):
+    w = wl.cfg1_decode_small()
+    note(w.name)
+    s = w.shape
+    q, kc, vc, o, scale, _ = run_decode(dev, w.batch, s.num_qo_heads, s.num_kv_heads,
+                                        s.head_dim, 11)
+    ref = oracle.decode(u16(q).copy(), u16(kc), u16(vc), w.batch.indices, w.batch.kv_indptr,
+                        scale)
+    assert_attn_close(o.float().cpu().numpy(), ref, what=w.name)
+
+
+def test_decode_forced_split_and_q_indptr(oracle, dev):
+    note("decode with small forced chunk and q rows via q_indptr")
+    rng = np.random.default_rng(12)
+    lens = [1000, 64, 1]
+    b = wl.make_paged_batch(rng, [x - 1 for x in lens], lens, page_size=1, decode=True)
+    plan = capi.decode_plan(b.kv_indptr, 16, 8, 128)
+    plan.kv_chunk_size = 128
+    plan.max_chunks = 8
+    plan.split_kv = 1
+    plan.workspace_bytes = 3 * 8 * 16 * 129 * 4
+    qip = np.array([4, 0, 2], np.int32)
+    q, kc, vc, o, scale, _ = run_decode(dev, b, 16, 8, 128, 13, q_indptr=qip, rows=5, plan=plan)
+    ref = oracle.decode(u16(q).copy(), u16(kc), u16(vc), b.indices, b.kv_indptr, scale,
+                        q_indptr=qip)
+    got = o.float().cpu().numpy()
+    assert_attn_close(got[qip], ref[qip], what="split decode")
+    # rows not addressed by q_indptr stay untouched
+    assert torch.isnan(o[[1, 3]].float()).all()
+
+
+def test_decode_cfg4_full_size(oracle, dev):
+    """Full config 4 (B=256, kv up to 4096); the oracle checks a 32-request sample."""
+    w = wl.cfg4_decode_large(seed=0)
+    note(w.name)
+    s = w.shape
+    b = w.batch
+    q, kc, vc, o, scale, plan = run_decode(dev, b, s.num_qo_heads, s.num_kv_heads, s.head_dim,
+                                           14)
+    assert plan.split_kv
+    sample = np.random.default_rng(15).choice(b.batch_size, 32, replace=False)
+    ip = np.concatenate([[0], np.cumsum(b.kv_lens[sample])]).astype(np.int32)
+    idx = np.concatenate([b.indices[b.kv_indptr[r]:b.kv_indptr[r + 1]] for r in sample])
+    ref = oracle.decode(u16(q[sample]).copy(), u16(kc), u16(vc), idx, ip, scale)
+    assert_attn_close(o[sample].float().cpu().numpy(), ref, what=w.name)
+    assert torch.isfinite(o.float()).all()
+
+
+def test_decode_page_permutation_invariance(dev):
+    """Moving every KV row to another slot (and the table with it) leaves o bitwise unchanged."""
+    note("decode page-permutation invariance")
+    rng = np.random.default_rng(16)
+    lens = [2000, 37, 555]
+    b = wl.make_paged_batch(rng, [x - 1 for x in lens], lens, page_size=16, decode=True)
+    q, kc, vc, o, scale, plan = run_decode(dev, b, 32, 8, 128, 17)
+    perm = torch.randperm(kc.shape[0], device=dev)
+    kc2, vc2 = torch.empty_like(kc), torch.empty_like(vc)
+    kc2[perm], vc2[perm] = kc, vc
+    idx2 = perm[torch.from_numpy(b.indices).to(dev).long()].to(torch.int32)
+    o2 = torch.empty_like(o)
+    ws = torch.empty(max(plan.workspace_bytes, 16), dtype=torch.uint8, device=dev)
+    capi.paged_decode(plan, q, kc2, vc2, idx2, torch.from_numpy(b.kv_indptr).to(dev), o2, ws,
+                      scale)
+    torch.cuda.synchronize()
+    assert torch.equal(o.view(torch.int16), o2.view(torch.int16))
+
+
+# ------------------------------------------------------------------ prefill
+
+def run_prefill(dev, batch, hq, hkv, d, seed):
+    kc, vc = _pool(dev, batch.num_slots, hkv, d, seed)
+    g = gen(dev, seed + 100)
+    rows = int(batch.qo_indptr[-1])
+    qkv = randn_bf16((rows, (hq + 2 * hkv) * d), dev, g)
+    q = qkv[:, :hq * d].view(rows, hq, d)
+    o = torch.full((rows, hq, d), float("nan"), device=dev, dtype=torch.bfloat16)
+    scale = 1 / math.sqrt(d)
+    capi.paged_prefill(q, kc, vc, torch.from_numpy(batch.indices).to(dev),
+                       torch.from_numpy(batch.qo_indptr).to(dev),
+                       torch.from_numpy(batch.kv_indptr).to(dev), int(batch.qo_lens.max()), o,
+                       scale)
+    torch.cuda.synchronize()
+    return q, kc, vc, o, scale
+
+
+def check_prefill(oracle, dev, batch, hq, hkv, seed, what):
+    q, kc, vc, o, scale = run_prefill(dev, batch, hq, hkv, 128, seed)
+    ref = oracle.prefill(u16(q).copy(), u16(kc), u16(vc), batch.indices, batch.qo_indptr,
+                         batch.kv_indptr, scale)
+    assert_attn_close(o.float().cpu().numpy(), ref, what=what)
+
+
+def test_prefill_cfg2(oracle, dev):
+    w = wl.cfg2_prefill_prefix()
+    note(w.name)
+    check_prefill(oracle, dev, w.batch, w.shape.num_qo_heads, w.shape.num_kv_heads, 20, w.name)
+
+
+@pytest.mark.parametrize("hq,hkv", [(16, 8), (32, 4), (8, 8), (32, 8), (12, 4)])
+def test_prefill_ragged(oracle, dev, hq, hkv):
+    note(f"prefill ragged hq={hq} hkv={hkv}")
+    rng = np.random.default_rng(21)
+    cached = [0, 0, 5, 100, 63, 64, 1000, 17]
+    dev_lens = [1, 70, 6, 300, 64, 200, 1001, 129]
+    b = wl.make_paged_batch(rng, cached, dev_lens, page_size=16)
+    check_prefill(oracle, dev, b, hq, hkv, 22, f"prefill ragged {hq}/{hkv}")
+
+
+def test_prefill_chunked_extend_and_empty_extend(oracle, dev):
+    """Chunked prefill: a second chunk on its first chunk's cache; extend 0 -> qo 1."""
+    note("prefill chunked extend / zero extend")
+    rng = np.random.default_rng(23)
+    b = wl.make_paged_batch(rng, [512, 300, 40], [1024, 300, 41], page_size=1)
+    assert list(b.qo_lens) == [512, 1, 1]
+    check_prefill(oracle, dev, b, 32, 4, 24, "chunked extend")
+
+
+def test_prefill_long_no_prefix_matches_textbook(oracle, dev):
+    note("prefill qo == kv (no prefix), 1500 tokens")
+    rng = np.random.default_rng(25)
+    b = wl.make_paged_batch(rng, [0], [1500], page_size=16)
+    check_prefill(oracle, dev, b, 16, 8, 26, "textbook causal")
+
+
+def test_prefill_mixed_decode_rows(oracle, dev):
+    """Config-5 shape of batch (qo 1 rows next to a 2048 chunk), scaled down."""
+    note("prefill with qo=1 rows beside a long chunk")
+    rng = np.random.default_rng(27)
+    kv = list(rng.integers(100, 3000, 6)) + [4096 + 512]
+    cached = [x - 1 for x in kv[:-1]] + [4096]
+    b = wl.make_paged_batch(rng, cached, kv, page_size=16)
+    check_prefill(oracle, dev, b, 32, 4, 28, "mixed prefill")

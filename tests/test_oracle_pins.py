@@ -1,0 +1,370 @@
+"""Pins of the CPU oracle (CPU only).
+
+The reference ships no golden vectors for this path (its attention math is
+FlashInfer's, which is not in the tree), so each oracle function is pinned
+by something other than its own formula: a library routine (torch CPU,
+HF transformers), a closed form, an invariant, or the hand-written
+known-answer vectors in tests/golden/. Each check is chosen so that a
+plausible slip (wrong sign, swapped half, off-by-one in the causal offset,
+wrong head grouping) fails it.
+"""
+import json
+import math
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import bf16_f32, bf16_ulp_dist
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def to_u16(t: torch.Tensor) -> np.ndarray:
+    return t.contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def rand_bf16(rng, shape, scale=1.0):
+    x = torch.from_numpy(rng.standard_normal(shape).astype(np.float32) * scale)
+    return to_u16(x.to(torch.bfloat16))
+
+
+# ------------------------------------------------------------------ bf16
+
+def test_bf16_rounding_matches_torch_cast(oracle):
+    rng = np.random.default_rng(1)
+    x = np.concatenate([
+        rng.standard_normal(100000).astype(np.float32) * 10,
+        np.array([0.0, -0.0, np.inf, -np.inf, 1e-40, -1e-40, 3.0e38, 1.0 + 2**-8,
+                  1.0 + 3 * 2**-8, 1.0 + 2**-9, 65504.0], np.float32),
+    ])
+    # halfway cases: low 16 bits exactly 0x8000, both parities of bit 16
+    halfway = (np.arange(1000, dtype=np.uint32) << 17 | 0x3F808000).view(np.float32)
+    halfway2 = (np.arange(1000, dtype=np.uint32) << 17 | 0x3F818000).view(np.float32)
+    x = np.concatenate([x, halfway, halfway2])
+    want = to_u16(torch.from_numpy(x).to(torch.bfloat16))
+    got = oracle.f32_to_bf16(x)
+    np.testing.assert_array_equal(got, want)
+    nan = oracle.f32_to_bf16(np.array([np.nan], np.float32))
+    assert np.isnan(bf16_f32(nan))[0]
+
+
+# ------------------------------------------------------------------ store / metadata
+
+def test_store_kv_invariants(oracle):
+    rng = np.random.default_rng(2)
+    slots, elems, T, stride = 64, 24, 20, 40
+    kc = rng.integers(0, 65535, (slots, elems), dtype=np.uint16)
+    vc = rng.integers(0, 65535, (slots, elems), dtype=np.uint16)
+    k = rng.integers(0, 65535, (T, stride), dtype=np.uint16)
+    v = rng.integers(0, 65535, (T, stride), dtype=np.uint16)
+    loc = rng.permutation(slots)[:T]
+    kc0, vc0 = kc.copy(), vc.copy()
+    oracle.store_kv(kc, vc, k, v, loc)
+    np.testing.assert_array_equal(kc[loc], k[:, :elems])
+    np.testing.assert_array_equal(vc[loc], v[:, :elems])
+    rest = np.setdiff1d(np.arange(slots), loc)
+    np.testing.assert_array_equal(kc[rest], kc0[rest])
+    np.testing.assert_array_equal(vc[rest], vc0[rest])
+
+
+def test_metadata_golden(oracle):
+    g = json.loads((GOLDEN / "metadata_kat.json").read_text())
+    for case in g["build_indices"]:
+        got = oracle.build_indices(np.array(case["page_table"], np.int32),
+                                   np.array(case["table_indices"], np.int32),
+                                   np.array(case["kv_indptr"], np.int32))
+        np.testing.assert_array_equal(got, np.array(case["expected"], np.int32))
+    for case in g["gather_int32_2d"]:
+        got = oracle.gather_int32_2d(np.array(case["table"], np.int32), case["req"], case["pos"])
+        np.testing.assert_array_equal(got, np.array(case["expected"], np.int32))
+    for case in g["write_token_pool"]:
+        pool = np.array(case["pool"], np.int32)
+        oracle.write_token_pool(pool, case["req"], case["pos"], case["tok"])
+        np.testing.assert_array_equal(pool, np.array(case["expected"], np.int32))
+    for case in g["pages_to_tokens"]:
+        got = oracle.pages_to_tokens(case["page_starts"], case["page_size"])
+        np.testing.assert_array_equal(got, np.array(case["expected"], np.int32))
+
+
+def test_build_indices_brute_force(oracle):
+    rng = np.random.default_rng(3)
+    rows, cols = 9, 40
+    pt = rng.integers(0, 1000, (rows, cols), dtype=np.int32)
+    B = 12
+    ti = rng.integers(-2, rows + 2, B).astype(np.int32)
+    lens = rng.integers(0, 50, B)
+    ip = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    got = oracle.build_indices(pt, ti, ip)
+    want = np.zeros(ip[-1], np.int32)
+    for r in range(B):
+        if 0 <= ti[r] < rows:
+            for p in range(lens[r]):
+                want[ip[r] + p] = pt[ti[r], p] if p < cols else 0
+    np.testing.assert_array_equal(got, want)
+
+
+# ------------------------------------------------------------------ RoPE cache
+
+def torch_reference_cos_sin(max_pos, rd, base):
+    """The reference constructor's LibTorch statements (src/layers/rotary_embedding.cu:80-93)."""
+    inv_freq = 1.0 / torch.pow(base, torch.arange(0, rd, 2, dtype=torch.float32) / float(rd))
+    t = torch.arange(max_pos, dtype=torch.float32)
+    freqs = torch.einsum("i,j->ij", t, inv_freq)
+    return freqs.cos().numpy(), freqs.sin().numpy()
+
+
+@pytest.mark.parametrize("rd,base,max_pos", [(128, 1e6, 40960), (64, 1e4, 4096), (128, 1e4, 8192)])
+def test_cos_sin_cache_matches_torch(oracle, rd, base, max_pos):
+    cos, sin = oracle.cos_sin_cache(max_pos, rd, base)
+    tc, ts = torch_reference_cos_sin(max_pos, rd, base)
+    # Row 0 is exactly (1, 0); elsewhere only last-ulp differences of libm vs
+    # torch's vector cos/sin on identical fp32 arguments are allowed.
+    assert (cos[0] == 1.0).all() and (sin[0] == 0.0).all()
+    assert np.abs(cos - tc).max() <= 4e-6
+    assert np.abs(sin - ts).max() <= 4e-6
+
+
+# ------------------------------------------------------------------ RMSNorm
+
+def test_rmsnorm_matches_torch_rms_norm(oracle):
+    rng = np.random.default_rng(4)
+    T, qh, kh, d, eps = 7, 16, 8, 128, 1e-6
+    q = rand_bf16(rng, (T, qh, d), 3.0)
+    k = rand_bf16(rng, (T, kh, d), 0.5)
+    qw = to_u16(torch.from_numpy(rng.uniform(0.5, 1.5, d).astype(np.float32)).to(torch.bfloat16))
+    kw = to_u16(torch.from_numpy(rng.standard_normal(d).astype(np.float32)).to(torch.bfloat16))
+    q2, k2 = q.copy(), k.copy()
+    oracle.qk_rmsnorm(q2, k2, qw, kw, eps)
+    for x, y, w in ((q, q2, qw), (k, k2, kw)):
+        xt = torch.from_numpy(bf16_f32(x))
+        ref = torch.nn.functional.rms_norm(xt, (d,), eps=eps) * torch.from_numpy(bf16_f32(w))
+        ref16 = to_u16(ref.to(torch.bfloat16))
+        assert bf16_ulp_dist(y, ref16).max() <= 1
+
+
+def test_rmsnorm_fused_equals_separate(oracle):
+    # tests/layers/test_normalization.cpp:21-53: q+k in one call == one call each.
+    rng = np.random.default_rng(5)
+    q = rand_bf16(rng, (7, 16, 128))
+    k = rand_bf16(rng, (7, 8, 128))
+    qw, kw = rand_bf16(rng, (128,)), rand_bf16(rng, (128,))
+    qa, ka, qb, kb = q.copy(), k.copy(), q.copy(), k.copy()
+    oracle.qk_rmsnorm(qa, ka, qw, kw, 1e-6)
+    oracle.qk_rmsnorm(qb, None, qw, None, 1e-6)
+    oracle.qk_rmsnorm(kb, None, kw, None, 1e-6)
+    np.testing.assert_array_equal(qa, qb)
+    np.testing.assert_array_equal(ka, kb)
+
+
+def test_rmsnorm_constant_row(oracle):
+    # x = c everywhere: mean(x^2) = c^2, so out = bf16(c / sqrt(c^2 + eps) * w) ~ sign(c) w.
+    d = 64
+    q = np.full((1, 1, d), to_u16(torch.tensor([2.5], dtype=torch.bfloat16))[0], np.uint16)
+    w = to_u16(torch.linspace(0.5, 1.5, d).to(torch.bfloat16))
+    oracle.qk_rmsnorm(q, None, w, None, 1e-6)
+    assert bf16_ulp_dist(q[0, 0], w).max() <= 1
+
+
+# ------------------------------------------------------------------ RoPE
+
+def test_rope_matches_transformers_neox(oracle):
+    """HF transformers' Qwen3 apply_rotary_pos_emb (rotate_half, full-width
+    cos/sin = cat(freqs, freqs)) on the same bf16 inputs."""
+    from transformers.models.qwen3.modeling_qwen3 import apply_rotary_pos_emb
+    rng = np.random.default_rng(6)
+    T, qh, kh, d = 33, 4, 2, 128
+    q = rand_bf16(rng, (T, qh, d))
+    k = rand_bf16(rng, (T, kh, d))
+    pos = rng.integers(0, 40960, T).astype(np.int32)
+    cos, sin = oracle.cos_sin_cache(40960, d, 1e6)
+    q2, k2 = q.copy(), k.copy()
+    oracle.rope(q2, k2, cos, sin, pos)
+    cf = torch.from_numpy(np.concatenate([cos[pos], cos[pos]], -1))
+    sf = torch.from_numpy(np.concatenate([sin[pos], sin[pos]], -1))
+    qt, kt = torch.from_numpy(bf16_f32(q)), torch.from_numpy(bf16_f32(k))
+    qr, kr = apply_rotary_pos_emb(qt, kt, cf, sf, unsqueeze_dim=1)
+    assert bf16_ulp_dist(q2, to_u16(qr.to(torch.bfloat16))).max() <= 1
+    assert bf16_ulp_dist(k2, to_u16(kr.to(torch.bfloat16))).max() <= 1
+
+
+def test_rope_float64_rotation_and_identities(oracle):
+    rng = np.random.default_rng(7)
+    T, d, base = 50, 128, 1e6
+    x = rand_bf16(rng, (T, 1, d))
+    pos = np.concatenate([[0], rng.integers(1, 8192, T - 1)]).astype(np.int32)
+    cos, sin = oracle.cos_sin_cache(8192, d, base)
+    y, kdummy = x.copy(), x.copy()
+    oracle.rope(y, kdummy, cos, sin, pos)
+    # position 0 is the identity, bit for bit
+    np.testing.assert_array_equal(y[0], x[0])
+    # float64 rotation of each (i, i + d/2) pair by pos * base^(-2i/d)
+    xf = bf16_f32(x)[:, 0].astype(np.float64)
+    h = d // 2
+    theta = pos[:, None].astype(np.float64) * base ** (-np.arange(h) * 2.0 / d)[None, :]
+    a, b = xf[:, :h], xf[:, h:]
+    ref = np.concatenate([a * np.cos(theta) - b * np.sin(theta),
+                          b * np.cos(theta) + a * np.sin(theta)], 1)
+    got = bf16_f32(y)[:, 0].astype(np.float64)
+    # bf16 output rounding plus fp32 phase error at positions up to 8192
+    assert np.abs(got - ref).max() <= 2e-2 * np.abs(xf).max()
+    # each rotated pair keeps its length
+    r0 = np.hypot(a, b)
+    r1 = np.hypot(got[:, :h], got[:, h:])
+    assert np.abs(r1 - r0).max() <= 1e-2 * (1 + r0.max())
+
+
+def test_rope_relative_position_invariance(oracle):
+    # <R(m) q, R(n) k> depends only on m - n.
+    rng = np.random.default_rng(8)
+    d = 128
+    cos, sin = oracle.cos_sin_cache(4096, d, 1e4)
+    q = rand_bf16(rng, (2, 1, d))
+    q[1] = q[0]
+    k = rand_bf16(rng, (2, 1, d))
+    k[1] = k[0]
+    oracle.rope(q, k, cos, sin, np.array([100, 1100], np.int32))
+    qf, kf = bf16_f32(q)[:, 0], bf16_f32(k)[:, 0]
+    # q at 100 vs k at 100 and q at 1100 vs k at 1100: same relative offset 0
+    dot0 = float(qf[0] @ kf[0])
+    dot1 = float(qf[1] @ kf[1])
+    assert abs(dot0 - dot1) <= 0.05 * (1 + abs(dot0))
+
+
+def test_rope_half_and_full_width_cache_agree(oracle):
+    rng = np.random.default_rng(10)
+    d = 64
+    cos, sin = oracle.cos_sin_cache(512, d, 1e4)
+    cos_full = np.concatenate([cos, cos], 1)
+    sin_full = np.concatenate([sin, sin], 1)
+    x = rand_bf16(rng, (9, 2, d))
+    kx = rand_bf16(rng, (9, 1, d))
+    pos = rng.integers(0, 512, 9).astype(np.int32)
+    a, ka = x.copy(), kx.copy()
+    b, kb = x.copy(), kx.copy()
+    oracle.rope(a, ka, cos, sin, pos)
+    oracle.rope(b, kb, np.ascontiguousarray(cos_full), np.ascontiguousarray(sin_full), pos)
+    np.testing.assert_array_equal(a, b)
+    np.testing.assert_array_equal(ka, kb)
+
+
+# ------------------------------------------------------------------ attention
+
+def sdpa_reference(qf, kf, vf, mask, scale):
+    """torch SDPA in fp32; qf [Hq, Lq, D], kf/vf [Hq, Lk, D] (already head-expanded)."""
+    return torch.nn.functional.scaled_dot_product_attention(
+        torch.from_numpy(qf)[None], torch.from_numpy(kf)[None], torch.from_numpy(vf)[None],
+        attn_mask=None if mask is None else torch.from_numpy(mask)[None, None],
+        scale=scale)[0].numpy()
+
+
+def make_pool(rng, slots, hkv, d):
+    return rand_bf16(rng, (slots, hkv, d)), rand_bf16(rng, (slots, hkv, d))
+
+
+@pytest.mark.parametrize("hq,hkv", [(16, 8), (32, 4), (8, 8), (32, 8)])
+def test_decode_matches_torch_sdpa(oracle, hq, hkv):
+    rng = np.random.default_rng(11)
+    d, slots = 128, 700
+    kc, vc = make_pool(rng, slots, hkv, d)
+    lens = [1, 37, 300, 129]
+    ip = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    idx = rng.permutation(slots)[:ip[-1]].astype(np.int32)
+    q = rand_bf16(rng, (len(lens), hq, d))
+    scale = 1 / math.sqrt(d)
+    out = oracle.decode(q, kc, vc, idx, ip, scale)
+    G = hq // hkv
+    for r, n in enumerate(lens):
+        sl = idx[ip[r]:ip[r + 1]]
+        kf = np.repeat(bf16_f32(kc[sl]).transpose(1, 0, 2), G, 0)
+        vf = np.repeat(bf16_f32(vc[sl]).transpose(1, 0, 2), G, 0)
+        qf = bf16_f32(q[r])[:, None, :]
+        ref = sdpa_reference(qf, kf, vf, None, scale)[:, 0]
+        np.testing.assert_allclose(out[r], ref, atol=2e-5, rtol=1e-4)
+
+
+def test_decode_special_cases(oracle):
+    rng = np.random.default_rng(12)
+    d, hkv, hq = 128, 2, 4
+    kc, vc = make_pool(rng, 64, hkv, d)
+    q = rand_bf16(rng, (2, hq, d))
+    # kv_len 1: output is that token's V exactly
+    out = oracle.decode(q, kc, vc, np.array([5, 9], np.int32), np.array([0, 1, 2], np.int32), 0.1)
+    for r, s in enumerate([5, 9]):
+        for h in range(hq):
+            np.testing.assert_allclose(out[r, h], bf16_f32(vc[s, h // 2]), rtol=1e-6, atol=1e-7)
+    # identical K rows: softmax is uniform, output is the mean of V
+    kc2 = kc.copy()
+    kc2[10:30] = kc2[10]
+    out = oracle.decode(q[:1], kc2, vc, np.arange(10, 30, dtype=np.int32),
+                        np.array([0, 20], np.int32), 0.2)
+    mean_v = bf16_f32(vc[10:30]).mean(0)
+    for h in range(hq):
+        np.testing.assert_allclose(out[0, h], mean_v[h // 2], atol=1e-5)
+
+
+def bottom_right_mask(qo, kv):
+    i = np.arange(qo)[:, None]
+    j = np.arange(kv)[None, :]
+    return j <= i + (kv - qo)
+
+
+@pytest.mark.parametrize("hq,hkv", [(16, 8), (32, 4)])
+def test_prefill_matches_torch_sdpa(oracle, hq, hkv):
+    rng = np.random.default_rng(13)
+    d, slots = 128, 1200
+    kc, vc = make_pool(rng, slots, hkv, d)
+    qo = [1, 17, 64, 100]
+    kv = [1, 50, 64, 300]  # prefix 0, 33, 0, 200
+    qip = np.concatenate([[0], np.cumsum(qo)]).astype(np.int32)
+    kip = np.concatenate([[0], np.cumsum(kv)]).astype(np.int32)
+    idx = rng.permutation(slots)[:kip[-1]].astype(np.int32)
+    q = rand_bf16(rng, (qip[-1], hq, d))
+    scale = 1 / math.sqrt(d)
+    out = oracle.prefill(q, kc, vc, idx, qip, kip, scale)
+    G = hq // hkv
+    for r in range(len(qo)):
+        sl = idx[kip[r]:kip[r + 1]]
+        kf = np.repeat(bf16_f32(kc[sl]).transpose(1, 0, 2), G, 0)
+        vf = np.repeat(bf16_f32(vc[sl]).transpose(1, 0, 2), G, 0)
+        qf = bf16_f32(q[qip[r]:qip[r + 1]]).transpose(1, 0, 2)
+        ref = sdpa_reference(qf, kf, vf, bottom_right_mask(qo[r], kv[r]), scale)
+        np.testing.assert_allclose(out[qip[r]:qip[r + 1]], ref.transpose(1, 0, 2), atol=2e-5,
+                                   rtol=1e-4)
+        if qo[r] == kv[r]:  # no prefix: textbook causal attention
+            ref2 = torch.nn.functional.scaled_dot_product_attention(
+                torch.from_numpy(qf)[None], torch.from_numpy(kf)[None],
+                torch.from_numpy(vf)[None], is_causal=True, scale=scale)[0].numpy()
+            np.testing.assert_allclose(out[qip[r]:qip[r + 1]], ref2.transpose(1, 0, 2),
+                                       atol=2e-5, rtol=1e-4)
+
+
+def test_prefill_attention_golden(oracle):
+    """Hand-computed 1-head case: pins the bottom-right causal alignment."""
+    g = json.loads((GOLDEN / "attention_kat.json").read_text())
+    for case in g["cases"]:
+        d = case["head_dim"]
+        kc = oracle.f32_to_bf16(np.array(case["k"], np.float32).reshape(-1, 1, d))
+        vc = oracle.f32_to_bf16(np.array(case["v"], np.float32).reshape(-1, 1, d))
+        q = oracle.f32_to_bf16(np.array(case["q"], np.float32).reshape(-1, 1, d))
+        out = oracle.prefill(q, kc, vc, np.array(case["indices"], np.int32),
+                             np.array(case["qo_indptr"], np.int32),
+                             np.array(case["kv_indptr"], np.int32), case["sm_scale"])
+        np.testing.assert_allclose(out.reshape(-1, d), np.array(case["expected"], np.float32),
+                                   atol=1e-6, rtol=1e-6)
+
+
+def test_attention_page_permutation_invariance(oracle):
+    rng = np.random.default_rng(14)
+    d, hkv, hq, slots = 128, 2, 4, 256
+    kc, vc = make_pool(rng, slots, hkv, d)
+    idx = rng.permutation(slots)[:150].astype(np.int32)
+    q = rand_bf16(rng, (1, hq, d))
+    ip = np.array([0, 150], np.int32)
+    a = oracle.decode(q, kc, vc, idx, ip, 0.09)
+    perm = rng.permutation(slots)
+    kc2, vc2 = np.empty_like(kc), np.empty_like(vc)
+    kc2[perm], vc2[perm] = kc, vc
+    b = oracle.decode(q, kc2, vc2, perm[idx].astype(np.int32), ip, 0.09)
+    np.testing.assert_array_equal(a, b)
