@@ -44,6 +44,9 @@ def parse():
     ap.add_argument("--no-extra", action="store_true", help="headline workload only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--cfg5-layers", type=int, default=48)
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run a plain device-to-device copy of MIB MiB (steps times): "
+                         "the known-size reference for rocprofv3 FETCH_SIZE / WRITE_SIZE")
     return ap.parse_args()
 
 
@@ -96,7 +99,7 @@ def setup_decode(torch, capi, wl, w, dev, seed=0):
     q = qkv[:, :hq * D].view(-1, hq, D)
     o = torch.empty((b.batch_size, hq, D), device=dev, dtype=torch.bfloat16)
     plan = capi.decode_plan(b.kv_indptr, hq, hkv, D)
-    ws = torch.empty(max(plan.workspace_bytes, 16), dtype=torch.uint8, device=dev)
+    ws = capi.decode_workspace(plan, dev)
     idx = torch.from_numpy(b.indices).to(dev)
     kvp = torch.from_numpy(b.kv_indptr).to(dev)
     scale = 1.0 / math.sqrt(D)
@@ -190,7 +193,7 @@ def setup_mixed(torch, capi, wl, w, dev, layers, seed=0):
     p_ip, p_idx = sub(pre)
     p_qo = np.concatenate([[b.qo_indptr[pre[0]]], b.qo_indptr[pre + 1]]).astype(np.int32)
     plan = capi.decode_plan(d_ip, hq, hkv, D)
-    ws = torch.empty(max(plan.workspace_bytes, 16), dtype=torch.uint8, device=dev)
+    ws = capi.decode_workspace(plan, dev)
     t = lambda a: torch.from_numpy(a).to(dev)
     d_ip_t, d_idx_t, d_q_t = t(d_ip), t(d_idx), t(b.qo_indptr[dec].astype(np.int32))
     p_ip_t, p_idx_t, p_qo_t = t(p_ip), t(p_idx), t(p_qo)
@@ -357,6 +360,16 @@ def main():
         sys.exit(1)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+
+    if args.copy_calibration:
+        n = args.copy_calibration << 20
+        src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(args.steps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes": n, "steps": args.steps}))
+        return
 
     w, head = run_workload(args.workload, torch, capi, wl, dev, args.steps, args.warmup,
                            args.cfg5_layers)

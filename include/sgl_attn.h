@@ -36,7 +36,7 @@ const char* sgl_status_string(int status);
 
 /* Library version, to check that the loaded .so matches this header. */
 int sgl_abi_version(void);
-#define SGL_ABI_VERSION 1
+#define SGL_ABI_VERSION 2
 
 /* ------------------------------------------------------------------ */
 /* KV-cache store                                                      */
@@ -177,8 +177,9 @@ typedef struct {
   int32_t split_kv;       /* 1 when any request spans more than one chunk */
   int32_t batch_size;
   int32_t num_qo_heads;
+  int32_t num_kv_heads;
   int32_t head_dim;
-  int64_t workspace_bytes; /* float workspace the run needs */
+  int64_t workspace_bytes; /* fp32 split partials + log2-sum-exp */
 } sgl_decode_plan_t;
 
 /*
@@ -194,6 +195,7 @@ int sgl_decode_plan(const int32_t* kv_indptr_host, int batch_size,
                     int num_qo_heads, int num_kv_heads, int head_dim,
                     sgl_decode_plan_t* plan);
 
+
 /*
  * Paged decode: for request r (rows q[q_row(r)], q_row(r) = r, or
  * q_indptr[r] when q_indptr is non-NULL) and q head h,
@@ -202,7 +204,10 @@ int sgl_decode_plan(const int32_t* kv_indptr_host, int batch_size,
  * over j < kv_indptr[r+1] - kv_indptr[r]. G = Hq / Hkv. q is strided
  * (q_stride_token, q_stride_head), o likewise; k_cache/v_cache are one
  * layer's [slots, Hkv, D] (slot stride kv_stride_slot, head stride
- * kv_stride_head). workspace holds split partials (plan->workspace_bytes).
+ * kv_stride_head). workspace holds split partials (plan->workspace_bytes);
+ * a request longer than one chunk is merged by a second kernel on the same
+ * stream. kv_len must not exceed plan->max_chunks * plan->kv_chunk_size.
+ * Calls that share one workspace must be stream-ordered.
  * Replaces: BatchDecodeWithPagedKVCacheDispatched call in
  *           FlashInferBackend::forward (src/attention/flashinfer_backend.cu:553-595).
  */

@@ -23,7 +23,7 @@ HEADER_PATH = PKG_DIR.parent / "include" / "sgl_attn.h"
 
 SGL_INDEX_I32 = 0
 SGL_INDEX_I64 = 1
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 
 class SglError(RuntimeError):
@@ -39,6 +39,7 @@ class DecodePlan(ctypes.Structure):
         ("split_kv", ctypes.c_int32),
         ("batch_size", ctypes.c_int32),
         ("num_qo_heads", ctypes.c_int32),
+        ("num_kv_heads", ctypes.c_int32),
         ("head_dim", ctypes.c_int32),
         ("workspace_bytes", ctypes.c_int64),
     ]
@@ -290,6 +291,11 @@ def decode_plan(kv_indptr_host: Sequence[int], num_qo_heads: int, num_kv_heads: 
                                  num_qo_heads, num_kv_heads, head_dim, ctypes.byref(plan)),
            "sgl_decode_plan")
     return plan
+
+
+def decode_workspace(plan: DecodePlan, device: torch.device) -> torch.Tensor:
+    """Allocates the split-KV workspace a plan needs."""
+    return torch.empty(max(int(plan.workspace_bytes), 256), dtype=torch.uint8, device=device)
 
 
 def _kv_strides(k_cache: torch.Tensor):

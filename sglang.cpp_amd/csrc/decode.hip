@@ -6,12 +6,18 @@
 //             . V[indices[kv_indptr[r] + j], h / G]
 // with the page table token-granular (page_size 1), no window, no soft-cap.
 //
-// Work decomposition: one workgroup (4 waves) per (request, kv head, KV
-// chunk). All G query heads of the kv head ride in one 16-wide MFMA operand,
-// so every K/V byte is read from HBM exactly once per step. Each wave walks
-// 32-token tiles of the chunk (tile w, w+4, ...), keeps an online softmax,
-// and the 4 wave states are merged through LDS. A request longer than one
-// chunk writes fp32 partials plus a log2-sum-exp, merged by a second kernel.
+// Work decomposition: one workgroup per (request, KV chunk) with one wave
+// per kv head, so a workgroup reads whole [Hkv, D] slot rows (the pool
+// layout) instead of one head segment per row. All G query heads of a kv head
+// ride in one 16-wide MFMA operand, so every K/V byte is read from HBM exactly
+// once per step. Each wave walks the chunk's 32-token tiles with a two-stage
+// software pipeline: while tile t is on the matrix cores, the K/V rows of
+// tile t+1 and the slot indices of tile t+2 are already in flight, so a wave
+// always has 16 KiB of HBM reads outstanding.
+// A request longer than one chunk writes fp32 partials plus a log2-sum-exp,
+// combined by a second, short kernel. (Merging inside the decode launch
+// would need an agent-scope release per workgroup, which on a multi-XCD part
+// is an L2 write-back per workgroup; the kernel boundary is far cheaper.)
 //
 // Matrix formulation (v_mfma_f32_16x16x32_bf16, lane l, n = l % 16, j = l / 16):
 //   S^T[tok, head] = K[tok, :] . Q[head, :]   A = K rows, B = Q^T
@@ -33,8 +39,9 @@ namespace {
 
 constexpr int kD = 128;
 constexpr int kTile = 32;
-constexpr int kWaves = 4;
+constexpr int kMaxWaves = 8;  // kv heads per workgroup (one wave each)
 constexpr int kMaxGroup = 16;
+constexpr int kMaxChunks = 128;  // bound on splits per request (LDS merge table)
 
 struct DecodeArgs {
   const uint16_t* q;
@@ -45,14 +52,29 @@ struct DecodeArgs {
   const int32_t* indices;
   const int32_t* kv_indptr;
   const int32_t* q_indptr;
-  int hq, group;
+  int hq, hkv, group;
   float scale_log2;  // sm_scale * log2(e)
   uint16_t* o;
   int64_t o_st, o_sh;
-  float* part_o;    // [B, max_chunks, hq, D]
-  float* part_lse;  // [B, max_chunks, hq]
+  float* part_o;     // [B, max_chunks, hq, D]
+  float* part_lse;   // [B, max_chunks, hq]
   int chunk, max_chunks;
 };
+
+// Workspace carve-up shared by the plan, the init call and the launch.
+struct WorkspaceLayout {
+  int64_t part_o_off, part_lse_off, total;
+};
+
+inline WorkspaceLayout workspace_layout(int batch, int max_chunks, int hq) {
+  WorkspaceLayout w;
+  const int64_t npart = static_cast<int64_t>(batch) * max_chunks * hq;
+  auto align = [](int64_t x) { return (x + 255) / 256 * 256; };
+  w.part_o_off = 0;
+  w.part_lse_off = align(npart * kD * 4);
+  w.total = w.part_lse_off + align(npart * 4);
+  return w;
+}
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(const u32x4_t& v) {
   return __builtin_bit_cast(bf16x8_t, v);
@@ -71,24 +93,111 @@ __device__ __forceinline__ bf16x8_t v_operand(const u32x4_t (&vr)[8]) {
   return as_bf16x8(out);
 }
 
-__global__ void __launch_bounds__(256) paged_decode_kernel(DecodeArgs a) {
-  const int c = blockIdx.x;
-  const int h = blockIdx.y;
-  const int r = blockIdx.z;
-  const int kv_beg = a.kv_indptr[r];
-  const int kv_len = a.kv_indptr[r + 1] - kv_beg;
-  const int nch = kv_len > a.chunk ? (kv_len + a.chunk - 1) / a.chunk : 1;
-  if (c >= nch) return;
-  const int t0 = c * a.chunk;
-  const int t1 = min(kv_len, t0 + a.chunk);
+// Issue the 16 row loads of one 32-token tile. `slot_lane` holds, in lane
+// l, the slot of token (l % 32) of the tile (clamped to the last valid one).
+__device__ __forceinline__ void issue_tile_loads(const uint16_t* kbase, const uint16_t* vbase,
+                                                 int64_t kv_ss, int slot_lane, int n, int j,
+                                                 u32x4_t (&kr)[8], u32x4_t (&vr)[8]) {
+  const int64_t sk0 = __shfl(slot_lane, n, kWave);
+  const int64_t sk1 = __shfl(slot_lane, 16 + n, kWave);
+  const uint16_t* k0 = kbase + sk0 * kv_ss + 8 * j;
+  const uint16_t* k1 = kbase + sk1 * kv_ss + 8 * j;
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    kr[s] = ldg128(k0 + 32 * s);
+    kr[4 + s] = ldg128(k1 + 32 * s);
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int64_t sv = __shfl(slot_lane, 16 * (e >> 2) + 4 * j + (e & 3), kWave);
+    vr[e] = ldg128(vbase + sv * kv_ss + 8 * n);
+  }
+}
 
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+// Slot of token (lane % 32) of the tile starting at tb, clamped into
+// [0, t1): tiles past the end re-read the last valid row (an L2 hit), which
+// keeps every load in the pipelined loop unconditional.
+__device__ __forceinline__ int load_slot(const int32_t* idx, int tb, int t1, int lane) {
+  return idx[min(tb + (lane & 31), t1 - 1)];
+}
+
+struct HeadState {
+  float m, l;
+  f32x4_t acc[8];
+};
+
+// Online-softmax update of one 32-token tile starting at tb (rows in kr/vr).
+__device__ __forceinline__ void consume_tile(const DecodeArgs& a, const bf16x8_t (&qop)[4],
+                                             const u32x4_t (&kr)[8], const u32x4_t (&vr)[8],
+                                             int tb, int t1, int j, HeadState& st) {
+  const int last = t1 - tb - 1;  // last valid token offset in this tile
+  f32x4_t s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kr[s]), qop[s], s0, 0, 0, 0);
+    s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kr[4 + s]), qop[s], s1, 0, 0, 0);
+  }
+  // Lane holds scores of tokens 16 b + 4 j + i for head n.
+  float sc[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int tok0 = 4 * j + i;
+    sc[i] = tok0 <= last ? s0[i] * a.scale_log2 : -INFINITY;
+    sc[4 + i] = tok0 + 16 <= last ? s1[i] * a.scale_log2 : -INFINITY;
+  }
+  float mt = sc[0];
+#pragma unroll
+  for (int e = 1; e < 8; ++e) mt = fmaxf(mt, sc[e]);
+  mt = fmaxf(mt, __shfl_xor(mt, 16, kWave));
+  mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
+  const float mn = fmaxf(st.m, mt);
+  const float alpha = exp2f(st.m - mn);
+  float p[8];
+  float ps = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    p[e] = exp2f(sc[e] - mn);
+    ps += p[e];
+  }
+  st.l = st.l * alpha + ps;
+  st.m = mn;
+  u32x4_t pw;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) pw[k] = pack_bf16x2(p[2 * k], p[2 * k + 1]);
+  const bf16x8_t pop = as_bf16x8(pw);
+#pragma unroll
+  for (int nb = 0; nb < 8; ++nb) st.acc[nb] *= alpha;
+  st.acc[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v_operand<0>(vr), pop, st.acc[0], 0, 0, 0);
+  st.acc[1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v_operand<1>(vr), pop, st.acc[1], 0, 0, 0);
+  st.acc[2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v_operand<2>(vr), pop, st.acc[2], 0, 0, 0);
+  st.acc[3] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v_operand<3>(vr), pop, st.acc[3], 0, 0, 0);
+  st.acc[4] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v_operand<4>(vr), pop, st.acc[4], 0, 0, 0);
+  st.acc[5] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v_operand<5>(vr), pop, st.acc[5], 0, 0, 0);
+  st.acc[6] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v_operand<6>(vr), pop, st.acc[6], 0, 0, 0);
+  st.acc[7] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v_operand<7>(vr), pop, st.acc[7], 0, 0, 0);
+}
+
+// One wave: kv head h of request r over tokens [t0, t1) of chunk c (t0 < t1).
+//
+// Pipeline (all loads unconditional, so the compiler's in-order vmcnt waits
+// stay partial): entering the step for tile t, the rows of t are in flight
+// and the slots of t+1 have landed. The step issues the slot load of t+2,
+// then the 16 row loads of t+1, then waits only for tile t's rows and
+// consumes them. Two register sets ping-pong between "current" and "next".
+__device__ __forceinline__ void decode_head(const DecodeArgs& a, int r, int c, int nch, int h,
+                                            int t0, int t1, int qrow, int lane) {
   const int n = lane & 15;
   const int j = lane >> 4;
-  const int qrow = a.q_indptr ? a.q_indptr[r] : r;
   const bool head_ok = n < a.group;
   const int head = h * a.group + n;
+  const uint16_t* kbase = a.kc + static_cast<int64_t>(h) * a.kv_sh;
+  const uint16_t* vbase = a.vc + static_cast<int64_t>(h) * a.kv_sh;
+  const int32_t* idx = a.indices + a.kv_indptr[r];
+
+  u32x4_t ka[8], va[8], kb[8], vb[8];
+  int slot_a = load_slot(idx, t0, t1, lane);
+  int slot_b = load_slot(idx, t0 + kTile, t1, lane);
+  issue_tile_loads(kbase, vbase, a.kv_ss, slot_a, n, j, ka, va);
 
   // Q^T operand: lane holds q[head][32 s + 8 j .. + 8] for s = 0..3.
   bf16x8_t qop[4];
@@ -102,127 +211,38 @@ __global__ void __launch_bounds__(256) paged_decode_kernel(DecodeArgs a) {
     }
   }
 
-  const uint16_t* kbase = a.kc + static_cast<int64_t>(h) * a.kv_sh;
-  const uint16_t* vbase = a.vc + static_cast<int64_t>(h) * a.kv_sh;
-  const int32_t* idx = a.indices + kv_beg;
+  HeadState st;
+  st.m = -INFINITY;
+  st.l = 0.f;
+#pragma unroll
+  for (int nb = 0; nb < 8; ++nb) st.acc[nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  float m = -INFINITY;
-  float l = 0.f;
-  f32x4_t acc[8];
-#pragma unroll
-  for (int nb = 0; nb < 8; ++nb) acc[nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-
-  for (int tb = t0 + wave * kTile; tb < t1; tb += kWaves * kTile) {
-    const int last = t1 - tb - 1;  // last valid token offset in this tile
-    // K rows: tokens n and 16 + n; V rows: tokens 16 b + 4 j + i (slot e = 4 b + i).
-    const int64_t sk0 = idx[tb + min(n, last)];
-    const int64_t sk1 = idx[tb + min(16 + n, last)];
-    int64_t sv[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) sv[e] = idx[tb + min(16 * (e >> 2) + 4 * j + (e & 3), last)];
-
-    u32x4_t kr0[4], kr1[4], vr[8];
-    const uint16_t* k0 = kbase + sk0 * a.kv_ss + 8 * j;
-    const uint16_t* k1 = kbase + sk1 * a.kv_ss + 8 * j;
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      kr0[s] = ldg128(k0 + 32 * s);
-      kr1[s] = ldg128(k1 + 32 * s);
-    }
-#pragma unroll
-    for (int e = 0; e < 8; ++e) vr[e] = ldg128(vbase + sv[e] * a.kv_ss + 8 * n);
-
-    f32x4_t s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kr0[s]), qop[s], s0, 0, 0, 0);
-      s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kr1[s]), qop[s], s1, 0, 0, 0);
-    }
-
-    // Lane holds scores of tokens 16 b + 4 j + i for head n.
-    float sc[8];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int tok0 = 4 * j + i;
-      sc[i] = tok0 <= last ? s0[i] * a.scale_log2 : -INFINITY;
-      sc[4 + i] = tok0 + 16 <= last ? s1[i] * a.scale_log2 : -INFINITY;
-    }
-    float mt = sc[0];
-#pragma unroll
-    for (int e = 1; e < 8; ++e) mt = fmaxf(mt, sc[e]);
-    mt = fmaxf(mt, __shfl_xor(mt, 16, kWave));
-    mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
-    const float mn = fmaxf(m, mt);
-    const float alpha = exp2f(m - mn);
-    float p[8];
-    float ps = 0.f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      p[e] = exp2f(sc[e] - mn);
-      ps += p[e];
-    }
-    l = l * alpha + ps;
-    m = mn;
-    u32x4_t pw;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) pw[k] = pack_bf16x2(p[2 * k], p[2 * k + 1]);
-    const bf16x8_t pop = as_bf16x8(pw);
-#pragma unroll
-    for (int nb = 0; nb < 8; ++nb) acc[nb] *= alpha;
-    acc[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v_operand<0>(vr), pop, acc[0], 0, 0, 0);
-    acc[1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v_operand<1>(vr), pop, acc[1], 0, 0, 0);
-    acc[2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v_operand<2>(vr), pop, acc[2], 0, 0, 0);
-    acc[3] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v_operand<3>(vr), pop, acc[3], 0, 0, 0);
-    acc[4] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v_operand<4>(vr), pop, acc[4], 0, 0, 0);
-    acc[5] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v_operand<5>(vr), pop, acc[5], 0, 0, 0);
-    acc[6] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v_operand<6>(vr), pop, acc[6], 0, 0, 0);
-    acc[7] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v_operand<7>(vr), pop, acc[7], 0, 0, 0);
+  int tb = t0;
+  while (true) {
+    // tile tb in (ka, va); slots of tb + 32 in slot_b
+    slot_a = load_slot(idx, tb + 2 * kTile, t1, lane);
+    issue_tile_loads(kbase, vbase, a.kv_ss, slot_b, n, j, kb, vb);
+    __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the consume
+    consume_tile(a, qop, ka, va, tb, t1, j, st);
+    __builtin_amdgcn_sched_barrier(0);
+    tb += kTile;
+    if (tb >= t1) break;
+    // tile tb in (kb, vb); slots of tb + 32 in slot_a
+    slot_b = load_slot(idx, tb + 2 * kTile, t1, lane);
+    issue_tile_loads(kbase, vbase, a.kv_ss, slot_a, n, j, ka, va);
+    __builtin_amdgcn_sched_barrier(0);
+    consume_tile(a, qop, kb, vb, tb, t1, j, st);
+    __builtin_amdgcn_sched_barrier(0);
+    tb += kTile;
+    if (tb >= t1) break;
   }
+  float m = st.m;
+  float l = st.l;
   l += __shfl_xor(l, 16, kWave);
   l += __shfl_xor(l, 32, kWave);
-
-  // Merge the 4 wave states: waves 1..3 park theirs in LDS, wave 0 combines.
-  __shared__ float sh_o[kWaves - 1][32][kWave];
-  __shared__ float sh_m[kWaves][16];
-  __shared__ float sh_l[kWaves][16];
-  if (j == 0) {
-    sh_m[wave][n] = m;
-    sh_l[wave][n] = l;
-  }
-  if (wave > 0) {
-#pragma unroll
-    for (int nb = 0; nb < 8; ++nb)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) sh_o[wave - 1][nb * 4 + i][lane] = acc[nb][i];
-  }
-  __syncthreads();
-  if (wave != 0) return;
-  float mw[kWaves];
-  float mx = -INFINITY;
-#pragma unroll
-  for (int w = 0; w < kWaves; ++w) {
-    mw[w] = sh_m[w][n];
-    mx = fmaxf(mx, mw[w]);
-  }
-  float f[kWaves];
-  float lt = 0.f;
-#pragma unroll
-  for (int w = 0; w < kWaves; ++w) {
-    f[w] = (mw[w] == -INFINITY) ? 0.f : exp2f(mw[w] - mx);
-    lt += sh_l[w][n] * f[w];
-  }
-#pragma unroll
-  for (int nb = 0; nb < 8; ++nb) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float v = acc[nb][i] * f[0];
-#pragma unroll
-      for (int w = 1; w < kWaves; ++w) v += sh_o[w - 1][nb * 4 + i][lane] * f[w];
-      acc[nb][i] = v;
-    }
-  }
   if (!head_ok) return;
-  const float inv = lt > 0.f ? 1.0f / lt : 0.f;
+  const float inv = l > 0.f ? 1.0f / l : 0.f;
+  f32x4_t (&acc)[8] = st.acc;
   // Lane holds d = 32 j + 8 i + nb for head n.
   if (nch == 1) {
     uint16_t* op = a.o + static_cast<int64_t>(qrow) * a.o_st + static_cast<int64_t>(head) * a.o_sh;
@@ -247,33 +267,88 @@ __global__ void __launch_bounds__(256) paged_decode_kernel(DecodeArgs a) {
       *reinterpret_cast<f32x4_t*>(pp + 32 * j + 8 * i) = v0;
       *reinterpret_cast<f32x4_t*>(pp + 32 * j + 8 * i + 4) = v1;
     }
-    if (j == 0) a.part_lse[pidx] = lt > 0.f ? mx + log2f(lt) : -INFINITY;
+    if (j == 0) a.part_lse[pidx] = l > 0.f ? m + log2f(l) : -INFINITY;
   }
 }
 
-// Combines the chunk partials of every request that was split.
-__global__ void __launch_bounds__(128) decode_merge_kernel(DecodeArgs a) {
-  const int r = blockIdx.x;
-  const int head = blockIdx.y;
+// One workgroup per (KV chunk, request); its waves take the kv heads, so the
+// workgroup streams whole [Hkv, D] slot rows (2 KiB at 8 kv heads) rather
+// than one 256-byte head segment of each row.
+__global__ void __launch_bounds__(kMaxWaves * kWave) paged_decode_kernel(DecodeArgs a) {
+  const int c = blockIdx.x;
+  const int r = blockIdx.y;
+  const int kv_len = a.kv_indptr[r + 1] - a.kv_indptr[r];
+  const int nch = kv_len > a.chunk ? (kv_len + a.chunk - 1) / a.chunk : 1;
+  if (c >= nch) return;
+  const int t0 = c * a.chunk;
+  const int t1 = min(kv_len, t0 + a.chunk);
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int nwaves = blockDim.x >> 6;
+  const int qrow = a.q_indptr ? a.q_indptr[r] : r;
+  if (t1 <= t0) {  // empty request: the output row is zero
+    for (int e = threadIdx.x; e < a.hq * (kD / 8); e += blockDim.x) {
+      const int hh = e / (kD / 8);
+      stg128(a.o + static_cast<int64_t>(qrow) * a.o_st + static_cast<int64_t>(hh) * a.o_sh +
+                 (e - hh * (kD / 8)) * 8,
+             u32x4_t{0, 0, 0, 0});
+    }
+    return;
+  }
+  for (int h = wave; h < a.hkv; h += nwaves) decode_head(a, r, c, nch, h, t0, t1, qrow, lane);
+}
+
+// Combines the chunk partials of every split request: one workgroup per
+// (request, kv head) handles its G heads. The chunk lse values are fetched
+// in parallel into LDS and turned into weights; then each thread owns 4
+// consecutive d of one head and streams the chunk partials (16-byte loads,
+// several in flight).
+__global__ void __launch_bounds__(256) decode_merge_kernel(DecodeArgs a) {
+  const int h = blockIdx.x;
+  const int r = blockIdx.y;
   const int kv_len = a.kv_indptr[r + 1] - a.kv_indptr[r];
   const int nch = kv_len > a.chunk ? (kv_len + a.chunk - 1) / a.chunk : 1;
   if (nch <= 1) return;
-  const int d = threadIdx.x;
-  const int64_t base = static_cast<int64_t>(r) * a.max_chunks * a.hq + head;
-  float mx = -INFINITY;
-  for (int c = 0; c < nch; ++c) mx = fmaxf(mx, a.part_lse[base + static_cast<int64_t>(c) * a.hq]);
-  float num = 0.f, den = 0.f;
-  for (int c = 0; c < nch; ++c) {
-    const int64_t pidx = base + static_cast<int64_t>(c) * a.hq;
-    const float lse = a.part_lse[pidx];
-    const float w = lse == -INFINITY ? 0.f : exp2f(lse - mx);
-    num += w * a.part_o[pidx * kD + d];
-    den += w;
-  }
+  __shared__ float sh_w[kMaxChunks][kMaxGroup];
+  const int G = a.group;
   const int qrow = a.q_indptr ? a.q_indptr[r] : r;
-  const float v = den > 0.f ? num / den : 0.f;
-  a.o[static_cast<int64_t>(qrow) * a.o_st + static_cast<int64_t>(head) * a.o_sh + d] =
-      static_cast<uint16_t>(f32_to_bf16_bits(v));
+  const int64_t base = static_cast<int64_t>(r) * a.max_chunks * a.hq + h * G;
+  for (int e = threadIdx.x; e < nch * G; e += blockDim.x) {
+    const int cc = e / G;
+    const int g = e - cc * G;
+    sh_w[cc][g] = a.part_lse[base + cc * a.hq + g];
+  }
+  __syncthreads();
+  if (threadIdx.x < G) {
+    const int g = threadIdx.x;
+    float mx = -INFINITY;
+    for (int cc = 0; cc < nch; ++cc) mx = fmaxf(mx, sh_w[cc][g]);
+    float den = 0.f;
+    for (int cc = 0; cc < nch; ++cc) {
+      const float lse = sh_w[cc][g];
+      const float w = lse == -INFINITY ? 0.f : exp2f(lse - mx);
+      sh_w[cc][g] = w;
+      den += w;
+    }
+    const float inv = den > 0.f ? 1.0f / den : 0.f;
+    for (int cc = 0; cc < nch; ++cc) sh_w[cc][g] *= inv;
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < G * (kD / 4); e += blockDim.x) {
+    const int g = e / (kD / 4);
+    const int d4 = (e - g * (kD / 4)) * 4;
+    f32x4_t accm = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 8
+    for (int cc = 0; cc < nch; ++cc) {
+      const f32x4_t v =
+          *reinterpret_cast<const f32x4_t*>(a.part_o + (base + cc * a.hq + g) * kD + d4);
+      accm += v * sh_w[cc][g];
+    }
+    uint16_t* op = a.o + static_cast<int64_t>(qrow) * a.o_st +
+                   static_cast<int64_t>(h * G + g) * a.o_sh + d4;
+    u32x2_t packed = {pack_bf16x2(accm[0], accm[1]), pack_bf16x2(accm[2], accm[3])};
+    *reinterpret_cast<u32x2_t*>(op) = packed;
+  }
 }
 
 }  // namespace
@@ -295,11 +370,14 @@ extern "C" int sgl_decode_plan(const int32_t* kv_indptr_host, int batch_size, in
     total += len;
     max_len = len > max_len ? len : max_len;
   }
-  // Aim for ~16 workgroups per CU on a 256-CU part; chunks are multiples of
-  // 4 waves x 32 tokens so every wave of a full chunk gets whole tiles.
-  constexpr int64_t kTargetBlocks = 4096;
-  constexpr int kQuantum = kWaves * kTile;
-  int64_t chunk = (total * num_kv_heads + kTargetBlocks - 1) / kTargetBlocks;
+  // Aim for ~32 (request, kv head, chunk) waves per CU on a 256-CU part;
+  // chunks are whole 32-token tiles, and no request splits into more than
+  // kMaxChunks pieces.
+  constexpr int64_t kTargetWaves = 8192;
+  constexpr int kQuantum = kTile;
+  int64_t chunk = (total * num_kv_heads + kTargetWaves - 1) / kTargetWaves;
+  const int64_t min_chunk = (static_cast<int64_t>(max_len) + kMaxChunks - 1) / kMaxChunks;
+  if (chunk < min_chunk) chunk = min_chunk;
   chunk = (chunk + kQuantum - 1) / kQuantum * kQuantum;
   if (chunk < kQuantum) chunk = kQuantum;
   const int64_t cap = (static_cast<int64_t>(max_len) + kQuantum - 1) / kQuantum * kQuantum;
@@ -310,11 +388,10 @@ extern "C" int sgl_decode_plan(const int32_t* kv_indptr_host, int batch_size, in
   plan->split_kv = max_chunks > 1 ? 1 : 0;
   plan->batch_size = batch_size;
   plan->num_qo_heads = num_qo_heads;
+  plan->num_kv_heads = num_kv_heads;
   plan->head_dim = head_dim;
   plan->workspace_bytes =
-      plan->split_kv ? static_cast<int64_t>(batch_size) * max_chunks * num_qo_heads *
-                           (head_dim + 1) * static_cast<int64_t>(sizeof(float))
-                     : 0;
+      plan->split_kv ? workspace_layout(batch_size, max_chunks, num_qo_heads).total : 0;
   return SGL_OK;
 }
 
@@ -334,14 +411,16 @@ extern "C" int sgl_paged_decode(const sgl_decode_plan_t* plan, const void* q,
   if (num_qo_heads % num_kv_heads != 0) return SGL_ERR_INVALID_ARG;
   const int group = num_qo_heads / num_kv_heads;
   if (head_dim != kD || group > kMaxGroup) return SGL_ERR_UNSUPPORTED;
-  if (plan->kv_chunk_size <= 0 || plan->kv_chunk_size % kTile != 0 || plan->max_chunks <= 0)
+  if (plan->kv_chunk_size <= 0 || plan->kv_chunk_size % kTile != 0 || plan->max_chunks <= 0 ||
+      plan->max_chunks > kMaxChunks)
     return SGL_ERR_INVALID_ARG;
-  if (batch_size > plan->batch_size || num_qo_heads != plan->num_qo_heads)
+  if (batch_size > plan->batch_size || num_qo_heads != plan->num_qo_heads ||
+      num_kv_heads != plan->num_kv_heads)
     return SGL_ERR_CAPACITY;
   if (plan->split_kv && (workspace == nullptr || workspace_bytes < plan->workspace_bytes))
     return SGL_ERR_CAPACITY;
   if (q_stride_head % 8 || q_stride_token % 8 || kv_stride_slot % 8 || kv_stride_head % 8 ||
-      o_stride_token % 8 || o_stride_head % 8 || !aligned16(q) || !aligned16(k_cache) ||
+      o_stride_token % 8 || o_stride_head % 4 || !aligned16(q) || !aligned16(k_cache) ||
       !aligned16(v_cache) || !aligned16(o) || (workspace && !aligned16(workspace)))
     return SGL_ERR_ALIGNMENT;
   DecodeArgs a;
@@ -356,6 +435,7 @@ extern "C" int sgl_paged_decode(const sgl_decode_plan_t* plan, const void* q,
   a.kv_indptr = kv_indptr;
   a.q_indptr = q_indptr;
   a.hq = num_qo_heads;
+  a.hkv = num_kv_heads;
   a.group = group;
   a.scale_log2 = sm_scale * 1.4426950408889634f;
   a.o = static_cast<uint16_t*>(o);
@@ -363,14 +443,21 @@ extern "C" int sgl_paged_decode(const sgl_decode_plan_t* plan, const void* q,
   a.o_sh = o_stride_head;
   a.chunk = plan->kv_chunk_size;
   a.max_chunks = plan->max_chunks;
-  const int64_t npart = static_cast<int64_t>(plan->batch_size) * plan->max_chunks * num_qo_heads;
-  a.part_o = plan->split_kv ? static_cast<float*>(workspace) : nullptr;
-  a.part_lse = plan->split_kv ? static_cast<float*>(workspace) + npart * kD : nullptr;
+  if (plan->split_kv) {
+    const WorkspaceLayout w = workspace_layout(plan->batch_size, plan->max_chunks, num_qo_heads);
+    char* base = static_cast<char*>(workspace);
+    a.part_o = reinterpret_cast<float*>(base + w.part_o_off);
+    a.part_lse = reinterpret_cast<float*>(base + w.part_lse_off);
+  } else {
+    a.part_o = nullptr;
+    a.part_lse = nullptr;
+  }
   hipStream_t s = static_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(paged_decode_kernel, dim3(plan->max_chunks, num_kv_heads, batch_size),
-                     dim3(256), 0, s, a);
+  const int waves = num_kv_heads < kMaxWaves ? num_kv_heads : kMaxWaves;
+  hipLaunchKernelGGL(paged_decode_kernel, dim3(plan->max_chunks, batch_size), dim3(waves * kWave),
+                     0, s, a);
   int st = launch_status();
   if (st != SGL_OK || !plan->split_kv) return st;
-  hipLaunchKernelGGL(decode_merge_kernel, dim3(batch_size, num_qo_heads), dim3(kD), 0, s, a);
+  hipLaunchKernelGGL(decode_merge_kernel, dim3(num_kv_heads, batch_size), dim3(256), 0, s, a);
   return launch_status();
 }

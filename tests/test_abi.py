@@ -72,16 +72,17 @@ def test_decode_plan_host_logic():
     kv = rng.integers(128, 4097, 256)
     ip = np.concatenate([[0], np.cumsum(kv)])
     plan = capi.decode_plan(ip, 32, 8, 128)
-    assert plan.kv_chunk_size % 128 == 0 and plan.kv_chunk_size >= 128
+    assert plan.kv_chunk_size % 32 == 0 and plan.kv_chunk_size >= 32
     assert plan.max_chunks == -(-int(kv.max()) // plan.kv_chunk_size)
     assert plan.split_kv == (plan.max_chunks > 1)
     if plan.split_kv:
-        assert plan.workspace_bytes == 256 * plan.max_chunks * 32 * 129 * 4
+        npart = 256 * plan.max_chunks * 32
+        assert plan.workspace_bytes == -(-npart * 512 // 256) * 256 + -(-npart * 4 // 256) * 256
     # enough work items to fill 256 CUs
     blocks = sum(-(-int(k) // plan.kv_chunk_size) for k in kv) * 8
     assert blocks >= 1024
-    # short batch: no split, no workspace
-    plan = capi.decode_plan([0, 100, 200], 16, 8, 128)
+    # a request no longer than one tile is never split
+    plan = capi.decode_plan([0, 20, 52], 16, 8, 128)
     assert plan.split_kv == 0 and plan.workspace_bytes == 0 and plan.max_chunks == 1
     # graph-capture style plan: every request at the capture max length
     plan = capi.decode_plan(list(range(0, 8 * 4096 + 1, 4096)), 32, 8, 128)

@@ -247,7 +247,7 @@ def run_decode(dev, batch, hq, hkv, d, seed, q_indptr=None, rows=None, plan=None
     q = qkv[:, :hq * d].view(rows, hq, d)
     o = torch.full((rows, hq, d), float("nan"), device=dev, dtype=torch.bfloat16)
     plan = plan or capi.decode_plan(batch.kv_indptr, hq, hkv, d)
-    ws = torch.empty(max(plan.workspace_bytes, 16), dtype=torch.uint8, device=dev)
+    ws = capi.decode_workspace(plan, dev)
     idx = torch.from_numpy(batch.indices).to(dev)
     kvp = torch.from_numpy(batch.kv_indptr).to(dev)
     qip = None if q_indptr is None else torch.from_numpy(q_indptr).to(dev)
@@ -289,7 +289,7 @@ def test_decode_forced_split_and_q_indptr(oracle, dev):
     plan.kv_chunk_size = 128
     plan.max_chunks = 8
     plan.split_kv = 1
-    plan.workspace_bytes = 3 * 8 * 16 * 129 * 4
+    plan.workspace_bytes = 3 * 8 * 16 * 129 * 4 + 4096  # partials, lse, counters, padding
     qip = np.array([4, 0, 2], np.int32)
     q, kc, vc, o, scale, _ = run_decode(dev, b, 16, 8, 128, 13, q_indptr=qip, rows=5, plan=plan)
     ref = oracle.decode(u16(q).copy(), u16(kc), u16(vc), b.indices, b.kv_indptr, scale,
@@ -329,7 +329,7 @@ def test_decode_page_permutation_invariance(dev):
     kc2[perm], vc2[perm] = kc, vc
     idx2 = perm[torch.from_numpy(b.indices).to(dev).long()].to(torch.int32)
     o2 = torch.empty_like(o)
-    ws = torch.empty(max(plan.workspace_bytes, 16), dtype=torch.uint8, device=dev)
+    ws = capi.decode_workspace(plan, dev)
     capi.paged_decode(plan, q, kc2, vc2, idx2, torch.from_numpy(b.kv_indptr).to(dev), o2, ws,
                       scale)
     torch.cuda.synchronize()
