@@ -36,7 +36,7 @@ const char* sgl_status_string(int status);
 
 /* Library version, to check that the loaded .so matches this header. */
 int sgl_abi_version(void);
-#define SGL_ABI_VERSION 2
+#define SGL_ABI_VERSION 3
 
 /* ------------------------------------------------------------------ */
 /* KV-cache store                                                      */
@@ -172,9 +172,10 @@ int sgl_fused_qknorm_rope_store(void* qkv, int64_t qkv_stride_token,
 
 /* Split-KV decode plan (host). */
 typedef struct {
-  int32_t kv_chunk_size;  /* tokens per split; multiple of 32 */
-  int32_t max_chunks;     /* grid extent along the split axis */
-  int32_t split_kv;       /* 1 when any request spans more than one chunk */
+  int32_t kv_chunk_size;  /* W: tokens per work unit (multiple of 16, <= 2048) */
+  int32_t max_chunks;     /* partial slots per request (pieces a request may span) */
+  int32_t split_kv;       /* 1 when a request of the planned batch spans units */
+  int32_t num_units;      /* work units = workgroups launched */
   int32_t batch_size;
   int32_t num_qo_heads;
   int32_t num_kv_heads;
@@ -183,10 +184,14 @@ typedef struct {
 } sgl_decode_plan_t;
 
 /*
- * Chooses the split size from the host copy of kv_indptr so the launch
- * has enough work items to fill the GPU, and the workspace that size
- * implies. Pass a kv_indptr with every request at its maximum length to
- * build a plan that stays valid for any shorter batch (graph capture).
+ * Token-balanced schedule from the host copy of kv_indptr: the batch's
+ * flattened token stream is cut into num_units units of kv_chunk_size
+ * tokens, one per resident workgroup (the count comes from the device's CU
+ * count, 256 when no device is visible), and the workspace for the partials
+ * of requests that span units is sized. Pass a kv_indptr with every request
+ * at its maximum length to build a plan valid for any batch of at most
+ * batch_size requests with total and per-request lengths no larger
+ * (graph capture).
  * Replaces: FlashInfer DecodePlan as called from
  *           FlashInferBackend::initialize_decode_metadata_once
  *           (src/attention/flashinfer_backend.cu:354-397).

@@ -23,7 +23,7 @@ HEADER_PATH = PKG_DIR.parent / "include" / "sgl_attn.h"
 
 SGL_INDEX_I32 = 0
 SGL_INDEX_I64 = 1
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 
 class SglError(RuntimeError):
@@ -37,6 +37,7 @@ class DecodePlan(ctypes.Structure):
         ("kv_chunk_size", ctypes.c_int32),
         ("max_chunks", ctypes.c_int32),
         ("split_kv", ctypes.c_int32),
+        ("num_units", ctypes.c_int32),
         ("batch_size", ctypes.c_int32),
         ("num_qo_heads", ctypes.c_int32),
         ("num_kv_heads", ctypes.c_int32),

@@ -1,4 +1,4 @@
-// Split-KV paged decode on gfx950 matrix cores.
+// Split-KV paged decode on gfx950.
 //
 // Reference semantics: FlashInferBackend::forward, decode branch
 // (src/attention/flashinfer_backend.cu:553-595): for request r and q head h,
@@ -6,30 +6,30 @@
 //             . V[indices[kv_indptr[r] + j], h / G]
 // with the page table token-granular (page_size 1), no window, no soft-cap.
 //
-// Work decomposition: one workgroup per (request, KV chunk) with one wave
-// per kv head, so a workgroup reads whole [Hkv, D] slot rows (the pool
-// layout) instead of one head segment per row. All G query heads of a kv head
-// ride in one 16-wide MFMA operand, so every K/V byte is read from HBM exactly
-// once per step. Each wave walks the chunk's 32-token tiles with a two-stage
-// software pipeline: while tile t is on the matrix cores, the K/V rows of
-// tile t+1 and the slot indices of tile t+2 are already in flight, so a wave
-// always has 16 KiB of HBM reads outstanding.
+// Design rule (measured on MI355X): HBM gather bandwidth is set by how many
+// waves each CU keeps in flight, not by how many bytes one wave has
+// outstanding — 8 waves/CU top out near 3.4 TB/s, 24 waves/CU reach ~5.9 TB/s
+// on random 256-byte rows. So this kernel is built to stay under 80 VGPRs
+// (6 waves per SIMD):
+//   * Work: one workgroup per (request, KV chunk), one wave per kv head, so
+//     a workgroup streams whole [Hkv, D] slot rows. All G query heads of a kv
+//     head share each K/V byte, which is read from HBM once per step.
+//   * 16-token steps. S^T[tok, head] = K . Q^T runs on the matrix cores
+//     (v_mfma_f32_16x16x32_bf16; K operand straight from HBM, 16 rows x 64 B
+//     per load; the Q^T operand is re-read from a per-wave LDS copy instead
+//     of pinning 16 registers). P.V runs on the vector ALUs with each lane
+//     owning two head-dim columns for all G heads (2G accumulators instead of
+//     the 32 a 16-wide MFMA tile would need); V arrives as one 256-byte row
+//     per load instruction at a wave-uniform address, so slot indices come
+//     through scalar loads. P and the rescale factors are broadcast through a
+//     per-wave LDS scratch.
+//   * Rolling prefetch: K of step t+1 is issued as soon as the QK products of
+//     step t have read their operands, V of step t+1 right after the P.V of
+//     step t, so each wave keeps ~8 KiB in flight with no second buffer.
 // A request longer than one chunk writes fp32 partials plus a log2-sum-exp,
-// combined by a second, short kernel. (Merging inside the decode launch
-// would need an agent-scope release per workgroup, which on a multi-XCD part
-// is an L2 write-back per workgroup; the kernel boundary is far cheaper.)
-//
-// Matrix formulation (v_mfma_f32_16x16x32_bf16, lane l, n = l % 16, j = l / 16):
-//   S^T[tok, head] = K[tok, :] . Q[head, :]   A = K rows, B = Q^T
-//   O^T[d, head]  += V^T[d, tok] . P^T[tok, head]
-// Both products put the query head on the lane's column n, so the softmax
-// max/sum and the rescale of O are lane-local apart from one 4-way exchange.
-// The k index of each product is a summation index: A and B only have to
-// agree on which token (or d) sits in each lane's k slots, so the V operand
-// uses the d-order d = 8 * m + nb (m = MFMA row, nb = which of 8 MFMAs). With
-// that order a lane needs V[tok][8n .. 8n+7] for its 8 tokens — one 16-byte
-// load per token, 16 lanes covering a whole 256-byte row — and an in-register
-// 8x8 transpose of bf16 halves (v_perm) builds the operands.
+// combined by a second, short kernel. (Merging inside the decode launch would
+// need an agent-scope release per workgroup, which on a multi-XCD part is an
+// L2 write-back per workgroup; the kernel boundary is far cheaper.)
 #include <math.h>
 
 #include "common.h"
@@ -38,10 +38,16 @@ namespace sgl {
 namespace {
 
 constexpr int kD = 128;
-constexpr int kTile = 32;
-constexpr int kMaxWaves = 8;  // kv heads per workgroup (one wave each)
+constexpr int kStep = 16;       // tokens per pipeline step
+constexpr int kTile = 32;       // chunk granularity (tokens)
+constexpr int kMaxKvHeads = 16; // kv heads per workgroup (one wave each)
 constexpr int kMaxGroup = 16;
-constexpr int kMaxChunks = 128;  // bound on splits per request (LDS merge table)
+constexpr int kMaxChunks = 128; // bound on splits per request (merge table)
+constexpr int kMaxChunkTokens = 2048;  // slot indices of a chunk staged in LDS
+constexpr int kQPitch = kD + 8; // LDS row pitch (bf16) of the Q^T copy
+// Word 3 of a raw buffer resource on gfx9-class parts: 32-bit data format,
+// no swizzle, no index stride.
+constexpr int kBufferRsrcWord3 = 0x00020000;
 
 struct DecodeArgs {
   const uint16_t* q;
@@ -58,10 +64,19 @@ struct DecodeArgs {
   int64_t o_st, o_sh;
   float* part_o;     // [B, max_chunks, hq, D]
   float* part_lse;   // [B, max_chunks, hq]
-  int chunk, max_chunks;
+  int chunk;         // tokens per work unit (W)
+  int max_chunks;    // partial slots per request (max pieces)
+  int batch;
 };
 
-// Workspace carve-up shared by the plan, the init call and the launch.
+// Per-wave LDS scratch.
+struct WaveLds {
+  uint16_t q[16 * kQPitch];  // Q rows of the wave's G heads (zero rows past G)
+  float p[kStep][16];        // P[tok][head] of the current step; reused for m / l
+  float alpha[16];           // per-head rescale factor of the current step
+};
+
+// Workspace carve-up shared by the plan and the launch.
 struct WorkspaceLayout {
   int64_t part_o_off, part_lse_off, total;
 };
@@ -80,222 +95,254 @@ __device__ __forceinline__ bf16x8_t as_bf16x8(const u32x4_t& v) {
   return __builtin_bit_cast(bf16x8_t, v);
 }
 
-// Operand for MFMA nb of O^T: slot e takes bf16 element nb of row vr[e].
-template <int nb>
-__device__ __forceinline__ bf16x8_t v_operand(const u32x4_t (&vr)[8]) {
-  constexpr int w = nb / 2;
-  constexpr uint32_t sel = (nb & 1) ? 0x07060302u : 0x05040100u;
-  u32x4_t out;
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    out[k] = __builtin_amdgcn_perm(vr[2 * k + 1][w], vr[2 * k][w], sel);
-  }
-  return as_bf16x8(out);
+// Orders LDS traffic between lanes of one wave (the LDS executes a wave's
+// operations in order; this only stops the compiler from moving them).
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// Issue the 16 row loads of one 32-token tile. `slot_lane` holds, in lane
-// l, the slot of token (l % 32) of the tile (clamped to the last valid one).
-__device__ __forceinline__ void issue_tile_loads(const uint16_t* kbase, const uint16_t* vbase,
-                                                 int64_t kv_ss, int slot_lane, int n, int j,
-                                                 u32x4_t (&kr)[8], u32x4_t (&vr)[8]) {
-  const int64_t sk0 = __shfl(slot_lane, n, kWave);
-  const int64_t sk1 = __shfl(slot_lane, 16 + n, kWave);
-  const uint16_t* k0 = kbase + sk0 * kv_ss + 8 * j;
-  const uint16_t* k1 = kbase + sk1 * kv_ss + 8 * j;
+// V rows of tokens [tb, tb + 16) of the chunk, clamped to `end - 1`; `sidx`
+// holds the chunk's slots (LDS), indexed from the chunk start t0. Each row is
+// read through a buffer resource built in scalar registers from its
+// wave-uniform address, so the only per-lane part is the 32-bit byte offset
+// 4 * lane (lane owns d = 2 lane, 2 lane + 1 of the 256-byte head row).
+__device__ __forceinline__ void load_v_step(const uint16_t* vbase, int64_t kv_ss,
+                                            const int32_t* sidx, int t0, int tb, int end,
+                                            int lane, uint32_t (&vr)[kStep]) {
+  const uint32_t lane_off = static_cast<uint32_t>(lane) * 4u;
+  const char* vb = reinterpret_cast<const char*>(vbase);
+  const int64_t row_bytes = kv_ss * 2;
 #pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    kr[s] = ldg128(k0 + 32 * s);
-    kr[4 + s] = ldg128(k1 + 32 * s);
-  }
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const int64_t sv = __shfl(slot_lane, 16 * (e >> 2) + 4 * j + (e & 3), kWave);
-    vr[e] = ldg128(vbase + sv * kv_ss + 8 * n);
+  for (int k = 0; k < kStep; ++k) {
+    const int tok = tb + k < end ? tb + k : end - 1;
+    const int slot = __builtin_amdgcn_readfirstlane(sidx[tok - t0]);
+    const char* row = vb + static_cast<int64_t>(slot) * row_bytes;
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(row), 0, kD * 2, kBufferRsrcWord3);
+    vr[k] = __builtin_amdgcn_raw_buffer_load_b32(rs, lane_off, 0, 0);
   }
 }
 
-// Slot of token (lane % 32) of the tile starting at tb, clamped into
-// [0, t1): tiles past the end re-read the last valid row (an L2 hit), which
-// keeps every load in the pipelined loop unconditional.
-__device__ __forceinline__ int load_slot(const int32_t* idx, int tb, int t1, int lane) {
-  return idx[min(tb + (lane & 31), t1 - 1)];
+// K operand of a 16-token step: lane (n, j) holds K[tok n][32 s + 8 j .. + 8].
+__device__ __forceinline__ void load_k_step(const uint16_t* kbase, int64_t kv_ss, int slot, int j,
+                                            u32x4_t (&kr)[4]) {
+  const uint16_t* row = kbase + static_cast<int64_t>(slot) * kv_ss + 8 * j;
+#pragma unroll
+  for (int s = 0; s < 4; ++s) kr[s] = ldg128(row + 32 * s);
 }
 
-struct HeadState {
-  float m, l;
-  f32x4_t acc[8];
-};
-
-// Online-softmax update of one 32-token tile starting at tb (rows in kr/vr).
-__device__ __forceinline__ void consume_tile(const DecodeArgs& a, const bf16x8_t (&qop)[4],
-                                             const u32x4_t (&kr)[8], const u32x4_t (&vr)[8],
-                                             int tb, int t1, int j, HeadState& st) {
-  const int last = t1 - tb - 1;  // last valid token offset in this tile
-  f32x4_t s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kr[s]), qop[s], s0, 0, 0, 0);
-    s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kr[4 + s]), qop[s], s1, 0, 0, 0);
-  }
-  // Lane holds scores of tokens 16 b + 4 j + i for head n.
-  float sc[8];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int tok0 = 4 * j + i;
-    sc[i] = tok0 <= last ? s0[i] * a.scale_log2 : -INFINITY;
-    sc[4 + i] = tok0 + 16 <= last ? s1[i] * a.scale_log2 : -INFINITY;
-  }
-  float mt = sc[0];
-#pragma unroll
-  for (int e = 1; e < 8; ++e) mt = fmaxf(mt, sc[e]);
-  mt = fmaxf(mt, __shfl_xor(mt, 16, kWave));
-  mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
-  const float mn = fmaxf(st.m, mt);
-  const float alpha = exp2f(st.m - mn);
-  float p[8];
-  float ps = 0.f;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    p[e] = exp2f(sc[e] - mn);
-    ps += p[e];
-  }
-  st.l = st.l * alpha + ps;
-  st.m = mn;
-  u32x4_t pw;
-#pragma unroll
-  for (int k = 0; k < 4; ++k) pw[k] = pack_bf16x2(p[2 * k], p[2 * k + 1]);
-  const bf16x8_t pop = as_bf16x8(pw);
-#pragma unroll
-  for (int nb = 0; nb < 8; ++nb) st.acc[nb] *= alpha;
-  st.acc[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v_operand<0>(vr), pop, st.acc[0], 0, 0, 0);
-  st.acc[1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v_operand<1>(vr), pop, st.acc[1], 0, 0, 0);
-  st.acc[2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v_operand<2>(vr), pop, st.acc[2], 0, 0, 0);
-  st.acc[3] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v_operand<3>(vr), pop, st.acc[3], 0, 0, 0);
-  st.acc[4] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v_operand<4>(vr), pop, st.acc[4], 0, 0, 0);
-  st.acc[5] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v_operand<5>(vr), pop, st.acc[5], 0, 0, 0);
-  st.acc[6] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v_operand<6>(vr), pop, st.acc[6], 0, 0, 0);
-  st.acc[7] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v_operand<7>(vr), pop, st.acc[7], 0, 0, 0);
-}
-
-// One wave: kv head h of request r over tokens [t0, t1) of chunk c (t0 < t1).
-//
-// Pipeline (all loads unconditional, so the compiler's in-order vmcnt waits
-// stay partial): entering the step for tile t, the rows of t are in flight
-// and the slots of t+1 have landed. The step issues the slot load of t+2,
-// then the 16 row loads of t+1, then waits only for tile t's rows and
-// consumes them. Two register sets ping-pong between "current" and "next".
-__device__ __forceinline__ void decode_head(const DecodeArgs& a, int r, int c, int nch, int h,
-                                            int t0, int t1, int qrow, int lane) {
+template <int GP>
+__device__ __forceinline__ void decode_head(const DecodeArgs& a, WaveLds& L, const int32_t* sidx,
+                                            int r, int c, int nch, int h, int t0, int t1, int qrow,
+                                            int lane) {
+  // sidx: slots of tokens [t0, t1) (indexed from t0); c: partial slot of this
+  // piece of request r; nch == 1 when the piece is the whole request.
   const int n = lane & 15;
   const int j = lane >> 4;
-  const bool head_ok = n < a.group;
-  const int head = h * a.group + n;
+  const int G = a.group;
   const uint16_t* kbase = a.kc + static_cast<int64_t>(h) * a.kv_sh;
   const uint16_t* vbase = a.vc + static_cast<int64_t>(h) * a.kv_sh;
-  const int32_t* idx = a.indices + a.kv_indptr[r];
 
-  u32x4_t ka[8], va[8], kb[8], vb[8];
-  int slot_a = load_slot(idx, t0, t1, lane);
-  int slot_b = load_slot(idx, t0 + kTile, t1, lane);
-  issue_tile_loads(kbase, vbase, a.kv_ss, slot_a, n, j, ka, va);
+  // Q rows of this kv head's G query heads -> LDS (16 rows x 16 chunks).
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int row = u * 4 + (lane >> 4);
+    const int ch = lane & 15;
+    u32x4_t v = {0, 0, 0, 0};
+    if (row < G)
+      v = ldg128(a.q + static_cast<int64_t>(qrow) * a.q_st +
+                 static_cast<int64_t>(h * G + row) * a.q_sh + ch * 8);
+    *reinterpret_cast<u32x4_t*>(L.q + row * kQPitch + ch * 8) = v;
+  }
+  wave_lds_sync();
 
-  // Q^T operand: lane holds q[head][32 s + 8 j .. + 8] for s = 0..3.
-  bf16x8_t qop[4];
-  {
-    const uint16_t* qp = a.q + static_cast<int64_t>(qrow) * a.q_st +
-                         static_cast<int64_t>(head_ok ? head : 0) * a.q_sh + 8 * j;
+  // Prologue: K and V rows of the first step in flight.
+  u32x4_t kr[4];
+  uint32_t vr[kStep];
+  // Issue order K then V, as inside the loop: the wait counts at the loop
+  // head are the merge of both paths, so the orders must agree.
+  load_k_step(kbase, a.kv_ss, sidx[min(t0 + n, t1 - 1) - t0], j, kr);
+  __builtin_amdgcn_sched_barrier(0);
+  load_v_step(vbase, a.kv_ss, sidx, t0, t0, t1, lane, vr);
+  __builtin_amdgcn_sched_barrier(0);
+
+  float m = -INFINITY;  // running max of head n (lane-replicated over j)
+  float l = 0.f;        // partial sum over this lane's tokens of head n
+  float acc[GP][2];
+#pragma unroll
+  for (int g = 0; g < GP; ++g) acc[g][0] = acc[g][1] = 0.f;
+
+  for (int t = t0; t < t1; t += kStep) {
+    const int tn = t + kStep;
+    const int kslot_next = sidx[min(tn + n, t1 - 1) - t0];
+    // S^T for the 16 tokens of this step (rows tok 4 j + i, column head n).
+    f32x4_t sacc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      u32x4_t v = head_ok ? ldg128(qp + 32 * s) : u32x4_t{0, 0, 0, 0};
-      qop[s] = as_bf16x8(v);
+      const bf16x8_t qop = *reinterpret_cast<const bf16x8_t*>(L.q + n * kQPitch + 32 * s + 8 * j);
+      sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kr[s]), qop, sacc, 0, 0, 0);
     }
-  }
+    __builtin_amdgcn_sched_barrier(0);
+    load_k_step(kbase, a.kv_ss, kslot_next, j, kr);  // K of the next step
+    __builtin_amdgcn_sched_barrier(0);
 
-  HeadState st;
-  st.m = -INFINITY;
-  st.l = 0.f;
+    const int last = t1 - t - 1;
+    float sc[4];
+    float mt = -INFINITY;
 #pragma unroll
-  for (int nb = 0; nb < 8; ++nb) st.acc[nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int i = 0; i < 4; ++i) {
+      sc[i] = (4 * j + i <= last) ? sacc[i] * a.scale_log2 : -INFINITY;
+      mt = fmaxf(mt, sc[i]);
+    }
+    mt = fmaxf(mt, __shfl_xor(mt, 16, kWave));
+    mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
+    const float mn = fmaxf(m, mt);
+    const float alpha = exp2f(m - mn);
+    float ps = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float p = exp2f(sc[i] - mn);
+      L.p[4 * j + i][n] = p;
+      ps += p;
+    }
+    l = l * alpha + ps;
+    m = mn;
+    if (j == 0) L.alpha[n] = alpha;
+    wave_lds_sync();
 
-  int tb = t0;
-  while (true) {
-    // tile tb in (ka, va); slots of tb + 32 in slot_b
-    slot_a = load_slot(idx, tb + 2 * kTile, t1, lane);
-    issue_tile_loads(kbase, vbase, a.kv_ss, slot_b, n, j, kb, vb);
-    __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the consume
-    consume_tile(a, qop, ka, va, tb, t1, j, st);
+#pragma unroll
+    for (int g4 = 0; g4 < GP; g4 += 4) {
+      const f32x4_t al = *reinterpret_cast<const f32x4_t*>(&L.alpha[g4]);
+#pragma unroll
+      for (int u = 0; u < 4 && g4 + u < GP; ++u) {
+        acc[g4 + u][0] *= al[u];
+        acc[g4 + u][1] *= al[u];
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < kStep; ++k) {
+      const float v0 = bf16_lo(vr[k]);
+      const float v1 = bf16_hi(vr[k]);
+#pragma unroll
+      for (int g4 = 0; g4 < GP; g4 += 4) {
+        const f32x4_t pk = *reinterpret_cast<const f32x4_t*>(&L.p[k][g4]);
+#pragma unroll
+        for (int u = 0; u < 4 && g4 + u < GP; ++u) {
+          acc[g4 + u][0] += pk[u] * v0;
+          acc[g4 + u][1] += pk[u] * v1;
+        }
+      }
+      // Bound how far the scheduler hoists the P reads (register pressure).
+      if ((k & 3) == 3) __builtin_amdgcn_sched_barrier(0);
+    }
     __builtin_amdgcn_sched_barrier(0);
-    tb += kTile;
-    if (tb >= t1) break;
-    // tile tb in (kb, vb); slots of tb + 32 in slot_a
-    slot_b = load_slot(idx, tb + 2 * kTile, t1, lane);
-    issue_tile_loads(kbase, vbase, a.kv_ss, slot_a, n, j, ka, va);
+    load_v_step(vbase, a.kv_ss, sidx, t0, tn, t1, lane, vr);  // V of the next step
     __builtin_amdgcn_sched_barrier(0);
-    consume_tile(a, qop, kb, vb, tb, t1, j, st);
-    __builtin_amdgcn_sched_barrier(0);
-    tb += kTile;
-    if (tb >= t1) break;
+    wave_lds_sync();  // this step's readers of L.p / L.alpha are done
   }
-  float m = st.m;
-  float l = st.l;
+
+  // Per-head totals: l over the 4 lane groups, then broadcast m, l via LDS.
   l += __shfl_xor(l, 16, kWave);
   l += __shfl_xor(l, 32, kWave);
-  if (!head_ok) return;
-  const float inv = l > 0.f ? 1.0f / l : 0.f;
-  f32x4_t (&acc)[8] = st.acc;
-  // Lane holds d = 32 j + 8 i + nb for head n.
-  if (nch == 1) {
-    uint16_t* op = a.o + static_cast<int64_t>(qrow) * a.o_st + static_cast<int64_t>(head) * a.o_sh;
+  if (j == 0) {
+    L.p[0][n] = m;
+    L.p[1][n] = l;
+  }
+  wave_lds_sync();
+  const int64_t pbase = (static_cast<int64_t>(r) * a.max_chunks + c) * a.hq + h * G;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float v[8];
-#pragma unroll
-      for (int nb = 0; nb < 8; ++nb) v[nb] = acc[nb][i] * inv;
-      stg128(op + 32 * j + 8 * i, pack8(v));
+  for (int g = 0; g < GP; ++g) {
+    if (g >= G) break;
+    const float mg = L.p[0][g];
+    const float lg = L.p[1][g];
+    const float inv = lg > 0.f ? 1.0f / lg : 0.f;
+    const float o0 = acc[g][0] * inv;
+    const float o1 = acc[g][1] * inv;
+    if (nch == 1) {
+      uint16_t* op = a.o + static_cast<int64_t>(qrow) * a.o_st +
+                     static_cast<int64_t>(h * G + g) * a.o_sh + 2 * lane;
+      *reinterpret_cast<uint32_t*>(op) = pack_bf16x2(o0, o1);
+    } else {
+      float* pp = a.part_o + (pbase + g) * kD + 2 * lane;
+      *reinterpret_cast<float2*>(pp) = make_float2(o0, o1);
+      if (lane == 0) a.part_lse[pbase + g] = lg > 0.f ? mg + log2f(lg) : -INFINITY;
     }
-  } else {
-    const int64_t pidx = (static_cast<int64_t>(r) * a.max_chunks + c) * a.hq + head;
-    float* pp = a.part_o + pidx * kD;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      f32x4_t v0, v1;
-#pragma unroll
-      for (int nb = 0; nb < 4; ++nb) {
-        v0[nb] = acc[nb][i] * inv;
-        v1[nb] = acc[nb + 4][i] * inv;
-      }
-      *reinterpret_cast<f32x4_t*>(pp + 32 * j + 8 * i) = v0;
-      *reinterpret_cast<f32x4_t*>(pp + 32 * j + 8 * i + 4) = v1;
-    }
-    if (j == 0) a.part_lse[pidx] = l > 0.f ? m + log2f(l) : -INFINITY;
   }
 }
 
-// One workgroup per (KV chunk, request); its waves take the kv heads, so the
-// workgroup streams whole [Hkv, D] slot rows (2 KiB at 8 kv heads) rather
-// than one 256-byte head segment of each row.
-__global__ void __launch_bounds__(kMaxWaves * kWave) paged_decode_kernel(DecodeArgs a) {
-  const int c = blockIdx.x;
-  const int r = blockIdx.y;
-  const int kv_len = a.kv_indptr[r + 1] - a.kv_indptr[r];
-  const int nch = kv_len > a.chunk ? (kv_len + a.chunk - 1) / a.chunk : 1;
-  if (c >= nch) return;
-  const int t0 = c * a.chunk;
-  const int t1 = min(kv_len, t0 + a.chunk);
+// Zero output row of an empty request (kv_len 0).
+__device__ __forceinline__ void zero_row(const DecodeArgs& a, int qrow) {
+  for (int e = threadIdx.x; e < a.hq * (kD / 8); e += blockDim.x) {
+    const int hh = e / (kD / 8);
+    stg128(a.o + static_cast<int64_t>(qrow) * a.o_st + static_cast<int64_t>(hh) * a.o_sh +
+               (e - hh * (kD / 8)) * 8,
+           u32x4_t{0, 0, 0, 0});
+  }
+}
+
+// Persistent, token-balanced schedule: the flattened token stream of the
+// batch (request r owns [kv_indptr[r], kv_indptr[r+1])) is cut into units of
+// W tokens; workgroup u takes unit u, i.e. the tokens [u W, (u+1) W), which
+// may cover the tail of one request, whole requests and the head of another.
+// Every workgroup gets the same number of tokens, so all stay resident until
+// the end instead of leaving a tail of long requests. A request that spans
+// several units is written as partials (piece p = unit - first unit of the
+// request) and merged by decode_merge_kernel. Waves take the kv heads.
+template <int GP>
+__global__ void __launch_bounds__(kMaxKvHeads * kWave)
+    __attribute__((amdgpu_waves_per_eu(GP <= 8 ? 6 : 4))) paged_decode_kernel(DecodeArgs a) {
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  const int u = blockIdx.x;
+  const int W = a.chunk;
+  const int total = a.kv_indptr[a.batch];
+  const int tok0 = u * W;
+  const int tok1 = min(total, tok0 + W);
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int nwaves = blockDim.x >> 6;
-  const int qrow = a.q_indptr ? a.q_indptr[r] : r;
-  if (t1 <= t0) {  // empty request: the output row is zero
-    for (int e = threadIdx.x; e < a.hq * (kD / 8); e += blockDim.x) {
-      const int hh = e / (kD / 8);
-      stg128(a.o + static_cast<int64_t>(qrow) * a.o_st + static_cast<int64_t>(hh) * a.o_sh +
-                 (e - hh * (kD / 8)) * 8,
-             u32x4_t{0, 0, 0, 0});
-    }
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform per wave
+  const bool last_unit = tok1 == total;
+
+  if (tok0 >= tok1) {
+    // Past the end of the token stream: only an all-empty batch needs work.
+    if (total == 0 && u == 0)
+      for (int r = 0; r < a.batch; ++r) zero_row(a, a.q_indptr ? a.q_indptr[r] : r);
     return;
   }
-  for (int h = wave; h < a.hkv; h += nwaves) decode_head(a, r, c, nch, h, t0, t1, qrow, lane);
+  // First i in [0, batch] with kv_indptr[i] >= tok0 (uniform binary search).
+  int lo = 0, hi = a.batch;
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    if (a.kv_indptr[mid] < tok0) lo = mid + 1; else hi = mid;
+  }
+  // Request lo - 1 runs across tok0 when its end kv_indptr[lo] lies past tok0.
+  int r = (lo > 0 && a.kv_indptr[lo] > tok0) ? lo - 1 : lo;
+
+  // Stage the unit's slot indices (shared by every kv head) in LDS.
+  int32_t* sidx = reinterpret_cast<int32_t*>(smem + a.hkv * sizeof(WaveLds));
+  for (int e = threadIdx.x; e < tok1 - tok0; e += blockDim.x) sidx[e] = a.indices[tok0 + e];
+  __syncthreads();
+  WaveLds& L = reinterpret_cast<WaveLds*>(smem)[wave];
+
+  for (; r < a.batch; ++r) {
+    const int rb = a.kv_indptr[r];
+    const int re = a.kv_indptr[r + 1];
+    // Requests starting at or past tok1 belong to later units, except empty
+    // requests at the very end of the stream, which the last unit owns.
+    if (rb >= tok1 && !(last_unit && rb == total)) break;
+    const int qrow = a.q_indptr ? a.q_indptr[r] : r;
+    if (re == rb) {  // empty request: zero output row
+      zero_row(a, qrow);
+      continue;
+    }
+    const int s0 = max(rb, tok0);
+    const int s1 = min(re, tok1);
+    if (s1 <= s0) continue;
+    const int first_unit = rb / W;
+    const int pieces = (re - 1) / W - first_unit + 1;
+    decode_head<GP>(a, L, sidx + (s0 - tok0), r, u - first_unit, pieces, wave, 0, s1 - s0, qrow,
+                    lane);
+  }
 }
 
 // Combines the chunk partials of every split request: one workgroup per
@@ -306,8 +353,10 @@ __global__ void __launch_bounds__(kMaxWaves * kWave) paged_decode_kernel(DecodeA
 __global__ void __launch_bounds__(256) decode_merge_kernel(DecodeArgs a) {
   const int h = blockIdx.x;
   const int r = blockIdx.y;
-  const int kv_len = a.kv_indptr[r + 1] - a.kv_indptr[r];
-  const int nch = kv_len > a.chunk ? (kv_len + a.chunk - 1) / a.chunk : 1;
+  const int rb = a.kv_indptr[r];
+  const int re = a.kv_indptr[r + 1];
+  if (re <= rb) return;
+  const int nch = (re - 1) / a.chunk - rb / a.chunk + 1;  // pieces of request r
   if (nch <= 1) return;
   __shared__ float sh_w[kMaxChunks][kMaxGroup];
   const int G = a.group;
@@ -356,42 +405,78 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(DecodeArgs a) {
 
 using namespace sgl;
 
+// Compute units of device 0 (256 on MI355X); 256 when no device is visible,
+// so the plan is also computable on a host without a GPU.
+static int device_cu_count() {
+  static int cached = 0;
+  if (cached == 0) {
+    int n = 0, dev = 0, cus = 0;
+    if (hipGetDeviceCount(&n) == hipSuccess && n > 0 && hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+        cus > 0)
+      cached = cus;
+    else
+      cached = 256;
+    (void)hipGetLastError();
+  }
+  return cached;
+}
+
 extern "C" int sgl_decode_plan(const int32_t* kv_indptr_host, int batch_size, int num_qo_heads,
                                int num_kv_heads, int head_dim, sgl_decode_plan_t* plan) {
   if (!plan || !kv_indptr_host || batch_size < 0 || num_qo_heads <= 0 || num_kv_heads <= 0)
     return SGL_ERR_INVALID_ARG;
   if (num_qo_heads % num_kv_heads != 0) return SGL_ERR_INVALID_ARG;
-  if (head_dim != kD || num_qo_heads / num_kv_heads > kMaxGroup) return SGL_ERR_UNSUPPORTED;
+  const int group = num_qo_heads / num_kv_heads;
+  if (head_dim != kD || group > kMaxGroup || num_kv_heads > kMaxKvHeads)
+    return SGL_ERR_UNSUPPORTED;
   int64_t total = 0;
   int max_len = 0;
   for (int r = 0; r < batch_size; ++r) {
     const int len = kv_indptr_host[r + 1] - kv_indptr_host[r];
-    if (len < 0) return SGL_ERR_INVALID_ARG;
+    if (len < 0 || kv_indptr_host[r] < 0) return SGL_ERR_INVALID_ARG;
     total += len;
     max_len = len > max_len ? len : max_len;
   }
-  // Aim for ~32 (request, kv head, chunk) waves per CU on a 256-CU part;
-  // chunks are whole 32-token tiles, and no request splits into more than
-  // kMaxChunks pieces.
-  constexpr int64_t kTargetWaves = 8192;
-  constexpr int kQuantum = kTile;
-  int64_t chunk = (total * num_kv_heads + kTargetWaves - 1) / kTargetWaves;
-  const int64_t min_chunk = (static_cast<int64_t>(max_len) + kMaxChunks - 1) / kMaxChunks;
-  if (chunk < min_chunk) chunk = min_chunk;
-  chunk = (chunk + kQuantum - 1) / kQuantum * kQuantum;
-  if (chunk < kQuantum) chunk = kQuantum;
-  const int64_t cap = (static_cast<int64_t>(max_len) + kQuantum - 1) / kQuantum * kQuantum;
-  if (cap > 0 && chunk > cap) chunk = cap;
-  const int max_chunks = max_len > chunk ? static_cast<int>((max_len + chunk - 1) / chunk) : 1;
-  plan->kv_chunk_size = static_cast<int32_t>(chunk);
-  plan->max_chunks = max_chunks;
-  plan->split_kv = max_chunks > 1 ? 1 : 0;
+  if (total > 0x7fffffff) return SGL_ERR_UNSUPPORTED;
+  // One work unit per resident workgroup: 24 waves per CU (6 per SIMD at
+  // <= 80 VGPRs; 16 for the 16-head group variant), one wave per kv head.
+  const int waves_per_cu = group <= 8 ? 24 : 16;
+  const int64_t units_target =
+      static_cast<int64_t>(device_cu_count()) * (waves_per_cu / num_kv_heads > 0
+                                                     ? waves_per_cu / num_kv_heads : 1);
+  constexpr int64_t kMinUnit = 64;  // keeps per-unit set-up small next to the stream
+  int64_t W = (total + units_target - 1) / units_target;
+  W = (W + kStep - 1) / kStep * kStep;
+  if (W < kMinUnit) W = kMinUnit;
+  // A request of length L touches at most ceil(L / W) + 1 units.
+  const int64_t w_for_pieces = (static_cast<int64_t>(max_len) + kMaxChunks - 2) / (kMaxChunks - 1);
+  if (W < w_for_pieces) W = (w_for_pieces + kStep - 1) / kStep * kStep;
+  if (W > kMaxChunkTokens) {
+    if (w_for_pieces > kMaxChunkTokens) return SGL_ERR_UNSUPPORTED;
+    W = kMaxChunkTokens;
+  }
+  const int64_t units = total > 0 ? (total + W - 1) / W : 1;
+  int max_pieces = 1;
+  for (int r = 0; r < batch_size; ++r) {
+    const int rb = kv_indptr_host[r], re = kv_indptr_host[r + 1];
+    if (re > rb) {
+      const int pieces = static_cast<int>((re - 1) / W - rb / W + 1);
+      max_pieces = pieces > max_pieces ? pieces : max_pieces;
+    }
+  }
+  // Capacity for any batch no longer than this one: pieces <= ceil(L / W) + 1.
+  const int cap_pieces = static_cast<int>((max_len + W - 1) / W) + (max_len > 0 ? 1 : 0);
+  plan->kv_chunk_size = static_cast<int32_t>(W);
+  plan->max_chunks = cap_pieces > max_pieces ? cap_pieces : max_pieces;
+  plan->split_kv = max_pieces > 1 ? 1 : 0;
+  plan->num_units = static_cast<int32_t>(units);
   plan->batch_size = batch_size;
   plan->num_qo_heads = num_qo_heads;
   plan->num_kv_heads = num_kv_heads;
   plan->head_dim = head_dim;
   plan->workspace_bytes =
-      plan->split_kv ? workspace_layout(batch_size, max_chunks, num_qo_heads).total : 0;
+      plan->max_chunks > 1 ? workspace_layout(batch_size, plan->max_chunks, num_qo_heads).total : 0;
   return SGL_OK;
 }
 
@@ -410,14 +495,15 @@ extern "C" int sgl_paged_decode(const sgl_decode_plan_t* plan, const void* q,
   if (!q || !k_cache || !v_cache || !indices || !kv_indptr || !o) return SGL_ERR_INVALID_ARG;
   if (num_qo_heads % num_kv_heads != 0) return SGL_ERR_INVALID_ARG;
   const int group = num_qo_heads / num_kv_heads;
-  if (head_dim != kD || group > kMaxGroup) return SGL_ERR_UNSUPPORTED;
-  if (plan->kv_chunk_size <= 0 || plan->kv_chunk_size % kTile != 0 || plan->max_chunks <= 0 ||
+  if (head_dim != kD || group > kMaxGroup || num_kv_heads > kMaxKvHeads) return SGL_ERR_UNSUPPORTED;
+  if (plan->kv_chunk_size <= 0 || plan->kv_chunk_size % kStep != 0 ||
+      plan->kv_chunk_size > kMaxChunkTokens || plan->max_chunks <= 0 ||
       plan->max_chunks > kMaxChunks)
     return SGL_ERR_INVALID_ARG;
   if (batch_size > plan->batch_size || num_qo_heads != plan->num_qo_heads ||
       num_kv_heads != plan->num_kv_heads)
     return SGL_ERR_CAPACITY;
-  if (plan->split_kv && (workspace == nullptr || workspace_bytes < plan->workspace_bytes))
+  if (plan->max_chunks > 1 && (workspace == nullptr || workspace_bytes < plan->workspace_bytes))
     return SGL_ERR_CAPACITY;
   if (q_stride_head % 8 || q_stride_token % 8 || kv_stride_slot % 8 || kv_stride_head % 8 ||
       o_stride_token % 8 || o_stride_head % 4 || !aligned16(q) || !aligned16(k_cache) ||
@@ -443,7 +529,8 @@ extern "C" int sgl_paged_decode(const sgl_decode_plan_t* plan, const void* q,
   a.o_sh = o_stride_head;
   a.chunk = plan->kv_chunk_size;
   a.max_chunks = plan->max_chunks;
-  if (plan->split_kv) {
+  a.batch = batch_size;
+  if (plan->max_chunks > 1) {
     const WorkspaceLayout w = workspace_layout(plan->batch_size, plan->max_chunks, num_qo_heads);
     char* base = static_cast<char*>(workspace);
     a.part_o = reinterpret_cast<float*>(base + w.part_o_off);
@@ -453,11 +540,21 @@ extern "C" int sgl_paged_decode(const sgl_decode_plan_t* plan, const void* q,
     a.part_lse = nullptr;
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const int waves = num_kv_heads < kMaxWaves ? num_kv_heads : kMaxWaves;
-  hipLaunchKernelGGL(paged_decode_kernel, dim3(plan->max_chunks, batch_size), dim3(waves * kWave),
-                     0, s, a);
+  const dim3 grid(plan->num_units);
+  const dim3 block(num_kv_heads * kWave);
+  const size_t lds = static_cast<size_t>(num_kv_heads) * sizeof(WaveLds) +
+                    static_cast<size_t>(plan->kv_chunk_size) * sizeof(int32_t);
+  if (plan->num_units <= 0) return SGL_ERR_INVALID_ARG;
+  if (group <= 2)
+    hipLaunchKernelGGL(paged_decode_kernel<2>, grid, block, lds, s, a);
+  else if (group <= 4)
+    hipLaunchKernelGGL(paged_decode_kernel<4>, grid, block, lds, s, a);
+  else if (group <= 8)
+    hipLaunchKernelGGL(paged_decode_kernel<8>, grid, block, lds, s, a);
+  else
+    hipLaunchKernelGGL(paged_decode_kernel<16>, grid, block, lds, s, a);
   int st = launch_status();
-  if (st != SGL_OK || !plan->split_kv) return st;
+  if (st != SGL_OK || plan->max_chunks <= 1) return st;
   hipLaunchKernelGGL(decode_merge_kernel, dim3(num_kv_heads, batch_size), dim3(256), 0, s, a);
   return launch_status();
 }

@@ -72,18 +72,21 @@ def test_decode_plan_host_logic():
     kv = rng.integers(128, 4097, 256)
     ip = np.concatenate([[0], np.cumsum(kv)])
     plan = capi.decode_plan(ip, 32, 8, 128)
-    assert plan.kv_chunk_size % 32 == 0 and plan.kv_chunk_size >= 32
-    assert plan.max_chunks == -(-int(kv.max()) // plan.kv_chunk_size)
-    assert plan.split_kv == (plan.max_chunks > 1)
-    if plan.split_kv:
-        npart = 256 * plan.max_chunks * 32
-        assert plan.workspace_bytes == -(-npart * 512 // 256) * 256 + -(-npart * 4 // 256) * 256
-    # enough work items to fill 256 CUs
-    blocks = sum(-(-int(k) // plan.kv_chunk_size) for k in kv) * 8
-    assert blocks >= 1024
-    # a request no longer than one tile is never split
+    assert plan.kv_chunk_size % 16 == 0 and plan.kv_chunk_size >= 64
+    W = plan.kv_chunk_size
+    # units cover the token stream exactly
+    assert plan.num_units == -(-int(kv.sum()) // W)
+    # pieces per request: units its token span touches
+    pieces = [(ip[r + 1] - 1) // W - ip[r] // W + 1 for r in range(256)]
+    assert plan.max_chunks >= max(pieces) and plan.max_chunks <= -(-int(kv.max()) // W) + 1
+    assert plan.split_kv == (max(pieces) > 1)
+    npart = 256 * plan.max_chunks * 32
+    assert plan.workspace_bytes == -(-npart * 512 // 256) * 256 + -(-npart * 4 // 256) * 256
+    # one unit per resident workgroup: 3 per CU at 8 kv heads on 256 CUs
+    assert 700 <= plan.num_units <= 800
+    # a batch shorter than one unit is a single unit; a request inside it is whole
     plan = capi.decode_plan([0, 20, 52], 16, 8, 128)
-    assert plan.split_kv == 0 and plan.workspace_bytes == 0 and plan.max_chunks == 1
+    assert plan.num_units == 1 and plan.split_kv == 0
     # graph-capture style plan: every request at the capture max length
     plan = capi.decode_plan(list(range(0, 8 * 4096 + 1, 4096)), 32, 8, 128)
     assert plan.max_chunks * plan.kv_chunk_size >= 4096
