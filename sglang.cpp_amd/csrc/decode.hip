@@ -72,8 +72,6 @@ struct DecodeArgs {
 // Per-wave LDS scratch.
 struct WaveLds {
   uint16_t q[16 * kQPitch];  // Q rows of the wave's G heads (zero rows past G)
-  float p[kStep][16];        // P[tok][head] of the current step; reused for m / l
-  float alpha[16];           // per-head rescale factor of the current step
 };
 
 // Workspace carve-up shared by the plan and the launch.
@@ -103,28 +101,6 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// V rows of tokens [tb, tb + 16) of the chunk, clamped to `end - 1`; `sidx`
-// holds the chunk's slots (LDS), indexed from the chunk start t0. Each row is
-// read through a buffer resource built in scalar registers from its
-// wave-uniform address, so the only per-lane part is the 32-bit byte offset
-// 4 * lane (lane owns d = 2 lane, 2 lane + 1 of the 256-byte head row).
-__device__ __forceinline__ void load_v_step(const uint16_t* vbase, int64_t kv_ss,
-                                            const int32_t* sidx, int t0, int tb, int end,
-                                            int lane, uint32_t (&vr)[kStep]) {
-  const uint32_t lane_off = static_cast<uint32_t>(lane) * 4u;
-  const char* vb = reinterpret_cast<const char*>(vbase);
-  const int64_t row_bytes = kv_ss * 2;
-#pragma unroll
-  for (int k = 0; k < kStep; ++k) {
-    const int tok = tb + k < end ? tb + k : end - 1;
-    const int slot = __builtin_amdgcn_readfirstlane(sidx[tok - t0]);
-    const char* row = vb + static_cast<int64_t>(slot) * row_bytes;
-    const __amdgpu_buffer_rsrc_t rs =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(row), 0, kD * 2, kBufferRsrcWord3);
-    vr[k] = __builtin_amdgcn_raw_buffer_load_b32(rs, lane_off, 0, 0);
-  }
-}
-
 // K operand of a 16-token step: lane (n, j) holds K[tok n][32 s + 8 j .. + 8].
 __device__ __forceinline__ void load_k_step(const uint16_t* kbase, int64_t kv_ss, int slot, int j,
                                             u32x4_t (&kr)[4]) {
@@ -133,51 +109,85 @@ __device__ __forceinline__ void load_k_step(const uint16_t* kbase, int64_t kv_ss
   for (int s = 0; s < 4; ++s) kr[s] = ldg128(row + 32 * s);
 }
 
-template <int GP>
+// V rows of a 16-token step: lane (n, j) holds V[tok 4 j + e][8 n .. 8 n + 7]
+// for e < 4, so each load instruction reads four whole 256-byte rows.
+// Tokens at or past `len` re-read the last valid row (an L2 hit).
+__device__ __forceinline__ void load_v_step(const uint16_t* vbase, int64_t kv_ss,
+                                            const int32_t* sidx, int tb, int len, int n, int j,
+                                            u32x4_t (&vr)[4]) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int tok = min(tb + 4 * j + e, len - 1);
+    vr[e] = ldg128(vbase + static_cast<int64_t>(sidx[tok]) * kv_ss + 8 * n);
+  }
+}
+
+// A operand of O^T MFMA nb: V^T[d = 8 n + nb][tok 4 j + e] for e < 4, built
+// from the four rows by byte permutes (bf16 element nb of each row).
+template <int nb>
+__device__ __forceinline__ bf16x4_t v_operand(const u32x4_t (&vr)[4]) {
+  constexpr int w = nb / 2;
+  constexpr uint32_t sel = (nb & 1) ? 0x07060302u : 0x05040100u;
+  u32x2_t out;
+  out[0] = __builtin_amdgcn_perm(vr[1][w], vr[0][w], sel);
+  out[1] = __builtin_amdgcn_perm(vr[3][w], vr[2][w], sel);
+  return __builtin_bit_cast(bf16x4_t, out);
+}
+
+#define SGL_PV(nb)                                                                   \
+  acc[nb] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(v_operand<nb>(vr), pop, acc[nb], \
+                                                      0, 0, 0)
+
+// One wave: kv head h of request r over the `len` tokens whose slots are
+// sidx[0, len); c is the partial slot of this piece of request r, nch == 1
+// when the piece is the whole request.
+//
+// Per 16-token step (v_mfma, lane l, n = l % 16, j = l / 16):
+//   S^T[tok, head] = K . Q^T          4 x 16x16x32: rows tok, columns head
+//   O^T[d, head]  += V^T . P^T        8 x 16x16x16: k = the step's 16 tokens
+// S^T's accumulator layout (lane holds tokens 4 j .. 4 j + 3 of head n) is
+// exactly the B operand P^T the second product needs, and both put the head
+// on the lane's column, so max, sum and the rescale of O are lane-local apart
+// from one exchange across the four lane groups.
 __device__ __forceinline__ void decode_head(const DecodeArgs& a, WaveLds& L, const int32_t* sidx,
-                                            int r, int c, int nch, int h, int t0, int t1, int qrow,
+                                            int r, int c, int nch, int h, int len, int qrow,
                                             int lane) {
-  // sidx: slots of tokens [t0, t1) (indexed from t0); c: partial slot of this
-  // piece of request r; nch == 1 when the piece is the whole request.
   const int n = lane & 15;
   const int j = lane >> 4;
   const int G = a.group;
+  const bool head_ok = n < G;
   const uint16_t* kbase = a.kc + static_cast<int64_t>(h) * a.kv_sh;
   const uint16_t* vbase = a.vc + static_cast<int64_t>(h) * a.kv_sh;
 
   // Q rows of this kv head's G query heads -> LDS (16 rows x 16 chunks).
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
-    const int row = u * 4 + (lane >> 4);
-    const int ch = lane & 15;
+    const int row = u * 4 + j;
     u32x4_t v = {0, 0, 0, 0};
     if (row < G)
       v = ldg128(a.q + static_cast<int64_t>(qrow) * a.q_st +
-                 static_cast<int64_t>(h * G + row) * a.q_sh + ch * 8);
-    *reinterpret_cast<u32x4_t*>(L.q + row * kQPitch + ch * 8) = v;
+                 static_cast<int64_t>(h * G + row) * a.q_sh + n * 8);
+    *reinterpret_cast<u32x4_t*>(L.q + row * kQPitch + n * 8) = v;
   }
   wave_lds_sync();
 
-  // Prologue: K and V rows of the first step in flight.
-  u32x4_t kr[4];
-  uint32_t vr[kStep];
-  // Issue order K then V, as inside the loop: the wait counts at the loop
-  // head are the merge of both paths, so the orders must agree.
-  load_k_step(kbase, a.kv_ss, sidx[min(t0 + n, t1 - 1) - t0], j, kr);
+  // Prologue: K and V rows of the first step in flight, K issued first as
+  // inside the loop (the loop-head wait counts merge both paths).
+  u32x4_t kr[4], vr[4];
+  load_k_step(kbase, a.kv_ss, sidx[min(n, len - 1)], j, kr);
   __builtin_amdgcn_sched_barrier(0);
-  load_v_step(vbase, a.kv_ss, sidx, t0, t0, t1, lane, vr);
+  load_v_step(vbase, a.kv_ss, sidx, 0, len, n, j, vr);
   __builtin_amdgcn_sched_barrier(0);
 
-  float m = -INFINITY;  // running max of head n (lane-replicated over j)
+  float m = -INFINITY;  // running max of head n (replicated over j)
   float l = 0.f;        // partial sum over this lane's tokens of head n
-  float acc[GP][2];
+  f32x4_t acc[8];
 #pragma unroll
-  for (int g = 0; g < GP; ++g) acc[g][0] = acc[g][1] = 0.f;
+  for (int nb = 0; nb < 8; ++nb) acc[nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  for (int t = t0; t < t1; t += kStep) {
+  for (int t = 0; t < len; t += kStep) {
     const int tn = t + kStep;
-    const int kslot_next = sidx[min(tn + n, t1 - 1) - t0];
-    // S^T for the 16 tokens of this step (rows tok 4 j + i, column head n).
+    const int kslot_next = sidx[min(tn + n, len - 1)];
     f32x4_t sacc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
@@ -188,7 +198,7 @@ __device__ __forceinline__ void decode_head(const DecodeArgs& a, WaveLds& L, con
     load_k_step(kbase, a.kv_ss, kslot_next, j, kr);  // K of the next step
     __builtin_amdgcn_sched_barrier(0);
 
-    const int last = t1 - t - 1;
+    const int last = len - t - 1;
     float sc[4];
     float mt = -INFINITY;
 #pragma unroll
@@ -200,77 +210,54 @@ __device__ __forceinline__ void decode_head(const DecodeArgs& a, WaveLds& L, con
     mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
     const float mn = fmaxf(m, mt);
     const float alpha = exp2f(m - mn);
-    float ps = 0.f;
+    float p[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float p = exp2f(sc[i] - mn);
-      L.p[4 * j + i][n] = p;
-      ps += p;
-    }
-    l = l * alpha + ps;
+    for (int i = 0; i < 4; ++i) p[i] = exp2f(sc[i] - mn);
+    l = l * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
     m = mn;
-    if (j == 0) L.alpha[n] = alpha;
-    wave_lds_sync();
-
+    u32x2_t pw = {pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3])};
+    const bf16x4_t pop = __builtin_bit_cast(bf16x4_t, pw);
 #pragma unroll
-    for (int g4 = 0; g4 < GP; g4 += 4) {
-      const f32x4_t al = *reinterpret_cast<const f32x4_t*>(&L.alpha[g4]);
-#pragma unroll
-      for (int u = 0; u < 4 && g4 + u < GP; ++u) {
-        acc[g4 + u][0] *= al[u];
-        acc[g4 + u][1] *= al[u];
-      }
-    }
-#pragma unroll
-    for (int k = 0; k < kStep; ++k) {
-      const float v0 = bf16_lo(vr[k]);
-      const float v1 = bf16_hi(vr[k]);
-#pragma unroll
-      for (int g4 = 0; g4 < GP; g4 += 4) {
-        const f32x4_t pk = *reinterpret_cast<const f32x4_t*>(&L.p[k][g4]);
-#pragma unroll
-        for (int u = 0; u < 4 && g4 + u < GP; ++u) {
-          acc[g4 + u][0] += pk[u] * v0;
-          acc[g4 + u][1] += pk[u] * v1;
-        }
-      }
-      // Bound how far the scheduler hoists the P reads (register pressure).
-      if ((k & 3) == 3) __builtin_amdgcn_sched_barrier(0);
-    }
+    for (int nb = 0; nb < 8; ++nb) acc[nb] *= alpha;
+    SGL_PV(0); SGL_PV(1); SGL_PV(2); SGL_PV(3);
+    SGL_PV(4); SGL_PV(5); SGL_PV(6); SGL_PV(7);
     __builtin_amdgcn_sched_barrier(0);
-    load_v_step(vbase, a.kv_ss, sidx, t0, tn, t1, lane, vr);  // V of the next step
+    load_v_step(vbase, a.kv_ss, sidx, tn, len, n, j, vr);  // V of the next step
     __builtin_amdgcn_sched_barrier(0);
-    wave_lds_sync();  // this step's readers of L.p / L.alpha are done
   }
-
-  // Per-head totals: l over the 4 lane groups, then broadcast m, l via LDS.
   l += __shfl_xor(l, 16, kWave);
   l += __shfl_xor(l, 32, kWave);
-  if (j == 0) {
-    L.p[0][n] = m;
-    L.p[1][n] = l;
-  }
-  wave_lds_sync();
-  const int64_t pbase = (static_cast<int64_t>(r) * a.max_chunks + c) * a.hq + h * G;
+  if (!head_ok) return;
+  const float inv = l > 0.f ? 1.0f / l : 0.f;
+  const int head = h * G + n;
+  // Lane holds O[head n][d = 32 j + 8 i + nb] in acc[nb][i].
+  if (nch == 1) {
+    uint16_t* op = a.o + static_cast<int64_t>(qrow) * a.o_st + static_cast<int64_t>(head) * a.o_sh;
 #pragma unroll
-  for (int g = 0; g < GP; ++g) {
-    if (g >= G) break;
-    const float mg = L.p[0][g];
-    const float lg = L.p[1][g];
-    const float inv = lg > 0.f ? 1.0f / lg : 0.f;
-    const float o0 = acc[g][0] * inv;
-    const float o1 = acc[g][1] * inv;
-    if (nch == 1) {
-      uint16_t* op = a.o + static_cast<int64_t>(qrow) * a.o_st +
-                     static_cast<int64_t>(h * G + g) * a.o_sh + 2 * lane;
-      *reinterpret_cast<uint32_t*>(op) = pack_bf16x2(o0, o1);
-    } else {
-      float* pp = a.part_o + (pbase + g) * kD + 2 * lane;
-      *reinterpret_cast<float2*>(pp) = make_float2(o0, o1);
-      if (lane == 0) a.part_lse[pbase + g] = lg > 0.f ? mg + log2f(lg) : -INFINITY;
+    for (int i = 0; i < 4; ++i) {
+      float v[8];
+#pragma unroll
+      for (int nb = 0; nb < 8; ++nb) v[nb] = acc[nb][i] * inv;
+      stg128(op + 32 * j + 8 * i, pack8(v));
     }
+  } else {
+    const int64_t pidx = (static_cast<int64_t>(r) * a.max_chunks + c) * a.hq + head;
+    float* pp = a.part_o + pidx * kD;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f32x4_t v0, v1;
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb) {
+        v0[nb] = acc[nb][i] * inv;
+        v1[nb] = acc[nb + 4][i] * inv;
+      }
+      *reinterpret_cast<f32x4_t*>(pp + 32 * j + 8 * i) = v0;
+      *reinterpret_cast<f32x4_t*>(pp + 32 * j + 8 * i + 4) = v1;
+    }
+    if (j == 0) a.part_lse[pidx] = l > 0.f ? m + log2f(l) : -INFINITY;
   }
 }
+#undef SGL_PV
 
 // Zero output row of an empty request (kv_len 0).
 __device__ __forceinline__ void zero_row(const DecodeArgs& a, int qrow) {
@@ -290,9 +277,8 @@ __device__ __forceinline__ void zero_row(const DecodeArgs& a, int qrow) {
 // the end instead of leaving a tail of long requests. A request that spans
 // several units is written as partials (piece p = unit - first unit of the
 // request) and merged by decode_merge_kernel. Waves take the kv heads.
-template <int GP>
 __global__ void __launch_bounds__(kMaxKvHeads * kWave)
-    __attribute__((amdgpu_waves_per_eu(GP <= 8 ? 6 : 4))) paged_decode_kernel(DecodeArgs a) {
+    __attribute__((amdgpu_waves_per_eu(5))) paged_decode_kernel(DecodeArgs a) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const int u = blockIdx.x;
   const int W = a.chunk;
@@ -340,8 +326,7 @@ __global__ void __launch_bounds__(kMaxKvHeads * kWave)
     if (s1 <= s0) continue;
     const int first_unit = rb / W;
     const int pieces = (re - 1) / W - first_unit + 1;
-    decode_head<GP>(a, L, sidx + (s0 - tok0), r, u - first_unit, pieces, wave, 0, s1 - s0, qrow,
-                    lane);
+    decode_head(a, L, sidx + (s0 - tok0), r, u - first_unit, pieces, wave, s1 - s0, qrow, lane);
   }
 }
 
@@ -441,7 +426,7 @@ extern "C" int sgl_decode_plan(const int32_t* kv_indptr_host, int batch_size, in
   if (total > 0x7fffffff) return SGL_ERR_UNSUPPORTED;
   // One work unit per resident workgroup: 24 waves per CU (6 per SIMD at
   // <= 80 VGPRs; 16 for the 16-head group variant), one wave per kv head.
-  const int waves_per_cu = group <= 8 ? 24 : 16;
+  const int waves_per_cu = 20;  // 5 waves per SIMD at <= 96 VGPRs
   const int64_t units_target =
       static_cast<int64_t>(device_cu_count()) * (waves_per_cu / num_kv_heads > 0
                                                      ? waves_per_cu / num_kv_heads : 1);
@@ -545,14 +530,7 @@ extern "C" int sgl_paged_decode(const sgl_decode_plan_t* plan, const void* q,
   const size_t lds = static_cast<size_t>(num_kv_heads) * sizeof(WaveLds) +
                     static_cast<size_t>(plan->kv_chunk_size) * sizeof(int32_t);
   if (plan->num_units <= 0) return SGL_ERR_INVALID_ARG;
-  if (group <= 2)
-    hipLaunchKernelGGL(paged_decode_kernel<2>, grid, block, lds, s, a);
-  else if (group <= 4)
-    hipLaunchKernelGGL(paged_decode_kernel<4>, grid, block, lds, s, a);
-  else if (group <= 8)
-    hipLaunchKernelGGL(paged_decode_kernel<8>, grid, block, lds, s, a);
-  else
-    hipLaunchKernelGGL(paged_decode_kernel<16>, grid, block, lds, s, a);
+  hipLaunchKernelGGL(paged_decode_kernel, grid, block, lds, s, a);
   int st = launch_status();
   if (st != SGL_OK || plan->max_chunks <= 1) return st;
   hipLaunchKernelGGL(decode_merge_kernel, dim3(num_kv_heads, batch_size), dim3(256), 0, s, a);
