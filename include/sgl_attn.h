@@ -36,7 +36,7 @@ const char* sgl_status_string(int status);
 
 /* Library version, to check that the loaded .so matches this header. */
 int sgl_abi_version(void);
-#define SGL_ABI_VERSION 3
+#define SGL_ABI_VERSION 5
 
 /* ------------------------------------------------------------------ */
 /* KV-cache store                                                      */
@@ -172,7 +172,8 @@ int sgl_fused_qknorm_rope_store(void* qkv, int64_t qkv_stride_token,
 
 /* Split-KV decode plan (host). */
 typedef struct {
-  int32_t kv_chunk_size;  /* W: tokens per work unit (multiple of 16, <= 2048) */
+  int32_t kv_chunk_size;  /* W_max: largest unit in tokens (multiple of 16, <= 2048) */
+  int32_t min_chunk_size; /* W_min: smallest unit (bounds pieces per request) */
   int32_t max_chunks;     /* partial slots per request (pieces a request may span) */
   int32_t split_kv;       /* 1 when a request of the planned batch spans units */
   int32_t num_units;      /* work units = workgroups launched */
@@ -185,13 +186,15 @@ typedef struct {
 
 /*
  * Token-balanced schedule from the host copy of kv_indptr: the batch's
- * flattened token stream is cut into num_units units of kv_chunk_size
- * tokens, one per resident workgroup (the count comes from the device's CU
- * count, 256 when no device is visible), and the workspace for the partials
- * of requests that span units is sized. Pass a kv_indptr with every request
- * at its maximum length to build a plan valid for any batch of at most
- * batch_size requests with total and per-request lengths no larger
- * (graph capture).
+ * flattened token stream is cut into num_units equal units, one per
+ * resident workgroup (the count comes from the device's CU count, 256 when
+ * no device is visible). The launch picks the unit size on the device,
+ * clamp(ceil(total / num_units), min_chunk_size, kv_chunk_size) rounded to
+ * 16 tokens, from kv_indptr[batch], so a plan built from a kv_indptr with
+ * every request at its maximum length stays valid and balanced for any batch
+ * of at most batch_size requests whose per-request and total lengths are no
+ * larger (graph capture / replay without re-planning). The workspace holds
+ * the partials of requests that span units.
  * Replaces: FlashInfer DecodePlan as called from
  *           FlashInferBackend::initialize_decode_metadata_once
  *           (src/attention/flashinfer_backend.cu:354-397).
@@ -232,7 +235,9 @@ int sgl_paged_decode(const sgl_decode_plan_t* plan, const void* q,
  * request r, qo_len = qo_indptr[r+1]-qo_indptr[r]) attends kv j with
  * j <= i + kv_len - qo_len (bottom-right alignment), kv_len =
  * kv_indptr[r+1]-kv_indptr[r], slots from indices[kv_indptr[r] + j].
- * max_qo_len bounds qo_len over the batch (sizes the grid).
+ * Request r's query (and output) rows start at q_start[r], or at
+ * qo_indptr[r] when q_start is NULL (a subset of a batch's requests can so
+ * be run in place). max_qo_len bounds qo_len over the batch (sizes the grid).
  * Replaces: BatchPrefillWithPagedKVCacheDispatched<..., kCausal, ...> in
  *           FlashInferBackend::forward (src/attention/flashinfer_backend.cu:596-679).
  */
@@ -241,7 +246,8 @@ int sgl_paged_prefill(const void* q, int64_t q_stride_token,
                       const void* v_cache, int64_t kv_stride_slot,
                       int64_t kv_stride_head, const int32_t* indices,
                       const int32_t* qo_indptr, const int32_t* kv_indptr,
-                      int batch_size, int max_qo_len, int num_qo_heads,
+                      const int32_t* q_start, int batch_size, int max_qo_len,
+                      int num_qo_heads,
                       int num_kv_heads, int head_dim, float sm_scale, void* o,
                       int64_t o_stride_token, int64_t o_stride_head,
                       void* stream);

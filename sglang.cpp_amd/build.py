@@ -23,8 +23,8 @@ LIB_PATH = PKG_DIR / LIB_NAME
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
-# Packed-fp32 VALU ops are disabled for all device code (see the toolchain
-# notes in DESIGN.md); hipcc's host pass warns that it does not know the
+# Packed-fp32 VALU ops are disabled for all device code (some packed fp32
+# forms have given silently wrong results on these parts); hipcc's host pass warns that it does not know the
 # feature, which is harmless.
 HIP_FLAGS = [
     f"--offload-arch={ARCH}",
@@ -72,8 +72,69 @@ def build_lib(jobs: int = 8) -> Path:
     return LIB_PATH
 
 
+BACKEND_NAME = "sgl_backend"
+BACKEND_SOURCES = ["backend/hip_backend.cpp", "backend/bindings.cpp"]
+
+
+def backend_path() -> Path:
+    import sysconfig
+    return PKG_DIR / (BACKEND_NAME + sysconfig.get_config_var("EXT_SUFFIX"))
+
+
+def build_backend(jobs: int = 8) -> Path:
+    """Build the C++ backend extension (host code only, LibTorch + pybind11).
+
+    Compiled with g++ directly against torch's headers; it links
+    libsgl_attn.so from this directory (rpath $ORIGIN), so all device work
+    stays in the HIP library.
+    """
+    import sysconfig
+
+    import torch
+    from torch.utils import cpp_extension
+
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    cflags = [
+        "-O2", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-function",
+        "-D__HIP_PLATFORM_AMD__", "-DUSE_ROCM", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+        "-DTORCH_EXTENSION_NAME=" + BACKEND_NAME, "-DTORCH_API_INCLUDE_EXTENSION_H",
+        f"-I{sysconfig.get_paths()['include']}", "-I/opt/rocm/include", f"-I{REPO / 'include'}",
+        *[f"-I{p}" for p in cpp_extension.include_paths()],
+    ]
+    BUILD_DIR.mkdir(exist_ok=True)
+    objs = []
+
+    def cc(name: str) -> Path:
+        src = CSRC / name
+        obj = BUILD_DIR / (Path(name).stem + ".cpp.o")
+        res = subprocess.run(["g++", *cflags, "-c", str(src), "-o", str(obj)],
+                             capture_output=True, text=True)
+        if res.returncode != 0:
+            raise RuntimeError(f"g++ failed for {name}:\n{res.stdout}\n{res.stderr}")
+        if res.stderr.strip():
+            sys.stderr.write(res.stderr)
+        return obj
+
+    with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
+        objs = list(ex.map(cc, BACKEND_SOURCES))
+    torch_lib = Path(torch.__file__).resolve().parent / "lib"
+    out = backend_path()
+    tmp = out.with_name(out.name + ".tmp")
+    cmd = ["g++", "-shared", *map(str, objs), "-o", str(tmp),
+           f"-L{PKG_DIR}", "-l:" + LIB_NAME, "-Wl,-rpath,$ORIGIN",
+           f"-L{torch_lib}", f"-Wl,-rpath,{torch_lib}",
+           "-lc10", "-ltorch", "-ltorch_cpu", "-ltorch_python", "-lc10_hip", "-ltorch_hip",
+           "-L/opt/rocm/lib", "-lamdhip64"]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"backend link failed:\n{res.stdout}\n{res.stderr}")
+    os.replace(tmp, out)
+    return out
+
+
 def build(jobs: int = 8) -> None:
     build_lib(jobs)
+    build_backend(jobs)
 
 
 if __name__ == "__main__":

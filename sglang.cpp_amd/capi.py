@@ -23,7 +23,7 @@ HEADER_PATH = PKG_DIR.parent / "include" / "sgl_attn.h"
 
 SGL_INDEX_I32 = 0
 SGL_INDEX_I64 = 1
-ABI_VERSION = 3
+ABI_VERSION = 5
 
 
 class SglError(RuntimeError):
@@ -35,6 +35,7 @@ class SglError(RuntimeError):
 class DecodePlan(ctypes.Structure):
     _fields_ = [
         ("kv_chunk_size", ctypes.c_int32),
+        ("min_chunk_size", ctypes.c_int32),
         ("max_chunks", ctypes.c_int32),
         ("split_kv", ctypes.c_int32),
         ("num_units", ctypes.c_int32),
@@ -72,8 +73,8 @@ _SIGNATURES = {
     "sgl_paged_decode": ([ctypes.POINTER(DecodePlan), _vp, _i64, _i64, _vp, _vp, _i64, _i64,
                           _vp, _vp, _vp, _i32, _i32, _i32, _i32, _f32, _vp, _i64, _i64, _vp,
                           _i64, _vp], _i32),
-    "sgl_paged_prefill": ([_vp, _i64, _i64, _vp, _vp, _i64, _i64, _vp, _vp, _vp, _i32, _i32,
-                           _i32, _i32, _i32, _f32, _vp, _i64, _i64, _vp], _i32),
+    "sgl_paged_prefill": ([_vp, _i64, _i64, _vp, _vp, _i64, _i64, _vp, _vp, _vp, _vp, _i32,
+                           _i32, _i32, _i32, _i32, _f32, _vp, _i64, _i64, _vp], _i32),
 }
 
 
@@ -330,8 +331,9 @@ def paged_decode(plan: DecodePlan, q: torch.Tensor, k_cache: torch.Tensor,
 
 def paged_prefill(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                   indices: torch.Tensor, qo_indptr: torch.Tensor, kv_indptr: torch.Tensor,
-                  max_qo_len: int, o: torch.Tensor, sm_scale: Optional[float] = None) -> None:
-    dev = _need_gpu(q, k_cache, v_cache, indices, qo_indptr, kv_indptr, o)
+                  max_qo_len: int, o: torch.Tensor, sm_scale: Optional[float] = None,
+                  q_start: Optional[torch.Tensor] = None) -> None:
+    dev = _need_gpu(q, k_cache, v_cache, indices, qo_indptr, kv_indptr, o, q_start)
     if q.dtype != torch.bfloat16 or k_cache.dtype != torch.bfloat16 or o.dtype != torch.bfloat16:
         raise ValueError("prefill supports bf16 q / KV / o only")
     hq, D = q.shape[1], q.shape[2]
@@ -342,6 +344,7 @@ def paged_prefill(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
     B = qo_indptr.shape[0] - 1
     scale = 1.0 / math.sqrt(D) if sm_scale is None else sm_scale
     _check(lib().sgl_paged_prefill(_p(q), q.stride(0), q.stride(1), _p(k_cache), _p(v_cache), ss,
-                                   sh, _p(indices), _p(qo_indptr), _p(kv_indptr), B, max_qo_len,
+                                   sh, _p(indices), _p(qo_indptr), _p(kv_indptr), _p(q_start), B,
+                                   max_qo_len,
                                    hq, hkv, D, scale, _p(o), o.stride(0), o.stride(1),
                                    _stream(dev)), "sgl_paged_prefill")

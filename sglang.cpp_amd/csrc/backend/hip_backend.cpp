@@ -1,0 +1,508 @@
+// MI355X attention backend over libsgl_attn.so (see hip_backend.h).
+#include "hip_backend.h"
+
+#include <ATen/hip/HIPContext.h>
+#include <c10/hip/HIPCachingAllocator.h>
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+
+namespace sglang {
+namespace {
+
+void* current_stream(const torch::Device& dev) {
+  return static_cast<void*>(at::hip::getCurrentHIPStream(dev.index()).stream());
+}
+
+const torch::TensorOptions kI32 = torch::TensorOptions().dtype(torch::kInt32);
+
+void check_bf16(const torch::Tensor& t, const char* what) {
+  // The reference backend hard-codes bf16 and would reinterpret fp16 data;
+  // this one refuses it instead.
+  TORCH_CHECK(t.scalar_type() == torch::kBFloat16, what, " must be bf16, got ", t.scalar_type());
+}
+
+}  // namespace
+
+void check_sgl(int status, const char* what) {
+  TORCH_CHECK(status == SGL_OK, what, " failed: ", sgl_status_string(status), " (status ", status,
+              ")");
+}
+
+// ---------------------------------------------------------------- KV pool
+
+MHAKVCache::MHAKVCache(int num_kv_heads, int num_layers, int head_dim, int num_pages,
+                       int page_size, torch::Dtype dtype, torch::Device device)
+    : device_(device), num_layers_(num_layers), kv_heads_(num_kv_heads), head_dim_(head_dim) {
+  TORCH_CHECK(num_kv_heads > 0 && num_layers > 0 && head_dim > 0 && num_pages > 0 &&
+                  page_size > 0,
+              "MHAKVCache: sizes must be positive");
+  const int64_t slots = static_cast<int64_t>(num_pages) * page_size;
+  kv_buffer_ = torch::empty({2, num_layers, slots, num_kv_heads, head_dim},
+                            torch::TensorOptions().dtype(dtype).device(device));
+}
+
+torch::Tensor MHAKVCache::k_cache(int layer_id) const { return kv_buffer_[0][layer_id]; }
+torch::Tensor MHAKVCache::v_cache(int layer_id) const { return kv_buffer_[1][layer_id]; }
+
+void MHAKVCache::store_kv(const torch::Tensor& key, const torch::Tensor& val,
+                          const torch::Tensor& out_loc, int layer_id) {
+  // Same checks as the reference (src/kvcache/mha_kvcache.cu:111-141).
+  TORCH_CHECK(key.is_cuda() && val.is_cuda() && out_loc.is_cuda(),
+              "key, val and out_loc must be device tensors");
+  TORCH_CHECK(key.scalar_type() == val.scalar_type(), "key and val dtype must match");
+  TORCH_CHECK(key.scalar_type() == kv_buffer_.scalar_type(), "key dtype must match the pool");
+  TORCH_CHECK(key.stride(-1) == 1 && val.stride(-1) == 1,
+              "key and val last dimension must be contiguous");
+  TORCH_CHECK(out_loc.dim() == 1, "out_loc must be rank 1");
+  auto k = key.dim() == 2 ? key.view({-1, kv_heads_, head_dim_}) : key;
+  auto v = val.dim() == 2 ? val.view({-1, kv_heads_, head_dim_}) : val;
+  TORCH_CHECK(k.dim() == 3 && v.dim() == 3, "key and val must be rank 2 or 3");
+  TORCH_CHECK(k.size(0) == v.size(0) && k.size(0) == out_loc.size(0),
+              "key, val and out_loc token counts must match");
+  TORCH_CHECK(k.size(1) == kv_heads_ && v.size(1) == kv_heads_ && k.size(2) == head_dim_ &&
+                  v.size(2) == head_dim_,
+              "key and val shape must match KV cache layout");
+  TORCH_CHECK(layer_id >= 0 && layer_id < num_layers_, "layer_id out of range");
+  const int64_t tokens = k.size(0);
+  if (tokens == 0) return;
+  int index_dtype;
+  if (out_loc.scalar_type() == torch::kInt32) {
+    index_dtype = SGL_INDEX_I32;
+  } else {
+    TORCH_CHECK(out_loc.scalar_type() == torch::kInt64, "out_loc must be int32 or int64");
+    index_dtype = SGL_INDEX_I64;
+  }
+  auto kb = k_cache(layer_id);
+  auto vb = v_cache(layer_id);
+  check_sgl(sgl_store_kv(kb.data_ptr(), vb.data_ptr(), k.data_ptr(), v.data_ptr(),
+                         out_loc.data_ptr(), index_dtype, tokens,
+                         static_cast<int64_t>(kv_heads_) * head_dim_, k.stride(0), v.stride(0),
+                         current_stream(device_)),
+            "sgl_store_kv");
+}
+
+// ---------------------------------------------------------------- metadata
+
+torch::Tensor HipAttnMetadata::get_last_indices(int bs) const {
+  // Same as the reference (flashinfer_backend.cu:83-85): indptr[1 .. bs] - 1.
+  return indptr.slice(0, 1, bs + 1) - 1;
+}
+
+void HipAttnMetadata::record_stream(c10::Stream stream) const {
+  for (const torch::Tensor* t : {&indptr, &last_rows, &dec_kv_indptr, &dec_indices, &dec_q_rows,
+                                 &dec_table_idx, &pre_qo_indptr, &pre_kv_indptr, &pre_indices,
+                                 &pre_q_start, &pre_table_idx}) {
+    if (t->defined() && t->is_cuda() && t->numel() > 0)
+      c10::hip::HIPCachingAllocator::recordStream(t->storage().data_ptr(),
+                                                  c10::hip::HIPStream(stream));
+  }
+}
+
+// ---------------------------------------------------------------- backend
+
+HipAttnBackend::HipAttnBackend(std::shared_ptr<BaseKVCachePool> kv_cache, int num_qo_heads,
+                               int num_kv_heads, int head_dim)
+    : kv_cache_(std::move(kv_cache)),
+      num_qo_heads_(num_qo_heads),
+      num_kv_heads_(num_kv_heads),
+      head_dim_(head_dim) {
+  TORCH_CHECK(kv_cache_, "HipAttnBackend needs a KV pool");
+  TORCH_CHECK(num_qo_heads > 0 && num_kv_heads > 0 && num_qo_heads % num_kv_heads == 0,
+              "num_qo_heads must be a positive multiple of num_kv_heads");
+  TORCH_CHECK(head_dim == 128, "HipAttnBackend is built for head_dim 128");
+  TORCH_CHECK(kv_cache_->dtype() == torch::kBFloat16, "HipAttnBackend needs a bf16 KV pool");
+}
+
+void HipAttnBackend::set_page_table(const torch::Tensor& page_table) {
+  TORCH_CHECK(page_table.dim() == 2 && page_table.scalar_type() == torch::kInt32 &&
+                  page_table.stride(1) == 1,
+              "page table must be a 2-D int32 tensor with unit column stride");
+  TORCH_CHECK(page_table.device() == kv_cache_->device(), "page table must be on the pool device");
+  page_table_ = page_table;
+}
+
+torch::Tensor& HipAttnBackend::workspace(int64_t bytes) {
+  if (!workspace_.defined() || workspace_.numel() < bytes) {
+    workspace_ = torch::empty({std::max<int64_t>(bytes, 256)},
+                              torch::TensorOptions().dtype(torch::kUInt8).device(
+                                  kv_cache_->device()));
+  }
+  return workspace_;
+}
+
+torch::Tensor HipAttnBackend::to_device(const std::vector<int32_t>& host, HipAttnMetadata& meta) {
+  const int64_t n = static_cast<int64_t>(host.size());
+  auto pinned = torch::empty({n}, kI32.pinned_memory(true));
+  if (n > 0) std::memcpy(pinned.data_ptr<int32_t>(), host.data(), sizeof(int32_t) * n);
+  meta.host_staging.push_back(pinned);  // alive until the async copy has run
+  return pinned.to(kv_cache_->device(), /*non_blocking=*/true);
+}
+
+std::shared_ptr<HipAttnMetadata> HipAttnBackend::metadata_of(Batch& batch) const {
+  auto meta = std::dynamic_pointer_cast<HipAttnMetadata>(batch.attn_metadata);
+  TORCH_CHECK(meta, "HipAttnBackend requires HipAttnMetadata (call prepare_metadata first)");
+  return meta;
+}
+
+// Decode rows for the requests `reqs` of the batch (indices into padded_reqs),
+// their queries at rows q_rows.
+void HipAttnBackend::build_decode_rows(HipAttnMetadata& meta, const std::vector<int>& reqs,
+                                       const std::vector<int32_t>& q_rows, const Batch& batch) {
+  const int n = static_cast<int>(reqs.size());
+  std::vector<int32_t> kv_indptr(n + 1, 0), table_idx(n);
+  for (int i = 0; i < n; ++i) {
+    const auto& req = batch.padded_reqs[reqs[i]];
+    kv_indptr[i + 1] = kv_indptr[i] + req->device_len();
+    table_idx[i] = req->table_idx;
+  }
+  meta.num_decode = n;
+  meta.dec_kv_indptr = to_device(kv_indptr, meta);
+  meta.dec_table_idx = to_device(table_idx, meta);
+  meta.dec_q_rows = to_device(q_rows, meta);
+  meta.dec_indices = torch::empty({std::max(kv_indptr[n], 1)}, kI32.device(kv_cache_->device()));
+  check_sgl(sgl_build_decode_indices(page_table_.data_ptr<int32_t>(), page_table_.size(0),
+                                     page_table_.stride(0), page_table_.size(1),
+                                     meta.dec_table_idx.data_ptr<int32_t>(),
+                                     meta.dec_kv_indptr.data_ptr<int32_t>(),
+                                     meta.dec_indices.data_ptr<int32_t>(), n,
+                                     current_stream(kv_cache_->device())),
+            "sgl_build_decode_indices");
+  check_sgl(sgl_decode_plan(kv_indptr.data(), n, num_qo_heads_, num_kv_heads_, head_dim_,
+                            &meta.dec_plan),
+            "sgl_decode_plan");
+  workspace(meta.dec_plan.workspace_bytes);
+}
+
+void HipAttnBackend::prepare_metadata(Batch& batch) {
+  TORCH_CHECK(page_table_.defined(), "HipAttnBackend: set_page_table() first");
+  auto meta = std::make_shared<HipAttnMetadata>();
+  meta->is_prefill = batch.is_prefill();
+  const int bs = batch.padded_size();
+  for (const auto& req : batch.padded_reqs) {
+    meta->seq_lens.push_back(req->device_len());
+    meta->cached_lens.push_back(req->cached_len);
+  }
+  meta->kv_indptr_host.assign(1, 0);
+  for (const auto& req : batch.padded_reqs)
+    meta->kv_indptr_host.push_back(meta->kv_indptr_host.back() + req->device_len());
+
+  if (batch.is_decode()) {
+    // Reference: decode branch of prepare_metadata (flashinfer_backend.cu:408-464).
+    std::vector<int> all(bs);
+    std::vector<int32_t> rows(bs);
+    for (int i = 0; i < bs; ++i) all[i] = rows[i] = i;
+    build_decode_rows(*meta, all, rows, batch);
+    meta->qo_indptr_host.resize(bs + 1);
+    for (int i = 0; i <= bs; ++i) meta->qo_indptr_host[i] = i;
+    meta->indptr = meta->dec_kv_indptr;
+    batch.attn_metadata = meta;
+    return;
+  }
+
+  // Prefill branch (flashinfer_backend.cu:466-519): qo_len = max(1, extend),
+  // kv_len = device_len; with no cache hit anywhere qo_indptr = kv_indptr.
+  std::vector<int32_t> qo_lens(bs);
+  bool all_no_cache_hit = true;
+  for (int i = 0; i < bs; ++i) {
+    qo_lens[i] = std::max(1, batch.padded_reqs[i]->extend_len());
+    all_no_cache_hit = all_no_cache_hit && batch.padded_reqs[i]->cached_len == 0;
+  }
+  if (all_no_cache_hit) {
+    meta->qo_indptr_host = meta->kv_indptr_host;
+  } else {
+    meta->qo_indptr_host.assign(1, 0);
+    for (int i = 0; i < bs; ++i)
+      meta->qo_indptr_host.push_back(meta->qo_indptr_host.back() + qo_lens[i]);
+  }
+  meta->indptr = to_device(meta->qo_indptr_host, *meta);
+
+  // Route: one-token requests to the split-KV decode kernel, the rest to the
+  // causal prefill kernel; each writes its own rows of o.
+  std::vector<int> dec, pre;
+  for (int i = 0; i < bs; ++i) {
+    const int q_len = meta->qo_indptr_host[i + 1] - meta->qo_indptr_host[i];
+    (q_len == 1 ? dec : pre).push_back(i);
+  }
+  if (!dec.empty()) {
+    std::vector<int32_t> rows;
+    for (int i : dec) rows.push_back(meta->qo_indptr_host[i]);
+    build_decode_rows(*meta, dec, rows, batch);
+  }
+  if (!pre.empty()) {
+    const int n = static_cast<int>(pre.size());
+    std::vector<int32_t> qo_indptr(n + 1, 0), kv_indptr(n + 1, 0), q_start(n), table_idx(n);
+    int max_qo = 0;
+    for (int i = 0; i < n; ++i) {
+      const int r = pre[i];
+      const int q_len = meta->qo_indptr_host[r + 1] - meta->qo_indptr_host[r];
+      qo_indptr[i + 1] = qo_indptr[i] + q_len;
+      kv_indptr[i + 1] = kv_indptr[i] + batch.padded_reqs[r]->device_len();
+      q_start[i] = meta->qo_indptr_host[r];
+      table_idx[i] = batch.padded_reqs[r]->table_idx;
+      max_qo = std::max(max_qo, q_len);
+    }
+    meta->num_prefill = n;
+    meta->max_qo_len = max_qo;
+    meta->pre_qo_indptr = to_device(qo_indptr, *meta);
+    meta->pre_kv_indptr = to_device(kv_indptr, *meta);
+    meta->pre_q_start = to_device(q_start, *meta);
+    meta->pre_table_idx = to_device(table_idx, *meta);
+    meta->pre_indices = torch::empty({std::max(kv_indptr[n], 1)}, kI32.device(kv_cache_->device()));
+    // Device gather replaces the reference's torch::cat of page-table slices.
+    check_sgl(sgl_build_prefill_indices(page_table_.data_ptr<int32_t>(), page_table_.size(0),
+                                        page_table_.stride(0), page_table_.size(1),
+                                        meta->pre_table_idx.data_ptr<int32_t>(),
+                                        meta->pre_kv_indptr.data_ptr<int32_t>(),
+                                        meta->pre_indices.data_ptr<int32_t>(), n,
+                                        current_stream(kv_cache_->device())),
+              "sgl_build_prefill_indices");
+  }
+  batch.attn_metadata = meta;
+}
+
+torch::Tensor HipAttnBackend::forward(const torch::Tensor& q, const torch::Tensor& k,
+                                      const torch::Tensor& v, int layer_id, Batch& batch) {
+  // Reference: FlashInferBackend::forward (flashinfer_backend.cu:522-681):
+  // store the new tokens' K/V, then paged attention over the pool.
+  auto k_3d = k.dim() == 2 ? k.view({-1, num_kv_heads_, head_dim_}) : k;
+  auto v_3d = v.dim() == 2 ? v.view({-1, num_kv_heads_, head_dim_}) : v;
+  kv_cache_->store_kv(k_3d, v_3d, batch.out_loc, layer_id);
+  return attend(q.view({-1, num_qo_heads_, head_dim_}), layer_id, batch);
+}
+
+torch::Tensor HipAttnBackend::attend(const torch::Tensor& q_in, int layer_id, Batch& batch) {
+  auto meta = metadata_of(batch);
+  auto q = q_in.dim() == 2 ? q_in.view({-1, num_qo_heads_, head_dim_}) : q_in;
+  check_bf16(q, "q");
+  TORCH_CHECK(q.dim() == 3 && q.size(1) == num_qo_heads_ && q.size(2) == head_dim_ &&
+                  q.stride(2) == 1,
+              "q must be [T, num_qo_heads, head_dim] with a contiguous last dim");
+  auto o = torch::empty({q.size(0), num_qo_heads_, head_dim_}, q.options());
+  auto kc = kv_cache_->k_cache(layer_id).view({-1, num_kv_heads_, head_dim_});
+  auto vc = kv_cache_->v_cache(layer_id).view({-1, num_kv_heads_, head_dim_});
+  void* stream = current_stream(kv_cache_->device());
+  const float sm_scale = 1.0f / std::sqrt(static_cast<float>(head_dim_));
+  if (meta->num_decode > 0) {
+    auto& ws = workspace(meta->dec_plan.workspace_bytes);
+    check_sgl(sgl_paged_decode(&meta->dec_plan, q.data_ptr(), q.stride(0), q.stride(1),
+                               kc.data_ptr(), vc.data_ptr(), kc.stride(0), kc.stride(1),
+                               meta->dec_indices.data_ptr<int32_t>(),
+                               meta->dec_kv_indptr.data_ptr<int32_t>(),
+                               meta->dec_q_rows.data_ptr<int32_t>(), meta->num_decode,
+                               num_qo_heads_, num_kv_heads_, head_dim_, sm_scale, o.data_ptr(),
+                               o.stride(0), o.stride(1), ws.data_ptr(), ws.numel(), stream),
+              "sgl_paged_decode");
+  }
+  if (meta->num_prefill > 0) {
+    check_sgl(sgl_paged_prefill(q.data_ptr(), q.stride(0), q.stride(1), kc.data_ptr(),
+                                vc.data_ptr(), kc.stride(0), kc.stride(1),
+                                meta->pre_indices.data_ptr<int32_t>(),
+                                meta->pre_qo_indptr.data_ptr<int32_t>(),
+                                meta->pre_kv_indptr.data_ptr<int32_t>(),
+                                meta->pre_q_start.data_ptr<int32_t>(), meta->num_prefill,
+                                meta->max_qo_len, num_qo_heads_, num_kv_heads_, head_dim_,
+                                sm_scale, o.data_ptr(), o.stride(0), o.stride(1), stream),
+              "sgl_paged_prefill");
+  }
+  return o.view({-1, num_qo_heads_ * head_dim_});
+}
+
+// ---------------------------------------------------------------- graphs
+//
+// Capture buffers have fixed addresses sized at init (the reference's
+// DecodeCaptureData, flashinfer_backend.cu:193-219). A decode plan per batch
+// size is built once for the worst case (every request at max_seq_len); the
+// decode kernel sizes its work units on the device from kv_indptr, so replay
+// only refreshes buffer contents — no host split planning, no pinned ring
+// (replaces flashinfer_backend.cu:267-352).
+
+void HipAttnBackend::init_capture_graph(int max_seq_len, const std::vector<int>& bs_list) {
+  capture_.reset();
+  if (bs_list.empty()) return;
+  TORCH_CHECK(max_seq_len > 0, "max_seq_len must be positive");
+  auto cap = std::make_unique<CaptureState>();
+  cap->max_seq_len = max_seq_len;
+  cap->max_bs = *std::max_element(bs_list.begin(), bs_list.end());
+  const auto dev = kI32.device(kv_cache_->device());
+  cap->kv_indptr = torch::zeros({cap->max_bs + 1}, dev);
+  cap->indices = torch::zeros({static_cast<int64_t>(cap->max_bs) * max_seq_len}, dev);
+  cap->q_rows = torch::arange(cap->max_bs, dev);
+  int64_t ws_bytes = 0;
+  for (int bs : bs_list) {
+    std::vector<int32_t> worst(bs + 1);
+    for (int i = 0; i <= bs; ++i) worst[i] = i * max_seq_len;
+    sgl_decode_plan_t plan;
+    check_sgl(sgl_decode_plan(worst.data(), bs, num_qo_heads_, num_kv_heads_, head_dim_, &plan),
+              "sgl_decode_plan");
+    cap->plans[bs] = plan;
+    ws_bytes = std::max<int64_t>(ws_bytes, plan.workspace_bytes);
+  }
+  workspace(ws_bytes);
+  capture_ = std::move(cap);
+}
+
+void HipAttnBackend::prepare_for_capture(Batch& batch) {
+  TORCH_CHECK(batch.is_decode(), "HipAttnBackend capture only supports decode batches");
+  TORCH_CHECK(capture_, "Decode capture state is not initialized");
+  TORCH_CHECK(page_table_.defined(), "HipAttnBackend: set_page_table() first");
+  const int bs = batch.padded_size();
+  auto it = capture_->plans.find(bs);
+  TORCH_CHECK(it != capture_->plans.end(), "No decode capture plan for batch size ", bs);
+  auto meta = std::make_shared<HipAttnMetadata>();
+  meta->use_capture_buffers = true;
+  meta->num_decode = bs;
+  meta->dec_plan = it->second;
+  meta->dec_kv_indptr = capture_->kv_indptr.slice(0, 0, bs + 1);
+  meta->dec_indices = capture_->indices.slice(0, 0, static_cast<int64_t>(bs) * capture_->max_seq_len);
+  meta->dec_q_rows = capture_->q_rows.slice(0, 0, bs);
+  meta->indptr = meta->dec_kv_indptr;
+  // Worst-case contents: every request at max_seq_len over its own row.
+  std::vector<int32_t> worst(bs + 1), table_idx(bs);
+  for (int i = 0; i <= bs; ++i) worst[i] = i * capture_->max_seq_len;
+  for (int i = 0; i < bs; ++i) table_idx[i] = batch.padded_reqs[i]->table_idx;
+  meta->kv_indptr_host = worst;
+  meta->dec_kv_indptr.copy_(to_device(worst, *meta));
+  meta->dec_table_idx = to_device(table_idx, *meta);
+  check_sgl(sgl_build_decode_indices(page_table_.data_ptr<int32_t>(), page_table_.size(0),
+                                     page_table_.stride(0), page_table_.size(1),
+                                     meta->dec_table_idx.data_ptr<int32_t>(),
+                                     meta->dec_kv_indptr.data_ptr<int32_t>(),
+                                     meta->dec_indices.data_ptr<int32_t>(), bs,
+                                     current_stream(kv_cache_->device())),
+            "sgl_build_decode_indices");
+  workspace(meta->dec_plan.workspace_bytes);
+  capture_->metadata[bs] = meta;
+  batch.attn_metadata = meta;
+}
+
+void HipAttnBackend::prepare_for_replay(Batch& batch) {
+  TORCH_CHECK(batch.is_decode(), "HipAttnBackend replay only supports decode batches");
+  TORCH_CHECK(capture_, "Decode capture state is not initialized");
+  auto meta = metadata_of(batch);
+  const int bs = batch.padded_size();
+  auto it = capture_->metadata.find(bs);
+  TORCH_CHECK(it != capture_->metadata.end(), "No decode capture metadata for batch size ", bs);
+  auto& cap = it->second;
+  TORCH_CHECK(static_cast<int>(meta->kv_indptr_host.size()) == bs + 1,
+              "Invalid kv_indptr size for replay");
+  for (int i = 0; i < bs; ++i) {
+    TORCH_CHECK(meta->kv_indptr_host[i + 1] - meta->kv_indptr_host[i] <= capture_->max_seq_len,
+                "request longer than the captured max_seq_len");
+  }
+  const int64_t total = meta->kv_indptr_host[bs];
+  cap->dec_kv_indptr.copy_(meta->dec_kv_indptr, /*non_blocking=*/true);
+  if (total > 0)
+    cap->dec_indices.slice(0, 0, total).copy_(meta->dec_indices.slice(0, 0, total),
+                                              /*non_blocking=*/true);
+  cap->kv_indptr_host = meta->kv_indptr_host;
+  batch.attn_metadata = cap;
+}
+
+// ---------------------------------------------------------------- layers
+
+RMSNorm::RMSNorm(int size, float eps, torch::Device device) : eps_(eps) {
+  weight = torch::ones({size}, torch::TensorOptions().dtype(torch::kBFloat16).device(device));
+}
+
+void RMSNorm::forward_inplace_3d_strided(torch::Tensor& x) const {
+  TORCH_CHECK(x.is_cuda() && x.dim() == 3 && x.stride(2) == 1,
+              "Strided RMSNorm expects a rank-3 device tensor with a contiguous last dim");
+  check_bf16(x, "x");
+  TORCH_CHECK(weight.size(0) == x.size(2), "RMSNorm weight size must match last dimension");
+  check_sgl(sgl_qk_rmsnorm(x.data_ptr(), nullptr, weight.data_ptr(), nullptr, x.size(0), x.size(1),
+                           0, x.size(2), x.stride(0), x.stride(1), 0, 0, eps_,
+                           current_stream(x.device())),
+            "sgl_qk_rmsnorm");
+}
+
+void fused_qk_rmsnorm_inplace_3d_strided(torch::Tensor& q, torch::Tensor& k, const RMSNorm& q_norm,
+                                         const RMSNorm& k_norm) {
+  TORCH_CHECK(q.is_cuda() && k.is_cuda(), "q and k must be device tensors");
+  TORCH_CHECK(q.dim() == 3 && k.dim() == 3, "Fused QK RMSNorm expects rank-3 tensors");
+  TORCH_CHECK(q.stride(2) == 1 && k.stride(2) == 1, "Last dimension must be contiguous");
+  TORCH_CHECK(q.size(0) == k.size(0) && q.size(2) == k.size(2), "q / k shapes must agree");
+  TORCH_CHECK(q_norm.eps() == k_norm.eps(), "Q and K RMSNorm eps must match");
+  check_bf16(q, "q");
+  check_bf16(k, "k");
+  check_sgl(sgl_qk_rmsnorm(q.data_ptr(), k.data_ptr(), q_norm.weight.data_ptr(),
+                           k_norm.weight.data_ptr(), q.size(0), q.size(1), k.size(1), q.size(2),
+                           q.stride(0), q.stride(1), k.stride(0), k.stride(1), q_norm.eps(),
+                           current_stream(q.device())),
+            "sgl_qk_rmsnorm");
+}
+
+RotaryEmbedding::RotaryEmbedding(int head_size, int rotary_dim, int max_position_embeddings,
+                                 float base, torch::Device device)
+    : head_size_(head_size), rotary_dim_(rotary_dim) {
+  TORCH_CHECK(rotary_dim > 0 && rotary_dim % 2 == 0 && rotary_dim <= head_size,
+              "rotary_dim must be even and <= head_size");
+  auto opts = torch::TensorOptions().dtype(torch::kFloat32).device(device);
+  cos_cache_ = torch::empty({max_position_embeddings, rotary_dim / 2}, opts);
+  sin_cache_ = torch::empty_like(cos_cache_);
+  check_sgl(sgl_rope_cos_sin_cache(cos_cache_.data_ptr<float>(), sin_cache_.data_ptr<float>(),
+                                   max_position_embeddings, rotary_dim, base,
+                                   current_stream(device)),
+            "sgl_rope_cos_sin_cache");
+}
+
+void RotaryEmbedding::forward_inplace(const torch::Tensor& positions, torch::Tensor& query,
+                                      torch::Tensor& key) const {
+  TORCH_CHECK(query.is_cuda() && key.is_cuda() && positions.is_cuda(),
+              "Inputs must be device tensors");
+  TORCH_CHECK(positions.scalar_type() == torch::kInt32, "positions must be int32");
+  check_bf16(query, "query");
+  check_bf16(key, "key");
+  check_sgl(sgl_rope(query.data_ptr(), key.data_ptr(), cos_cache_.data_ptr<float>(),
+                     sin_cache_.data_ptr<float>(), positions.data_ptr<int32_t>(),
+                     positions.size(0), query.size(1), key.size(1), rotary_dim_, query.size(2),
+                     cos_cache_.size(1), query.stride(0), query.stride(1), key.stride(0),
+                     key.stride(1), current_stream(query.device())),
+            "sgl_rope");
+}
+
+AttentionLayer::AttentionLayer(int layer_id, int num_qo_heads, int num_kv_heads, int head_dim,
+                               std::shared_ptr<HipAttnBackend> backend,
+                               std::shared_ptr<RotaryEmbedding> rotary,
+                               std::shared_ptr<RMSNorm> q_norm, std::shared_ptr<RMSNorm> k_norm)
+    : layer_id_(layer_id),
+      num_qo_heads_(num_qo_heads),
+      num_kv_heads_(num_kv_heads),
+      head_dim_(head_dim),
+      backend_(std::move(backend)),
+      rotary_(std::move(rotary)),
+      q_norm_(std::move(q_norm)),
+      k_norm_(std::move(k_norm)) {
+  TORCH_CHECK(backend_ && rotary_, "AttentionLayer needs a backend and a rotary embedding");
+  TORCH_CHECK(static_cast<bool>(q_norm_) == static_cast<bool>(k_norm_),
+              "the fused pass needs both q and k norms or neither");
+  TORCH_CHECK(rotary_->rotary_dim() == head_dim, "the fused pass uses full-width rotary");
+}
+
+torch::Tensor AttentionLayer::forward(const torch::Tensor& qkv, const torch::Tensor& positions,
+                                      Batch& batch) {
+  TORCH_CHECK(qkv.dim() == 2 && qkv.stride(1) == 1, "qkv must be [T, (Hq + 2 Hkv) D]");
+  check_bf16(qkv, "qkv");
+  TORCH_CHECK(qkv.size(1) == (num_qo_heads_ + 2 * num_kv_heads_) * head_dim_,
+              "qkv width does not match the head counts");
+  TORCH_CHECK(positions.scalar_type() == torch::kInt32 && batch.out_loc.scalar_type() == torch::kInt32,
+              "positions and out_loc must be int32 for the fused pass");
+  TORCH_CHECK(batch.out_loc.size(0) == qkv.size(0) && positions.size(0) == qkv.size(0),
+              "positions and out_loc need one entry per token");
+  auto kc = backend_->kv_cache()->k_cache(layer_id_);
+  auto vc = backend_->kv_cache()->v_cache(layer_id_);
+  check_sgl(sgl_fused_qknorm_rope_store(
+                qkv.data_ptr(), qkv.stride(0), kc.data_ptr(), vc.data_ptr(),
+                q_norm_ ? q_norm_->weight.data_ptr() : nullptr,
+                k_norm_ ? k_norm_->weight.data_ptr() : nullptr, rotary_->cos_cache().data_ptr<float>(),
+                rotary_->sin_cache().data_ptr<float>(), positions.data_ptr<int32_t>(),
+                batch.out_loc.data_ptr<int32_t>(), qkv.size(0), num_qo_heads_, num_kv_heads_,
+                head_dim_, q_norm_ ? q_norm_->eps() : 0.f, current_stream(qkv.device())),
+            "sgl_fused_qknorm_rope_store");
+  auto q = qkv.narrow(1, 0, num_qo_heads_ * head_dim_).view({-1, num_qo_heads_, head_dim_});
+  return backend_->attend(q, layer_id_, batch);
+}
+
+}  // namespace sglang

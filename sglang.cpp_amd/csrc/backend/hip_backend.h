@@ -1,0 +1,177 @@
+// MI355X attention backend: the reference's BaseAttnBackend contract over the
+// gfx950 HIP kernels of libsgl_attn.so. LibTorch tensors are containers only;
+// all compute goes through the C ABI in include/sgl_attn.h.
+//
+// Replaces: FlashInferBackend (include/sglang/attention/flashinfer_backend.h:16-100,
+//           src/attention/flashinfer_backend.cu), MHAKVCache
+//           (include/sglang/kvcache/mha_kvcache.h:16-41), RMSNorm qk paths and
+//           RotaryEmbedding (include/sglang/layers/{normalization,rotary_embedding}.h),
+//           AttentionLayer::forward (src/layers/attention_layer.cc:17-51).
+#pragma once
+
+#include <c10/core/Stream.h>
+#include <torch/torch.h>
+
+#include <map>
+#include <memory>
+#include <vector>
+
+#include "../../../include/sgl_attn.h"
+#include "attn_types.h"
+
+namespace sglang {
+
+// Throws c10::Error (as TORCH_CHECK does) with the library's status text.
+void check_sgl(int status, const char* what);
+
+// KV pool [2, L, slots, Hkv, D]; k_cache(l) / v_cache(l) are [slots, Hkv, D].
+// Slots = num_pages * page_size (token-granular, as the reference pool).
+class MHAKVCache : public BaseKVCachePool {
+ public:
+  MHAKVCache(int num_kv_heads, int num_layers, int head_dim, int num_pages, int page_size,
+             torch::Dtype dtype, torch::Device device);
+  torch::Tensor k_cache(int layer_id) const override;
+  torch::Tensor v_cache(int layer_id) const override;
+  // k[t] -> k_cache[out_loc[t]], v likewise (src/kvcache/mha_kvcache.cu:111-155).
+  void store_kv(const torch::Tensor& key, const torch::Tensor& val, const torch::Tensor& out_loc,
+                int layer_id) override;
+  torch::Device device() const override { return device_; }
+  torch::Dtype dtype() const override { return kv_buffer_.scalar_type(); }
+  int num_layers() const override { return num_layers_; }
+  const torch::Tensor& buffer() const { return kv_buffer_; }
+
+ private:
+  torch::Tensor kv_buffer_;
+  torch::Device device_;
+  int num_layers_, kv_heads_, head_dim_;
+};
+
+// Per-batch metadata (the reference's FlashInferAttnMetadata,
+// include/sglang/attention/flashinfer_backend.h:16-37).
+struct HipAttnMetadata : public BaseAttnMetadata {
+  bool is_prefill = false;
+  std::vector<int> seq_lens, cached_lens;
+  std::vector<int32_t> qo_indptr_host, kv_indptr_host;
+  torch::Tensor indptr;  // qo_indptr (prefill) / kv_indptr (decode), device
+  torch::Tensor last_rows;  // row of each request's last query token, device
+
+  // Decode rows: every request of a decode batch, and the qo_len == 1
+  // requests of a prefill-phase batch (mixed chunked-prefill + decode steps).
+  int num_decode = 0;
+  torch::Tensor dec_kv_indptr, dec_indices, dec_q_rows, dec_table_idx;
+  sgl_decode_plan_t dec_plan{};
+
+  // Prefill rows: requests of a prefill-phase batch with qo_len > 1.
+  int num_prefill = 0;
+  int max_qo_len = 0;
+  torch::Tensor pre_qo_indptr, pre_kv_indptr, pre_indices, pre_q_start, pre_table_idx;
+
+  bool use_capture_buffers = false;
+  std::vector<torch::Tensor> host_staging;  // pinned buffers of pending H2D copies
+
+  torch::Tensor get_last_indices(int bs) const override;
+  // Marks the device tensors as used on `stream` (the scheduler prepares
+  // metadata on its own stream; scheduler.cc:171-179 does this by downcast).
+  void record_stream(c10::Stream stream) const;
+};
+
+class HipAttnBackend : public BaseAttnBackend {
+ public:
+  HipAttnBackend(std::shared_ptr<BaseKVCachePool> kv_cache, int num_qo_heads, int num_kv_heads,
+                 int head_dim);
+
+  // Context::page_table (include/sglang/core/context.h:19-20): [rows, W] int32,
+  // token-granular, device.
+  void set_page_table(const torch::Tensor& page_table);
+
+  void prepare_metadata(Batch& batch) override;
+  torch::Tensor forward(const torch::Tensor& q, const torch::Tensor& k, const torch::Tensor& v,
+                        int layer_id, Batch& batch) override;
+  void init_capture_graph(int max_seq_len, const std::vector<int>& bs_list) override;
+  void prepare_for_capture(Batch& batch) override;
+  void prepare_for_replay(Batch& batch) override;
+
+  // Attention over the pool only (K/V of the new tokens already stored, e.g.
+  // by the fused norm + RoPE + store pass). q: [T, Hq, D] view; returns
+  // [T, Hq * D].
+  torch::Tensor attend(const torch::Tensor& q, int layer_id, Batch& batch);
+
+  int num_qo_heads() const { return num_qo_heads_; }
+  int num_kv_heads() const { return num_kv_heads_; }
+  int head_dim() const { return head_dim_; }
+  const std::shared_ptr<BaseKVCachePool>& kv_cache() const { return kv_cache_; }
+
+ private:
+  std::shared_ptr<HipAttnMetadata> metadata_of(Batch& batch) const;
+  torch::Tensor& workspace(int64_t bytes);
+  torch::Tensor to_device(const std::vector<int32_t>& host, HipAttnMetadata& meta);
+  void build_decode_rows(HipAttnMetadata& meta, const std::vector<int>& reqs,
+                         const std::vector<int32_t>& q_rows, const Batch& batch);
+
+  struct CaptureState {
+    int max_seq_len = 0;
+    int max_bs = 0;
+    torch::Tensor kv_indptr;  // [max_bs + 1]
+    torch::Tensor indices;    // [max_bs * max_seq_len]
+    torch::Tensor q_rows;     // [max_bs]: 0..max_bs-1
+    std::map<int, sgl_decode_plan_t> plans;
+    std::map<int, std::shared_ptr<HipAttnMetadata>> metadata;
+  };
+
+  std::shared_ptr<BaseKVCachePool> kv_cache_;
+  int num_qo_heads_, num_kv_heads_, head_dim_;
+  torch::Tensor page_table_;
+  torch::Tensor workspace_;
+  std::unique_ptr<CaptureState> capture_;
+};
+
+// q/k RMSNorm module (weight [D], bf16).
+class RMSNorm {
+ public:
+  RMSNorm(int size, float eps, torch::Device device);
+  void forward_inplace_3d_strided(torch::Tensor& x) const;  // normalization.cu:271-316
+  float eps() const { return eps_; }
+  torch::Tensor weight;
+
+ private:
+  float eps_;
+};
+
+// normalization.cu:318-384
+void fused_qk_rmsnorm_inplace_3d_strided(torch::Tensor& q, torch::Tensor& k, const RMSNorm& q_norm,
+                                         const RMSNorm& k_norm);
+
+// NeoX RoPE with a half-width fp32 cos/sin cache built on the device
+// (rotary_embedding.cu:75-94 builds the same table with LibTorch-CPU ops).
+class RotaryEmbedding {
+ public:
+  RotaryEmbedding(int head_size, int rotary_dim, int max_position_embeddings, float base,
+                  torch::Device device);
+  void forward_inplace(const torch::Tensor& positions, torch::Tensor& query,
+                       torch::Tensor& key) const;
+  const torch::Tensor& cos_cache() const { return cos_cache_; }
+  const torch::Tensor& sin_cache() const { return sin_cache_; }
+  int rotary_dim() const { return rotary_dim_; }
+
+ private:
+  int head_size_, rotary_dim_;
+  torch::Tensor cos_cache_, sin_cache_;
+};
+
+// qkv [T, (Hq + 2 Hkv) D] -> o [T, Hq D]: qk-norm, RoPE and the KV store in
+// one fused pass, then paged attention (attention_layer.cc:17-51).
+class AttentionLayer {
+ public:
+  AttentionLayer(int layer_id, int num_qo_heads, int num_kv_heads, int head_dim,
+                 std::shared_ptr<HipAttnBackend> backend, std::shared_ptr<RotaryEmbedding> rotary,
+                 std::shared_ptr<RMSNorm> q_norm, std::shared_ptr<RMSNorm> k_norm);
+  torch::Tensor forward(const torch::Tensor& qkv, const torch::Tensor& positions, Batch& batch);
+
+ private:
+  int layer_id_, num_qo_heads_, num_kv_heads_, head_dim_;
+  std::shared_ptr<HipAttnBackend> backend_;
+  std::shared_ptr<RotaryEmbedding> rotary_;
+  std::shared_ptr<RMSNorm> q_norm_, k_norm_;
+};
+
+}  // namespace sglang

@@ -64,10 +64,22 @@ struct DecodeArgs {
   int64_t o_st, o_sh;
   float* part_o;     // [B, max_chunks, hq, D]
   float* part_lse;   // [B, max_chunks, hq]
-  int chunk;         // tokens per work unit (W)
+  int chunk;         // W_max: largest unit (LDS staging capacity)
+  int chunk_min;     // W_min: smallest unit (bounds the pieces per request)
   int max_chunks;    // partial slots per request (max pieces)
   int batch;
+  int num_units;     // workgroups of the decode launch
 };
+
+// Unit size for this launch: the batch's tokens spread evenly over the
+// launched units, in whole 16-token steps, within the plan's [W_min, W_max].
+// Read from kv_indptr on the device, so a plan built for a worst-case batch
+// (graph capture) stays balanced for the shorter batch actually replayed.
+__device__ __forceinline__ int unit_tokens(const DecodeArgs& a, int total) {
+  int w = (total + a.num_units - 1) / a.num_units;
+  w = (w + 15) / 16 * 16;
+  return max(a.chunk_min, min(a.chunk, w));
+}
 
 // Per-wave LDS scratch.
 struct WaveLds {
@@ -281,8 +293,8 @@ __global__ void __launch_bounds__(kMaxKvHeads * kWave)
     __attribute__((amdgpu_waves_per_eu(5))) paged_decode_kernel(DecodeArgs a) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const int u = blockIdx.x;
-  const int W = a.chunk;
   const int total = a.kv_indptr[a.batch];
+  const int W = unit_tokens(a, total);
   const int tok0 = u * W;
   const int tok1 = min(total, tok0 + W);
   const int lane = threadIdx.x & 63;
@@ -341,7 +353,8 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(DecodeArgs a) {
   const int rb = a.kv_indptr[r];
   const int re = a.kv_indptr[r + 1];
   if (re <= rb) return;
-  const int nch = (re - 1) / a.chunk - rb / a.chunk + 1;  // pieces of request r
+  const int W = unit_tokens(a, a.kv_indptr[a.batch]);
+  const int nch = (re - 1) / W - rb / W + 1;  // pieces of request r
   if (nch <= 1) return;
   __shared__ float sh_w[kMaxChunks][kMaxGroup];
   const int G = a.group;
@@ -431,29 +444,33 @@ extern "C" int sgl_decode_plan(const int32_t* kv_indptr_host, int batch_size, in
       static_cast<int64_t>(device_cu_count()) * (waves_per_cu / num_kv_heads > 0
                                                      ? waves_per_cu / num_kv_heads : 1);
   constexpr int64_t kMinUnit = 64;  // keeps per-unit set-up small next to the stream
-  int64_t W = (total + units_target - 1) / units_target;
-  W = (W + kStep - 1) / kStep * kStep;
-  if (W < kMinUnit) W = kMinUnit;
-  // A request of length L touches at most ceil(L / W) + 1 units.
-  const int64_t w_for_pieces = (static_cast<int64_t>(max_len) + kMaxChunks - 2) / (kMaxChunks - 1);
-  if (W < w_for_pieces) W = (w_for_pieces + kStep - 1) / kStep * kStep;
-  if (W > kMaxChunkTokens) {
-    if (w_for_pieces > kMaxChunkTokens) return SGL_ERR_UNSUPPORTED;
-    W = kMaxChunkTokens;
-  }
+  auto round16 = [](int64_t x) { return (x + kStep - 1) / kStep * kStep; };
+  // W_min bounds the pieces of the longest request: ceil(L / W) + 1 <= kMaxChunks.
+  int64_t w_min = round16((static_cast<int64_t>(max_len) + kMaxChunks - 2) / (kMaxChunks - 1));
+  if (w_min < kMinUnit) w_min = kMinUnit;
+  if (w_min > kMaxChunkTokens) return SGL_ERR_UNSUPPORTED;
+  int64_t W = round16((total + units_target - 1) / units_target);
+  if (W < w_min) W = w_min;
+  if (W > kMaxChunkTokens) W = kMaxChunkTokens;
   const int64_t units = total > 0 ? (total + W - 1) / W : 1;
+  // The device picks w = clamp(round16(ceil(total / units)), w_min, W) <= W.
+  int64_t w_dev = round16((total + units - 1) / units);
+  if (w_dev < w_min) w_dev = w_min;
+  if (w_dev > W) w_dev = W;
   int max_pieces = 1;
   for (int r = 0; r < batch_size; ++r) {
     const int rb = kv_indptr_host[r], re = kv_indptr_host[r + 1];
     if (re > rb) {
-      const int pieces = static_cast<int>((re - 1) / W - rb / W + 1);
+      const int pieces = static_cast<int>((re - 1) / w_dev - rb / w_dev + 1);
       max_pieces = pieces > max_pieces ? pieces : max_pieces;
     }
   }
-  // Capacity for any batch no longer than this one: pieces <= ceil(L / W) + 1.
-  const int cap_pieces = static_cast<int>((max_len + W - 1) / W) + (max_len > 0 ? 1 : 0);
+  // Capacity for any batch no longer than this one (any unit size >= w_min).
+  const int cap_pieces =
+      max_len > 0 ? static_cast<int>((max_len + w_min - 1) / w_min) + 1 : 1;
   plan->kv_chunk_size = static_cast<int32_t>(W);
-  plan->max_chunks = cap_pieces > max_pieces ? cap_pieces : max_pieces;
+  plan->min_chunk_size = static_cast<int32_t>(w_min);
+  plan->max_chunks = cap_pieces;
   plan->split_kv = max_pieces > 1 ? 1 : 0;
   plan->num_units = static_cast<int32_t>(units);
   plan->batch_size = batch_size;
@@ -482,6 +499,7 @@ extern "C" int sgl_paged_decode(const sgl_decode_plan_t* plan, const void* q,
   const int group = num_qo_heads / num_kv_heads;
   if (head_dim != kD || group > kMaxGroup || num_kv_heads > kMaxKvHeads) return SGL_ERR_UNSUPPORTED;
   if (plan->kv_chunk_size <= 0 || plan->kv_chunk_size % kStep != 0 ||
+      plan->min_chunk_size <= 0 || plan->min_chunk_size > plan->kv_chunk_size ||
       plan->kv_chunk_size > kMaxChunkTokens || plan->max_chunks <= 0 ||
       plan->max_chunks > kMaxChunks)
     return SGL_ERR_INVALID_ARG;
@@ -513,8 +531,10 @@ extern "C" int sgl_paged_decode(const sgl_decode_plan_t* plan, const void* q,
   a.o_st = o_stride_token;
   a.o_sh = o_stride_head;
   a.chunk = plan->kv_chunk_size;
+  a.chunk_min = plan->min_chunk_size;
   a.max_chunks = plan->max_chunks;
   a.batch = batch_size;
+  a.num_units = plan->num_units;
   if (plan->max_chunks > 1) {
     const WorkspaceLayout w = workspace_layout(plan->batch_size, plan->max_chunks, num_qo_heads);
     char* base = static_cast<char*>(workspace);

@@ -45,6 +45,7 @@ struct PrefillArgs {
   const int32_t* indices;
   const int32_t* qo_indptr;
   const int32_t* kv_indptr;
+  const int32_t* q_start;  // optional first query row per request
   int group;
   float scale_log2;
   uint16_t* o;
@@ -90,8 +91,8 @@ __global__ void __launch_bounds__(kThreads, 2) paged_prefill_kernel(PrefillArgs 
   const int h = blockIdx.y;
   // Heaviest (latest) query tiles first: causal work grows with the tile index.
   const int tile = a.tiles_per_req - 1 - blockIdx.x;
-  const int qo_beg = a.qo_indptr[r];
-  const int qo_len = a.qo_indptr[r + 1] - qo_beg;
+  const int qo_len = a.qo_indptr[r + 1] - a.qo_indptr[r];
+  const int qo_beg = a.q_start ? a.q_start[r] : a.qo_indptr[r];
   const int kv_beg = a.kv_indptr[r];
   const int kv_len = a.kv_indptr[r + 1] - kv_beg;
   const int G = a.group;
@@ -263,7 +264,8 @@ extern "C" int sgl_paged_prefill(const void* q, int64_t q_stride_token, int64_t 
                                  const void* k_cache, const void* v_cache, int64_t kv_stride_slot,
                                  int64_t kv_stride_head, const int32_t* indices,
                                  const int32_t* qo_indptr, const int32_t* kv_indptr,
-                                 int batch_size, int max_qo_len, int num_qo_heads,
+                                 const int32_t* q_start, int batch_size, int max_qo_len,
+                                 int num_qo_heads,
                                  int num_kv_heads, int head_dim, float sm_scale, void* o,
                                  int64_t o_stride_token, int64_t o_stride_head, void* stream) {
   if (batch_size < 0 || max_qo_len < 0 || num_qo_heads <= 0 || num_kv_heads <= 0)
@@ -291,6 +293,7 @@ extern "C" int sgl_paged_prefill(const void* q, int64_t q_stride_token, int64_t 
   a.indices = indices;
   a.qo_indptr = qo_indptr;
   a.kv_indptr = kv_indptr;
+  a.q_start = q_start;
   a.group = group;
   a.scale_log2 = sm_scale * 1.4426950408889634f;
   a.o = static_cast<uint16_t*>(o);

@@ -39,12 +39,13 @@ def assert_attn_close(got: np.ndarray, ref: np.ndarray, atol=ATOL, rtol=RTOL, wh
             f"(atol {atol}, rtol {rtol}); worst at {i}: got {got[i]}, ref {ref[i]}")
 
 
-def assert_bf16_close(got: np.ndarray, ref: np.ndarray, atol: float = 1e-6, what: str = "",
+def assert_bf16_close(got: np.ndarray, ref: np.ndarray, atol=1e-6, what: str = "",
                       max_ulp: int = 1):
     """bf16 results of fp32 math with the same rounding points: within one bf16
     ulp of the oracle, or within atol absolute where the fp32 result sits near
     zero after cancellation (x c - y s), where one fp32 ulp of difference in the
-    inputs (fused multiply-add vs separate rounding) spans many bf16 ulps."""
+    inputs (fused multiply-add vs separate rounding) spans many bf16 ulps.
+    atol may be an array (a per-element bound) broadcastable to ref."""
     dist = bf16_ulp_dist(got, ref)
     diff = np.abs(bf16_f32(got).astype(np.float64) - bf16_f32(ref).astype(np.float64))
     bad = (dist > max_ulp) & (diff > atol)

@@ -61,7 +61,7 @@ def test_argument_checks_reject_before_launch():
     # fused: misaligned qkv
     assert lib.sgl_fused_qknorm_rope_store(18, 128 * 4, 16, 16, None, None, 16, 16, 16, 16, 4, 2,
                                            1, 128, ctypes.c_float(1e-6), None) == -4
-    assert lib.sgl_paged_prefill(16, 0, 0, 16, 16, 0, 0, 16, 16, 16, 2, 4, 16, 8, 64,
+    assert lib.sgl_paged_prefill(16, 0, 0, 16, 16, 0, 0, 16, 16, 16, None, 2, 4, 16, 8, 64,
                                  ctypes.c_float(0.1), 16, 0, 0, None) == -2  # head_dim 64
 
 
@@ -74,22 +74,27 @@ def test_decode_plan_host_logic():
     plan = capi.decode_plan(ip, 32, 8, 128)
     assert plan.kv_chunk_size % 16 == 0 and plan.kv_chunk_size >= 64
     W = plan.kv_chunk_size
+    assert plan.min_chunk_size <= W and plan.min_chunk_size % 16 == 0
     # units cover the token stream exactly
     assert plan.num_units == -(-int(kv.sum()) // W)
-    # pieces per request: units its token span touches
-    pieces = [(ip[r + 1] - 1) // W - ip[r] // W + 1 for r in range(256)]
-    assert plan.max_chunks >= max(pieces) and plan.max_chunks <= -(-int(kv.max()) // W) + 1
+    # the unit size the device picks, and the pieces per request it implies
+    w = min(W, max(plan.min_chunk_size, -(-(-(-int(kv.sum()) // plan.num_units)) // 16) * 16))
+    pieces = [(ip[r + 1] - 1) // w - ip[r] // w + 1 for r in range(256)]
+    assert plan.max_chunks >= max(pieces)
+    assert plan.max_chunks == -(-int(kv.max()) // plan.min_chunk_size) + 1 <= 128
     assert plan.split_kv == (max(pieces) > 1)
     npart = 256 * plan.max_chunks * 32
     assert plan.workspace_bytes == -(-npart * 512 // 256) * 256 + -(-npart * 4 // 256) * 256
-    # one unit per resident workgroup: 3 per CU at 8 kv heads on 256 CUs
-    assert 700 <= plan.num_units <= 800
+    # one unit per resident workgroup: 2 per CU at 8 kv heads on 256 CUs
+    assert 500 <= plan.num_units <= 520
     # a batch shorter than one unit is a single unit; a request inside it is whole
     plan = capi.decode_plan([0, 20, 52], 16, 8, 128)
     assert plan.num_units == 1 and plan.split_kv == 0
-    # graph-capture style plan: every request at the capture max length
-    plan = capi.decode_plan(list(range(0, 8 * 4096 + 1, 4096)), 32, 8, 128)
-    assert plan.max_chunks * plan.kv_chunk_size >= 4096
+    # graph-capture style plan: every request at the capture max length; any
+    # shorter replay batch fits its piece capacity
+    plan = capi.decode_plan(list(range(0, 8 * 32768 + 1, 32768)), 32, 8, 128)
+    assert (plan.max_chunks - 1) * plan.min_chunk_size >= 32768
+    assert plan.max_chunks <= 128
     with pytest.raises(capi.SglError):
         capi.decode_plan([0, 10], 48, 2, 128)  # group 24 > 16
     with pytest.raises(capi.SglError):

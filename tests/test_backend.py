@@ -1,0 +1,263 @@
+"""The C++ backend (HipAttnBackend, MHAKVCache, AttentionLayer) against the
+CPU oracle, through the reference's BaseAttnBackend call sequence
+(prepare_metadata -> forward; init_capture_graph -> prepare_for_capture ->
+capture -> prepare_for_replay -> replay), as the reference's engine drives it
+(src/core/engine.cc, src/core/graph_runner.cc)."""
+import math
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import pkg, wl
+from helpers import assert_attn_close, u16
+
+D = 128
+
+
+def note(msg):
+    print(f"[case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def sb():
+    return pkg.backend.load()
+
+
+def test_backend_module_surface(sb):
+    """Loads on CPU too: every reference-named class is exported."""
+    for name in ["Req", "Batch", "MHAKVCache", "HipAttnBackend", "RMSNorm", "RotaryEmbedding",
+                 "AttentionLayer", "fused_qk_rmsnorm_inplace_3d_strided"]:
+        assert hasattr(sb, name), name
+    r = sb.Req(3, 10, 25)
+    assert (r.table_idx, r.cached_len, r.device_len(), r.extend_len()) == (3, 10, 25, 15)
+
+
+def _gen(dev, seed):
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    return g
+
+
+def _randn(shape, dev, g, scale=1.0):
+    return (torch.randn(shape, device=dev, generator=g) * scale).to(torch.bfloat16)
+
+
+class Setup:
+    """Pool + backend + batch for a PagedBatch."""
+
+    def __init__(self, sb, dev, b, hq, hkv, seed, layers=2):
+        self.b, self.hq, self.hkv = b, hq, hkv
+        self.cache = sb.MHAKVCache(hkv, layers, D, b.num_pages + 1, b.page_size, 0)
+        g = _gen(dev, seed)
+        buf = self.cache.buffer()
+        buf.copy_(_randn(tuple(buf.shape), dev, g))
+        self.backend = sb.HipAttnBackend(self.cache, hq, hkv, D)
+        self.backend.set_page_table(torch.from_numpy(b.page_table).to(dev))
+        reqs = [sb.Req(int(b.table_idx[i]), int(b.cached_lens[i]), int(b.device_lens[i]))
+                for i in range(b.batch_size)]
+        self.batch = sb.Batch(not b.is_decode, reqs, torch.from_numpy(b.positions).to(dev),
+                              torch.from_numpy(b.out_loc).to(dev))
+        T = int(b.qo_indptr[-1])
+        self.q = _randn((T, hq * D), dev, g)
+        self.k = _randn((T, hkv * D), dev, g)
+        self.v = _randn((T, hkv * D), dev, g)
+
+    def expected(self, oracle, layer, scale):
+        """Oracle: store the new tokens in a host copy of the pool, then attend."""
+        b = self.b
+        kc = u16(self.k_before[layer]).copy()
+        vc = u16(self.v_before[layer]).copy()
+        T = self.q.shape[0]
+        kc[b.out_loc] = u16(self.k).reshape(T, self.hkv, D)
+        vc[b.out_loc] = u16(self.v).reshape(T, self.hkv, D)
+        q = u16(self.q).reshape(T, self.hq, D).copy()
+        if b.is_decode:
+            ref = oracle.decode(q, kc, vc, b.indices, b.kv_indptr, scale)
+        else:
+            ref = oracle.prefill(q, kc, vc, b.indices, b.qo_indptr, b.kv_indptr, scale)
+        return ref.reshape(T, -1), kc, vc
+
+    def snapshot(self):
+        L = self.cache.buffer().shape[1]
+        self.k_before = [self.cache.k_cache(l).clone() for l in range(L)]
+        self.v_before = [self.cache.v_cache(l).clone() for l in range(L)]
+
+
+def _run_forward(oracle, s, layer=1):
+    s.snapshot()
+    s.backend.prepare_metadata(s.batch)
+    o = s.backend.forward(s.q, s.k, s.v, layer, s.batch)
+    torch.cuda.synchronize()
+    ref, kc, vc = s.expected(oracle, layer, 1 / math.sqrt(D))
+    assert_attn_close(o.float().cpu().numpy(), ref, what="backend forward")
+    # the store is bit exact, and only this layer's pool changed
+    np.testing.assert_array_equal(u16(s.cache.k_cache(layer)), kc)
+    np.testing.assert_array_equal(u16(s.cache.v_cache(layer)), vc)
+    other = 1 - layer
+    assert torch.equal(s.cache.k_cache(other), s.k_before[other])
+    return o
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("hq,hkv", [(16, 8), (32, 4)])
+def test_backend_decode_forward(oracle, dev, sb, hq, hkv):
+    note(f"backend decode forward {hq}/{hkv}")
+    rng = np.random.default_rng(40)
+    lens = [1, 37, 900, 4096, 129]
+    b = wl.make_paged_batch(rng, [x - 1 for x in lens], lens, page_size=16, decode=True)
+    s = Setup(sb, dev, b, hq, hkv, 41)
+    _run_forward(oracle, s)
+    assert s.batch.num_decode_rows() == len(lens) and s.batch.num_prefill_rows() == 0
+    # decode: get_last_indices = kv_indptr[1..bs] - 1 (as the reference's metadata)
+    got = s.batch.get_last_indices(len(lens)).cpu().numpy()
+    np.testing.assert_array_equal(got, b.kv_indptr[1:] - 1)
+
+
+@pytest.mark.gpu
+def test_backend_prefill_no_cache_hit(oracle, dev, sb):
+    note("backend prefill, no cache hit")
+    rng = np.random.default_rng(42)
+    lens = [1, 77, 640, 2000]
+    b = wl.make_paged_batch(rng, [0] * 4, lens, page_size=16)
+    s = Setup(sb, dev, b, 16, 8, 43)
+    _run_forward(oracle, s)
+    # the length-1 request goes through the decode kernel
+    assert s.batch.num_decode_rows() == 1 and s.batch.num_prefill_rows() == 3
+    np.testing.assert_array_equal(s.batch.get_last_indices(4).cpu().numpy(),
+                                  b.qo_indptr[1:] - 1)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("hq,hkv", [(32, 8), (32, 4)])
+def test_backend_prefill_prefix_and_mixed(oracle, dev, sb, hq, hkv):
+    """Prefix hits, a chunked-prefill chunk and extend-1 rows in one batch."""
+    note(f"backend mixed prefill {hq}/{hkv}")
+    rng = np.random.default_rng(44)
+    cached = [0, 100, 2047, 1024, 5, 3000]
+    dev_lens = [300, 101, 2048, 2048, 6, 3100]
+    b = wl.make_paged_batch(rng, cached, dev_lens, page_size=1)
+    s = Setup(sb, dev, b, hq, hkv, 45)
+    _run_forward(oracle, s, layer=0)
+    assert s.batch.num_decode_rows() == 3 and s.batch.num_prefill_rows() == 3
+    np.testing.assert_array_equal(s.batch.qo_indptr_host(), b.qo_indptr)
+    np.testing.assert_array_equal(s.batch.get_last_indices(6).cpu().numpy(),
+                                  b.qo_indptr[1:] - 1)
+
+
+@pytest.mark.gpu
+def test_backend_rejects_fp16_q(dev, sb):
+    rng = np.random.default_rng(46)
+    b = wl.make_paged_batch(rng, [9], [10], page_size=16, decode=True)
+    s = Setup(sb, dev, b, 16, 8, 47)
+    s.backend.prepare_metadata(s.batch)
+    with pytest.raises(RuntimeError, match="bf16"):
+        s.backend.attend(s.q.to(torch.float16), 0, s.batch)
+
+
+@pytest.mark.gpu
+def test_attention_layer_matches_unfused_modules(dev, sb):
+    """AttentionLayer (fused qk-norm + RoPE + store, then attention) equals the
+    reference's module sequence: fused_qk_rmsnorm, RotaryEmbedding, forward."""
+    note("attention layer fused vs modules")
+    rng = np.random.default_rng(48)
+    hq, hkv = 32, 8
+    b = wl.make_paged_batch(rng, [0, 50, 999], [33, 51, 1400], page_size=16)
+    s1 = Setup(sb, dev, b, hq, hkv, 49)
+    s2 = Setup(sb, dev, b, hq, hkv, 49)
+    g = _gen(dev, 50)
+    rot = sb.RotaryEmbedding(D, D, 8192, 1e6, 0)
+    qn, kn = sb.RMSNorm(D, 1e-6, 0), sb.RMSNorm(D, 1e-6, 0)
+    qn.weight = _randn((D,), dev, g, 0.5) + 1
+    kn.weight = _randn((D,), dev, g, 0.5) + 1
+    T = s1.q.shape[0]
+    qkv = torch.cat([s1.q, s1.k, s1.v], dim=1)
+    layer = sb.AttentionLayer(1, hq, hkv, D, s1.backend, rot, qn, kn)
+    s1.backend.prepare_metadata(s1.batch)
+    o1 = layer.forward(qkv.clone(), s1.batch.positions, s1.batch)
+
+    qkv2 = qkv.clone()
+    q = qkv2[:, :hq * D].view(T, hq, D)
+    k = qkv2[:, hq * D:(hq + hkv) * D].view(T, hkv, D)
+    v = qkv2[:, (hq + hkv) * D:].view(T, hkv, D)
+    sb.fused_qk_rmsnorm_inplace_3d_strided(q, k, qn, kn)
+    rot.forward_inplace(s2.batch.positions, q, k)
+    s2.backend.prepare_metadata(s2.batch)
+    o2 = s2.backend.forward(q, k, v, 1, s2.batch)
+    torch.cuda.synchronize()
+    assert torch.equal(o1.view(torch.int16), o2.view(torch.int16))
+    assert torch.equal(s1.cache.buffer().view(torch.int16), s2.cache.buffer().view(torch.int16))
+
+
+@pytest.mark.gpu
+def test_backend_decode_graph_capture_replay(oracle, dev, sb):
+    """Capture forward once at the worst case, replay on batches of new lengths;
+    every replay matches the oracle and the eager forward of the same batch."""
+    note("backend decode graph capture / replay")
+    hq, hkv, max_seq, bs = 32, 8, 1024, 8
+    rng = np.random.default_rng(51)
+    # one page-table row per request at max_seq, plus the spare row
+    full = wl.make_paged_batch(rng, [max_seq - 1] * bs, [max_seq] * bs, page_size=16,
+                               decode=True)
+    cache = sb.MHAKVCache(hkv, 1, D, full.num_pages + 1, 16, 0)
+    g = _gen(dev, 52)
+    cache.buffer().copy_(_randn(tuple(cache.buffer().shape), dev, g))
+    backend = sb.HipAttnBackend(cache, hq, hkv, D)
+    page_table = torch.from_numpy(full.page_table).to(dev)
+    backend.set_page_table(page_table)
+    backend.init_capture_graph(max_seq, [4, bs])
+
+    static_q = torch.zeros(bs, hq * D, device=dev, dtype=torch.bfloat16)
+    static_k = torch.zeros(bs, hkv * D, device=dev, dtype=torch.bfloat16)
+    static_v = torch.zeros_like(static_k)
+    static_loc = torch.from_numpy(full.out_loc).to(dev)
+    reqs = [sb.Req(i, max_seq - 1, max_seq) for i in range(bs)]
+    cap = sb.Batch(False, reqs, torch.zeros(bs, dtype=torch.int32, device=dev), static_loc)
+    backend.prepare_for_capture(cap)
+    assert cap.uses_capture_buffers()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        backend.forward(static_q, static_k, static_v, 0, cap)  # warm-up
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        static_o = backend.forward(static_q, static_k, static_v, 0, cap)
+
+    scale = 1 / math.sqrt(D)
+    pt = full.page_table
+    for it in range(4):
+        lens = rng.integers(1, max_seq + 1, bs)
+        if it == 3:
+            lens[:] = max_seq
+        loc = np.array([pt[i, lens[i] - 1] for i in range(bs)], np.int32)
+        q = _randn((bs, hq * D), dev, g)
+        k = _randn((bs, hkv * D), dev, g)
+        v = _randn((bs, hkv * D), dev, g)
+        rb = sb.Batch(False, [sb.Req(i, int(n) - 1, int(n)) for i, n in enumerate(lens)],
+                      torch.from_numpy(lens.astype(np.int32) - 1).to(dev),
+                      torch.from_numpy(loc).to(dev))
+        backend.prepare_metadata(rb)
+        backend.prepare_for_replay(rb)
+        static_q.copy_(q)
+        static_k.copy_(k)
+        static_v.copy_(v)
+        static_loc.copy_(rb.out_loc)
+        graph.replay()
+        torch.cuda.synchronize()
+        got = static_o.float().cpu().numpy()
+        kc, vc = u16(cache.k_cache(0)), u16(cache.v_cache(0))
+        ip = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+        idx = np.concatenate([pt[i, :lens[i]] for i in range(bs)]).astype(np.int32)
+        ref = oracle.decode(u16(q).reshape(bs, hq, D).copy(), kc, vc, idx, ip, scale)
+        assert_attn_close(got, ref.reshape(bs, -1), what=f"replay {it}")
+        # eager forward of the same batch (the store rewrites the same values)
+        eb = sb.Batch(False, [sb.Req(i, int(n) - 1, int(n)) for i, n in enumerate(lens)],
+                      rb.positions, rb.out_loc)
+        backend.prepare_metadata(eb)
+        o_eager = backend.forward(q, k, v, 0, eb)
+        torch.cuda.synchronize()
+        assert_attn_close(o_eager.float().cpu().numpy(), ref.reshape(bs, -1),
+                          what=f"eager {it}")

@@ -14,7 +14,8 @@ import pytest
 import torch
 
 from conftest import capi, wl
-from helpers import assert_attn_close, assert_bf16_close, bf16_ulp_dist, from_u16, u16
+from helpers import (assert_attn_close, assert_bf16_close, bf16_f32, bf16_ulp_dist, from_u16,
+                     u16)
 
 pytestmark = pytest.mark.gpu
 
@@ -213,6 +214,14 @@ def test_fused_qknorm_rope_store(oracle, dev, T, hq, hkv, d):
     kh = h[:, hq * d:(hq + hkv) * d].reshape(T, hkv, d).copy()
     vh = h[:, (hq + hkv) * d:].reshape(T, hkv * d).copy()
     oracle.qk_rmsnorm(qh, kh, u16(qw), u16(kw), 1e-6)
+    # The norm's bf16 output may sit one ulp from the oracle's; RoPE then
+    # carries that input difference into x cos - y sin with |cos|, |sin| <= 1,
+    # i.e. up to ulp(x) + ulp(y) <= 2^-7 (|x| + |y|) absolute, which under
+    # cancellation spans several ulps of the (small) output.
+    def carried(xh):
+        x = np.abs(bf16_f32(xh).astype(np.float64))
+        return 2.0 ** -7 * (x + np.roll(x, d // 2, axis=-1)) + 1e-6
+    q_tol, k_tol = carried(qh), carried(kh).reshape(T, -1)
     oracle.rope(qh, kh, cos.cpu().numpy(), sin.cpu().numpy(), pos.cpu().numpy())
     kc_ref, vc_ref = u16(kc).reshape(T, -1).copy(), u16(vc).reshape(T, -1).copy()
     oracle.store_kv(kc_ref, vc_ref, kh.reshape(T, -1), vh, loc.cpu().numpy())
@@ -223,10 +232,15 @@ def test_fused_qknorm_rope_store(oracle, dev, T, hq, hkv, d):
     assert torch.equal(qkv.view(torch.int16), qkv2.view(torch.int16))
     assert torch.equal(kc.view(torch.int16), kc2.view(torch.int16))
     assert torch.equal(vc.view(torch.int16), vc2.view(torch.int16))
-    # vs oracle: two chained bf16 roundings (norm, then RoPE), each within one
-    # ulp, so <= 2 ulps overall; exact placement (V is a pure copy)
-    assert_bf16_close(u16(qkv)[:, :hq * d].reshape(T, hq, d), qh, what="fused q", max_ulp=2)
-    assert_bf16_close(u16(kc).reshape(T, -1), kc_ref, what="fused k cache", max_ulp=2)
+    # vs oracle: within 2 ulps (two chained roundings, norm then RoPE), or
+    # within the norm's rounding carried through the rotation (above);
+    # exact placement (V is a pure copy)
+    assert_bf16_close(u16(qkv)[:, :hq * d].reshape(T, hq, d), qh, what="fused q", max_ulp=2,
+                      atol=q_tol)
+    kc_tol = np.full(kc_ref.shape, 1e-6)
+    kc_tol[loc.cpu().numpy()] = k_tol
+    assert_bf16_close(u16(kc).reshape(T, -1), kc_ref, what="fused k cache", max_ulp=2,
+                      atol=kc_tol)
     np.testing.assert_array_equal(u16(vc).reshape(T, -1), vc_ref)
 
 
@@ -286,10 +300,14 @@ def test_decode_forced_split_and_q_indptr(oracle, dev):
     lens = [1000, 64, 1]
     b = wl.make_paged_batch(rng, [x - 1 for x in lens], lens, page_size=1, decode=True)
     plan = capi.decode_plan(b.kv_indptr, 16, 8, 128)
+    # 128-token units: ceil(1065 / 128) = 9 units; a 1000-token request spans
+    # at most ceil(1000 / 128) + 1 = 9 pieces.
     plan.kv_chunk_size = 128
-    plan.max_chunks = 8
+    plan.min_chunk_size = 128
+    plan.num_units = 9
+    plan.max_chunks = 9
     plan.split_kv = 1
-    plan.workspace_bytes = 3 * 8 * 16 * 129 * 4 + 4096  # partials, lse, counters, padding
+    plan.workspace_bytes = 3 * 9 * 16 * (128 + 1) * 4 + 4096  # partial o and lse, padding
     qip = np.array([4, 0, 2], np.int32)
     q, kc, vc, o, scale, _ = run_decode(dev, b, 16, 8, 128, 13, q_indptr=qip, rows=5, plan=plan)
     ref = oracle.decode(u16(q).copy(), u16(kc), u16(vc), b.indices, b.kv_indptr, scale,
