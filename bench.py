@@ -1,6 +1,6 @@
 """Benchmark of the MI355X attention hot path (one GPU).
 
-Default workload (the headline line): BASELINE config 4 — ragged paged
+Default workload (the headline line): benchmark configuration 4 — ragged paged
 decode at the Qwen3-8B attention shape (32 q / 8 kv heads, head_dim 128,
 bf16), batch 256, kv lengths ~ U[128, 4096], page_size 16, seeded random
 page table, split-KV. One step = one sgl_paged_decode call (the decode

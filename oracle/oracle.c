@@ -9,7 +9,7 @@
  * (allen-shaw/sglang.cpp). Attention outputs are fp32 (an fp32-softmax
  * reference); the elementwise kernels reproduce the reference's bf16
  * rounding points exactly. How each function is pinned (closed forms,
- * library routines, invariants) is listed in DESIGN.md; none is left
+ * library routines, invariants) is in tests/test_oracle_pins.py; none is left
  * unpinned.
  *
  * Build: oracle/Makefile (gcc, OpenMP). Floating-point contraction is off so

@@ -1,6 +1,6 @@
 // Python bindings of the C++ attention backend (module sgl_backend). The
 // classes keep the reference's names so a test reads like the reference's
-// own use of them (src/core/engine.cc, src/layers/attention_layer.cc).
+// own use of them (src/engine/engine.cc, src/layers/attention_layer.cc).
 #include <pybind11/pybind11.h>
 #include <pybind11/stl.h>
 #include <torch/extension.h>

@@ -1,4 +1,4 @@
-"""Seeded synthetic inputs for the attention hot path (the BASELINE configs).
+"""Seeded synthetic inputs for the attention hot path (the five benchmark configurations).
 
 Page tables are built the way the reference's scheduler builds them:
 CacheManager hands out page starts (slot of a page's first token,

@@ -2,7 +2,7 @@
 import numpy as np
 import torch
 
-ATOL = 2e-2  # attention outputs vs the fp32-softmax oracle (BASELINE tolerance)
+ATOL = 2e-2  # attention outputs vs the fp32-softmax oracle (the stated parity tolerance)
 RTOL = 1e-2
 
 

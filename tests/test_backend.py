@@ -2,7 +2,7 @@
 CPU oracle, through the reference's BaseAttnBackend call sequence
 (prepare_metadata -> forward; init_capture_graph -> prepare_for_capture ->
 capture -> prepare_for_replay -> replay), as the reference's engine drives it
-(src/core/engine.cc, src/core/graph_runner.cc)."""
+(src/engine/engine.cc:557-561 and GraphRunner, src/engine/engine.cc:670-743)."""
 import math
 import sys
 
