@@ -198,6 +198,10 @@ __device__ __forceinline__ void decode_head(const DecodeArgs& a, WaveLds& L, con
   for (int nb = 0; nb < 8; ++nb) acc[nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
   for (int t = 0; t < len; t += kStep) {
+    // Keep the workgroup's waves (one per kv head) in step: together they
+    // read each token's whole [Hkv, D] row, which DRAM serves better as one
+    // burst than as per-head pieces spread over time.
+    __builtin_amdgcn_s_barrier();
     const int tn = t + kStep;
     const int kslot_next = sidx[min(tn + n, len - 1)];
     f32x4_t sacc = {0.f, 0.f, 0.f, 0.f};
@@ -437,9 +441,10 @@ extern "C" int sgl_decode_plan(const int32_t* kv_indptr_host, int batch_size, in
     max_len = len > max_len ? len : max_len;
   }
   if (total > 0x7fffffff) return SGL_ERR_UNSUPPORTED;
-  // One work unit per resident workgroup: 24 waves per CU (6 per SIMD at
-  // <= 80 VGPRs; 16 for the 16-head group variant), one wave per kv head.
-  const int waves_per_cu = 20;  // 5 waves per SIMD at <= 96 VGPRs
+  // One work unit per resident workgroup, one wave per kv head, 16 waves per
+  // CU: measured on MI355X, more concurrent row streams per CU lose DRAM
+  // locality faster than they add latency hiding, fewer starve the CU.
+  const int waves_per_cu = 16;
   const int64_t units_target =
       static_cast<int64_t>(device_cu_count()) * (waves_per_cu / num_kv_heads > 0
                                                      ? waves_per_cu / num_kv_heads : 1);
