@@ -35,8 +35,11 @@ __device__ __forceinline__ uint32_t f32_to_bf16_bits(float x) {
 }
 
 // Pack two fp32 into one word of two bf16 (a in the low half).
+// One v_cvt_pk_bf16_f32 (round to nearest even, as the scalar conversion).
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
-  return f32_to_bf16_bits(a) | (f32_to_bf16_bits(b) << 16);
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
 }
 
 // Round-trip through bf16 (the value a bf16 store then load would give).

@@ -35,6 +35,7 @@ constexpr int kBM = 128;   // packed query rows per workgroup (32 per wave)
 constexpr int kBN = 64;    // kv tokens per LDS tile
 constexpr int kPitch = kD + 8;  // LDS row pitch in bf16 (272 B: rotates banks per row)
 constexpr int kThreads = 256;
+constexpr float kRescaleSlack = 8.f;  // log2 units: p <= 256 between rescales
 
 struct PrefillArgs {
   const uint16_t* q;
@@ -52,6 +53,16 @@ struct PrefillArgs {
   int64_t o_st, o_sh;
   int tiles_per_req;  // gridDim.x
 };
+
+// ds_read_b64_tr_b16: within each group of 16 lanes, lane i receives
+// element i % 4 of the 4-element (8-byte) pieces addressed by lanes
+// 4 e + i / 4, e < 4 -- a 4 x 16 -> 16 x 4 transpose of 16-bit data.
+__device__ __forceinline__ bf16x4_t ds_read_tr16(const uint16_t* p) {
+  typedef short s16x4 __attribute__((ext_vector_type(4)));
+  const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s16x4*)(p));
+  return __builtin_bit_cast(bf16x4_t, v);
+}
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(const u32x4_t& v) {
   return __builtin_bit_cast(bf16x8_t, v);
@@ -157,6 +168,10 @@ __global__ void __launch_bounds__(kThreads, 2) paged_prefill_kernel(PrefillArgs 
     if (has_next) load_tile(a, kbase, vbase, idx, tile0 + kBN, kv_len, kr, vr);
     const uint16_t* ks = smem[t & 1][0];
     const uint16_t* vs = smem[t & 1][1];
+    // This lane's transpose-read source: group g = lane / 16 takes tokens
+    // 4 (g / 2) + (lane % 16) / 4 and columns 16 (g % 2) + 4 (lane % 4).
+    const uint16_t* vtr = vs + (4 * (lane >> 5) + ((lane & 15) >> 2)) * kPitch +
+                          16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 
     // S^T for tokens [32 mb, 32 mb + 32) of the tile.
     f32x16_t st[2];
@@ -171,40 +186,49 @@ __global__ void __launch_bounds__(kThreads, 2) paged_prefill_kernel(PrefillArgs 
         st[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(kv), qop[s], st[mb], 0, 0, 0);
       }
     }
-    // Scores -> log2 domain with the causal / length mask.
-    const bool need_mask = tile0 + kBN > first_masked || tile0 + kBN > kv_len;
+    // Causal / length mask, only on tiles that reach past a row's last
+    // visible token (a wave-uniform test, so full tiles skip it entirely).
+    if (tile0 + kBN > first_masked || tile0 + kBN > kv_len) {
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int tok = tile0 + 32 * mb + 8 * (v >> 2) + 4 * hl + (v & 3);
+          if (tok > allow || tok >= kv_len) st[mb][v] = -INFINITY;
+        }
+    }
     float mt = -INFINITY;
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb) {
+    for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        float x = st[mb][v] * a.scale_log2;
-        if (need_mask) {
-          const int tok = tile0 + 32 * mb + 8 * (v >> 2) + 4 * hl + (v & 3);
-          if (tok > allow || tok >= kv_len) x = -INFINITY;
-        }
-        st[mb][v] = x;
-        mt = fmaxf(mt, x);
-      }
+      for (int v = 0; v < 16; ++v) mt = fmaxf(mt, st[mb][v]);
+    mt = fmaxf(mt, __shfl_xor(mt, 32, kWave)) * a.scale_log2;
+    // Lazy rescaling: the reference point m (log2 domain) only moves when a
+    // row's max exceeds it by more than kRescaleSlack, so most tiles skip the
+    // O rescale. Exact: every p and l use the same m; p <= 2^kRescaleSlack.
+    const bool move = mt > m + kRescaleSlack;
+    if (__builtin_amdgcn_ballot_w64(move) != 0) {
+      const float mn = move ? mt : m;
+      const float alpha = __builtin_amdgcn_exp2f(m - mn);  // 0 on the first tile
+      l *= alpha;
+      m = mn;
+#pragma unroll
+      for (int db = 0; db < 4; ++db) acc[db] *= alpha;
     }
-    mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
-    const float mn = fmaxf(m, mt);
-    const float msafe = mn == -INFINITY ? 0.f : mn;
-    const float alpha = exp2f(m - msafe);
+    const float neg_m = m == -INFINITY ? 0.f : -m;  // a row with nothing visible yet
     float ps = 0.f;
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        const float p = exp2f(st[mb][v] - msafe);
+        // v_exp_f32 directly: arguments are <= kRescaleSlack, and results
+        // below 2^-126 flush to zero, which a bf16 weight could not hold.
+        const float p = __builtin_amdgcn_exp2f(fmaf(st[mb][v], a.scale_log2, neg_m));
         st[mb][v] = p;
         ps += p;
       }
     }
-    l = l * alpha + ps;
-    m = mn;
-#pragma unroll
-    for (int db = 0; db < 4; ++db) acc[db] *= alpha;
+    l += ps;
 
     // O^T += V^T P^T over 4 k-steps of 16 tokens.
 #pragma unroll
@@ -215,21 +239,18 @@ __global__ void __launch_bounds__(kThreads, 2) paged_prefill_kernel(PrefillArgs 
 #pragma unroll
       for (int k = 0; k < 4; ++k) pw[k] = pack_bf16x2(st[mb][vb + 2 * k], st[mb][vb + 2 * k + 1]);
       const bf16x8_t pop = as_bf16x8(pw);
-      // Slot e <-> token 16 ks4 + 8 (e / 4) + 4 hl + e % 4; lane reads V[tok][4c .. 4c+3].
-      u32x2_t vrow[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int tok = 16 * ks4 + 8 * (e >> 2) + 4 * hl + (e & 3);
-        vrow[e] = *reinterpret_cast<const u32x2_t*>(vs + tok * kPitch + 4 * c);
-      }
+      // Slots 0-3 <-> tokens 16 ks4 + 4 hl + (0..3), slots 4-7 <-> the same + 8
+      // (the S^T accumulator order). V^T rows come straight from the
+      // row-major tile with transpose reads: in each 16-lane group, lane j
+      // points at V[tok0 + j / 4][d0 + 4 (j % 4) ..] and lane i receives
+      // V[tok0 + e][d0 + i] for e < 4.
 #pragma unroll
       for (int db = 0; db < 4; ++db) {
-        const int w = db >> 1;
-        const uint32_t sel = (db & 1) ? 0x07060302u : 0x05040100u;
-        u32x4_t vo;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) vo[k] = __builtin_amdgcn_perm(vrow[2 * k + 1][w], vrow[2 * k][w], sel);
-        acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(vo), pop, acc[db], 0, 0, 0);
+        const uint16_t* vp = vtr + (16 * ks4) * kPitch + 32 * db;
+        const bf16x4_t lo = ds_read_tr16(vp);
+        const bf16x4_t hi = ds_read_tr16(vp + 8 * kPitch);
+        const bf16x8_t vop = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+        acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vop, pop, acc[db], 0, 0, 0);
       }
     }
 
@@ -240,19 +261,17 @@ __global__ void __launch_bounds__(kThreads, 2) paged_prefill_kernel(PrefillArgs 
   l += __shfl_xor(l, 32, kWave);
   if (!row_ok) return;
   const float inv = l > 0.f ? 1.0f / l : 0.f;
-  // acc[db][4 g + i] holds d = 32 g + 16 hl + 4 i + db.
+  // acc[db][4 g + i] holds d = 32 db + 8 g + 4 hl + i.
   uint16_t* op =
       a.o + static_cast<int64_t>(qo_beg + qtok) * a.o_st + static_cast<int64_t>(qhead) * a.o_sh;
 #pragma unroll
-  for (int g = 0; g < 4; ++g) {
-    float v[16];
+  for (int db = 0; db < 4; ++db)
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int db = 0; db < 4; ++db) v[4 * i + db] = acc[db][4 * g + i] * inv;
-    stg128(op + 32 * g + 16 * hl, pack8(v));
-    stg128(op + 32 * g + 16 * hl + 8, pack8(v + 8));
-  }
+    for (int g = 0; g < 4; ++g) {
+      const u32x2_t w = {pack_bf16x2(acc[db][4 * g] * inv, acc[db][4 * g + 1] * inv),
+                         pack_bf16x2(acc[db][4 * g + 2] * inv, acc[db][4 * g + 3] * inv)};
+      *reinterpret_cast<u32x2_t*>(op + 32 * db + 8 * g + 4 * hl) = w;
+    }
 }
 
 }  // namespace
