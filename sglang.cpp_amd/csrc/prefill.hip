@@ -33,7 +33,6 @@ namespace {
 constexpr int kD = 128;
 constexpr int kBM = 128;   // packed query rows per workgroup (32 per wave)
 constexpr int kBN = 64;    // kv tokens per LDS tile
-constexpr int kPitch = kD + 8;  // LDS row pitch in bf16 (272 B: rotates banks per row)
 constexpr int kThreads = 256;
 constexpr float kRescaleSlack = 8.f;  // log2 units: p <= 256 between rescales
 
@@ -57,43 +56,179 @@ struct PrefillArgs {
 // ds_read_b64_tr_b16: within each group of 16 lanes, lane i receives
 // element i % 4 of the 4-element (8-byte) pieces addressed by lanes
 // 4 e + i / 4, e < 4 -- a 4 x 16 -> 16 x 4 transpose of 16-bit data.
-__device__ __forceinline__ bf16x4_t ds_read_tr16(const uint16_t* p) {
-  typedef short s16x4 __attribute__((ext_vector_type(4)));
-  const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (__attribute__((address_space(3))) s16x4*)(p));
-  return __builtin_bit_cast(bf16x4_t, v);
+// Issued as inline asm: the compiler's wait insertion treats the builtin as
+// touching any LDS and would stall it on the in-flight LDS gathers of the
+// next tile. The caller waits with lds_wait() before using the results.
+__device__ __forceinline__ u32x2_t ds_read_tr16(const uint16_t* p) {
+  const uint32_t addr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
+      (__attribute__((address_space(3))) const void*)(p)));
+  u32x2_t v;
+  asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(v) : "v"(addr));
+  return v;
+}
+
+// lgkmcnt(0), tied to the values it guards so no use is scheduled above it.
+__device__ __forceinline__ void lds_wait(u32x2_t (&v)[8]) {
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]),
+                 "+v"(v[6]), "+v"(v[7]));
 }
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(const u32x4_t& v) {
   return __builtin_bit_cast(bf16x8_t, v);
 }
 
-// Gather one 64-token K and V tile into registers: thread handles 16-byte
-// chunks tid + 256 u (u < 4) of each 16 KiB tile.
-__device__ __forceinline__ void load_tile(const PrefillArgs& a, const uint16_t* kbase,
-                                          const uint16_t* vbase, const int32_t* idx, int tile0,
-                                          int kv_len, u32x4_t (&kr)[4], u32x4_t (&vr)[4]) {
+// K/V tiles live in LDS as 64 rows of 256 bytes with no padding; row r's
+// logical 16-byte chunk c sits at physical chunk c ^ swz(r). swz takes every
+// value 0..15 over 16 consecutive rows (conflict-free ds_read_b128 of 16
+// rows' same chunk) and gives the 4 rows of an aligned quad distinct upper
+// bits (conflict-free transpose reads of 4 rows x 64 bytes).
+__device__ __forceinline__ int swz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
+
+struct Tile {
+  uint16_t k[kBN * kD];
+  uint16_t v[kBN * kD];
+};
+
+// Slot indices of one 64-token tile for this thread's four rows: row
+// 16 u + 4 wave + lane / 16 (u < 4), i.e. (threadIdx.x + 256 u) / 16.
+__device__ __forceinline__ void load_slots(const int32_t* idx, int tile0, int kv_len,
+                                           int32_t (&sl)[4]) {
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
-    const int id = threadIdx.x + kThreads * u;
-    const int tok = id >> 4;
-    const int ch = id & 15;
-    const int t = min(tile0 + tok, kv_len - 1);
-    const int64_t slot = idx[t];
-    kr[u] = ldg128(kbase + slot * a.kv_ss + ch * 8);
-    vr[u] = ldg128(vbase + slot * a.kv_ss + ch * 8);
+    const int tok = (threadIdx.x + kThreads * u) >> 4;
+    sl[u] = idx[min(tile0 + tok, kv_len - 1)];
   }
 }
 
-__device__ __forceinline__ void store_tile(uint16_t* ks, uint16_t* vs, const u32x4_t (&kr)[4],
-                                           const u32x4_t (&vr)[4]) {
+// Gathers one K/V tile straight into LDS (global_load_lds_dwordx4: lane i of
+// a wave writes LDS bytes [16 i, 16 i + 16) after the wave's base), so the
+// prefetch holds no registers. Lane i takes physical chunk i % 16 of its row
+// and therefore loads logical chunk (i % 16) ^ swz(row).
+__device__ __forceinline__ void issue_tile(const PrefillArgs& a, const uint16_t* kbase,
+                                           const uint16_t* vbase, const int32_t (&sl)[4],
+                                           Tile& T, int wave, int lane) {
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
-    const int id = threadIdx.x + kThreads * u;
-    const int tok = id >> 4;
-    const int ch = id & 15;
-    *reinterpret_cast<u32x4_t*>(ks + tok * kPitch + ch * 8) = kr[u];
-    *reinterpret_cast<u32x4_t*>(vs + tok * kPitch + ch * 8) = vr[u];
+    const int row = 16 * u + 4 * wave + (lane >> 4);
+    const int ch = (lane & 15) ^ swz(row);
+    const int64_t off = static_cast<int64_t>(sl[u]) * a.kv_ss + ch * 8;
+    const int lds_row = 16 * u + 4 * wave;  // wave-uniform destination base
+    __builtin_amdgcn_global_load_lds(
+        kbase + off, (__attribute__((address_space(3))) void*)(T.k + lds_row * kD), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(
+        vbase + off, (__attribute__((address_space(3))) void*)(T.v + lds_row * kD), 16, 0, 0);
+  }
+}
+
+// Waits until this wave's LDS gathers have landed (vmcnt(0); expcnt and
+// lgkmcnt left at their maxima).
+__device__ __forceinline__ void wait_gathers() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+struct RowState {
+  f32x16_t acc[4];  // O^T: acc[db][4 g + i] holds d = 32 db + 8 g + 4 hl + i
+  float m, l;
+};
+
+// One 64-token tile of S^T = K Q^T, online softmax and O^T += V^T P^T.
+__device__ __forceinline__ void compute_tile(const PrefillArgs& a, const Tile& T,
+                                             const bf16x8_t (&qop)[8], RowState& st_,
+                                             int tile0, int first_masked, int allow, int kv_len,
+                                             int lane) {
+  const int c = lane & 31;
+  const int hl = lane >> 5;
+  // S^T for tokens [32 mb, 32 mb + 32): lane reads row 32 mb + c, logical
+  // chunk 2 s + hl (d = 16 s + 8 hl .. + 8).
+  const int sw = swz(c);
+  f32x16_t st[2];
+#pragma unroll
+  for (int mb = 0; mb < 2; ++mb) {
+#pragma unroll
+    for (int v = 0; v < 16; ++v) st[mb][v] = 0.f;
+    const uint16_t* krow = T.k + (32 * mb + c) * kD;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      const u32x4_t kv = *reinterpret_cast<const u32x4_t*>(krow + ((2 * s + hl) ^ sw) * 8);
+      st[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(kv), qop[s], st[mb], 0, 0, 0);
+    }
+  }
+  // Causal / length mask, only on tiles that reach past a row's last visible
+  // token (a wave-uniform test, so full tiles skip it entirely).
+  if (tile0 + kBN > first_masked || tile0 + kBN > kv_len) {
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int tok = tile0 + 32 * mb + 8 * (v >> 2) + 4 * hl + (v & 3);
+        if (tok > allow || tok >= kv_len) st[mb][v] = -INFINITY;
+      }
+  }
+  float mt = -INFINITY;
+#pragma unroll
+  for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) mt = fmaxf(mt, st[mb][v]);
+  mt = fmaxf(mt, __shfl_xor(mt, 32, kWave)) * a.scale_log2;
+  // Lazy rescaling: the reference point m (log2 domain) only moves when a
+  // row's max exceeds it by more than kRescaleSlack, so most tiles skip the O
+  // rescale. Exact: every p and l use the same m; p <= 2^kRescaleSlack.
+  const bool move = mt > st_.m + kRescaleSlack;
+  if (__builtin_amdgcn_ballot_w64(move) != 0) {
+    const float mn = move ? mt : st_.m;
+    const float alpha = __builtin_amdgcn_exp2f(st_.m - mn);  // 0 on the first tile
+    st_.l *= alpha;
+    st_.m = mn;
+#pragma unroll
+    for (int db = 0; db < 4; ++db) st_.acc[db] *= alpha;
+  }
+  const float neg_m = st_.m == -INFINITY ? 0.f : -st_.m;  // nothing visible yet
+  float ps = 0.f;
+#pragma unroll
+  for (int mb = 0; mb < 2; ++mb) {
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      // v_exp_f32 directly: arguments are <= kRescaleSlack, and results below
+      // 2^-126 flush to zero, which a bf16 weight could not hold anyway.
+      const float p = __builtin_amdgcn_exp2f(fmaf(st[mb][v], a.scale_log2, neg_m));
+      st[mb][v] = p;
+      ps += p;
+    }
+  }
+  st_.l += ps;
+
+  // O^T += V^T P^T over 4 k-steps of 16 tokens. P^T slots 0-3 <-> tokens
+  // 16 ks4 + 4 hl + (0..3), slots 4-7 <-> the same + 8 (the S^T accumulator
+  // order). V^T comes from the row-major tile by transpose reads: in each
+  // 16-lane group, lane j points at V[tok0 + j / 4][d0 + 4 (j % 4) ..] and
+  // lane i receives V[tok0 + e][d0 + i] for e < 4. Source lane l: row
+  // 4 (l / 32) + (l % 16) / 4 (+ 8 for the upper slots), logical chunk
+  // 4 db + 2 ((l / 16) % 2) + (l % 4) / 2, byte 8 (l % 2) within it.
+  const int vrow = 4 * (lane >> 5) + ((lane & 15) >> 2);
+  const int g = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
+  const int row_hi = (lane >> 2) & 3;  // swz(row) >> 2 (row % 4)
+#pragma unroll
+  for (int ks4 = 0; ks4 < 4; ++ks4) {
+    const int mb = ks4 >> 1;
+    const int vb = (ks4 & 1) * 8;
+    u32x4_t pw;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) pw[k] = pack_bf16x2(st[mb][vb + 2 * k], st[mb][vb + 2 * k + 1]);
+    const bf16x8_t pop = as_bf16x8(pw);
+    u32x2_t vr[8];  // [2 db + hi]
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int hi = 0; hi < 2; ++hi) {
+        const int row = 16 * ks4 + vrow + 8 * hi;
+        const int phys = ((db ^ row_hi) << 2) | (g ^ ((row >> 2) & 3));
+        vr[2 * db + hi] = ds_read_tr16(T.v + row * kD + phys * 8 + 4 * (lane & 1));
+      }
+    lds_wait(vr);
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+      const u32x4_t w = {vr[2 * db][0], vr[2 * db][1], vr[2 * db + 1][0], vr[2 * db + 1][1]};
+      st_.acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(w), pop, st_.acc[db], 0, 0, 0);
+    }
   }
 }
 
@@ -113,7 +248,7 @@ __global__ void __launch_bounds__(kThreads, 2) paged_prefill_kernel(PrefillArgs 
   const int off = kv_len - qo_len;  // causal offset (cached prefix length)
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int c = lane & 31;
   const int hl = lane >> 5;
 
@@ -143,133 +278,62 @@ __global__ void __launch_bounds__(kThreads, 2) paged_prefill_kernel(PrefillArgs 
   // First token index at which some row of the workgroup may be masked.
   const int first_masked = row0 / G + off + 1;
 
-  __shared__ __attribute__((aligned(16))) uint16_t smem[2][2][kBN * kPitch];
+  // Two statically distinct buffers (the loop is unrolled by two), so the
+  // compiler sees that reads of one never alias the gathers into the other.
+  __shared__ Tile tile_a, tile_b;
 
   const uint16_t* kbase = a.kc + static_cast<int64_t>(h) * a.kv_sh;
   const uint16_t* vbase = a.vc + static_cast<int64_t>(h) * a.kv_sh;
   const int32_t* idx = a.indices + kv_beg;
 
-  f32x16_t acc[4];
+  RowState rs;
 #pragma unroll
   for (int db = 0; db < 4; ++db)
 #pragma unroll
-    for (int v = 0; v < 16; ++v) acc[db][v] = 0.f;
-  float m = -INFINITY;
-  float l = 0.f;
+    for (int v = 0; v < 16; ++v) rs.acc[db][v] = 0.f;
+  rs.m = -INFINITY;
+  rs.l = 0.f;
 
-  u32x4_t kr[4], vr[4];
-  load_tile(a, kbase, vbase, idx, 0, kv_len, kr, vr);
-  store_tile(smem[0][0], smem[0][1], kr, vr);
+  // Slot indices run one tile ahead of the gather, which runs one tile ahead
+  // of the matrix cores.
+  int32_t sl[4];
+  load_slots(idx, 0, kv_len, sl);
+  issue_tile(a, kbase, vbase, sl, tile_a, wave, lane);
+  load_slots(idx, kBN, kv_len, sl);
+  wait_gathers();
   __syncthreads();
 
-  for (int t = 0; t < ntiles; ++t) {
-    const int tile0 = t * kBN;
-    const bool has_next = t + 1 < ntiles;
-    if (has_next) load_tile(a, kbase, vbase, idx, tile0 + kBN, kv_len, kr, vr);
-    const uint16_t* ks = smem[t & 1][0];
-    const uint16_t* vs = smem[t & 1][1];
-    // This lane's transpose-read source: group g = lane / 16 takes tokens
-    // 4 (g / 2) + (lane % 16) / 4 and columns 16 (g % 2) + 4 (lane % 4).
-    const uint16_t* vtr = vs + (4 * (lane >> 5) + ((lane & 15) >> 2)) * kPitch +
-                          16 * ((lane >> 4) & 1) + 4 * (lane & 3);
-
-    // S^T for tokens [32 mb, 32 mb + 32) of the tile.
-    f32x16_t st[2];
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb) {
-#pragma unroll
-      for (int v = 0; v < 16; ++v) st[mb][v] = 0.f;
-      const uint16_t* krow = ks + (32 * mb + c) * kPitch + 8 * hl;
-#pragma unroll
-      for (int s = 0; s < 8; ++s) {
-        const u32x4_t kv = *reinterpret_cast<const u32x4_t*>(krow + 16 * s);
-        st[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(kv), qop[s], st[mb], 0, 0, 0);
-      }
+  for (int t = 0; t < ntiles; t += 2) {
+    // Even tile: compute from tile_a, gather tile t + 1 into tile_b.
+    if (t + 1 < ntiles) {
+      issue_tile(a, kbase, vbase, sl, tile_b, wave, lane);
+      load_slots(idx, (t + 2) * kBN, kv_len, sl);
     }
-    // Causal / length mask, only on tiles that reach past a row's last
-    // visible token (a wave-uniform test, so full tiles skip it entirely).
-    if (tile0 + kBN > first_masked || tile0 + kBN > kv_len) {
-#pragma unroll
-      for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int tok = tile0 + 32 * mb + 8 * (v >> 2) + 4 * hl + (v & 3);
-          if (tok > allow || tok >= kv_len) st[mb][v] = -INFINITY;
-        }
+    compute_tile(a, tile_a, qop, rs, t * kBN, first_masked, allow, kv_len, lane);
+    wait_gathers();
+    __syncthreads();
+    if (t + 1 >= ntiles) break;
+    // Odd tile: compute from tile_b, gather tile t + 2 into tile_a.
+    if (t + 2 < ntiles) {
+      issue_tile(a, kbase, vbase, sl, tile_a, wave, lane);
+      load_slots(idx, (t + 3) * kBN, kv_len, sl);
     }
-    float mt = -INFINITY;
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) mt = fmaxf(mt, st[mb][v]);
-    mt = fmaxf(mt, __shfl_xor(mt, 32, kWave)) * a.scale_log2;
-    // Lazy rescaling: the reference point m (log2 domain) only moves when a
-    // row's max exceeds it by more than kRescaleSlack, so most tiles skip the
-    // O rescale. Exact: every p and l use the same m; p <= 2^kRescaleSlack.
-    const bool move = mt > m + kRescaleSlack;
-    if (__builtin_amdgcn_ballot_w64(move) != 0) {
-      const float mn = move ? mt : m;
-      const float alpha = __builtin_amdgcn_exp2f(m - mn);  // 0 on the first tile
-      l *= alpha;
-      m = mn;
-#pragma unroll
-      for (int db = 0; db < 4; ++db) acc[db] *= alpha;
-    }
-    const float neg_m = m == -INFINITY ? 0.f : -m;  // a row with nothing visible yet
-    float ps = 0.f;
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb) {
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        // v_exp_f32 directly: arguments are <= kRescaleSlack, and results
-        // below 2^-126 flush to zero, which a bf16 weight could not hold.
-        const float p = __builtin_amdgcn_exp2f(fmaf(st[mb][v], a.scale_log2, neg_m));
-        st[mb][v] = p;
-        ps += p;
-      }
-    }
-    l += ps;
-
-    // O^T += V^T P^T over 4 k-steps of 16 tokens.
-#pragma unroll
-    for (int ks4 = 0; ks4 < 4; ++ks4) {
-      const int mb = ks4 >> 1;
-      const int vb = (ks4 & 1) * 8;
-      u32x4_t pw;
-#pragma unroll
-      for (int k = 0; k < 4; ++k) pw[k] = pack_bf16x2(st[mb][vb + 2 * k], st[mb][vb + 2 * k + 1]);
-      const bf16x8_t pop = as_bf16x8(pw);
-      // Slots 0-3 <-> tokens 16 ks4 + 4 hl + (0..3), slots 4-7 <-> the same + 8
-      // (the S^T accumulator order). V^T rows come straight from the
-      // row-major tile with transpose reads: in each 16-lane group, lane j
-      // points at V[tok0 + j / 4][d0 + 4 (j % 4) ..] and lane i receives
-      // V[tok0 + e][d0 + i] for e < 4.
-#pragma unroll
-      for (int db = 0; db < 4; ++db) {
-        const uint16_t* vp = vtr + (16 * ks4) * kPitch + 32 * db;
-        const bf16x4_t lo = ds_read_tr16(vp);
-        const bf16x4_t hi = ds_read_tr16(vp + 8 * kPitch);
-        const bf16x8_t vop = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-        acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vop, pop, acc[db], 0, 0, 0);
-      }
-    }
-
-    if (has_next) store_tile(smem[(t + 1) & 1][0], smem[(t + 1) & 1][1], kr, vr);
+    compute_tile(a, tile_b, qop, rs, (t + 1) * kBN, first_masked, allow, kv_len, lane);
+    wait_gathers();
     __syncthreads();
   }
 
-  l += __shfl_xor(l, 32, kWave);
+  float l = rs.l + __shfl_xor(rs.l, 32, kWave);
   if (!row_ok) return;
   const float inv = l > 0.f ? 1.0f / l : 0.f;
-  // acc[db][4 g + i] holds d = 32 db + 8 g + 4 hl + i.
   uint16_t* op =
       a.o + static_cast<int64_t>(qo_beg + qtok) * a.o_st + static_cast<int64_t>(qhead) * a.o_sh;
 #pragma unroll
   for (int db = 0; db < 4; ++db)
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
-      const u32x2_t w = {pack_bf16x2(acc[db][4 * g] * inv, acc[db][4 * g + 1] * inv),
-                         pack_bf16x2(acc[db][4 * g + 2] * inv, acc[db][4 * g + 3] * inv)};
+      const u32x2_t w = {pack_bf16x2(rs.acc[db][4 * g] * inv, rs.acc[db][4 * g + 1] * inv),
+                         pack_bf16x2(rs.acc[db][4 * g + 2] * inv, rs.acc[db][4 * g + 3] * inv)};
       *reinterpret_cast<u32x2_t*>(op + 32 * db + 8 * g + 4 * hl) = w;
     }
 }
