@@ -25,6 +25,8 @@
 // per token and v_perm builds the operands.
 #include <math.h>
 
+#include <type_traits>
+
 #include "common.h"
 
 namespace sgl {
@@ -53,25 +55,57 @@ struct PrefillArgs {
   int tiles_per_req;  // gridDim.x
 };
 
-// ds_read_b64_tr_b16: within each group of 16 lanes, lane i receives
-// element i % 4 of the 4-element (8-byte) pieces addressed by lanes
-// 4 e + i / 4, e < 4 -- a 4 x 16 -> 16 x 4 transpose of 16-bit data.
-// Issued as inline asm: the compiler's wait insertion treats the builtin as
-// touching any LDS and would stall it on the in-flight LDS gathers of the
-// next tile. The caller waits with lds_wait() before using the results.
-__device__ __forceinline__ u32x2_t ds_read_tr16(const uint16_t* p) {
-  const uint32_t addr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
-      (__attribute__((address_space(3))) const void*)(p)));
-  u32x2_t v;
-  asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(v) : "v"(addr));
+// LDS reads of the tile loop are inline asm with compile-time offsets, and
+// their waits are explicit: the compiler's wait insertion cannot tell the
+// tile being read from the tile whose gather is in flight and would stall
+// every read on that gather, and hand-placed waits let each read run several
+// instructions ahead of its use. LDS operations complete in order, so
+// lgkmcnt(N) after a read means "this read and all older ones are done" once
+// at most N younger LGKM operations are outstanding.
+
+// Byte address of a generic pointer into LDS.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return static_cast<uint32_t>(
+      reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void*)(p)));
+}
+
+template <int OFF>
+__device__ __forceinline__ u32x4_t lds_read_b128(uint32_t addr) {
+  u32x4_t v;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
   return v;
 }
 
-// lgkmcnt(0), tied to the values it guards so no use is scheduled above it.
-__device__ __forceinline__ void lds_wait(u32x2_t (&v)[8]) {
-  asm volatile("s_waitcnt lgkmcnt(0)"
+// ds_read_b64_tr_b16: within each group of 16 lanes, lane i receives element
+// i % 4 of the 4-element (8-byte) pieces addressed by lanes 4 e + i / 4,
+// e < 4 -- a 4 x 16 -> 16 x 4 transpose of 16-bit data.
+template <int OFF>
+__device__ __forceinline__ u32x2_t lds_read_tr16(uint32_t addr) {
+  u32x2_t v;
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
+  return v;
+}
+
+// lgkmcnt(N), tied to the value it guards so no use is scheduled above it.
+template <int N, typename T>
+__device__ __forceinline__ void lgkm_wait(T& v) {
+  asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(v) : "i"(N));
+}
+
+template <int N>
+__device__ __forceinline__ void lgkm_wait8(u32x2_t (&v)[8]) {
+  asm volatile("s_waitcnt lgkmcnt(%8)"
                : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]),
-                 "+v"(v[6]), "+v"(v[7]));
+                 "+v"(v[6]), "+v"(v[7])
+               : "i"(N));
+}
+
+template <int I, int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<I + 1, N>(f);
+  }
 }
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(const u32x4_t& v) {
@@ -130,28 +164,48 @@ struct RowState {
   float m, l;
 };
 
-// One 64-token tile of S^T = K Q^T, online softmax and O^T += V^T P^T.
-__device__ __forceinline__ void compute_tile(const PrefillArgs& a, const Tile& T,
+// Per-lane LDS byte addresses of the tile loop (tile buffer 0; buffer 1 and
+// the unrolled positions are compile-time offsets).
+struct LaneAddr {
+  uint32_t k[8];  // K row c, logical chunk 2 s + hl, s < 8 (+ 32 rows: +8192)
+  uint32_t v[8];  // V transpose-read source for [2 db + hi] at ks4 = 0 (+ 4096 per ks4)
+};
+
+constexpr int kTileBytes = 2 * kBN * kD * 2;  // one K + V buffer (32 KiB)
+constexpr int kVOffset = kBN * kD * 2;       // V after K in a buffer
+static_assert(sizeof(Tile) == kTileBytes, "tile buffers are addressed by fixed offsets");
+
+// One 64-token tile of S^T = K Q^T, online softmax and O^T += V^T P^T, from
+// LDS buffer BUF.
+template <int BUF>
+__device__ __forceinline__ void compute_tile(const PrefillArgs& a, const LaneAddr& la,
                                              const bf16x8_t (&qop)[8], RowState& st_,
                                              int tile0, int first_masked, int allow, int kv_len,
                                              int lane) {
-  const int c = lane & 31;
   const int hl = lane >> 5;
-  // S^T for tokens [32 mb, 32 mb + 32): lane reads row 32 mb + c, logical
-  // chunk 2 s + hl (d = 16 s + 8 hl .. + 8).
-  const int sw = swz(c);
+  // S^T for tokens [32 mb, 32 mb + 32): MFMA i uses mb = i % 2, s = i / 2
+  // (the two accumulation chains alternate), its K operand read four MFMAs
+  // ahead.
   f32x16_t st[2];
 #pragma unroll
-  for (int mb = 0; mb < 2; ++mb) {
+  for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
     for (int v = 0; v < 16; ++v) st[mb][v] = 0.f;
-    const uint16_t* krow = T.k + (32 * mb + c) * kD;
-#pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      const u32x4_t kv = *reinterpret_cast<const u32x4_t*>(krow + ((2 * s + hl) ^ sw) * 8);
-      st[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(kv), qop[s], st[mb], 0, 0, 0);
-    }
-  }
+  u32x4_t kb[16];
+  auto kread = [&](auto I) {
+    constexpr int i = decltype(I)::value;
+    kb[i] = lds_read_b128<BUF * kTileBytes + (i & 1) * 32 * kD * 2>(la.k[i >> 1]);
+  };
+  static_for<0, 4>(kread);
+  static_for<0, 16>([&](auto I) {
+    constexpr int i = decltype(I)::value;
+    constexpr int younger = (15 - i) < 3 ? (15 - i) : 3;
+    lgkm_wait<younger>(kb[i]);
+    st[i & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(kb[i]), qop[i >> 1], st[i & 1],
+                                                        0, 0, 0);
+    if constexpr (i + 4 < 16) kread(std::integral_constant<int, i + 4>{});
+  });
+
   // Causal / length mask, only on tiles that reach past a row's last visible
   // token (a wave-uniform test, so full tiles skip it entirely).
   if (tile0 + kBN > first_masked || tile0 + kBN > kv_len) {
@@ -163,6 +217,17 @@ __device__ __forceinline__ void compute_tile(const PrefillArgs& a, const Tile& T
         if (tok > allow || tok >= kv_len) st[mb][v] = -INFINITY;
       }
   }
+  // V^T operands of the first k-step go out before the softmax math.
+  u32x2_t vr[4][8];  // [ks4][2 db + hi]
+  auto vread = [&](auto K) {
+    constexpr int ks4 = decltype(K)::value;
+    static_for<0, 8>([&](auto J) {
+      constexpr int j = decltype(J)::value;
+      vr[ks4][j] = lds_read_tr16<BUF * kTileBytes + ks4 * 16 * kD * 2>(la.v[j]);
+    });
+  };
+  vread(std::integral_constant<int, 0>{});
+
   float mt = -INFINITY;
 #pragma unroll
   for (int mb = 0; mb < 2; ++mb)
@@ -198,38 +263,25 @@ __device__ __forceinline__ void compute_tile(const PrefillArgs& a, const Tile& T
 
   // O^T += V^T P^T over 4 k-steps of 16 tokens. P^T slots 0-3 <-> tokens
   // 16 ks4 + 4 hl + (0..3), slots 4-7 <-> the same + 8 (the S^T accumulator
-  // order). V^T comes from the row-major tile by transpose reads: in each
-  // 16-lane group, lane j points at V[tok0 + j / 4][d0 + 4 (j % 4) ..] and
-  // lane i receives V[tok0 + e][d0 + i] for e < 4. Source lane l: row
-  // 4 (l / 32) + (l % 16) / 4 (+ 8 for the upper slots), logical chunk
-  // 4 db + 2 ((l / 16) % 2) + (l % 4) / 2, byte 8 (l % 2) within it.
-  const int vrow = 4 * (lane >> 5) + ((lane & 15) >> 2);
-  const int g = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
-  const int row_hi = (lane >> 2) & 3;  // swz(row) >> 2 (row % 4)
-#pragma unroll
-  for (int ks4 = 0; ks4 < 4; ++ks4) {
-    const int mb = ks4 >> 1;
-    const int vb = (ks4 & 1) * 8;
+  // order); V^T comes from the row-major tile by transpose reads, one k-step
+  // of reads ahead of its MFMAs.
+  static_for<0, 4>([&](auto K) {
+    constexpr int ks4 = decltype(K)::value;
+    if constexpr (ks4 + 1 < 4) vread(std::integral_constant<int, ks4 + 1>{});
+    constexpr int younger = ks4 + 1 < 4 ? 8 : 0;
     u32x4_t pw;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) pw[k] = pack_bf16x2(st[mb][vb + 2 * k], st[mb][vb + 2 * k + 1]);
+    for (int k = 0; k < 4; ++k)
+      pw[k] = pack_bf16x2(st[ks4 >> 1][(ks4 & 1) * 8 + 2 * k], st[ks4 >> 1][(ks4 & 1) * 8 + 2 * k + 1]);
     const bf16x8_t pop = as_bf16x8(pw);
-    u32x2_t vr[8];  // [2 db + hi]
-#pragma unroll
-    for (int db = 0; db < 4; ++db)
-#pragma unroll
-      for (int hi = 0; hi < 2; ++hi) {
-        const int row = 16 * ks4 + vrow + 8 * hi;
-        const int phys = ((db ^ row_hi) << 2) | (g ^ ((row >> 2) & 3));
-        vr[2 * db + hi] = ds_read_tr16(T.v + row * kD + phys * 8 + 4 * (lane & 1));
-      }
-    lds_wait(vr);
+    lgkm_wait8<younger>(vr[ks4]);
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
-      const u32x4_t w = {vr[2 * db][0], vr[2 * db][1], vr[2 * db + 1][0], vr[2 * db + 1][1]};
+      const u32x4_t w = {vr[ks4][2 * db][0], vr[ks4][2 * db][1], vr[ks4][2 * db + 1][0],
+                         vr[ks4][2 * db + 1][1]};
       st_.acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(w), pop, st_.acc[db], 0, 0, 0);
     }
-  }
+  });
 }
 
 __global__ void __launch_bounds__(kThreads, 2) paged_prefill_kernel(PrefillArgs a) {
@@ -278,13 +330,35 @@ __global__ void __launch_bounds__(kThreads, 2) paged_prefill_kernel(PrefillArgs 
   // First token index at which some row of the workgroup may be masked.
   const int first_masked = row0 / G + off + 1;
 
-  // Two statically distinct buffers (the loop is unrolled by two), so the
-  // compiler sees that reads of one never alias the gathers into the other.
-  __shared__ Tile tile_a, tile_b;
+  // Two K/V buffers; the loop is unrolled by two so each read names its
+  // buffer by a compile-time offset.
+  __shared__ Tile tiles[2];
 
   const uint16_t* kbase = a.kc + static_cast<int64_t>(h) * a.kv_sh;
   const uint16_t* vbase = a.vc + static_cast<int64_t>(h) * a.kv_sh;
   const int32_t* idx = a.indices + kv_beg;
+
+  LaneAddr la;
+  {
+    const uint32_t base = lds_addr(&tiles[0]);
+    const int sw = swz(c);
+#pragma unroll
+    for (int s = 0; s < 8; ++s) la.k[s] = base + c * kD * 2 + ((2 * s + hl) ^ sw) * 16;
+    // Transpose-read source of lane l: row 4 (l / 32) + (l % 16) / 4 (+ 8 for
+    // the upper slots), logical chunk 4 db + 2 ((l / 16) % 2) + (l % 4) / 2,
+    // byte 8 (l % 2) within it; the swizzle of row 16 ks4 + vrow + 8 hi does
+    // not depend on ks4.
+    const int vrow = 4 * (lane >> 5) + ((lane & 15) >> 2);
+    const int g = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int hi = 0; hi < 2; ++hi) {
+        const int row = vrow + 8 * hi;
+        const int phys = (4 * db + g) ^ swz(row);
+        la.v[2 * db + hi] = base + kVOffset + row * kD * 2 + phys * 16 + 8 * (lane & 1);
+      }
+  }
 
   RowState rs;
 #pragma unroll
@@ -298,27 +372,27 @@ __global__ void __launch_bounds__(kThreads, 2) paged_prefill_kernel(PrefillArgs 
   // of the matrix cores.
   int32_t sl[4];
   load_slots(idx, 0, kv_len, sl);
-  issue_tile(a, kbase, vbase, sl, tile_a, wave, lane);
+  issue_tile(a, kbase, vbase, sl, tiles[0], wave, lane);
   load_slots(idx, kBN, kv_len, sl);
   wait_gathers();
   __syncthreads();
 
   for (int t = 0; t < ntiles; t += 2) {
-    // Even tile: compute from tile_a, gather tile t + 1 into tile_b.
+    // Even tile: compute from buffer 0, gather tile t + 1 into buffer 1.
     if (t + 1 < ntiles) {
-      issue_tile(a, kbase, vbase, sl, tile_b, wave, lane);
+      issue_tile(a, kbase, vbase, sl, tiles[1], wave, lane);
       load_slots(idx, (t + 2) * kBN, kv_len, sl);
     }
-    compute_tile(a, tile_a, qop, rs, t * kBN, first_masked, allow, kv_len, lane);
+    compute_tile<0>(a, la, qop, rs, t * kBN, first_masked, allow, kv_len, lane);
     wait_gathers();
     __syncthreads();
     if (t + 1 >= ntiles) break;
-    // Odd tile: compute from tile_b, gather tile t + 2 into tile_a.
+    // Odd tile: compute from buffer 1, gather tile t + 2 into buffer 0.
     if (t + 2 < ntiles) {
-      issue_tile(a, kbase, vbase, sl, tile_a, wave, lane);
+      issue_tile(a, kbase, vbase, sl, tiles[0], wave, lane);
       load_slots(idx, (t + 3) * kBN, kv_len, sl);
     }
-    compute_tile(a, tile_b, qop, rs, (t + 1) * kBN, first_masked, allow, kv_len, lane);
+    compute_tile<1>(a, la, qop, rs, (t + 1) * kBN, first_masked, allow, kv_len, lane);
     wait_gathers();
     __syncthreads();
   }
