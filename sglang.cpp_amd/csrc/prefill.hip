@@ -36,6 +36,7 @@ constexpr int kD = 128;
 constexpr int kBM = 128;   // packed query rows per workgroup (32 per wave)
 constexpr int kBN = 64;    // kv tokens per LDS tile
 constexpr int kThreads = 256;
+constexpr int kXcds = 8;  // MI355X: 8 XCDs, each with its own L2
 constexpr float kRescaleSlack = 8.f;  // log2 units: p <= 256 between rescales
 
 struct PrefillArgs {
@@ -52,7 +53,8 @@ struct PrefillArgs {
   float scale_log2;
   uint16_t* o;
   int64_t o_st, o_sh;
-  int tiles_per_req;  // gridDim.x
+  int tiles_per_req;  // query tiles per (request, kv head)
+  int num_kv_heads;
 };
 
 // LDS reads of the tile loop are inline asm with compile-time offsets, and
@@ -135,23 +137,21 @@ __device__ __forceinline__ void load_slots(const int32_t* idx, int tile0, int kv
   }
 }
 
-// Gathers one K/V tile straight into LDS (global_load_lds_dwordx4: lane i of
-// a wave writes LDS bytes [16 i, 16 i + 16) after the wave's base), so the
-// prefetch holds no registers. Lane i takes physical chunk i % 16 of its row
-// and therefore loads logical chunk (i % 16) ^ swz(row).
-__device__ __forceinline__ void issue_tile(const PrefillArgs& a, const uint16_t* kbase,
-                                           const uint16_t* vbase, const int32_t (&sl)[4],
-                                           Tile& T, int wave, int lane) {
+// Gathers one K (or V) tile straight into LDS (global_load_lds_dwordx4:
+// lane i of a wave writes LDS bytes [16 i, 16 i + 16) after the wave's
+// base), so the prefetch holds no registers. Lane i takes physical chunk
+// i % 16 of its row and therefore loads logical chunk (i % 16) ^ swz(row).
+__device__ __forceinline__ void issue_half(const uint16_t* base, int64_t kv_ss,
+                                           const int32_t (&sl)[4], uint16_t* dst, int wave,
+                                           int lane) {
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
     const int row = 16 * u + 4 * wave + (lane >> 4);
     const int ch = (lane & 15) ^ swz(row);
-    const int64_t off = static_cast<int64_t>(sl[u]) * a.kv_ss + ch * 8;
     const int lds_row = 16 * u + 4 * wave;  // wave-uniform destination base
-    __builtin_amdgcn_global_load_lds(
-        kbase + off, (__attribute__((address_space(3))) void*)(T.k + lds_row * kD), 16, 0, 0);
-    __builtin_amdgcn_global_load_lds(
-        vbase + off, (__attribute__((address_space(3))) void*)(T.v + lds_row * kD), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(base + static_cast<int64_t>(sl[u]) * kv_ss + ch * 8,
+                                     (__attribute__((address_space(3))) void*)(dst + lds_row * kD),
+                                     16, 0, 0);
   }
 }
 
@@ -175,18 +175,12 @@ constexpr int kTileBytes = 2 * kBN * kD * 2;  // one K + V buffer (32 KiB)
 constexpr int kVOffset = kBN * kD * 2;       // V after K in a buffer
 static_assert(sizeof(Tile) == kTileBytes, "tile buffers are addressed by fixed offsets");
 
-// One 64-token tile of S^T = K Q^T, online softmax and O^T += V^T P^T, from
-// LDS buffer BUF.
+// S^T = K Q^T for one 64-token tile from LDS buffer BUF: tokens
+// [32 mb, 32 mb + 32) in st[mb]. MFMA i uses mb = i % 2, s = i / 2 (the two
+// accumulation chains alternate); its K operand is read four MFMAs ahead.
 template <int BUF>
-__device__ __forceinline__ void compute_tile(const PrefillArgs& a, const LaneAddr& la,
-                                             const bf16x8_t (&qop)[8], RowState& st_,
-                                             int tile0, int first_masked, int allow, int kv_len,
-                                             int lane) {
-  const int hl = lane >> 5;
-  // S^T for tokens [32 mb, 32 mb + 32): MFMA i uses mb = i % 2, s = i / 2
-  // (the two accumulation chains alternate), its K operand read four MFMAs
-  // ahead.
-  f32x16_t st[2];
+__device__ __forceinline__ void qk_tile(const LaneAddr& la, const bf16x8_t (&qop)[8],
+                                        f32x16_t (&st)[2]) {
 #pragma unroll
   for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
@@ -205,7 +199,12 @@ __device__ __forceinline__ void compute_tile(const PrefillArgs& a, const LaneAdd
                                                         0, 0, 0);
     if constexpr (i + 4 < 16) kread(std::integral_constant<int, i + 4>{});
   });
+}
 
+// Mask, running max and (lazy) rescale of the scores of the tile at tile0.
+__device__ __forceinline__ void softmax_head(const PrefillArgs& a, f32x16_t (&st)[2],
+                                             RowState& rs, int tile0, int first_masked,
+                                             int allow, int kv_len, int hl) {
   // Causal / length mask, only on tiles that reach past a row's last visible
   // token (a wave-uniform test, so full tiles skip it entirely).
   if (tile0 + kBN > first_masked || tile0 + kBN > kv_len) {
@@ -217,17 +216,6 @@ __device__ __forceinline__ void compute_tile(const PrefillArgs& a, const LaneAdd
         if (tok > allow || tok >= kv_len) st[mb][v] = -INFINITY;
       }
   }
-  // V^T operands of the first k-step go out before the softmax math.
-  u32x2_t vr[4][8];  // [ks4][2 db + hi]
-  auto vread = [&](auto K) {
-    constexpr int ks4 = decltype(K)::value;
-    static_for<0, 8>([&](auto J) {
-      constexpr int j = decltype(J)::value;
-      vr[ks4][j] = lds_read_tr16<BUF * kTileBytes + ks4 * 16 * kD * 2>(la.v[j]);
-    });
-  };
-  vread(std::integral_constant<int, 0>{});
-
   float mt = -INFINITY;
 #pragma unroll
   for (int mb = 0; mb < 2; ++mb)
@@ -237,19 +225,25 @@ __device__ __forceinline__ void compute_tile(const PrefillArgs& a, const LaneAdd
   // Lazy rescaling: the reference point m (log2 domain) only moves when a
   // row's max exceeds it by more than kRescaleSlack, so most tiles skip the O
   // rescale. Exact: every p and l use the same m; p <= 2^kRescaleSlack.
-  const bool move = mt > st_.m + kRescaleSlack;
+  const bool move = mt > rs.m + kRescaleSlack;
   if (__builtin_amdgcn_ballot_w64(move) != 0) {
-    const float mn = move ? mt : st_.m;
-    const float alpha = __builtin_amdgcn_exp2f(st_.m - mn);  // 0 on the first tile
-    st_.l *= alpha;
-    st_.m = mn;
+    const float mn = move ? mt : rs.m;
+    const float alpha = __builtin_amdgcn_exp2f(rs.m - mn);  // 0 on the first tile
+    rs.l *= alpha;
+    rs.m = mn;
 #pragma unroll
-    for (int db = 0; db < 4; ++db) st_.acc[db] *= alpha;
+    for (int db = 0; db < 4; ++db) rs.acc[db] *= alpha;
   }
-  const float neg_m = st_.m == -INFINITY ? 0.f : -st_.m;  // nothing visible yet
+}
+
+// p = 2^(s scale - m) in place, their sum into rs.l, packed to the bf16 P^T
+// operands of the four k-steps.
+__device__ __forceinline__ void softmax_exp(const PrefillArgs& a, f32x16_t (&st)[2],
+                                            RowState& rs, bf16x8_t (&pop)[4]) {
+  const float neg_m = rs.m == -INFINITY ? 0.f : -rs.m;  // nothing visible yet
   float ps = 0.f;
 #pragma unroll
-  for (int mb = 0; mb < 2; ++mb) {
+  for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
       // v_exp_f32 directly: arguments are <= kRescaleSlack, and results below
@@ -258,37 +252,70 @@ __device__ __forceinline__ void compute_tile(const PrefillArgs& a, const LaneAdd
       st[mb][v] = p;
       ps += p;
     }
-  }
-  st_.l += ps;
-
-  // O^T += V^T P^T over 4 k-steps of 16 tokens. P^T slots 0-3 <-> tokens
-  // 16 ks4 + 4 hl + (0..3), slots 4-7 <-> the same + 8 (the S^T accumulator
-  // order); V^T comes from the row-major tile by transpose reads, one k-step
-  // of reads ahead of its MFMAs.
-  static_for<0, 4>([&](auto K) {
-    constexpr int ks4 = decltype(K)::value;
-    if constexpr (ks4 + 1 < 4) vread(std::integral_constant<int, ks4 + 1>{});
-    constexpr int younger = ks4 + 1 < 4 ? 8 : 0;
+  rs.l += ps;
+  // P^T slots 0-3 <-> tokens 16 ks4 + 4 hl + (0..3), slots 4-7 <-> the same
+  // + 8 (the S^T accumulator order).
+#pragma unroll
+  for (int ks4 = 0; ks4 < 4; ++ks4) {
     u32x4_t pw;
 #pragma unroll
     for (int k = 0; k < 4; ++k)
       pw[k] = pack_bf16x2(st[ks4 >> 1][(ks4 & 1) * 8 + 2 * k], st[ks4 >> 1][(ks4 & 1) * 8 + 2 * k + 1]);
-    const bf16x8_t pop = as_bf16x8(pw);
-    lgkm_wait8<younger>(vr[ks4]);
+    pop[ks4] = as_bf16x8(pw);
+  }
+}
+
+// O^T += V^T P^T over the 4 k-steps of the tile in LDS buffer BUF. V^T comes
+// from the row-major tile by transpose reads, one k-step ahead of its MFMAs.
+template <int BUF>
+__device__ __forceinline__ void pv_tile(const LaneAddr& la, const bf16x8_t (&pop)[4],
+                                        RowState& rs) {
+  u32x2_t vr[4][8];  // [ks4][2 db + hi]
+  auto vread = [&](auto K) {
+    constexpr int ks4 = decltype(K)::value;
+    static_for<0, 8>([&](auto J) {
+      constexpr int j = decltype(J)::value;
+      vr[ks4][j] = lds_read_tr16<BUF * kTileBytes + ks4 * 16 * kD * 2>(la.v[j]);
+    });
+  };
+  vread(std::integral_constant<int, 0>{});
+  static_for<0, 4>([&](auto K) {
+    constexpr int ks4 = decltype(K)::value;
+    if constexpr (ks4 + 1 < 4) vread(std::integral_constant<int, ks4 + 1>{});
+    lgkm_wait8<(ks4 + 1 < 4 ? 8 : 0)>(vr[ks4]);
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
       const u32x4_t w = {vr[ks4][2 * db][0], vr[ks4][2 * db][1], vr[ks4][2 * db + 1][0],
                          vr[ks4][2 * db + 1][1]};
-      st_.acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(w), pop, st_.acc[db], 0, 0, 0);
+      rs.acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(w), pop[ks4], rs.acc[db], 0, 0, 0);
     }
   });
 }
 
 __global__ void __launch_bounds__(kThreads, 2) paged_prefill_kernel(PrefillArgs a) {
-  const int r = blockIdx.z;
-  const int h = blockIdx.y;
-  // Heaviest (latest) query tiles first: causal work grows with the tile index.
-  const int tile = a.tiles_per_req - 1 - blockIdx.x;
+  // Work item w = (request, kv head, query-tile position), head-major.
+  // Workgroups are dealt to the 8 XCDs round-robin by linear id, so when the
+  // count allows, XCD x takes the contiguous share [x S, (x + 1) S), S = N / 8:
+  // the tiles of one kv head stay on one or two XCDs, whose L2 then holds
+  // that head's K/V. Causal work grows with the tile index, and positions
+  // alternate between the heavy and the light end (T-1, 0, T-2, 1, ...), so
+  // every share carries about the same work; inside a share the heavy half
+  // is dispatched first, heaviest first, then the light half, heaviest first.
+  const int n_items = gridDim.x;
+  const int lin = blockIdx.x;
+  int w;
+  if (n_items % (2 * kXcds) == 0) {
+    const int share = n_items / kXcds;
+    const int j = lin / kXcds;
+    w = (lin % kXcds) * share + (j < share / 2 ? 2 * j : 2 * (share - 1 - j) + 1);
+  } else {
+    w = lin;
+  }
+  const int per_req = a.tiles_per_req * a.num_kv_heads;
+  const int r = w / per_req;
+  const int h = (w - r * per_req) / a.tiles_per_req;
+  const int pos = w - r * per_req - h * a.tiles_per_req;
+  const int tile = (pos & 1) ? (pos >> 1) : a.tiles_per_req - 1 - (pos >> 1);
   const int qo_len = a.qo_indptr[r + 1] - a.qo_indptr[r];
   const int qo_beg = a.q_start ? a.q_start[r] : a.qo_indptr[r];
   const int kv_beg = a.kv_indptr[r];
@@ -368,33 +395,47 @@ __global__ void __launch_bounds__(kThreads, 2) paged_prefill_kernel(PrefillArgs 
   rs.m = -INFINITY;
   rs.l = 0.f;
 
-  // Slot indices run one tile ahead of the gather, which runs one tile ahead
-  // of the matrix cores.
-  int32_t sl[4];
-  load_slots(idx, 0, kv_len, sl);
-  issue_tile(a, kbase, vbase, sl, tiles[0], wave, lane);
-  load_slots(idx, kBN, kv_len, sl);
+  // Software pipeline over 64-token tiles. Iteration t computes S(t + 1)
+  // on the matrix cores while the vector ALUs turn S(t) into P(t), then
+  // O += P(t) V(t). K tiles are therefore gathered one tile ahead of V
+  // tiles: during iteration t the gathers of K(t + 2) and V(t + 1) are in
+  // flight. Tile j's K and V use buffer j % 2. Slot indices of tile t + 2
+  // serve K(t + 2) now and V(t + 2) in the next iteration.
+  int32_t sl_k[4], sl_v[4];
+  load_slots(idx, 0, kv_len, sl_v);
+  issue_half(kbase, a.kv_ss, sl_v, tiles[0].k, wave, lane);
+  issue_half(vbase, a.kv_ss, sl_v, tiles[0].v, wave, lane);
+  load_slots(idx, kBN, kv_len, sl_v);
+  issue_half(kbase, a.kv_ss, sl_v, tiles[1].k, wave, lane);
+  load_slots(idx, 2 * kBN, kv_len, sl_k);
   wait_gathers();
   __syncthreads();
 
+  f32x16_t s_cur[2], s_next[2];
+  bf16x8_t pop[4];
+  qk_tile<0>(la, qop, s_cur);
+  __syncthreads();  // every wave has read K(0) before K(2) overwrites it
+
+  auto step = [&](auto B, int t) {
+    constexpr int buf = decltype(B)::value;  // t % 2
+    if (t + 2 < ntiles) issue_half(kbase, a.kv_ss, sl_k, tiles[buf].k, wave, lane);
+    if (t + 1 < ntiles) issue_half(vbase, a.kv_ss, sl_v, tiles[buf ^ 1].v, wave, lane);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) sl_v[u] = sl_k[u];
+    load_slots(idx, (t + 3) * kBN, kv_len, sl_k);
+    softmax_head(a, s_cur, rs, t * kBN, first_masked, allow, kv_len, hl);
+    qk_tile<buf ^ 1>(la, qop, s_next);  // S(t + 1); unused after the last tile
+    softmax_exp(a, s_cur, rs, pop);
+    pv_tile<buf>(la, pop, rs);
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb) s_cur[mb] = s_next[mb];
+    wait_gathers();
+    __syncthreads();
+  };
   for (int t = 0; t < ntiles; t += 2) {
-    // Even tile: compute from buffer 0, gather tile t + 1 into buffer 1.
-    if (t + 1 < ntiles) {
-      issue_tile(a, kbase, vbase, sl, tiles[1], wave, lane);
-      load_slots(idx, (t + 2) * kBN, kv_len, sl);
-    }
-    compute_tile<0>(a, la, qop, rs, t * kBN, first_masked, allow, kv_len, lane);
-    wait_gathers();
-    __syncthreads();
+    step(std::integral_constant<int, 0>{}, t);
     if (t + 1 >= ntiles) break;
-    // Odd tile: compute from buffer 1, gather tile t + 2 into buffer 0.
-    if (t + 2 < ntiles) {
-      issue_tile(a, kbase, vbase, sl, tiles[0], wave, lane);
-      load_slots(idx, (t + 3) * kBN, kv_len, sl);
-    }
-    compute_tile<1>(a, la, qop, rs, (t + 1) * kBN, first_masked, allow, kv_len, lane);
-    wait_gathers();
-    __syncthreads();
+    step(std::integral_constant<int, 1>{}, t + 1);
   }
 
   float l = rs.l + __shfl_xor(rs.l, 32, kWave);
@@ -438,7 +479,8 @@ extern "C" int sgl_paged_prefill(const void* q, int64_t q_stride_token, int64_t 
     return SGL_ERR_ALIGNMENT;
   const int group = num_qo_heads / num_kv_heads;
   const int64_t tiles = (static_cast<int64_t>(max_qo_len) * group + kBM - 1) / kBM;
-  if (tiles > 0x7fffffff) return SGL_ERR_INVALID_ARG;
+  const int64_t items = tiles * num_kv_heads * batch_size;
+  if (items > 0x7fffffff) return SGL_ERR_INVALID_ARG;
   PrefillArgs a;
   a.q = static_cast<const uint16_t*>(q);
   a.q_st = q_stride_token;
@@ -457,7 +499,8 @@ extern "C" int sgl_paged_prefill(const void* q, int64_t q_stride_token, int64_t 
   a.o_st = o_stride_token;
   a.o_sh = o_stride_head;
   a.tiles_per_req = static_cast<int>(tiles);
-  hipLaunchKernelGGL(paged_prefill_kernel, dim3(tiles, num_kv_heads, batch_size),
-                     dim3(kThreads), 0, static_cast<hipStream_t>(stream), a);
+  a.num_kv_heads = num_kv_heads;
+  hipLaunchKernelGGL(paged_prefill_kernel, dim3(static_cast<uint32_t>(items)), dim3(kThreads), 0,
+                     static_cast<hipStream_t>(stream), a);
   return launch_status();
 }
