@@ -53,8 +53,10 @@ def parse():
 # ------------------------------------------------------------------ helpers
 
 class Timer:
-    """Times K launches of fn: wall clock around the loop (synchronized) and
-    HIP events recorded on the stream the kernels run on."""
+    """Times K launches of fn: wall clock around the loop (synchronized on
+    both sides) and one pair of HIP events recorded on the stream the kernels
+    run on, bracketing the same K steps (per-step event pairs would add a
+    queue barrier between steps)."""
 
     def __init__(self, torch):
         self.torch = torch
@@ -65,17 +67,16 @@ class Timer:
         for _ in range(warmup):
             fn()
         torch.cuda.synchronize()
-        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-               for _ in range(steps)]
-        torch.cuda.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
         t0 = time.perf_counter()
-        for a, b in evs:
-            a.record(stream)
+        start.record(stream)
+        for _ in range(steps):
             fn()
-            b.record(stream)
+        end.record(stream)
         torch.cuda.synchronize()
         wall_ms = (time.perf_counter() - t0) * 1e3 / steps
-        ev_ms = float(np.mean([a.elapsed_time(b) for a, b in evs]))
+        ev_ms = start.elapsed_time(end) / steps
         return wall_ms, ev_ms
 
 
@@ -162,49 +163,40 @@ def setup_fused(torch, capi, wl, w, dev, seed=0):
     return step, wl.fused_store_bytes(s, T)
 
 
-def setup_mixed(torch, capi, wl, w, dev, layers, seed=0):
-    """Config 5: per layer, decode of the 64 qo=1 requests plus prefill of the
-    2048-token chunk, each layer on its own slice of a [2, L, slots, Hkv, D]
-    pool; the whole 48-layer step captured once and replayed as a hipGraph."""
+def setup_mixed(torch, wl, w, dev, layers, seed=0):
+    """Config 5 through the C++ backend (HipAttnBackend over an MHAKVCache
+    [2, L, slots, Hkv, D]): one prefill-phase batch of 64 qo=1 requests and a
+    2048-token chunk; per layer, forward = KV store of the new tokens, the
+    split-KV decode kernel on the qo=1 rows and the causal prefill kernel on
+    the chunk. The 48-layer step is captured once and replayed as a hipGraph."""
+    import __graft_entry__ as entry
+    sb = entry.load_package().backend.load()
     b, s = w.batch, w.shape
     hq, hkv, D = s.num_qo_heads, s.num_kv_heads, s.head_dim
     g = torch.Generator(device=dev)
     g.manual_seed(seed)
-    slots = b.num_slots
-    pool = torch.empty((2, layers, slots, hkv, D), device=dev, dtype=torch.bfloat16)
+    cache = sb.MHAKVCache(hkv, layers, D, b.num_pages + 1, b.page_size, dev.index or 0)
+    pool = cache.buffer()
     for l in range(layers):
         pool[0, l].normal_(generator=g)
         pool[1, l].normal_(generator=g)
+    backend = sb.HipAttnBackend(cache, hq, hkv, D)
+    page_table = torch.from_numpy(b.page_table).to(dev)
+    backend.set_page_table(page_table)
+    reqs = [sb.Req(int(b.table_idx[i]), int(b.cached_lens[i]), int(b.device_lens[i]))
+            for i in range(b.batch_size)]
+    batch = sb.Batch(True, reqs, torch.from_numpy(b.positions).to(dev),
+                     torch.from_numpy(b.out_loc).to(dev))
+    backend.prepare_metadata(batch)
     rows = int(b.qo_indptr[-1])
     qkv = torch.randn((rows, s.qkv_width), device=dev, generator=g).to(torch.bfloat16)
-    q = qkv[:, :hq * D].view(-1, hq, D)
-    o = torch.empty((rows, hq, D), device=dev, dtype=torch.bfloat16)
-    qo = b.qo_lens
-    dec = np.nonzero(qo == 1)[0]
-    pre = np.nonzero(qo > 1)[0]
-    kvl = b.kv_lens
-
-    def sub(reqs):
-        ip = np.concatenate([[0], np.cumsum(kvl[reqs])]).astype(np.int32)
-        idx = np.concatenate([b.indices[b.kv_indptr[r]:b.kv_indptr[r + 1]] for r in reqs])
-        return ip, idx.astype(np.int32)
-
-    d_ip, d_idx = sub(dec)
-    p_ip, p_idx = sub(pre)
-    p_qo = np.concatenate([[b.qo_indptr[pre[0]]], b.qo_indptr[pre + 1]]).astype(np.int32)
-    plan = capi.decode_plan(d_ip, hq, hkv, D)
-    ws = capi.decode_workspace(plan, dev)
-    t = lambda a: torch.from_numpy(a).to(dev)
-    d_ip_t, d_idx_t, d_q_t = t(d_ip), t(d_idx), t(b.qo_indptr[dec].astype(np.int32))
-    p_ip_t, p_idx_t, p_qo_t = t(p_ip), t(p_idx), t(p_qo)
-    max_qo = int(qo[pre].max())
-    scale = 1.0 / math.sqrt(D)
+    q = qkv[:, :hq * D]
+    k = qkv[:, hq * D:(hq + hkv) * D]
+    v = qkv[:, (hq + hkv) * D:]
 
     def layer_pass():
         for l in range(layers):
-            kc, vc = pool[0, l], pool[1, l]
-            capi.paged_decode(plan, q, kc, vc, d_idx_t, d_ip_t, o, ws, scale, d_q_t)
-            capi.paged_prefill(q, kc, vc, p_idx_t, p_qo_t, p_ip_t, max_qo, o, scale)
+            backend.forward(q, k, v, l, batch)
 
     layer_pass()
     torch.cuda.synchronize()
@@ -219,10 +211,14 @@ def setup_mixed(torch, capi, wl, w, dev, layers, seed=0):
         layer_pass()
     torch.cuda.synchronize()
 
+    qo, kvl = b.qo_lens, b.kv_lens
+    dec = np.nonzero(qo == 1)[0]
+    pre = np.nonzero(qo > 1)[0]
+    assert batch.num_decode_rows() == len(dec) and batch.num_prefill_rows() == len(pre)
     dec_bytes = wl.attention_bytes(s, qo[dec], kvl[dec], b.page_size) * layers
     pre_flops = wl.attention_flops(s, qo[pre], kvl[pre], causal=True) * layers
     pre_bytes = wl.attention_bytes(s, qo[pre], kvl[pre], b.page_size) * layers
-    return graph.replay, dec_bytes, pre_flops, pre_bytes, (graph, pool)
+    return graph.replay, dec_bytes, pre_flops, pre_bytes, (graph, cache, backend, batch, qkv)
 
 
 # ------------------------------------------------------------------ CPU baseline
@@ -332,8 +328,7 @@ def run_workload(name, torch, capi, wl, dev, steps, warmup, cfg5_layers):
         return w, rec
     if name == "cfg5":
         w = wl.cfg5_mixed(layers=cfg5_layers)
-        step, dec_bytes, pre_flops, pre_bytes, keep = setup_mixed(torch, capi, wl, w, dev,
-                                                                  cfg5_layers)
+        step, dec_bytes, pre_flops, pre_bytes, keep = setup_mixed(torch, wl, w, dev, cfg5_layers)
         wall, ev = timer.run(step, max(2, steps // 4), max(1, warmup // 2))
         t_roof = dec_bytes / (HBM_PEAK_GBS * 1e9) + pre_flops / (BF16_PEAK_TFLOPS * 1e12)
         rec = {"workload": w.name, "layers": cfg5_layers, "ms_per_step": wall, "graph_ms": ev,

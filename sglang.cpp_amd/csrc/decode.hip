@@ -293,8 +293,10 @@ __device__ __forceinline__ void zero_row(const DecodeArgs& a, int qrow) {
 // the end instead of leaving a tail of long requests. A request that spans
 // several units is written as partials (piece p = unit - first unit of the
 // request) and merged by decode_merge_kernel. Waves take the kv heads.
+// 128 VGPRs (4 waves per SIMD, the 16 per CU the schedule keeps resident):
+// a tighter budget spills, and scratch traffic in the step loop costs ~9%.
 __global__ void __launch_bounds__(kMaxKvHeads * kWave)
-    __attribute__((amdgpu_waves_per_eu(5))) paged_decode_kernel(DecodeArgs a) {
+    __attribute__((amdgpu_waves_per_eu(4))) paged_decode_kernel(DecodeArgs a) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const int u = blockIdx.x;
   const int total = a.kv_indptr[a.batch];
@@ -441,13 +443,14 @@ extern "C" int sgl_decode_plan(const int32_t* kv_indptr_host, int batch_size, in
     max_len = len > max_len ? len : max_len;
   }
   if (total > 0x7fffffff) return SGL_ERR_UNSUPPORTED;
-  // One work unit per resident workgroup, one wave per kv head, 16 waves per
-  // CU: measured on MI355X, more concurrent row streams per CU lose DRAM
-  // locality faster than they add latency hiding, fewer starve the CU.
-  const int waves_per_cu = 16;
-  const int64_t units_target =
-      static_cast<int64_t>(device_cu_count()) * (waves_per_cu / num_kv_heads > 0
-                                                     ? waves_per_cu / num_kv_heads : 1);
+  // One work unit per resident workgroup (one wave per kv head), about 12
+  // waves per CU but at least two workgroups: measured on MI355X, more
+  // concurrent row streams per CU lose DRAM locality faster than they add
+  // latency hiding, while a single 8-wave workgroup per CU starves it.
+  // At most 16 waves per CU are resident (the kernel's 128-VGPR budget).
+  int units_per_cu = 12 / num_kv_heads > 2 ? 12 / num_kv_heads : 2;
+  if (units_per_cu * num_kv_heads > 16) units_per_cu = 16 / num_kv_heads > 1 ? 16 / num_kv_heads : 1;
+  const int64_t units_target = static_cast<int64_t>(device_cu_count()) * units_per_cu;
   constexpr int64_t kMinUnit = 64;  // keeps per-unit set-up small next to the stream
   auto round16 = [](int64_t x) { return (x + kStep - 1) / kStep * kStep; };
   // W_min bounds the pieces of the longest request: ceil(L / W) + 1 <= kMaxChunks.
