@@ -181,6 +181,7 @@ def setup_mixed(torch, wl, w, dev, layers, seed=0):
         pool[0, l].normal_(generator=g)
         pool[1, l].normal_(generator=g)
     backend = sb.HipAttnBackend(cache, hq, hkv, D)
+    backend.set_overlap_mixed(os.environ.get("SGL_OVERLAP_MIXED", "1") != "0")
     page_table = torch.from_numpy(b.page_table).to(dev)
     backend.set_page_table(page_table)
     reqs = [sb.Req(int(b.table_idx[i]), int(b.cached_lens[i]), int(b.device_lens[i]))

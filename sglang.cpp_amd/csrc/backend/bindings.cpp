@@ -106,6 +106,8 @@ PYBIND11_MODULE(sgl_backend, m) {
       .def(py::init<std::shared_ptr<BaseKVCachePool>, int, int, int>(), py::arg("kv_cache"),
            py::arg("num_qo_heads"), py::arg("num_kv_heads"), py::arg("head_dim"))
       .def("set_page_table", &HipAttnBackend::set_page_table)
+      .def("set_overlap_mixed", &HipAttnBackend::set_overlap_mixed)
+      .def("overlap_mixed", &HipAttnBackend::overlap_mixed)
       .def("prepare_metadata", &HipAttnBackend::prepare_metadata)
       .def("forward", &HipAttnBackend::forward, py::arg("q"), py::arg("k"), py::arg("v"),
            py::arg("layer_id"), py::arg("batch"))

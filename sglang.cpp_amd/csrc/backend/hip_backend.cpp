@@ -26,6 +26,10 @@ void check_bf16(const torch::Tensor& t, const char* what) {
 
 }  // namespace
 
+void check_hip(hipError_t status, const char* what) {
+  TORCH_CHECK(status == hipSuccess, what, " failed: ", hipGetErrorString(status));
+}
+
 void check_sgl(int status, const char* what) {
   TORCH_CHECK(status == SGL_OK, what, " failed: ", sgl_status_string(status), " (status ", status,
               ")");
@@ -102,6 +106,24 @@ void HipAttnMetadata::record_stream(c10::Stream stream) const {
 }
 
 // ---------------------------------------------------------------- backend
+
+void* HipAttnBackend::side_stream() {
+  if (!side_stream_) {
+    // A pool stream at the default priority (streams of other priorities
+    // are avoided on purpose).
+    side_stream_ = at::hip::getStreamFromPool(/*isHighPriority=*/false,
+                                              kv_cache_->device().index())
+                       .stream();
+    check_hip(hipEventCreateWithFlags(&fork_event_, hipEventDisableTiming), "hipEventCreate");
+    check_hip(hipEventCreateWithFlags(&join_event_, hipEventDisableTiming), "hipEventCreate");
+  }
+  return side_stream_;
+}
+
+HipAttnBackend::~HipAttnBackend() {
+  if (fork_event_) (void)hipEventDestroy(fork_event_);
+  if (join_event_) (void)hipEventDestroy(join_event_);
+}
 
 HipAttnBackend::HipAttnBackend(std::shared_ptr<BaseKVCachePool> kv_cache, int num_qo_heads,
                                int num_kv_heads, int head_dim)
@@ -285,6 +307,20 @@ torch::Tensor HipAttnBackend::attend(const torch::Tensor& q_in, int layer_id, Ba
   auto vc = kv_cache_->v_cache(layer_id).view({-1, num_kv_heads_, head_dim_});
   void* stream = current_stream(kv_cache_->device());
   const float sm_scale = 1.0f / std::sqrt(static_cast<float>(head_dim_));
+  // A mixed batch runs the prefill rows on a side stream next to the decode
+  // rows (they write disjoint rows of o): the MFMA-bound prefill and the
+  // HBM-bound decode then share the GPU. Fork and join are event edges, so
+  // this also holds inside a captured graph. The persistent decode launch
+  // goes first so its workgroups are resident before the prefill tiles take
+  // the remaining slots (the other order measured no gain).
+  const bool fork = overlap_mixed_ && meta->num_decode > 0 && meta->num_prefill > 0;
+  void* pre_stream = stream;
+  if (fork) {
+    pre_stream = side_stream();
+    check_hip(hipEventRecord(fork_event_, static_cast<hipStream_t>(stream)), "hipEventRecord");
+    check_hip(hipStreamWaitEvent(static_cast<hipStream_t>(pre_stream), fork_event_, 0),
+              "hipStreamWaitEvent");
+  }
   if (meta->num_decode > 0) {
     auto& ws = workspace(meta->dec_plan.workspace_bytes);
     check_sgl(sgl_paged_decode(&meta->dec_plan, q.data_ptr(), q.stride(0), q.stride(1),
@@ -304,8 +340,13 @@ torch::Tensor HipAttnBackend::attend(const torch::Tensor& q_in, int layer_id, Ba
                                 meta->pre_kv_indptr.data_ptr<int32_t>(),
                                 meta->pre_q_start.data_ptr<int32_t>(), meta->num_prefill,
                                 meta->max_qo_len, num_qo_heads_, num_kv_heads_, head_dim_,
-                                sm_scale, o.data_ptr(), o.stride(0), o.stride(1), stream),
+                                sm_scale, o.data_ptr(), o.stride(0), o.stride(1), pre_stream),
               "sgl_paged_prefill");
+  }
+  if (fork) {
+    check_hip(hipEventRecord(join_event_, static_cast<hipStream_t>(pre_stream)), "hipEventRecord");
+    check_hip(hipStreamWaitEvent(static_cast<hipStream_t>(stream), join_event_, 0),
+              "hipStreamWaitEvent");
   }
   return o.view({-1, num_qo_heads_ * head_dim_});
 }

@@ -10,6 +10,7 @@
 #pragma once
 
 #include <c10/core/Stream.h>
+#include <hip/hip_runtime.h>
 #include <torch/torch.h>
 
 #include <map>
@@ -79,6 +80,9 @@ class HipAttnBackend : public BaseAttnBackend {
  public:
   HipAttnBackend(std::shared_ptr<BaseKVCachePool> kv_cache, int num_qo_heads, int num_kv_heads,
                  int head_dim);
+  ~HipAttnBackend() override;
+  HipAttnBackend(const HipAttnBackend&) = delete;
+  HipAttnBackend& operator=(const HipAttnBackend&) = delete;
 
   // Context::page_table (include/sglang/core/context.h:19-20): [rows, W] int32,
   // token-granular, device.
@@ -95,6 +99,11 @@ class HipAttnBackend : public BaseAttnBackend {
   // by the fused norm + RoPE + store pass). q: [T, Hq, D] view; returns
   // [T, Hq * D].
   torch::Tensor attend(const torch::Tensor& q, int layer_id, Batch& batch);
+
+  // Mixed batches: run the prefill rows on a side stream beside the decode
+  // rows (default on).
+  void set_overlap_mixed(bool on) { overlap_mixed_ = on; }
+  bool overlap_mixed() const { return overlap_mixed_; }
 
   int num_qo_heads() const { return num_qo_heads_; }
   int num_kv_heads() const { return num_kv_heads_; }
@@ -123,6 +132,12 @@ class HipAttnBackend : public BaseAttnBackend {
   torch::Tensor page_table_;
   torch::Tensor workspace_;
   std::unique_ptr<CaptureState> capture_;
+  // Side stream and fork/join events for mixed batches (created on first use).
+  void* side_stream();
+  void* side_stream_ = nullptr;
+  bool overlap_mixed_ = true;
+  hipEvent_t fork_event_ = nullptr;
+  hipEvent_t join_event_ = nullptr;
 };
 
 // q/k RMSNorm module (weight [D], bf16).
