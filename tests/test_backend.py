@@ -261,3 +261,43 @@ def test_backend_decode_graph_capture_replay(oracle, dev, sb):
         torch.cuda.synchronize()
         assert_attn_close(o_eager.float().cpu().numpy(), ref.reshape(bs, -1),
                           what=f"eager {it}")
+
+
+@pytest.mark.gpu
+def test_backend_mixed_batch_overlap_and_graph_replay(oracle, dev, sb):
+    """A mixed batch (qo=1 rows beside a prefill chunk): the side-stream
+    overlap gives the same bits as the serial order, and a captured graph of
+    the step replays to the eager result every time."""
+    note("backend mixed batch: overlap and graph replay")
+    rng = np.random.default_rng(53)
+    kv = [900, 3000, 17, 4096 + 512]
+    cached = [899, 2999, 16, 4096]
+    b = wl.make_paged_batch(rng, cached, kv, page_size=16)
+    s = Setup(sb, dev, b, 32, 4, 54, layers=1)
+    s.snapshot()
+    s.backend.prepare_metadata(s.batch)
+    assert s.batch.num_decode_rows() == 3 and s.batch.num_prefill_rows() == 1
+    s.backend.set_overlap_mixed(False)
+    o_serial = s.backend.forward(s.q, s.k, s.v, 0, s.batch).clone()
+    s.backend.set_overlap_mixed(True)
+    o_overlap = s.backend.forward(s.q, s.k, s.v, 0, s.batch).clone()
+    torch.cuda.synchronize()
+    assert torch.equal(o_serial.view(torch.int16), o_overlap.view(torch.int16))
+    ref, _, _ = s.expected(oracle, 0, 1 / math.sqrt(D))
+    assert_attn_close(o_overlap.float().cpu().numpy(), ref, what="mixed overlap")
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        s.backend.forward(s.q, s.k, s.v, 0, s.batch)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        o_graph = s.backend.forward(s.q, s.k, s.v, 0, s.batch)
+    for it in range(3):
+        o_graph.zero_()
+        graph.replay()
+        # eager work between replays, as a serving loop would have
+        o_eager = s.backend.forward(s.q, s.k, s.v, 0, s.batch)
+        torch.cuda.synchronize()
+        assert torch.equal(o_graph.view(torch.int16), o_eager.view(torch.int16)), f"replay {it}"
