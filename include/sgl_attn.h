@@ -36,7 +36,7 @@ const char* sgl_status_string(int status);
 
 /* Library version, to check that the loaded .so matches this header. */
 int sgl_abi_version(void);
-#define SGL_ABI_VERSION 5
+#define SGL_ABI_VERSION 6
 
 /* ------------------------------------------------------------------ */
 /* KV-cache store                                                      */
@@ -153,7 +153,9 @@ int sgl_rope(void* q, void* k, const float* cos_cache, const float* sin_cache,
  * [max_pos, D/2]), rounded to bf16 and written back in place; the rotated
  * k row and the raw v row are also written to k_cache / v_cache at slot
  * out_loc[t] (int32). Bitwise the same as running sgl_qk_rmsnorm, then
- * sgl_rope, then sgl_store_kv.
+ * sgl_rope, then sgl_store_kv. flags: 0, or SGL_FUSED_NO_K_WRITEBACK to
+ * leave the k part of qkv untouched (the rotated k goes to k_cache only;
+ * the reference writes it back, but nothing reads it after the store).
  * Replaces the sequence AttentionLayer::forward -> qk-norm -> RoPE ->
  * store_kv (src/layers/attention_layer.cc:27-47, flashinfer_backend.cu:530-532).
  */
@@ -164,7 +166,8 @@ int sgl_fused_qknorm_rope_store(void* qkv, int64_t qkv_stride_token,
                                 const int32_t* positions, const int32_t* out_loc,
                                 int64_t num_tokens, int num_qo_heads,
                                 int num_kv_heads, int head_dim, float eps,
-                                void* stream);
+                                int flags, void* stream);
+#define SGL_FUSED_NO_K_WRITEBACK 1
 
 /* ------------------------------------------------------------------ */
 /* Paged attention                                                     */

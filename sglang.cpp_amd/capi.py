@@ -23,7 +23,8 @@ HEADER_PATH = PKG_DIR.parent / "include" / "sgl_attn.h"
 
 SGL_INDEX_I32 = 0
 SGL_INDEX_I64 = 1
-ABI_VERSION = 5
+ABI_VERSION = 6
+FUSED_NO_K_WRITEBACK = 1  # SGL_FUSED_NO_K_WRITEBACK
 
 
 class SglError(RuntimeError):
@@ -68,7 +69,7 @@ _SIGNATURES = {
     "sgl_rope": ([_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                   _i64, _i64, _vp], _i32),
     "sgl_fused_qknorm_rope_store": ([_vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64,
-                                     _i32, _i32, _i32, _f32, _vp], _i32),
+                                     _i32, _i32, _i32, _f32, _i32, _vp], _i32),
     "sgl_decode_plan": ([_vp, _i32, _i32, _i32, _i32, ctypes.POINTER(DecodePlan)], _i32),
     "sgl_paged_decode": ([ctypes.POINTER(DecodePlan), _vp, _i64, _i64, _vp, _vp, _i64, _i64,
                           _vp, _vp, _vp, _i32, _i32, _i32, _i32, _f32, _vp, _i64, _i64, _vp,
@@ -270,7 +271,9 @@ def fused_qknorm_rope_store(qkv: torch.Tensor, k_cache: torch.Tensor, v_cache: t
                             q_weight: Optional[torch.Tensor], k_weight: Optional[torch.Tensor],
                             cos_cache: torch.Tensor, sin_cache: torch.Tensor,
                             positions: torch.Tensor, out_loc: torch.Tensor, num_qo_heads: int,
-                            num_kv_heads: int, head_dim: int, eps: float) -> None:
+                            num_kv_heads: int, head_dim: int, eps: float,
+                            write_k_back: bool = True) -> None:
+    """write_k_back=False leaves qkv's k part untouched (SGL_FUSED_NO_K_WRITEBACK)."""
     dev = _need_gpu(qkv, k_cache, v_cache, q_weight, k_weight, cos_cache, sin_cache, positions,
                     out_loc)
     if qkv.dtype != torch.bfloat16 or qkv.dim() != 2 or qkv.stride(1) != 1:
@@ -280,7 +283,8 @@ def fused_qknorm_rope_store(qkv: torch.Tensor, k_cache: torch.Tensor, v_cache: t
     _check(lib().sgl_fused_qknorm_rope_store(
         _p(qkv), qkv.stride(0), _p(k_cache), _p(v_cache), _p(q_weight), _p(k_weight),
         _p(cos_cache), _p(sin_cache), _p(positions), _p(out_loc), qkv.shape[0], num_qo_heads,
-        num_kv_heads, head_dim, eps, _stream(dev)), "sgl_fused_qknorm_rope_store")
+        num_kv_heads, head_dim, eps, 0 if write_k_back else FUSED_NO_K_WRITEBACK, _stream(dev)),
+        "sgl_fused_qknorm_rope_store")
 
 
 # ---------------------------------------------------------------- attention

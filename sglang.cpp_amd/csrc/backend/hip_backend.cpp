@@ -540,7 +540,9 @@ torch::Tensor AttentionLayer::forward(const torch::Tensor& qkv, const torch::Ten
                 k_norm_ ? k_norm_->weight.data_ptr() : nullptr, rotary_->cos_cache().data_ptr<float>(),
                 rotary_->sin_cache().data_ptr<float>(), positions.data_ptr<int32_t>(),
                 batch.out_loc.data_ptr<int32_t>(), qkv.size(0), num_qo_heads_, num_kv_heads_,
-                head_dim_, q_norm_ ? q_norm_->eps() : 0.f, current_stream(qkv.device())),
+                head_dim_, q_norm_ ? q_norm_->eps() : 0.f,
+                // k is read from the pool from here on; qkv's k part is dead
+                SGL_FUSED_NO_K_WRITEBACK, current_stream(qkv.device())),
             "sgl_fused_qknorm_rope_store");
   auto q = qkv.narrow(1, 0, num_qo_heads_ * head_dim_).view({-1, num_qo_heads_, head_dim_});
   return backend_->attend(q, layer_id_, batch);

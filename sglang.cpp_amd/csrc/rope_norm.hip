@@ -241,7 +241,8 @@ __global__ void __launch_bounds__(256) fused_qknorm_rope_store_kernel(
     uint16_t* __restrict__ v_cache, const uint16_t* __restrict__ qw,
     const uint16_t* __restrict__ kw, const float* __restrict__ cos_cache,
     const float* __restrict__ sin_cache, const int32_t* __restrict__ positions,
-    const int32_t* __restrict__ out_loc, int64_t num_tokens, int hq, int hkv, float eps) {
+    const int32_t* __restrict__ out_loc, int64_t num_tokens, int hq, int hkv, float eps,
+    bool k_back) {
   constexpr int ROWS = 256 / LPR;
   constexpr int D = LPR * 8;
   const int lane_in_row = threadIdx.x % LPR;
@@ -265,7 +266,7 @@ __global__ void __launch_bounds__(256) fused_qknorm_rope_store_kernel(
   const int64_t pos = positions[t];
   rope8<LPR>(x, cos_cache + pos * (D / 2), sin_cache + pos * (D / 2), lane_in_row);
   const u32x4_t packed = pack8(x);
-  stg128(src, packed);
+  if (is_q || k_back) stg128(src, packed);
   if (!is_q) {
     const int h = r - hq;
     stg128(k_cache + (slot * hkv + h) * D + lane_in_row * 8, packed);
@@ -383,8 +384,9 @@ extern "C" int sgl_fused_qknorm_rope_store(void* qkv, int64_t qkv_stride_token, 
                                            const float* sin_cache, const int32_t* positions,
                                            const int32_t* out_loc, int64_t num_tokens,
                                            int num_qo_heads, int num_kv_heads, int head_dim,
-                                           float eps, void* stream) {
+                                           float eps, int flags, void* stream) {
   if (num_tokens < 0 || num_qo_heads <= 0 || num_kv_heads <= 0) return SGL_ERR_INVALID_ARG;
+  if (flags & ~SGL_FUSED_NO_K_WRITEBACK) return SGL_ERR_INVALID_ARG;
   if (num_tokens == 0) return SGL_OK;
   if (!qkv || !k_cache || !v_cache || !cos_cache || !sin_cache || !positions || !out_loc)
     return SGL_ERR_INVALID_ARG;
@@ -406,7 +408,7 @@ extern "C" int sgl_fused_qknorm_rope_store(void* qkv, int64_t qkv_stride_token, 
   hipLaunchKernelGGL(fused_qknorm_rope_store_kernel<LPR_>, dim3(blocks_for(jobs, 256 / LPR_)), \
                      dim3(256), 0, s, base, qkv_stride_token, kc, vc, qw, kw, cos_cache,      \
                      sin_cache, positions, out_loc, num_tokens, num_qo_heads, num_kv_heads,   \
-                     eps);                                                                    \
+                     eps, (flags & SGL_FUSED_NO_K_WRITEBACK) == 0);                           \
   return launch_status();
   switch (head_dim) {
     case 64: SGL_FUSED_CASE(8)

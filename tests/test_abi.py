@@ -57,10 +57,13 @@ def test_argument_checks_reject_before_launch():
                         None) == -1  # odd rotary_dim
     # fused: head_dim not built
     assert lib.sgl_fused_qknorm_rope_store(16, 96 * 5, 16, 16, None, None, 16, 16, 16, 16, 4, 1,
-                                           2, 96, ctypes.c_float(1e-6), None) == -2
+                                           2, 96, ctypes.c_float(1e-6), 0, None) == -2
+    # fused: unknown flag bit
+    assert lib.sgl_fused_qknorm_rope_store(16, 128 * 4, 16, 16, None, None, 16, 16, 16, 16, 4, 2,
+                                           1, 128, ctypes.c_float(1e-6), 2, None) == -1
     # fused: misaligned qkv
     assert lib.sgl_fused_qknorm_rope_store(18, 128 * 4, 16, 16, None, None, 16, 16, 16, 16, 4, 2,
-                                           1, 128, ctypes.c_float(1e-6), None) == -4
+                                           1, 128, ctypes.c_float(1e-6), 0, None) == -4
     assert lib.sgl_paged_prefill(16, 0, 0, 16, 16, 0, 0, 16, 16, 16, None, 2, 4, 16, 8, 64,
                                  ctypes.c_float(0.1), 16, 0, 0, None) == -2  # head_dim 64
 

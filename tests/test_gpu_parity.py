@@ -196,9 +196,10 @@ def _fused_inputs(dev, T, hq, hkv, d, seed, slots=None):
     return qkv, kc, vc, qw, kw, pos, loc, cos, sin
 
 
+@pytest.mark.parametrize("k_back", [True, False])
 @pytest.mark.parametrize("T,hq,hkv,d", [(8192, 16, 8, 128), (100, 32, 4, 128), (77, 8, 2, 64)])
-def test_fused_qknorm_rope_store(oracle, dev, T, hq, hkv, d):
-    note(f"fused qknorm+rope+store T={T} hq={hq} hkv={hkv} d={d}")
+def test_fused_qknorm_rope_store(oracle, dev, T, hq, hkv, d, k_back):
+    note(f"fused qknorm+rope+store T={T} hq={hq} hkv={hkv} d={d} k_back={k_back}")
     qkv, kc, vc, qw, kw, pos, loc, cos, sin = _fused_inputs(dev, T, hq, hkv, d, 8)
     # separate GPU kernels in the reference order: norm -> rope -> store
     qkv2, kc2, vc2 = qkv.clone(), kc.clone(), vc.clone()
@@ -226,10 +227,16 @@ def test_fused_qknorm_rope_store(oracle, dev, T, hq, hkv, d):
     kc_ref, vc_ref = u16(kc).reshape(T, -1).copy(), u16(vc).reshape(T, -1).copy()
     oracle.store_kv(kc_ref, vc_ref, kh.reshape(T, -1), vh, loc.cpu().numpy())
     # fused
-    capi.fused_qknorm_rope_store(qkv, kc, vc, qw, kw, cos, sin, pos, loc, hq, hkv, d, 1e-6)
+    qkv_in = qkv.clone()
+    capi.fused_qknorm_rope_store(qkv, kc, vc, qw, kw, cos, sin, pos, loc, hq, hkv, d, 1e-6,
+                                 write_k_back=k_back)
     torch.cuda.synchronize()
     # fused == separate GPU kernels, bit for bit
-    assert torch.equal(qkv.view(torch.int16), qkv2.view(torch.int16))
+    if k_back:
+        assert torch.equal(qkv.view(torch.int16), qkv2.view(torch.int16))
+    else:  # q like the separate kernels, k and v parts of qkv untouched
+        assert torch.equal(qkv[:, :hq * d].view(torch.int16), qkv2[:, :hq * d].view(torch.int16))
+        assert torch.equal(qkv[:, hq * d:].view(torch.int16), qkv_in[:, hq * d:].view(torch.int16))
     assert torch.equal(kc.view(torch.int16), kc2.view(torch.int16))
     assert torch.equal(vc.view(torch.int16), vc2.view(torch.int16))
     # vs oracle: within 2 ulps (two chained roundings, norm then RoPE), or
