@@ -236,52 +236,51 @@ __device__ __forceinline__ void softmax_head(const PrefillArgs& a, f32x16_t (&st
   }
 }
 
-// p = 2^(s scale - m) in place, their sum into rs.l, packed to the bf16 P^T
-// operands of the four k-steps.
-__device__ __forceinline__ void softmax_exp(const PrefillArgs& a, f32x16_t (&st)[2],
-                                            RowState& rs, bf16x8_t (&pop)[4]) {
+// p = 2^(s scale - m) for the 32 scores of half mb (tokens [32 mb, 32 mb +
+// 32)), their sum into rs.l, packed to the bf16 P^T operands of k-steps
+// 2 mb and 2 mb + 1. P^T slots 0-3 <-> tokens 16 ks4 + 4 hl + (0..3), slots
+// 4-7 <-> the same + 8 (the S^T accumulator order).
+template <int MB>
+__device__ __forceinline__ void softmax_exp_half(const PrefillArgs& a, f32x16_t (&st)[2],
+                                                 RowState& rs, bf16x8_t (&pop)[4]) {
   const float neg_m = rs.m == -INFINITY ? 0.f : -rs.m;  // nothing visible yet
   float ps = 0.f;
 #pragma unroll
-  for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      // v_exp_f32 directly: arguments are <= kRescaleSlack, and results below
-      // 2^-126 flush to zero, which a bf16 weight could not hold anyway.
-      const float p = __builtin_amdgcn_exp2f(fmaf(st[mb][v], a.scale_log2, neg_m));
-      st[mb][v] = p;
-      ps += p;
-    }
+  for (int v = 0; v < 16; ++v) {
+    // v_exp_f32 directly: arguments are <= kRescaleSlack, and results below
+    // 2^-126 flush to zero, which a bf16 weight could not hold anyway.
+    const float p = __builtin_amdgcn_exp2f(fmaf(st[MB][v], a.scale_log2, neg_m));
+    st[MB][v] = p;
+    ps += p;
+  }
   rs.l += ps;
-  // P^T slots 0-3 <-> tokens 16 ks4 + 4 hl + (0..3), slots 4-7 <-> the same
-  // + 8 (the S^T accumulator order).
 #pragma unroll
-  for (int ks4 = 0; ks4 < 4; ++ks4) {
+  for (int ks = 0; ks < 2; ++ks) {
     u32x4_t pw;
 #pragma unroll
     for (int k = 0; k < 4; ++k)
-      pw[k] = pack_bf16x2(st[ks4 >> 1][(ks4 & 1) * 8 + 2 * k], st[ks4 >> 1][(ks4 & 1) * 8 + 2 * k + 1]);
-    pop[ks4] = as_bf16x8(pw);
+      pw[k] = pack_bf16x2(st[MB][ks * 8 + 2 * k], st[MB][ks * 8 + 2 * k + 1]);
+    pop[2 * MB + ks] = as_bf16x8(pw);
   }
 }
 
-// O^T += V^T P^T over the 4 k-steps of the tile in LDS buffer BUF. V^T comes
-// from the row-major tile by transpose reads, one k-step ahead of its MFMAs.
-template <int BUF>
-__device__ __forceinline__ void pv_tile(const LaneAddr& la, const bf16x8_t (&pop)[4],
-                                        RowState& rs) {
-  u32x2_t vr[4][8];  // [ks4][2 db + hi]
-  auto vread = [&](auto K) {
+// O^T += V^T P^T over k-steps [K0, K1) of the tile in LDS buffer BUF. V^T
+// comes from the row-major tile by transpose reads, one k-step ahead of its
+// MFMAs; the reads of k-step K0 are issued by the caller (pv_reads).
+template <int BUF, int KS>
+__device__ __forceinline__ void pv_reads(const LaneAddr& la, u32x2_t (&vr)[8]) {
+  static_for<0, 8>([&](auto J) {
+    constexpr int j = decltype(J)::value;
+    vr[j] = lds_read_tr16<BUF * kTileBytes + KS * 16 * kD * 2>(la.v[j]);
+  });
+}
+
+template <int BUF, int K0, int K1>
+__device__ __forceinline__ void pv_steps(const LaneAddr& la, const bf16x8_t (&pop)[4],
+                                         u32x2_t (&vr)[4][8], RowState& rs) {
+  static_for<K0, K1>([&](auto K) {
     constexpr int ks4 = decltype(K)::value;
-    static_for<0, 8>([&](auto J) {
-      constexpr int j = decltype(J)::value;
-      vr[ks4][j] = lds_read_tr16<BUF * kTileBytes + ks4 * 16 * kD * 2>(la.v[j]);
-    });
-  };
-  vread(std::integral_constant<int, 0>{});
-  static_for<0, 4>([&](auto K) {
-    constexpr int ks4 = decltype(K)::value;
-    if constexpr (ks4 + 1 < 4) vread(std::integral_constant<int, ks4 + 1>{});
+    if constexpr (ks4 + 1 < 4) pv_reads<BUF, ks4 + 1>(la, vr[ks4 + 1]);
     lgkm_wait8<(ks4 + 1 < 4 ? 8 : 0)>(vr[ks4]);
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
@@ -424,9 +423,16 @@ __global__ void __launch_bounds__(kThreads, 2) paged_prefill_kernel(PrefillArgs 
     for (int u = 0; u < 4; ++u) sl_v[u] = sl_k[u];
     load_slots(idx, (t + 3) * kBN, kv_len, sl_k);
     softmax_head(a, s_cur, rs, t * kBN, first_masked, allow, kv_len, hl);
+    // The VALU work of P(t) is split so each half runs beside MFMAs: the
+    // first half beside S(t + 1), the second beside the first half of
+    // O += P(t) V(t).
+    u32x2_t vr[4][8];
     qk_tile<buf ^ 1>(la, qop, s_next);  // S(t + 1); unused after the last tile
-    softmax_exp(a, s_cur, rs, pop);
-    pv_tile<buf>(la, pop, rs);
+    softmax_exp_half<0>(a, s_cur, rs, pop);
+    pv_reads<buf, 0>(la, vr[0]);
+    pv_steps<buf, 0, 2>(la, pop, vr, rs);
+    softmax_exp_half<1>(a, s_cur, rs, pop);
+    pv_steps<buf, 2, 4>(la, pop, vr, rs);
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb) s_cur[mb] = s_next[mb];
     wait_gathers();
