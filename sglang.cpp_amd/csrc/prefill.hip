@@ -33,9 +33,7 @@ namespace sgl {
 namespace {
 
 constexpr int kD = 128;
-constexpr int kBM = 128;   // packed query rows per workgroup (32 per wave)
 constexpr int kBN = 64;    // kv tokens per LDS tile
-constexpr int kThreads = 256;
 constexpr int kXcds = 8;  // MI355X: 8 XCDs, each with its own L2
 constexpr float kRescaleSlack = 8.f;  // log2 units: p <= 256 between rescales
 
@@ -126,13 +124,15 @@ struct Tile {
   uint16_t v[kBN * kD];
 };
 
-// Slot indices of one 64-token tile for this thread's four rows: row
-// 16 u + 4 wave + lane / 16 (u < 4), i.e. (threadIdx.x + 256 u) / 16.
+// Slot indices of one 64-token tile for this thread's rows: with W waves a
+// wave instruction covers 4 rows, so thread (wave, lane) takes rows
+// 4 W u + 4 wave + lane / 16, u < 16 / W, i.e. (threadIdx.x + 64 W u) / 16.
+template <int W>
 __device__ __forceinline__ void load_slots(const int32_t* idx, int tile0, int kv_len,
-                                           int32_t (&sl)[4]) {
+                                           int32_t (&sl)[16 / W]) {
 #pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const int tok = (threadIdx.x + kThreads * u) >> 4;
+  for (int u = 0; u < 16 / W; ++u) {
+    const int tok = (threadIdx.x + 64 * W * u) >> 4;
     sl[u] = idx[min(tile0 + tok, kv_len - 1)];
   }
 }
@@ -141,14 +141,15 @@ __device__ __forceinline__ void load_slots(const int32_t* idx, int tile0, int kv
 // lane i of a wave writes LDS bytes [16 i, 16 i + 16) after the wave's
 // base), so the prefetch holds no registers. Lane i takes physical chunk
 // i % 16 of its row and therefore loads logical chunk (i % 16) ^ swz(row).
+template <int W>
 __device__ __forceinline__ void issue_half(const uint16_t* base, int64_t kv_ss,
-                                           const int32_t (&sl)[4], uint16_t* dst, int wave,
+                                           const int32_t (&sl)[16 / W], uint16_t* dst, int wave,
                                            int lane) {
 #pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const int row = 16 * u + 4 * wave + (lane >> 4);
+  for (int u = 0; u < 16 / W; ++u) {
+    const int row = 4 * W * u + 4 * wave + (lane >> 4);
     const int ch = (lane & 15) ^ swz(row);
-    const int lds_row = 16 * u + 4 * wave;  // wave-uniform destination base
+    const int lds_row = 4 * W * u + 4 * wave;  // wave-uniform destination base
     __builtin_amdgcn_global_load_lds(base + static_cast<int64_t>(sl[u]) * kv_ss + ch * 8,
                                      (__attribute__((address_space(3))) void*)(dst + lds_row * kD),
                                      16, 0, 0);
@@ -291,7 +292,12 @@ __device__ __forceinline__ void pv_steps(const LaneAddr& la, const bf16x8_t (&po
   });
 }
 
-__global__ void __launch_bounds__(kThreads, 2) paged_prefill_kernel(PrefillArgs a) {
+// W waves per workgroup (32 packed query rows each): 4 waves and two
+// workgroups per CU, or 8 waves (256 rows sharing each K/V tile, half the
+// gather traffic per row) and one workgroup per CU.
+template <int W>
+__global__ void __launch_bounds__(64 * W, 8 / W) paged_prefill_kernel(PrefillArgs a) {
+  constexpr int kBM = 32 * W;
   // Work item w = (request, kv head, query-tile position), head-major.
   // Workgroups are dealt to the 8 XCDs round-robin by linear id, so when the
   // count allows, XCD x takes the contiguous share [x S, (x + 1) S), S = N / 8:
@@ -400,13 +406,13 @@ __global__ void __launch_bounds__(kThreads, 2) paged_prefill_kernel(PrefillArgs 
   // tiles: during iteration t the gathers of K(t + 2) and V(t + 1) are in
   // flight. Tile j's K and V use buffer j % 2. Slot indices of tile t + 2
   // serve K(t + 2) now and V(t + 2) in the next iteration.
-  int32_t sl_k[4], sl_v[4];
-  load_slots(idx, 0, kv_len, sl_v);
-  issue_half(kbase, a.kv_ss, sl_v, tiles[0].k, wave, lane);
-  issue_half(vbase, a.kv_ss, sl_v, tiles[0].v, wave, lane);
-  load_slots(idx, kBN, kv_len, sl_v);
-  issue_half(kbase, a.kv_ss, sl_v, tiles[1].k, wave, lane);
-  load_slots(idx, 2 * kBN, kv_len, sl_k);
+  int32_t sl_k[16 / W], sl_v[16 / W];
+  load_slots<W>(idx, 0, kv_len, sl_v);
+  issue_half<W>(kbase, a.kv_ss, sl_v, tiles[0].k, wave, lane);
+  issue_half<W>(vbase, a.kv_ss, sl_v, tiles[0].v, wave, lane);
+  load_slots<W>(idx, kBN, kv_len, sl_v);
+  issue_half<W>(kbase, a.kv_ss, sl_v, tiles[1].k, wave, lane);
+  load_slots<W>(idx, 2 * kBN, kv_len, sl_k);
   wait_gathers();
   __syncthreads();
 
@@ -417,11 +423,11 @@ __global__ void __launch_bounds__(kThreads, 2) paged_prefill_kernel(PrefillArgs 
 
   auto step = [&](auto B, int t) {
     constexpr int buf = decltype(B)::value;  // t % 2
-    if (t + 2 < ntiles) issue_half(kbase, a.kv_ss, sl_k, tiles[buf].k, wave, lane);
-    if (t + 1 < ntiles) issue_half(vbase, a.kv_ss, sl_v, tiles[buf ^ 1].v, wave, lane);
+    if (t + 2 < ntiles) issue_half<W>(kbase, a.kv_ss, sl_k, tiles[buf].k, wave, lane);
+    if (t + 1 < ntiles) issue_half<W>(vbase, a.kv_ss, sl_v, tiles[buf ^ 1].v, wave, lane);
 #pragma unroll
-    for (int u = 0; u < 4; ++u) sl_v[u] = sl_k[u];
-    load_slots(idx, (t + 3) * kBN, kv_len, sl_k);
+    for (int u = 0; u < 16 / W; ++u) sl_v[u] = sl_k[u];
+    load_slots<W>(idx, (t + 3) * kBN, kv_len, sl_k);
     softmax_head(a, s_cur, rs, t * kBN, first_masked, allow, kv_len, hl);
     // The VALU work of P(t) is split so each half runs beside MFMAs: the
     // first half beside S(t + 1), the second beside the first half of
@@ -464,6 +470,16 @@ __global__ void __launch_bounds__(kThreads, 2) paged_prefill_kernel(PrefillArgs 
 
 using namespace sgl;
 
+// Compute units of the current device (256 on MI355X; 256 when none is visible).
+static int device_cus() {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) == hipSuccess &&
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+      cus > 0)
+    return cus;
+  return 256;
+}
+
 extern "C" int sgl_paged_prefill(const void* q, int64_t q_stride_token, int64_t q_stride_head,
                                  const void* k_cache, const void* v_cache, int64_t kv_stride_slot,
                                  int64_t kv_stride_head, const int32_t* indices,
@@ -484,7 +500,15 @@ extern "C" int sgl_paged_prefill(const void* q, int64_t q_stride_token, int64_t 
       !aligned16(v_cache) || !aligned16(o))
     return SGL_ERR_ALIGNMENT;
   const int group = num_qo_heads / num_kv_heads;
-  const int64_t tiles = (static_cast<int64_t>(max_qo_len) * group + kBM - 1) / kBM;
+  // 8-wave workgroups pay off on long chunks that still fill every CU once
+  // (measured: 2048-token chunks at G = 8, 4096 at G = 4); short or few
+  // chunks keep 4-wave workgroups, two per CU.
+  const int64_t rows_max = static_cast<int64_t>(max_qo_len) * group;
+  const int64_t tiles8 = (rows_max + 255) / 256;
+  const bool wide = rows_max >= 8192 &&
+                    tiles8 * num_kv_heads * batch_size >= static_cast<int64_t>(device_cus());
+  const int bm = wide ? 256 : 128;
+  const int64_t tiles = (rows_max + bm - 1) / bm;
   const int64_t items = tiles * num_kv_heads * batch_size;
   if (items > 0x7fffffff) return SGL_ERR_INVALID_ARG;
   PrefillArgs a;
@@ -506,7 +530,11 @@ extern "C" int sgl_paged_prefill(const void* q, int64_t q_stride_token, int64_t 
   a.o_sh = o_stride_head;
   a.tiles_per_req = static_cast<int>(tiles);
   a.num_kv_heads = num_kv_heads;
-  hipLaunchKernelGGL(paged_prefill_kernel, dim3(static_cast<uint32_t>(items)), dim3(kThreads), 0,
-                     static_cast<hipStream_t>(stream), a);
+  if (wide)
+    hipLaunchKernelGGL(paged_prefill_kernel<8>, dim3(static_cast<uint32_t>(items)), dim3(512), 0,
+                       static_cast<hipStream_t>(stream), a);
+  else
+    hipLaunchKernelGGL(paged_prefill_kernel<4>, dim3(static_cast<uint32_t>(items)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), a);
   return launch_status();
 }

@@ -426,3 +426,13 @@ def test_prefill_mixed_decode_rows(oracle, dev):
     cached = [x - 1 for x in kv[:-1]] + [4096]
     b = wl.make_paged_batch(rng, cached, kv, page_size=16)
     check_prefill(oracle, dev, b, 32, 4, 28, "mixed prefill")
+
+
+@pytest.mark.parametrize("hq,hkv,B,qo,prefix", [(64, 4, 2, 512, 256), (32, 4, 1, 2048, 128)])
+def test_prefill_wide_workgroups(oracle, dev, hq, hkv, B, qo, prefix):
+    """Shapes that select the 8-wave (256-row) prefill workgroups: long
+    chunks (qo * G >= 8192) that still give every CU a workgroup."""
+    note(f"prefill 8-wave path hq={hq} hkv={hkv} B={B} qo={qo} prefix={prefix}")
+    rng = np.random.default_rng(29)
+    b = wl.make_paged_batch(rng, [prefix] * B, [prefix + qo] * B, page_size=16)
+    check_prefill(oracle, dev, b, hq, hkv, 30, "prefill 8-wave")
