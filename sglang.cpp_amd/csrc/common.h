@@ -71,11 +71,38 @@ __device__ __forceinline__ void stg128(void* p, const u32x4_t& v) {
 }
 
 // Sum over aligned groups of `width` lanes (width a power of two <= 64).
+// DPP lane exchange inside rows of 16 lanes (no LDS round trip, unlike the
+// ds_bpermute a generic __shfl_xor becomes). CTRL: 0xB1 = quad_perm
+// [1,0,3,2] (lane ^ 1), 0x4E = quad_perm [2,3,0,1] (lane ^ 2), 0x141 =
+// row_half_mirror (i -> 7 - i in each 8), 0x140 = row_mirror (i -> 15 - i),
+// 0x128 = row_ror:8 (i -> i ^ 8 in each 16).
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t x) {
+  return static_cast<uint32_t>(
+      __builtin_amdgcn_update_dpp(0, static_cast<int>(x), CTRL, 0xF, 0xF, false));
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float x) {
+  return __builtin_bit_cast(float, dpp_u32<CTRL>(__builtin_bit_cast(uint32_t, x)));
+}
+
+// Sum over aligned groups of `width` lanes (width a power of two <= 64); the
+// result is bitwise the same in every lane of a group.
 template <int width>
 __device__ __forceinline__ float group_sum(float x) {
+  if constexpr (width == 16) {
+    // Pairings whose two partners add the same two values (commutative), so
+    // all 16 lanes end with identical bits.
+    x += dpp_f32<0xB1>(x);
+    x += dpp_f32<0x4E>(x);
+    x += dpp_f32<0x141>(x);
+    x += dpp_f32<0x140>(x);
+    return x;
+  } else {
 #pragma unroll
-  for (int off = width / 2; off > 0; off >>= 1) x += __shfl_xor(x, off, kWave);
-  return x;
+    for (int off = width / 2; off > 0; off >>= 1) x += __shfl_xor(x, off, kWave);
+    return x;
+  }
 }
 
 template <int width>

@@ -52,7 +52,12 @@ __device__ __forceinline__ void rope8(float (&x)[8], const float* __restrict__ c
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const uint32_t w = pack_bf16x2(x[2 * i], x[2 * i + 1]);
-    const uint32_t pw = static_cast<uint32_t>(__shfl_xor(static_cast<int>(w), HALF, kWave));
+    uint32_t pw;
+    if constexpr (HALF == 8) {
+      pw = dpp_u32<0x128>(w);  // lane ^ 8 inside the 16-lane row
+    } else {
+      pw = static_cast<uint32_t>(__shfl_xor(static_cast<int>(w), HALF, kWave));
+    }
     p[2 * i] = bf16_lo(pw);
     p[2 * i + 1] = bf16_hi(pw);
   }
