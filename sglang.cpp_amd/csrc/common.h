@@ -70,6 +70,44 @@ __device__ __forceinline__ void stg128(void* p, const u32x4_t& v) {
   *reinterpret_cast<u32x4_t*>(p) = v;
 }
 
+// Combine each lane with lane ^ 16 / lane ^ 32 through gfx950's
+// v_permlane16_swap / v_permlane32_swap (register to register; a generic
+// __shfl_xor is an LDS ds_bpermute). Swapping a value with a copy of itself
+// leaves the two partners' values in the two registers, in the same order in
+// both lanes, so the combined value is bitwise equal across partners. Inline
+// asm: the compiler's builtin folds the two results of a self-swap into one.
+// The s_nop covers the VALU-write -> permlane-read hazard.
+template <bool kHalf32>
+__device__ __forceinline__ void swap_pair(float x, float& lo, float& hi) {
+  uint32_t a = __builtin_bit_cast(uint32_t, x), b = a;
+  if constexpr (kHalf32)
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+  else
+    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+  lo = __builtin_bit_cast(float, a);
+  hi = __builtin_bit_cast(float, b);
+}
+__device__ __forceinline__ float max_xor16(float x) {
+  float a, b;
+  swap_pair<false>(x, a, b);
+  return fmaxf(a, b);
+}
+__device__ __forceinline__ float max_xor32(float x) {
+  float a, b;
+  swap_pair<true>(x, a, b);
+  return fmaxf(a, b);
+}
+__device__ __forceinline__ float sum_xor16(float x) {
+  float a, b;
+  swap_pair<false>(x, a, b);
+  return a + b;
+}
+__device__ __forceinline__ float sum_xor32(float x) {
+  float a, b;
+  swap_pair<true>(x, a, b);
+  return a + b;
+}
+
 // Sum over aligned groups of `width` lanes (width a power of two <= 64).
 // DPP lane exchange inside rows of 16 lanes (no LDS round trip, unlike the
 // ds_bpermute a generic __shfl_xor becomes). CTRL: 0xB1 = quad_perm

@@ -227,8 +227,7 @@ __device__ __forceinline__ void decode_head(const DecodeArgs& a, WaveLds& L, con
       sc[i] = (4 * j + i <= last) ? sacc[i] * a.scale_log2 : -INFINITY;
       mt = fmaxf(mt, sc[i]);
     }
-    mt = fmaxf(mt, __shfl_xor(mt, 16, kWave));
-    mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
+    mt = max_xor32(max_xor16(mt));
     const float mn = fmaxf(m, mt);
     const float alpha = exp2f(m - mn);
     float p[4];
@@ -246,8 +245,7 @@ __device__ __forceinline__ void decode_head(const DecodeArgs& a, WaveLds& L, con
     load_v_step(vbase, a.kv_ss, sidx, tn, len, n, j, vr);  // V of the next step
     __builtin_amdgcn_sched_barrier(0);
   }
-  l += __shfl_xor(l, 16, kWave);
-  l += __shfl_xor(l, 32, kWave);
+  l = sum_xor32(sum_xor16(l));
   if (!head_ok) return;
   const float inv = l > 0.f ? 1.0f / l : 0.f;
   const int head = h * G + n;

@@ -222,7 +222,7 @@ __device__ __forceinline__ void softmax_head(const PrefillArgs& a, f32x16_t (&st
   for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
     for (int v = 0; v < 16; ++v) mt = fmaxf(mt, st[mb][v]);
-  mt = fmaxf(mt, __shfl_xor(mt, 32, kWave)) * a.scale_log2;
+  mt = max_xor32(mt) * a.scale_log2;
   // Lazy rescaling: the reference point m (log2 domain) only moves when a
   // row's max exceeds it by more than kRescaleSlack, so most tiles skip the O
   // rescale. Exact: every p and l use the same m; p <= 2^kRescaleSlack.
@@ -450,7 +450,7 @@ __global__ void __launch_bounds__(64 * W, 8 / W) paged_prefill_kernel(PrefillArg
     step(std::integral_constant<int, 1>{}, t + 1);
   }
 
-  float l = rs.l + __shfl_xor(rs.l, 32, kWave);
+  float l = sum_xor32(rs.l);
   if (!row_ok) return;
   const float inv = l > 0.f ? 1.0f / l : 0.f;
   uint16_t* op =
