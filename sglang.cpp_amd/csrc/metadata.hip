@@ -9,14 +9,17 @@
 namespace sgl {
 namespace {
 
-// One workgroup per request; 128-bit stores where the destination run is
-// 16-byte aligned. Each request's run is read as consecutive int32 of one
-// table row, so the loads coalesce.
+// kBlocksPerRequest workgroups per request stride over its run; a thread
+// moves 4 consecutive slots (one 16-byte load from the table row, whose
+// start is 16-byte aligned when the row stride is a multiple of 4), so a
+// 32K-token request is spread over several CUs instead of one.
+constexpr int kBlocksPerRequest = 8;
+
 __global__ void __launch_bounds__(256) build_indices_kernel(
     const int32_t* __restrict__ page_table, int64_t rows, int64_t stride, int64_t cols,
     const int32_t* __restrict__ table_indices, const int32_t* __restrict__ kv_indptr,
-    int32_t* __restrict__ indices, int batch_size) {
-  const int r = blockIdx.x;
+    int32_t* __restrict__ indices, int batch_size, bool vec) {
+  const int r = blockIdx.y;
   if (r >= batch_size) return;
   const int32_t row = table_indices[r];
   const int32_t start = kv_indptr[r];
@@ -24,8 +27,18 @@ __global__ void __launch_bounds__(256) build_indices_kernel(
   if (row < 0 || row >= rows || len <= 0) return;
   const int32_t* src = page_table + static_cast<int64_t>(row) * stride;
   int32_t* dst = indices + start;
-  for (int32_t p = threadIdx.x; p < len; p += blockDim.x) {
-    dst[p] = p < cols ? src[p] : 0;
+  for (int32_t p = (blockIdx.x * blockDim.x + threadIdx.x) * 4; p < len;
+       p += kBlocksPerRequest * blockDim.x * 4) {
+    if (vec && p + 4 <= cols) {
+      const u32x4_t v = ldg128(src + p);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (p + i < len) dst[p + i] = static_cast<int32_t>(v[i]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (p + i < len) dst[p + i] = p + i < cols ? src[p + i] : 0;
+    }
   }
 }
 
@@ -58,9 +71,10 @@ int launch_build_indices(const int32_t* page_table, int64_t rows, int64_t stride
   if (batch_size < 0 || rows < 0 || cols < 0 || stride < cols) return SGL_ERR_INVALID_ARG;
   if (batch_size == 0) return SGL_OK;
   if (!page_table || !table_indices || !kv_indptr || !indices) return SGL_ERR_INVALID_ARG;
-  hipLaunchKernelGGL(build_indices_kernel, dim3(batch_size), dim3(256), 0,
+  hipLaunchKernelGGL(build_indices_kernel, dim3(kBlocksPerRequest, batch_size), dim3(256), 0,
                      static_cast<hipStream_t>(stream), page_table, rows, stride, cols,
-                     table_indices, kv_indptr, indices, batch_size);
+                     table_indices, kv_indptr, indices, batch_size,
+                     (stride & 3) == 0 && aligned16(page_table));
   return launch_status();
 }
 
