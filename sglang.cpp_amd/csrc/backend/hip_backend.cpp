@@ -322,7 +322,11 @@ torch::Tensor HipAttnBackend::attend(const torch::Tensor& q_in, int layer_id, Ba
               "hipStreamWaitEvent");
   }
   if (meta->num_decode > 0) {
-    auto& ws = workspace(meta->dec_plan.workspace_bytes);
+    // Graph-captured launches use the capture workspace, whose address never
+    // changes; eager launches use the growable one.
+    torch::Tensor& ws = meta->use_capture_buffers ? capture_->workspace
+                                                  : workspace(meta->dec_plan.workspace_bytes);
+    TORCH_CHECK(ws.numel() >= meta->dec_plan.workspace_bytes, "decode workspace too small");
     check_sgl(sgl_paged_decode(&meta->dec_plan, q.data_ptr(), q.stride(0), q.stride(1),
                                kc.data_ptr(), vc.data_ptr(), kc.stride(0), kc.stride(1),
                                meta->dec_indices.data_ptr<int32_t>(),
@@ -381,7 +385,9 @@ void HipAttnBackend::init_capture_graph(int max_seq_len, const std::vector<int>&
     cap->plans[bs] = plan;
     ws_bytes = std::max<int64_t>(ws_bytes, plan.workspace_bytes);
   }
-  workspace(ws_bytes);
+  cap->workspace = torch::empty({std::max<int64_t>(ws_bytes, 256)},
+                                torch::TensorOptions().dtype(torch::kUInt8).device(
+                                    kv_cache_->device()));
   capture_ = std::move(cap);
 }
 
@@ -414,7 +420,6 @@ void HipAttnBackend::prepare_for_capture(Batch& batch) {
                                      meta->dec_indices.data_ptr<int32_t>(), bs,
                                      current_stream(kv_cache_->device())),
             "sgl_build_decode_indices");
-  workspace(meta->dec_plan.workspace_bytes);
   capture_->metadata[bs] = meta;
   batch.attn_metadata = meta;
 }

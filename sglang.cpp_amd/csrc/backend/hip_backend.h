@@ -123,6 +123,7 @@ class HipAttnBackend : public BaseAttnBackend {
     torch::Tensor kv_indptr;  // [max_bs + 1]
     torch::Tensor indices;    // [max_bs * max_seq_len]
     torch::Tensor q_rows;     // [max_bs]: 0..max_bs-1
+    torch::Tensor workspace;  // decode split workspace of the largest captured plan
     std::map<int, sgl_decode_plan_t> plans;
     std::map<int, std::shared_ptr<HipAttnMetadata>> metadata;
   };

@@ -262,6 +262,39 @@ def test_backend_decode_graph_capture_replay(oracle, dev, sb):
         assert_attn_close(o_eager.float().cpu().numpy(), ref.reshape(bs, -1),
                           what=f"eager {it}")
 
+    # An eager batch that needs a larger split workspace than any captured
+    # plan (64 requests over the same table rows) must not move the buffer
+    # the graph was captured with.
+    big = sb.Batch(False, [sb.Req(i % bs, max_seq - 1, max_seq) for i in range(64)],
+                   torch.full((64,), max_seq - 1, dtype=torch.int32, device=dev),
+                   static_loc.repeat(8))
+    backend.prepare_metadata(big)
+    qb = _randn((64, hq * D), dev, g)
+    kb = torch.cat([k] * 8)
+    vb = torch.cat([v] * 8)
+    backend.forward(qb, kb, vb, 0, big)
+    torch.cuda.synchronize()
+    lens = np.full(bs, max_seq)
+    loc = np.array([pt[i, max_seq - 1] for i in range(bs)], np.int32)
+    rb = sb.Batch(False, [sb.Req(i, max_seq - 1, max_seq) for i in range(bs)],
+                  torch.full((bs,), max_seq - 1, dtype=torch.int32, device=dev),
+                  torch.from_numpy(loc).to(dev))
+    backend.prepare_metadata(rb)
+    backend.prepare_for_replay(rb)
+    q = _randn((bs, hq * D), dev, g)
+    static_q.copy_(q)
+    static_k.copy_(k)
+    static_v.copy_(v)
+    static_loc.copy_(rb.out_loc)
+    graph.replay()
+    torch.cuda.synchronize()
+    kc, vc = u16(cache.k_cache(0)), u16(cache.v_cache(0))
+    ip = (np.arange(bs + 1) * max_seq).astype(np.int32)
+    idx = np.concatenate([pt[i, :max_seq] for i in range(bs)]).astype(np.int32)
+    ref = oracle.decode(u16(q).reshape(bs, hq, D).copy(), kc, vc, idx, ip, scale)
+    assert_attn_close(static_o.float().cpu().numpy(), ref.reshape(bs, -1),
+                      what="replay after workspace growth")
+
 
 @pytest.mark.gpu
 def test_backend_mixed_batch_overlap_and_graph_replay(oracle, dev, sb):
