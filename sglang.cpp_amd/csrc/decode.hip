@@ -260,6 +260,10 @@ __device__ __forceinline__ void decode_head(const DecodeArgs& a, WaveLds& L, con
       stg128(op + 32 * j + 8 * i, pack8(v));
     }
   } else {
+    // A batch longer than its plan allows (pieces beyond max_chunks) would
+    // write past the workspace: drop those pieces instead (the host-side
+    // checks keep a correct caller from getting here).
+    if (c >= a.max_chunks) return;
     const int64_t pidx = (static_cast<int64_t>(r) * a.max_chunks + c) * a.hq + head;
     float* pp = a.part_o + pidx * kD;
 #pragma unroll
@@ -363,7 +367,8 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(DecodeArgs a) {
   const int re = a.kv_indptr[r + 1];
   if (re <= rb) return;
   const int W = unit_tokens(a, a.kv_indptr[a.batch]);
-  const int nch = (re - 1) / W - rb / W + 1;  // pieces of request r
+  // Pieces of request r (never more than the workspace holds).
+  const int nch = min((re - 1) / W - rb / W + 1, a.max_chunks);
   if (nch <= 1) return;
   __shared__ float sh_w[kMaxChunks][kMaxGroup];
   const int G = a.group;
