@@ -43,7 +43,7 @@ constexpr int kTile = 32;       // chunk granularity (tokens)
 constexpr int kMaxKvHeads = 16; // kv heads per workgroup (one wave each)
 constexpr int kMaxGroup = 16;
 constexpr int kMaxChunks = 128; // bound on splits per request (merge table)
-constexpr int kMaxChunkTokens = 2048;  // slot indices of a chunk staged in LDS
+constexpr int kMaxChunkTokens = 8192;  // slot indices of a chunk staged in LDS (32 KiB)
 constexpr int kQPitch = kD + 8; // LDS row pitch (bf16) of the Q^T copy
 // Word 3 of a raw buffer resource on gfx9-class parts: 32-bit data format,
 // no swizzle, no index stride.
@@ -300,8 +300,9 @@ __device__ __forceinline__ void zero_row(const DecodeArgs& a, int qrow) {
 // the end instead of leaving a tail of long requests. A request that spans
 // several units is written as partials (piece p = unit - first unit of the
 // request) and merged by decode_merge_kernel. Waves take the kv heads.
-// 128 VGPRs (4 waves per SIMD, the 16 per CU the schedule keeps resident):
-// a tighter budget spills, and scratch traffic in the step loop costs ~9%.
+// Budget 128 VGPRs (up to 4 waves per SIMD, above the ~2 the schedule keeps
+// resident): a tighter budget spills, and scratch traffic in the step loop
+// costs ~9%.
 __global__ void __launch_bounds__(kMaxKvHeads * kWave)
     __attribute__((amdgpu_waves_per_eu(4))) paged_decode_kernel(DecodeArgs a) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
@@ -451,13 +452,12 @@ extern "C" int sgl_decode_plan(const int32_t* kv_indptr_host, int batch_size, in
     max_len = len > max_len ? len : max_len;
   }
   if (total > 0x7fffffff) return SGL_ERR_UNSUPPORTED;
-  // One work unit per resident workgroup (one wave per kv head), about 12
-  // waves per CU but at least two workgroups: measured on MI355X, more
-  // concurrent row streams per CU lose DRAM locality faster than they add
-  // latency hiding, while a single 8-wave workgroup per CU starves it.
-  // At most 16 waves per CU are resident (the kernel's 128-VGPR budget).
-  int units_per_cu = 12 / num_kv_heads > 2 ? 12 / num_kv_heads : 2;
-  if (units_per_cu * num_kv_heads > 16) units_per_cu = 16 / num_kv_heads > 1 ? 16 / num_kv_heads : 1;
+  // One work unit per resident workgroup (one wave per kv head), about 8
+  // waves per CU: measured on MI355X (Qwen3 shapes, 32q/8kv and 32q/4kv,
+  // short and 32K contexts), 8 concurrent row streams per CU beat 12 and 16
+  // by 3-4% (more streams lose DRAM locality faster than they add latency
+  // hiding), and 4 starve long contexts.
+  int units_per_cu = 8 / num_kv_heads > 1 ? 8 / num_kv_heads : 1;
   const int64_t units_target = static_cast<int64_t>(device_cu_count()) * units_per_cu;
   constexpr int64_t kMinUnit = 64;  // keeps per-unit set-up small next to the stream
   auto round16 = [](int64_t x) { return (x + kStep - 1) / kStep * kStep; };

@@ -7,22 +7,22 @@
 // visible to every new token), kv slots taken from the token-granular
 // indices[kv_indptr[r] + j].
 //
-// Work decomposition: one workgroup (4 waves) per (request, kv head, tile of
-// 128 packed query rows). The G query heads that share a kv head are packed
-// row-wise (packed row p -> token p / G, head h G + p % G), so each K/V tile
-// staged in LDS feeds G heads. K/V tiles of 64 tokens are gathered from the
-// pool (one 16-byte chunk per lane, slots from the index list) into a
-// double-buffered LDS ring; the global loads of tile t+1 are in flight
-// while tile t is on the matrix cores.
+// Work decomposition: one workgroup (4 or 8 waves, 32 query rows each) per
+// (request, kv head, query tile), or per pair of tiles from both ends of the
+// causal range (see paged_prefill_kernel). The G query heads that share a kv
+// head are packed row-wise (packed row p -> token p / G, head h G + p % G),
+// so each K/V tile staged in LDS feeds G heads. K/V tiles of 64 tokens are
+// gathered from the pool (one 16-byte chunk per lane, slots from the index
+// list) into a double-buffered LDS ring; the gathers of the next tiles are
+// in flight while the current one is on the matrix cores.
 //
 // Matrix formulation (v_mfma_f32_32x32x16_bf16, lane l, c = l % 32, hl = l / 32):
 //   S^T[tok, row] = K[tok, :] . Q[row, :]      (A = K from LDS, B = Q^T in VGPRs)
-//   O^T[d, row]  += V^T[d, tok] . P^T[tok, row] (A = V^T via in-register transpose)
+//   O^T[d, row]  += V^T[d, tok] . P^T[tok, row] (A = V^T by LDS transpose reads)
 // The query row sits on the lane's column c in both products, so the online
 // softmax (max, sum, rescale of O) is lane-local apart from one exchange with
-// lane l ^ 32. The V operand uses the d-order d = 4 m + db (m = MFMA row,
-// db = which of 4 MFMAs), so a lane reads V[tok][4c .. 4c+3] — 8 bytes —
-// per token and v_perm builds the operands.
+// lane l ^ 32. V^T comes straight from the row-major V tile through
+// ds_read_b64_tr_b16.
 #include <math.h>
 
 #include <type_traits>
@@ -140,19 +140,19 @@ __device__ __forceinline__ void load_slots(const int32_t* idx, int tile0, int kv
 // Gathers one K (or V) tile straight into LDS (global_load_lds_dwordx4:
 // lane i of a wave writes LDS bytes [16 i, 16 i + 16) after the wave's
 // base), so the prefetch holds no registers. Lane i takes physical chunk
-// i % 16 of its row and therefore loads logical chunk (i % 16) ^ swz(row).
+// i % 16 of its row and therefore loads logical chunk (i % 16) ^ swz(row);
+// row % 16 = 4 wave + i / 16 for every u, so lane_base (the head's row 0
+// plus that chunk) is fixed and each address is one 32 x 32 -> 64-bit
+// multiply-add of the slot.
 template <int W>
-__device__ __forceinline__ void issue_half(const uint16_t* base, int64_t kv_ss,
-                                           const int32_t (&sl)[16 / W], uint16_t* dst, int wave,
-                                           int lane) {
+__device__ __forceinline__ void issue_half(const char* lane_base, uint32_t ss_bytes,
+                                           const int32_t (&sl)[16 / W], uint16_t* dst, int wave) {
 #pragma unroll
   for (int u = 0; u < 16 / W; ++u) {
-    const int row = 4 * W * u + 4 * wave + (lane >> 4);
-    const int ch = (lane & 15) ^ swz(row);
     const int lds_row = 4 * W * u + 4 * wave;  // wave-uniform destination base
-    __builtin_amdgcn_global_load_lds(base + static_cast<int64_t>(sl[u]) * kv_ss + ch * 8,
-                                     (__attribute__((address_space(3))) void*)(dst + lds_row * kD),
-                                     16, 0, 0);
+    __builtin_amdgcn_global_load_lds(
+        lane_base + static_cast<uint64_t>(static_cast<uint32_t>(sl[u])) * ss_bytes,
+        (__attribute__((address_space(3))) void*)(dst + lds_row * kD), 16, 0, 0);
   }
 }
 
@@ -292,53 +292,82 @@ __device__ __forceinline__ void pv_steps(const LaneAddr& la, const bf16x8_t (&po
   });
 }
 
-// W waves per workgroup (32 packed query rows each): 4 waves and two
+// W waves per workgroup, 32 packed query rows each: 4 waves and two
 // workgroups per CU, or 8 waves (256 rows sharing each K/V tile, half the
-// gather traffic per row) and one workgroup per CU.
-template <int W>
+// gather traffic per row) and one workgroup per CU, where waves w and w + 4
+// share SIMD w % 4.
+//
+// Work item w = (request, kv head, query-tile position), head-major. The
+// rows of a request form query tiles (G heads of each token packed
+// row-wise), and tile i sees about (prefix + i) kv tiles. Workgroups are
+// dealt to the 8 XCDs round-robin by linear id, so when the count allows,
+// XCD x takes the contiguous share [x S, (x + 1) S), S = N / 8: the tiles of
+// one kv head stay on one or two XCDs, whose L2 then holds that head's K/V.
+//
+// kPair = false: one 32 W-row tile per item. Positions alternate between the
+// heavy and the light end (T-1, 0, T-2, 1, ...), so every share carries about
+// the same work; inside a share the heavy half is dispatched first, heaviest
+// first, then the light half, heaviest first. Suits launches of several
+// workgroups per CU, which the dispatcher balances.
+//
+// kPair = true (W = 8, at most one workgroup per CU): item p takes the
+// 16 W-row tiles T - 1 - p (waves 0-3) and p (waves 4-7), so every item
+// carries the same work and each SIMD holds one heavy and one light wave.
+// Both groups share each gathered K/V tile; a group whose rows can no
+// longer see the current tile skips its compute for that step.
+template <int W, bool kPair>
 __global__ void __launch_bounds__(64 * W, 8 / W) paged_prefill_kernel(PrefillArgs a) {
-  constexpr int kBM = 32 * W;
-  // Work item w = (request, kv head, query-tile position), head-major.
-  // Workgroups are dealt to the 8 XCDs round-robin by linear id, so when the
-  // count allows, XCD x takes the contiguous share [x S, (x + 1) S), S = N / 8:
-  // the tiles of one kv head stay on one or two XCDs, whose L2 then holds
-  // that head's K/V. Causal work grows with the tile index, and positions
-  // alternate between the heavy and the light end (T-1, 0, T-2, 1, ...), so
-  // every share carries about the same work; inside a share the heavy half
-  // is dispatched first, heaviest first, then the light half, heaviest first.
+  static_assert(!kPair || W == 8, "pairing splits 8 waves into two SIMD-sharing groups");
+  constexpr int kGM = kPair ? 16 * W : 32 * W;  // rows per group tile
   const int n_items = gridDim.x;
   const int lin = blockIdx.x;
-  int w;
-  if (n_items % (2 * kXcds) == 0) {
+  int w = lin;
+  if (kPair) {
+    if (n_items % kXcds == 0) w = (lin % kXcds) * (n_items / kXcds) + lin / kXcds;
+  } else if (n_items % (2 * kXcds) == 0) {
     const int share = n_items / kXcds;
     const int j = lin / kXcds;
     w = (lin % kXcds) * share + (j < share / 2 ? 2 * j : 2 * (share - 1 - j) + 1);
-  } else {
-    w = lin;
   }
   const int per_req = a.tiles_per_req * a.num_kv_heads;
   const int r = w / per_req;
   const int h = (w - r * per_req) / a.tiles_per_req;
   const int pos = w - r * per_req - h * a.tiles_per_req;
-  const int tile = (pos & 1) ? (pos >> 1) : a.tiles_per_req - 1 - (pos >> 1);
   const int qo_len = a.qo_indptr[r + 1] - a.qo_indptr[r];
   const int qo_beg = a.q_start ? a.q_start[r] : a.qo_indptr[r];
   const int kv_beg = a.kv_indptr[r];
   const int kv_len = a.kv_indptr[r + 1] - kv_beg;
   const int G = a.group;
   const int rows = qo_len * G;
-  const int row0 = tile * kBM;
-  if (row0 >= rows || kv_len <= 0) return;
-  const int off = kv_len - qo_len;  // causal offset (cached prefix length)
-
+  if (kv_len <= 0) return;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int c = lane & 31;
   const int hl = lane >> 5;
+  // Tile of group 0 (the whole workgroup without pairing) and this wave's
+  // group, its rows and its position in the group.
+  int tile0, row0, gwave;
+  bool grp_rows;
+  if (kPair) {
+    const int T = (rows + kGM - 1) / kGM;
+    tile0 = T - 1 - pos;
+    if (tile0 < pos) return;  // past this request's pairs
+    const int grp = wave / (W / 2);
+    grp_rows = grp == 0 || pos < tile0;  // group 1 is empty on the middle tile of an odd T
+    row0 = (grp == 0 ? tile0 : pos) * kGM;
+    gwave = wave % (W / 2);
+  } else {
+    tile0 = (pos & 1) ? (pos >> 1) : a.tiles_per_req - 1 - (pos >> 1);
+    if (tile0 * kGM >= rows) return;
+    grp_rows = true;
+    row0 = tile0 * kGM;
+    gwave = wave;
+  }
+  const int off = kv_len - qo_len;  // causal offset (cached prefix length)
 
   // This lane's query row.
-  const int prow = row0 + wave * 32 + c;
-  const bool row_ok = prow < rows;
+  const int prow = row0 + gwave * 32 + c;
+  const bool row_ok = grp_rows && prow < rows;
   const int qtok = row_ok ? prow / G : 0;
   const int qhead = h * G + (row_ok ? prow - (prow / G) * G : 0);
   const int allow = row_ok ? qtok + off : kv_len - 1;  // last visible kv token
@@ -355,11 +384,15 @@ __global__ void __launch_bounds__(64 * W, 8 / W) paged_prefill_kernel(PrefillArg
     }
   }
 
-  // kv range this workgroup needs: up to the last row's visible token.
-  const int last_row = min(rows, row0 + kBM) - 1;
-  const int kv_end = min(kv_len, last_row / G + off + 1);
-  const int ntiles = (kv_end + kBN - 1) / kBN;
-  // First token index at which some row of the workgroup may be masked.
+  // kv tiles a group needs: up to its last row's visible token. The
+  // workgroup gathers group 0's range, which contains group 1's.
+  auto tiles_for = [&](int r0) {
+    const int last_row = min(rows, r0 + kGM) - 1;
+    return (min(kv_len, last_row / G + off + 1) + kBN - 1) / kBN;
+  };
+  const int ntiles = tiles_for(tile0 * kGM);
+  const int my_tiles = !kPair ? ntiles : !grp_rows ? 0 : row0 == tile0 * kGM ? ntiles : tiles_for(row0);
+  // First token index at which some row of the group may be masked.
   const int first_masked = row0 / G + off + 1;
 
   // Two K/V buffers; the loop is unrolled by two so each read names its
@@ -369,6 +402,10 @@ __global__ void __launch_bounds__(64 * W, 8 / W) paged_prefill_kernel(PrefillArg
   const uint16_t* kbase = a.kc + static_cast<int64_t>(h) * a.kv_sh;
   const uint16_t* vbase = a.vc + static_cast<int64_t>(h) * a.kv_sh;
   const int32_t* idx = a.indices + kv_beg;
+  const uint32_t ss_bytes = static_cast<uint32_t>(a.kv_ss * 2);
+  const int lch = (lane & 15) ^ swz(4 * wave + (lane >> 4));
+  const char* klane = reinterpret_cast<const char*>(kbase) + lch * 16;
+  const char* vlane = reinterpret_cast<const char*>(vbase) + lch * 16;
 
   LaneAddr la;
   {
@@ -408,10 +445,10 @@ __global__ void __launch_bounds__(64 * W, 8 / W) paged_prefill_kernel(PrefillArg
   // serve K(t + 2) now and V(t + 2) in the next iteration.
   int32_t sl_k[16 / W], sl_v[16 / W];
   load_slots<W>(idx, 0, kv_len, sl_v);
-  issue_half<W>(kbase, a.kv_ss, sl_v, tiles[0].k, wave, lane);
-  issue_half<W>(vbase, a.kv_ss, sl_v, tiles[0].v, wave, lane);
+  issue_half<W>(klane, ss_bytes, sl_v, tiles[0].k, wave);
+  issue_half<W>(vlane, ss_bytes, sl_v, tiles[0].v, wave);
   load_slots<W>(idx, kBN, kv_len, sl_v);
-  issue_half<W>(kbase, a.kv_ss, sl_v, tiles[1].k, wave, lane);
+  issue_half<W>(klane, ss_bytes, sl_v, tiles[1].k, wave);
   load_slots<W>(idx, 2 * kBN, kv_len, sl_k);
   wait_gathers();
   __syncthreads();
@@ -423,24 +460,26 @@ __global__ void __launch_bounds__(64 * W, 8 / W) paged_prefill_kernel(PrefillArg
 
   auto step = [&](auto B, int t) {
     constexpr int buf = decltype(B)::value;  // t % 2
-    if (t + 2 < ntiles) issue_half<W>(kbase, a.kv_ss, sl_k, tiles[buf].k, wave, lane);
-    if (t + 1 < ntiles) issue_half<W>(vbase, a.kv_ss, sl_v, tiles[buf ^ 1].v, wave, lane);
+    if (t + 2 < ntiles) issue_half<W>(klane, ss_bytes, sl_k, tiles[buf].k, wave);
+    if (t + 1 < ntiles) issue_half<W>(vlane, ss_bytes, sl_v, tiles[buf ^ 1].v, wave);
 #pragma unroll
     for (int u = 0; u < 16 / W; ++u) sl_v[u] = sl_k[u];
     load_slots<W>(idx, (t + 3) * kBN, kv_len, sl_k);
-    softmax_head(a, s_cur, rs, t * kBN, first_masked, allow, kv_len, hl);
-    // The VALU work of P(t) is split so each half runs beside MFMAs: the
-    // first half beside S(t + 1), the second beside the first half of
-    // O += P(t) V(t).
-    u32x2_t vr[4][8];
-    qk_tile<buf ^ 1>(la, qop, s_next);  // S(t + 1); unused after the last tile
-    softmax_exp_half<0>(a, s_cur, rs, pop);
-    pv_reads<buf, 0>(la, vr[0]);
-    pv_steps<buf, 0, 2>(la, pop, vr, rs);
-    softmax_exp_half<1>(a, s_cur, rs, pop);
-    pv_steps<buf, 2, 4>(la, pop, vr, rs);
+    if (!kPair || t < my_tiles) {
+      softmax_head(a, s_cur, rs, t * kBN, first_masked, allow, kv_len, hl);
+      // The VALU work of P(t) is split so each half runs beside MFMAs: the
+      // first half beside S(t + 1), the second beside the first half of
+      // O += P(t) V(t).
+      u32x2_t vr[4][8];
+      qk_tile<buf ^ 1>(la, qop, s_next);  // S(t + 1); unused after the last tile
+      softmax_exp_half<0>(a, s_cur, rs, pop);
+      pv_reads<buf, 0>(la, vr[0]);
+      pv_steps<buf, 0, 2>(la, pop, vr, rs);
+      softmax_exp_half<1>(a, s_cur, rs, pop);
+      pv_steps<buf, 2, 4>(la, pop, vr, rs);
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb) s_cur[mb] = s_next[mb];
+      for (int mb = 0; mb < 2; ++mb) s_cur[mb] = s_next[mb];
+    }
     wait_gathers();
     __syncthreads();
   };
@@ -495,6 +534,8 @@ extern "C" int sgl_paged_prefill(const void* q, int64_t q_stride_token, int64_t 
     return SGL_ERR_INVALID_ARG;
   if (num_qo_heads % num_kv_heads != 0) return SGL_ERR_INVALID_ARG;
   if (head_dim != kD) return SGL_ERR_UNSUPPORTED;
+  // Gather addresses use 32-bit slot byte strides.
+  if (kv_stride_slot <= 0 || kv_stride_slot > 0x7fffffff) return SGL_ERR_UNSUPPORTED;
   if (q_stride_head % 8 || q_stride_token % 8 || kv_stride_slot % 8 || kv_stride_head % 8 ||
       o_stride_token % 8 || o_stride_head % 8 || !aligned16(q) || !aligned16(k_cache) ||
       !aligned16(v_cache) || !aligned16(o))
@@ -507,8 +548,14 @@ extern "C" int sgl_paged_prefill(const void* q, int64_t q_stride_token, int64_t 
   const int64_t tiles8 = (rows_max + 255) / 256;
   const bool wide = rows_max >= 8192 &&
                     tiles8 * num_kv_heads * batch_size >= static_cast<int64_t>(device_cus());
+  // Pairing (one tile from each end of the causal range per workgroup) when
+  // the launch is at most one workgroup per CU: the dispatcher cannot then
+  // even out unequal tiles, and measured it is 3-6% faster; with several
+  // workgroups per CU, heavy-first dispatch balances better.
+  const int64_t pairs = ((rows_max + 127) / 128 + 1) / 2;
+  const bool pair = wide && pairs * num_kv_heads * batch_size <= static_cast<int64_t>(device_cus());
   const int bm = wide ? 256 : 128;
-  const int64_t tiles = (rows_max + bm - 1) / bm;
+  const int64_t tiles = pair ? pairs : (rows_max + bm - 1) / bm;
   const int64_t items = tiles * num_kv_heads * batch_size;
   if (items > 0x7fffffff) return SGL_ERR_INVALID_ARG;
   PrefillArgs a;
@@ -530,11 +577,13 @@ extern "C" int sgl_paged_prefill(const void* q, int64_t q_stride_token, int64_t 
   a.o_sh = o_stride_head;
   a.tiles_per_req = static_cast<int>(tiles);
   a.num_kv_heads = num_kv_heads;
-  if (wide)
-    hipLaunchKernelGGL(paged_prefill_kernel<8>, dim3(static_cast<uint32_t>(items)), dim3(512), 0,
-                       static_cast<hipStream_t>(stream), a);
+  const dim3 grid(static_cast<uint32_t>(items));
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (pair)
+    hipLaunchKernelGGL((paged_prefill_kernel<8, true>), grid, dim3(512), 0, s, a);
+  else if (wide)
+    hipLaunchKernelGGL((paged_prefill_kernel<8, false>), grid, dim3(512), 0, s, a);
   else
-    hipLaunchKernelGGL(paged_prefill_kernel<4>, dim3(static_cast<uint32_t>(items)), dim3(256), 0,
-                       static_cast<hipStream_t>(stream), a);
+    hipLaunchKernelGGL((paged_prefill_kernel<4, false>), grid, dim3(256), 0, s, a);
   return launch_status();
 }

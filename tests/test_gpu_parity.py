@@ -436,3 +436,19 @@ def test_prefill_wide_workgroups(oracle, dev, hq, hkv, B, qo, prefix):
     rng = np.random.default_rng(29)
     b = wl.make_paged_batch(rng, [prefix] * B, [prefix + qo] * B, page_size=16)
     check_prefill(oracle, dev, b, hq, hkv, 30, "prefill 8-wave")
+
+
+@pytest.mark.parametrize("hq,hkv,qo,prefix", [
+    (32, 4, [1024, 584], [100, 333]),   # paired tiles; the short request has an odd tile count
+    (64, 4, [768, 700], [64, 0]),       # 8-wave tiles, more than one workgroup per CU (unpaired)
+])
+def test_prefill_wide_ragged(oracle, dev, hq, hkv, qo, prefix):
+    """Ragged batches on the 8-wave paths: with at most one workgroup per
+    CU each workgroup takes a tile from both ends of a request's causal range
+    (a shorter request has fewer pairs, and an odd count leaves the middle
+    tile's second group empty); otherwise heavy-first single tiles."""
+    note(f"prefill 8-wave ragged hq={hq} hkv={hkv} qo={qo} prefix={prefix}")
+    rng = np.random.default_rng(31)
+    b = wl.make_paged_batch(rng, prefix, [p + q for p, q in zip(prefix, qo)], page_size=16)
+    check_prefill(oracle, dev, b, hq, hkv, 32, "prefill 8-wave ragged")
+
