@@ -8,7 +8,10 @@ kernel plus its split merge) over the whole batch, inputs resident in HBM.
 
 The other configs are reported under "extra" (and as their own lines with
 --workload): cfg1 small decode, cfg2 prefill with prefix hits, cfg3 fused
-RoPE + qk-norm + KV store, cfg5 mixed 48-layer step replayed as a hipGraph.
+RoPE + qk-norm + KV store, cfg5 mixed 48-layer step replayed as a hipGraph;
+and the residual path around attention at the Qwen3-8B shape for an
+8192-token chunk: resid_norm (fused add + RMSNorm, hidden 4096) and
+resid_act (SiLU-and-mul, intermediate 12288).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload cfgN]
                        [--no-extra] [--no-cpu]
@@ -40,7 +43,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="cfg4",
-                    choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5"])
+                    choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5", "resid_norm", "resid_act"])
     ap.add_argument("--no-extra", action="store_true", help="headline workload only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--cfg5-layers", type=int, default=48)
@@ -302,8 +305,49 @@ def roofline_mfma(flops, kernel_ms, traffic_key):
             "traffic": load_traffic(traffic_key)}
 
 
+RESID_TOKENS, RESID_HIDDEN, RESID_INTER = 8192, 4096, 12288  # Qwen3-8B, one 8192-token chunk
+
+
+def setup_resid(torch, capi, name, dev, seed=0):
+    """Residual-path kernels at the Qwen3-8B shape (qwen3.cc:24-31 and
+    utils.cc:49 call them once per layer). Algorithmic bytes: fused add +
+    RMSNorm reads x and residual and writes both (8 T d) plus the weight;
+    SiLU-and-mul reads [T, 2d] and writes [T, d] (6 T d)."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    T = RESID_TOKENS
+    if name == "resid_norm":
+        d = RESID_HIDDEN
+        x = torch.randn((T, d), device=dev, generator=g).to(torch.bfloat16)
+        r = torch.randn((T, d), device=dev, generator=g).to(torch.bfloat16)
+        w = (torch.rand(d, device=dev, generator=g) + 0.5).to(torch.bfloat16)
+
+        def step():
+            # in place on x and r; repeated steps keep values finite (x is
+            # renormalised each time, r grows by at most ~|x| per step)
+            capi.fused_add_rmsnorm(x, r, w, 1e-6)
+
+        return step, 8 * T * d + 2 * d, {"tokens": T, "hidden": d}
+    d = RESID_INTER
+    inp = torch.randn((T, 2 * d), device=dev, generator=g).to(torch.bfloat16)
+    out = torch.empty((T, d), device=dev, dtype=torch.bfloat16)
+
+    def step():
+        capi.silu_and_mul(out, inp)
+
+    return step, 6 * T * d, {"tokens": T, "intermediate": d}
+
+
 def run_workload(name, torch, capi, wl, dev, steps, warmup, cfg5_layers):
     timer = Timer(torch)
+    if name in ("resid_norm", "resid_act"):
+        step, nbytes, shape = setup_resid(torch, capi, name, dev)
+        wall, ev = timer.run(step, steps, warmup)
+        kname = "fused_add_rmsnorm" if name == "resid_norm" else "silu_and_mul"
+        rec = {"workload": f"{name}_qwen3_8b_t{RESID_TOKENS}_bf16", **shape, "ms_per_step": wall,
+               "kernel_ms": ev, "bytes": nbytes, "GB/s": nbytes / (wall * 1e-3) / 1e9,
+               "roofline": roofline_hbm(nbytes, ev, f"{kname}_qwen3_8b")}
+        return None, rec
     if name in ("cfg1", "cfg4"):
         w = wl.cfg1_decode_small() if name == "cfg1" else wl.cfg4_decode_large()
         step, nbytes, flops, _ = setup_decode(torch, capi, wl, w, dev)
@@ -374,7 +418,7 @@ def main():
                            args.cfg5_layers)
     extra = {}
     if not args.no_extra:
-        for name in ("cfg1", "cfg2", "cfg3", "cfg4", "cfg5"):
+        for name in ("cfg1", "cfg2", "cfg3", "cfg4", "cfg5", "resid_norm", "resid_act"):
             if name == args.workload:
                 continue
             try:
@@ -399,7 +443,15 @@ def main():
         value, unit = head["TFLOP/s"], "TFLOP/s"
     else:
         value, unit = head["decode_bytes"] / (head["ms_per_step"] * 1e-3) / 1e9, "GB/s"
-    s = w.shape
+    if w is None:
+        config = {"workload": head["workload"], "parallelism": "single GPU",
+                  **{k: head[k] for k in ("tokens", "hidden", "intermediate") if k in head}}
+    else:
+        s = w.shape
+        config = {"workload": head["workload"], "batch": w.batch.batch_size,
+                  "num_qo_heads": s.num_qo_heads, "num_kv_heads": s.num_kv_heads,
+                  "head_dim": s.head_dim, "page_size": w.batch.page_size,
+                  "sum_kv": int(w.batch.kv_lens.sum()), "parallelism": "single GPU"}
     line = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -413,10 +465,7 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic: seeded N(0,1) bf16 Q/K/V, seeded random page permutation",
-        "config": {"workload": head["workload"], "batch": w.batch.batch_size,
-                   "num_qo_heads": s.num_qo_heads, "num_kv_heads": s.num_kv_heads,
-                   "head_dim": s.head_dim, "page_size": w.batch.page_size,
-                   "sum_kv": int(w.batch.kv_lens.sum()), "parallelism": "single GPU"},
+        "config": config,
         "roofline": head.get("roofline"),
         "cpu_baseline": cpu,
         "extra": extra,

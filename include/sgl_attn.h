@@ -31,12 +31,15 @@ extern "C" {
 #define SGL_INDEX_I32 0
 #define SGL_INDEX_I64 1
 
+#define SGL_DTYPE_BF16 0  /* 16-bit element types of the residual-path kernels */
+#define SGL_DTYPE_F16 1
+
 /* Human-readable text for a status code (static storage). */
 const char* sgl_status_string(int status);
 
 /* Library version, to check that the loaded .so matches this header. */
 int sgl_abi_version(void);
-#define SGL_ABI_VERSION 6
+#define SGL_ABI_VERSION 7
 
 /* ------------------------------------------------------------------ */
 /* KV-cache store                                                      */
@@ -254,6 +257,52 @@ int sgl_paged_prefill(const void* q, int64_t q_stride_token,
                       int num_kv_heads, int head_dim, float sm_scale, void* o,
                       int64_t o_stride_token, int64_t o_stride_head,
                       void* stream);
+
+/* ------------------------------------------------------------------ */
+/* Residual path: RMSNorm, fused add + RMSNorm, gated activations      */
+/* ------------------------------------------------------------------ */
+
+/*
+ * out[r, :] = T(x[r, :] * rsqrt(mean(x[r, :]^2) + eps) * weight) for
+ * r < rows, fp32 arithmetic, T = bf16 or fp16 (dtype SGL_DTYPE_*; weight
+ * has the same type). Rows of d elements, x_stride_row / out_stride_row
+ * elements apart; out may equal x (in place).
+ * Replaces: RMSNorm::forward / forward_inplace
+ *           (src/layers/normalization.cu:236-269).
+ */
+int sgl_rmsnorm(void* out, const void* x, const void* weight, int64_t rows,
+                int64_t d, int64_t x_stride_row, int64_t out_stride_row,
+                int dtype, float eps, void* stream);
+
+/*
+ * In place, per row: s = x + residual (fp32); residual = T(s);
+ * x = T(s * rsqrt(mean(s^2) + eps) * weight). Rows longer than 8192
+ * elements normalise T(s) instead of s (a second pass re-reads it).
+ * Replaces: RMSNorm::fused_add_forward_inplace
+ *           (src/layers/normalization.cu:386-416).
+ */
+int sgl_fused_add_rmsnorm(void* x, void* residual, const void* weight,
+                          int64_t rows, int64_t d, int64_t x_stride_row,
+                          int64_t residual_stride_row, int dtype, float eps,
+                          void* stream);
+
+/*
+ * out[t, i] = T(silu(in[t, i]) * in[t, d + i]), silu(x) = x / (1 + e^-x),
+ * for t < tokens, i < d; input rows hold 2 d elements (gate, then up).
+ * Replaces: silu_and_mul (src/layers/activation.cu:8-10, 15-45).
+ */
+int sgl_silu_and_mul(void* out, const void* input, int64_t tokens, int64_t d,
+                     int64_t in_stride_row, int64_t out_stride_row, int dtype,
+                     void* stream);
+
+/*
+ * As sgl_silu_and_mul with the tanh GELU
+ * gelu(x) = 0.5 x (1 + tanh(0.7978845608 (x + 0.044715 x^3))).
+ * Replaces: gelu_and_mul (src/layers/activation.cu:12-14, 47-77).
+ */
+int sgl_gelu_and_mul(void* out, const void* input, int64_t tokens, int64_t d,
+                     int64_t in_stride_row, int64_t out_stride_row, int dtype,
+                     void* stream);
 
 #ifdef __cplusplus
 }  /* extern "C" */

@@ -299,3 +299,85 @@ void oracle_prefill(const uint16_t* q, int64_t q_st, int64_t q_sh, const uint16_
     free(qf);
   }
 }
+
+/* ---------- residual path ----------
+ * RMSNorm::forward (src/layers/normalization.cu:236-269), fused add + RMSNorm
+ * (:386-416) and silu_and_mul / gelu_and_mul (src/layers/activation.cu:8-77),
+ * whose values FlashInfer v0.2.0.post1's norm / activation kernels compute in
+ * fp32 and round once to the tensor type T (bf16 or fp16). Here values are
+ * carried as fp32 arrays holding T-representable numbers; dtype 0 = bf16,
+ * 1 = fp16. The sum of squares is accumulated in double (any fp32 order is
+ * within the tests' one-ulp tolerance of it); the scale and products follow
+ * the fp32 steps. */
+
+/* Round to the nearest T value, ties to even. fp16: scale to the 11-bit
+ * quantum of the value's binade (subnormal quantum 2^-24) and round there;
+ * results above the largest finite fp16 (65504) become infinity. */
+static float round_t(float x, int dtype) {
+  if (dtype == 0) return bf16_to_f32(f32_to_bf16(x));
+  if (isnan(x) || isinf(x) || x == 0.f) return x;
+  const double a = fabs((double)x);
+  int e;
+  frexp(a, &e); /* a = m 2^e, m in [0.5, 1): leading bit 2^(e-1) */
+  int lead = e - 1;
+  if (lead < -14) lead = -14;
+  const double quantum = ldexp(1.0, lead - 10);
+  double r = nearbyint(a / quantum) * quantum;
+  if (r > 65504.0) r = INFINITY;
+  return (float)copysign(r, (double)x);
+}
+
+static void norm_row(const float* s, const float* w, float* out, int64_t d, float eps,
+                     int dtype) {
+  double acc = 0.0;
+  for (int64_t i = 0; i < d; ++i) acc += (double)s[i] * (double)s[i];
+  const float ss = (float)acc;
+  const float scale = 1.0f / sqrtf(ss / (float)d + eps);
+  for (int64_t i = 0; i < d; ++i) out[i] = round_t((s[i] * scale) * w[i], dtype);
+}
+
+/* out[r] = T(x[r] * rsqrt(mean(x[r]^2) + eps) * w); rows contiguous. */
+void oracle_rmsnorm(const float* x, const float* w, float* out, int64_t rows, int64_t d,
+                    float eps, int dtype) {
+#pragma omp parallel for schedule(static)
+  for (int64_t r = 0; r < rows; ++r) norm_row(x + r * d, w, out + r * d, d, eps, dtype);
+}
+
+/* s = x + residual (fp32); residual_out = T(s); x_out = T(norm(s) * w). */
+void oracle_fused_add_rmsnorm(const float* x, const float* residual, const float* w,
+                              float* x_out, float* residual_out, int64_t rows, int64_t d,
+                              float eps, int dtype) {
+#pragma omp parallel
+  {
+    float* s = (float*)malloc(sizeof(float) * (size_t)d);
+#pragma omp for schedule(static)
+    for (int64_t r = 0; r < rows; ++r) {
+      for (int64_t i = 0; i < d; ++i) {
+        s[i] = x[r * d + i] + residual[r * d + i];
+        residual_out[r * d + i] = round_t(s[i], dtype);
+      }
+      norm_row(s, w, x_out + r * d, d, eps, dtype);
+    }
+    free(s);
+  }
+}
+
+/* out[t, i] = T(act(in[t, i]) * in[t, d + i]); act 0 = silu x / (1 + e^-x),
+ * act 1 = tanh GELU 0.5 x (1 + tanh(0.7978845608 (x + 0.044715 x^3))),
+ * evaluated in double. in rows hold 2 d values, out rows d. */
+void oracle_act_and_mul(const float* in, float* out, int64_t tokens, int64_t d, int act,
+                        int dtype) {
+#pragma omp parallel for schedule(static)
+  for (int64_t t = 0; t < tokens; ++t) {
+    for (int64_t i = 0; i < d; ++i) {
+      const double x = in[t * 2 * d + i], y = in[t * 2 * d + d + i];
+      const double a = act == 0 ? x / (1.0 + exp(-x))
+                                : 0.5 * x * (1.0 + tanh(0.7978845608 * (x + 0.044715 * x * x * x)));
+      out[t * d + i] = round_t((float)(a * y), dtype);
+    }
+  }
+}
+
+void oracle_round_t(const float* in, float* out, int64_t n, int dtype) {
+  for (int64_t i = 0; i < n; ++i) out[i] = round_t(in[i], dtype);
+}

@@ -177,3 +177,53 @@ def prefill(q, k_cache, v_cache, indices, qo_indptr, kv_indptr, sm_scale: float)
                          ctypes.c_int(hq), ctypes.c_int(hkv), ctypes.c_int(D), F32(sm_scale),
                          _p(out))
     return out
+
+
+# ---------------------------------------------------------------- residual path
+# Values are fp32 arrays holding numbers representable in T (bf16 or fp16);
+# dtype is "bf16" or "fp16". Outputs are fp32 arrays of T-rounded values.
+
+_DT = {"bf16": 0, "fp16": 1}
+
+
+def _f32c(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def rmsnorm(x, w, eps: float, dtype: str) -> np.ndarray:
+    """RMSNorm::forward (src/layers/normalization.cu:236-269) on [rows, d]."""
+    x, w = _f32c(x), _f32c(w)
+    out = np.empty_like(x)
+    rows, d = x.shape
+    lib().oracle_rmsnorm(_p(x), _p(w), _p(out), I64(rows), I64(d), F32(eps),
+                         ctypes.c_int(_DT[dtype]))
+    return out
+
+
+def fused_add_rmsnorm(x, residual, w, eps: float, dtype: str):
+    """RMSNorm::fused_add_forward_inplace (src/layers/normalization.cu:386-416).
+    Returns (x_out, residual_out)."""
+    x, r, w = _f32c(x), _f32c(residual), _f32c(w)
+    xo, ro = np.empty_like(x), np.empty_like(x)
+    rows, d = x.shape
+    lib().oracle_fused_add_rmsnorm(_p(x), _p(r), _p(w), _p(xo), _p(ro), I64(rows), I64(d),
+                                   F32(eps), ctypes.c_int(_DT[dtype]))
+    return xo, ro
+
+
+def act_and_mul(inp, act: str, dtype: str) -> np.ndarray:
+    """silu_and_mul / gelu_and_mul (src/layers/activation.cu:8-77) on [T, 2d] -> [T, d]."""
+    inp = _f32c(inp)
+    T, d2 = inp.shape
+    out = np.empty((T, d2 // 2), np.float32)
+    lib().oracle_act_and_mul(_p(inp), _p(out), I64(T), I64(d2 // 2),
+                             ctypes.c_int({"silu": 0, "gelu": 1}[act]), ctypes.c_int(_DT[dtype]))
+    return out
+
+
+def round_t(x, dtype: str) -> np.ndarray:
+    """The oracle's rounding to the nearest T value (ties to even), as fp32."""
+    x = _f32c(x)
+    out = np.empty_like(x)
+    lib().oracle_round_t(_p(x), _p(out), I64(x.size), ctypes.c_int(_DT[dtype]))
+    return out

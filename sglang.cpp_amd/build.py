@@ -36,7 +36,7 @@ HIP_FLAGS = [
     f"-I{REPO / 'include'}",
 ]
 
-SOURCES = ["kv_store.hip", "metadata.hip", "rope_norm.hip", "decode.hip", "prefill.hip"]
+SOURCES = ["kv_store.hip", "metadata.hip", "rope_norm.hip", "decode.hip", "prefill.hip", "residual.hip"]
 
 
 def _compile(src: Path, obj: Path) -> None:

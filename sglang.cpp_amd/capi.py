@@ -23,7 +23,9 @@ HEADER_PATH = PKG_DIR.parent / "include" / "sgl_attn.h"
 
 SGL_INDEX_I32 = 0
 SGL_INDEX_I64 = 1
-ABI_VERSION = 6
+SGL_DTYPE_BF16 = 0
+SGL_DTYPE_F16 = 1
+ABI_VERSION = 7
 FUSED_NO_K_WRITEBACK = 1  # SGL_FUSED_NO_K_WRITEBACK
 
 
@@ -74,6 +76,10 @@ _SIGNATURES = {
     "sgl_paged_decode": ([ctypes.POINTER(DecodePlan), _vp, _i64, _i64, _vp, _vp, _i64, _i64,
                           _vp, _vp, _vp, _i32, _i32, _i32, _i32, _f32, _vp, _i64, _i64, _vp,
                           _i64, _vp], _i32),
+    "sgl_rmsnorm": ([_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i32, _f32, _vp], _i32),
+    "sgl_fused_add_rmsnorm": ([_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i32, _f32, _vp], _i32),
+    "sgl_silu_and_mul": ([_vp, _vp, _i64, _i64, _i64, _i64, _i32, _vp], _i32),
+    "sgl_gelu_and_mul": ([_vp, _vp, _i64, _i64, _i64, _i64, _i32, _vp], _i32),
     "sgl_paged_prefill": ([_vp, _i64, _i64, _vp, _vp, _i64, _i64, _vp, _vp, _vp, _vp, _i32,
                            _i32, _i32, _i32, _i32, _f32, _vp, _i64, _i64, _vp], _i32),
 }
@@ -251,6 +257,82 @@ def qk_rmsnorm(q: torch.Tensor, k: Optional[torch.Tensor], q_weight: torch.Tenso
                                 kh, d, q.stride(0), q.stride(1),
                                 0 if k is None else k.stride(0), 0 if k is None else k.stride(1),
                                 eps, _stream(dev)), "sgl_qk_rmsnorm")
+
+
+# ---------------------------------------------------------------- residual path
+
+def _dtype_code(*ts: torch.Tensor) -> int:
+    dt = ts[0].dtype
+    if any(t.dtype != dt for t in ts):
+        raise ValueError("tensors must share one dtype")
+    if dt == torch.bfloat16:
+        return SGL_DTYPE_BF16
+    if dt == torch.float16:
+        return SGL_DTYPE_F16
+    raise ValueError("residual-path kernels take bf16 or fp16")
+
+
+def _rows2d(t: torch.Tensor, what: str) -> tuple[int, int, int]:
+    """(rows, d, row stride) of a tensor viewed as [rows, d] with contiguous rows."""
+    if t.dim() < 2 or t.stride(-1) != 1:
+        raise ValueError(f"{what} must have rank >= 2 and a contiguous last dimension")
+    d = t.shape[-1]
+    rows = t.numel() // d if d else 0
+    if t.dim() == 2:
+        return rows, d, t.stride(0)
+    if not t.is_contiguous():
+        raise ValueError(f"{what} of rank > 2 must be contiguous")
+    return rows, d, d
+
+
+def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float,
+            out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """RMSNorm::forward (src/layers/normalization.cu:236-241); out=x is forward_inplace."""
+    out = torch.empty_like(x) if out is None else out
+    dev = _need_gpu(x, weight, out)
+    rows, d, xs = _rows2d(x, "x")
+    _, _, os_ = _rows2d(out, "out")
+    if out.shape != x.shape or weight.numel() != d:
+        raise ValueError("out must match x; weight must have d elements")
+    _check(lib().sgl_rmsnorm(_p(out), _p(x), _p(weight), rows, d, xs, os_,
+                             _dtype_code(x, weight, out), eps, _stream(dev)), "sgl_rmsnorm")
+    return out
+
+
+def fused_add_rmsnorm(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor,
+                      eps: float) -> None:
+    """RMSNorm::fused_add_forward_inplace (src/layers/normalization.cu:386-416), in place."""
+    dev = _need_gpu(x, residual, weight)
+    if x.dim() != 2 or residual.dim() != 2 or x.shape != residual.shape:
+        raise ValueError("FusedAddRMSNorm expects rank-2 tensors of one shape")
+    rows, d, xs = _rows2d(x, "x")
+    _, _, rs = _rows2d(residual, "residual")
+    if weight.numel() != d:
+        raise ValueError("weight must have d elements")
+    _check(lib().sgl_fused_add_rmsnorm(_p(x), _p(residual), _p(weight), rows, d, xs, rs,
+                                       _dtype_code(x, residual, weight), eps, _stream(dev)),
+           "sgl_fused_add_rmsnorm")
+
+
+def _act_and_mul(fn: str, out: torch.Tensor, input: torch.Tensor) -> None:
+    dev = _need_gpu(out, input)
+    if input.dim() != 2 or out.dim() != 2 or input.stride(1) != 1 or out.stride(1) != 1:
+        raise ValueError("input / out must be rank-2 with contiguous rows")
+    d = input.shape[1] // 2
+    if input.shape[1] != 2 * d or out.shape[0] != input.shape[0] or out.shape[1] != d:
+        raise ValueError("input must be [T, 2d] and out [T, d]")
+    _check(getattr(lib(), fn)(_p(out), _p(input), input.shape[0], d, input.stride(0),
+                              out.stride(0), _dtype_code(input, out), _stream(dev)), fn)
+
+
+def silu_and_mul(out: torch.Tensor, input: torch.Tensor) -> None:
+    """silu_and_mul (src/layers/activation.cu:15-45)."""
+    _act_and_mul("sgl_silu_and_mul", out, input)
+
+
+def gelu_and_mul(out: torch.Tensor, input: torch.Tensor) -> None:
+    """gelu_and_mul (src/layers/activation.cu:47-77)."""
+    _act_and_mul("sgl_gelu_and_mul", out, input)
 
 
 def rope(positions: torch.Tensor, q: torch.Tensor, k: torch.Tensor, cos_cache: torch.Tensor,

@@ -124,9 +124,17 @@ PYBIND11_MODULE(sgl_backend, m) {
            py::arg("size"), py::arg("eps"), py::arg("device") = 0)
       .def_readwrite("weight", &RMSNorm::weight)
       .def("eps", &RMSNorm::eps)
+      .def("forward", &RMSNorm::forward)
+      .def("forward_inplace", [](const RMSNorm& n, torch::Tensor x) { n.forward_inplace(x); })
       .def("forward_inplace_3d_strided", [](const RMSNorm& n, torch::Tensor x) {
         n.forward_inplace_3d_strided(x);
+      })
+      .def("fused_add_forward_inplace", [](const RMSNorm& n, torch::Tensor x, torch::Tensor r) {
+        n.fused_add_forward_inplace(x, r);
       });
+
+  m.def("silu_and_mul", [](torch::Tensor out, torch::Tensor input) { silu_and_mul(out, input); });
+  m.def("gelu_and_mul", [](torch::Tensor out, torch::Tensor input) { gelu_and_mul(out, input); });
 
   m.def("fused_qk_rmsnorm_inplace_3d_strided",
         [](torch::Tensor q, torch::Tensor k, const RMSNorm& qn, const RMSNorm& kn) {

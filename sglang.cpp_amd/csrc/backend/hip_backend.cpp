@@ -464,6 +464,91 @@ void RMSNorm::forward_inplace_3d_strided(torch::Tensor& x) const {
             "sgl_qk_rmsnorm");
 }
 
+namespace {
+// SGL_DTYPE_* of a 16-bit floating tensor; the reference's kernels take
+// fp16 and bf16 (normalization.cu:253-268, activation.cu:25-44).
+int half_dtype(const torch::Tensor& t, const char* what) {
+  if (t.scalar_type() == torch::kBFloat16) return SGL_DTYPE_BF16;
+  TORCH_CHECK(t.scalar_type() == torch::kFloat16, what, " must be bf16 or fp16");
+  return SGL_DTYPE_F16;
+}
+
+// [rows, d] view of a tensor whose rows are contiguous: rank 2 with any row
+// stride, or a contiguous tensor of higher rank.
+void rows_view(const torch::Tensor& t, int64_t& rows, int64_t& d, int64_t& stride,
+               const char* what) {
+  TORCH_CHECK(t.is_cuda() && t.dim() >= 2 && t.stride(-1) == 1, what,
+              " must be a device tensor of rank >= 2 with a contiguous last dim");
+  d = t.size(-1);
+  rows = d > 0 ? t.numel() / d : 0;
+  if (t.dim() == 2) {
+    stride = t.stride(0);
+  } else {
+    TORCH_CHECK(t.is_contiguous(), what, " of rank > 2 must be contiguous");
+    stride = d;
+  }
+}
+}  // namespace
+
+torch::Tensor RMSNorm::forward(const torch::Tensor& x) const {
+  auto out = torch::empty_like(x, x.options().memory_format(torch::MemoryFormat::Contiguous));
+  int64_t rows, d, xs, os, r2, d2;
+  rows_view(x, rows, d, xs, "x");
+  rows_view(out, r2, d2, os, "out");
+  TORCH_CHECK(weight.size(0) == d, "RMSNorm weight size must match last dimension");
+  const int dt = half_dtype(x, "x");
+  TORCH_CHECK(weight.scalar_type() == x.scalar_type(), "RMSNorm weight dtype must match x");
+  check_sgl(sgl_rmsnorm(out.data_ptr(), x.data_ptr(), weight.data_ptr(), rows, d, xs, os, dt, eps_,
+                        current_stream(x.device())),
+            "sgl_rmsnorm");
+  return out;
+}
+
+void RMSNorm::forward_inplace(torch::Tensor& x) const {
+  int64_t rows, d, xs;
+  rows_view(x, rows, d, xs, "x");
+  TORCH_CHECK(weight.size(0) == d, "RMSNorm weight size must match last dimension");
+  const int dt = half_dtype(x, "x");
+  TORCH_CHECK(weight.scalar_type() == x.scalar_type(), "RMSNorm weight dtype must match x");
+  check_sgl(sgl_rmsnorm(x.data_ptr(), x.data_ptr(), weight.data_ptr(), rows, d, xs, xs, dt, eps_,
+                        current_stream(x.device())),
+            "sgl_rmsnorm");
+}
+
+void RMSNorm::fused_add_forward_inplace(torch::Tensor& x, torch::Tensor& residual) const {
+  TORCH_CHECK(x.is_cuda() && residual.is_cuda(), "x and residual must be device tensors");
+  TORCH_CHECK(x.dim() == 2 && residual.dim() == 2, "FusedAddRMSNorm expects rank-2 tensors");
+  TORCH_CHECK(x.sizes() == residual.sizes(), "x and residual shapes must match");
+  TORCH_CHECK(x.size(-1) > 0, "RMSNorm last dimension must be positive");
+  TORCH_CHECK(weight.size(0) == x.size(1), "RMSNorm weight size must match last dimension");
+  TORCH_CHECK(x.stride(1) == 1 && residual.stride(1) == 1, "rows must be contiguous");
+  const int dt = half_dtype(x, "x");
+  TORCH_CHECK(residual.scalar_type() == x.scalar_type() && weight.scalar_type() == x.scalar_type(),
+              "x, residual and weight must share a dtype");
+  check_sgl(sgl_fused_add_rmsnorm(x.data_ptr(), residual.data_ptr(), weight.data_ptr(), x.size(0),
+                                  x.size(1), x.stride(0), residual.stride(0), dt, eps_,
+                                  current_stream(x.device())),
+            "sgl_fused_add_rmsnorm");
+}
+
+static void act_and_mul(bool gelu, torch::Tensor& out, const torch::Tensor& input) {
+  TORCH_CHECK(input.is_cuda() && out.is_cuda(), "Inputs must be device tensors");
+  TORCH_CHECK(input.dim() == 2 && out.dim() == 2 && input.stride(1) == 1 && out.stride(1) == 1,
+              "input / out must be rank-2 with contiguous rows");
+  const int64_t d = input.size(1) / 2;
+  TORCH_CHECK(input.size(1) == 2 * d && out.size(0) == input.size(0) && out.size(1) == d,
+              "input must be [T, 2d] and out [T, d]");
+  const int dt = half_dtype(input, "input");
+  TORCH_CHECK(out.scalar_type() == input.scalar_type(), "out dtype must match input");
+  auto fn = gelu ? sgl_gelu_and_mul : sgl_silu_and_mul;
+  check_sgl(fn(out.data_ptr(), input.data_ptr(), input.size(0), d, input.stride(0), out.stride(0),
+               dt, current_stream(input.device())),
+            gelu ? "sgl_gelu_and_mul" : "sgl_silu_and_mul");
+}
+
+void silu_and_mul(torch::Tensor& out, const torch::Tensor& input) { act_and_mul(false, out, input); }
+void gelu_and_mul(torch::Tensor& out, const torch::Tensor& input) { act_and_mul(true, out, input); }
+
 void fused_qk_rmsnorm_inplace_3d_strided(torch::Tensor& q, torch::Tensor& k, const RMSNorm& q_norm,
                                          const RMSNorm& k_norm) {
   TORCH_CHECK(q.is_cuda() && k.is_cuda(), "q and k must be device tensors");

@@ -141,11 +141,15 @@ class HipAttnBackend : public BaseAttnBackend {
   hipEvent_t join_event_ = nullptr;
 };
 
-// q/k RMSNorm module (weight [D], bf16).
+// RMSNorm module (weight [size], bf16 by default; fp16 weights serve fp16
+// activations). The q/k path is bf16 only.
 class RMSNorm {
  public:
   RMSNorm(int size, float eps, torch::Device device);
-  void forward_inplace_3d_strided(torch::Tensor& x) const;  // normalization.cu:271-316
+  torch::Tensor forward(const torch::Tensor& x) const;            // normalization.cu:236-241
+  void forward_inplace(torch::Tensor& x) const;                   // normalization.cu:243-269
+  void forward_inplace_3d_strided(torch::Tensor& x) const;        // normalization.cu:271-316
+  void fused_add_forward_inplace(torch::Tensor& x, torch::Tensor& residual) const;  // :386-416
   float eps() const { return eps_; }
   torch::Tensor weight;
 
@@ -156,6 +160,11 @@ class RMSNorm {
 // normalization.cu:318-384
 void fused_qk_rmsnorm_inplace_3d_strided(torch::Tensor& q, torch::Tensor& k, const RMSNorm& q_norm,
                                          const RMSNorm& k_norm);
+
+// Gated activations of the MLP: out [T, d] = act(input[:, :d]) * input[:, d:]
+// (activation.cu:15-77), bf16 or fp16.
+void silu_and_mul(torch::Tensor& out, const torch::Tensor& input);
+void gelu_and_mul(torch::Tensor& out, const torch::Tensor& input);
 
 // NeoX RoPE with a half-width fp32 cos/sin cache built on the device
 // (rotary_embedding.cu:75-94 builds the same table with LibTorch-CPU ops).

@@ -29,7 +29,8 @@ def sb():
 def test_backend_module_surface(sb):
     """Loads on CPU too: every reference-named class is exported."""
     for name in ["Req", "Batch", "MHAKVCache", "HipAttnBackend", "RMSNorm", "RotaryEmbedding",
-                 "AttentionLayer", "fused_qk_rmsnorm_inplace_3d_strided"]:
+                 "AttentionLayer", "fused_qk_rmsnorm_inplace_3d_strided", "silu_and_mul",
+                 "gelu_and_mul"]:
         assert hasattr(sb, name), name
     r = sb.Req(3, 10, 25)
     assert (r.table_idx, r.cached_len, r.device_len(), r.extend_len()) == (3, 10, 25, 15)
@@ -334,3 +335,41 @@ def test_backend_mixed_batch_overlap_and_graph_replay(oracle, dev, sb):
         o_eager = s.backend.forward(s.q, s.k, s.v, 0, s.batch)
         torch.cuda.synchronize()
         assert torch.equal(o_graph.view(torch.int16), o_eager.view(torch.int16)), f"replay {it}"
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_residual_modules_match_c_abi(dev, sb, dtype):
+    """RMSNorm.forward / forward_inplace / fused_add_forward_inplace and
+    silu_and_mul / gelu_and_mul (the reference's layer API, as
+    qwen3.cc:24-31,62 and utils.cc:49 call it) give the C ABI's bits; the
+    shapes are the reference tests' (test_normalization.cpp:5-19,
+    test_activation.cpp:5-29) and a Qwen3-8B layer's."""
+    from conftest import capi
+    note(f"residual modules {dtype}")
+    g = _gen(dev, 90)
+    for rows, d in [(10, 128), (300, 4096)]:
+        norm = sb.RMSNorm(d, 1e-6, 0)
+        norm.weight = (torch.rand(d, device=dev, generator=g) + 0.5).to(dtype)
+        x = torch.randn((rows, d), device=dev, generator=g).to(dtype)
+        r = torch.randn((rows, d), device=dev, generator=g).to(dtype)
+        want = capi.rmsnorm(x, norm.weight, 1e-6)
+        assert torch.equal(norm.forward(x), want)
+        y = x.clone()
+        norm.forward_inplace(y)
+        assert torch.equal(y, want)
+        x1, r1 = x.clone(), r.clone()
+        norm.fused_add_forward_inplace(x1, r1)
+        x2, r2 = x.clone(), r.clone()
+        capi.fused_add_rmsnorm(x2, r2, norm.weight, 1e-6)
+        assert torch.equal(x1, x2) and torch.equal(r1, r2)
+        assert torch.equal(r1, (x.float() + r.float()).to(dtype))
+    for fn, cfn in [(sb.silu_and_mul, capi.silu_and_mul), (sb.gelu_and_mul, capi.gelu_and_mul)]:
+        for tokens, d in [(10, 128), (64, 12288)]:
+            inp = torch.randn((tokens, 2 * d), device=dev, generator=g).to(dtype)
+            a = torch.empty((tokens, d), device=dev, dtype=dtype)
+            b = torch.empty_like(a)
+            fn(a, inp)
+            cfn(b, inp)
+            assert torch.equal(a, b)
+    torch.cuda.synchronize()

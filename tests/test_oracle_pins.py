@@ -368,3 +368,126 @@ def test_attention_page_permutation_invariance(oracle):
     kc2[perm], vc2[perm] = kc, vc
     b = oracle.decode(q, kc2, vc2, perm[idx].astype(np.int32), ip, 0.09)
     np.testing.assert_array_equal(a, b)
+
+
+# ------------------------------------------------------------------ residual path
+# RMSNorm over hidden rows, fused add + RMSNorm, SiLU/GELU-and-mul
+# (src/layers/normalization.cu:236-269,386-416; src/layers/activation.cu:8-77).
+
+RES_DTYPES = {"bf16": torch.bfloat16, "fp16": torch.float16}
+# One ulp of T relative to |v| is at most 2^-7 (bf16, 8-bit significand) or
+# 2^-10 (fp16, 11-bit significand).
+ULP = {"bf16": 2.0 ** -7, "fp16": 2.0 ** -10}
+
+
+def rand_t(rng, shape, dtype, scale=1.0):
+    x = torch.from_numpy(rng.standard_normal(shape).astype(np.float32) * scale)
+    return x.to(RES_DTYPES[dtype]).float().numpy()
+
+
+# Absolute slack: one fp16 subnormal step (fixed spacing 2^-24 below 2^-14);
+# for bf16, far-tail cancellations of 1 + tanh(u) in double (~1e-15).
+ATOL_T = {"bf16": 1e-12, "fp16": 2.0 ** -24}
+
+
+def assert_within_ulp(got, ref, dtype, what, max_ulp=1):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    bound = max_ulp * ULP[dtype] * np.maximum(np.abs(ref), np.abs(got)) + ATOL_T[dtype]
+    bad = np.abs(got - ref) > bound
+    assert not bad.any(), (f"{what}: {int(bad.sum())} of {bad.size} beyond {max_ulp} ulp; "
+                           f"e.g. got {got[bad][:4]} ref {ref[bad][:4]}")
+
+
+def test_round_t_matches_library_casts(oracle):
+    rng = np.random.default_rng(40)
+    v = (rng.standard_normal(200000) * 10.0 ** rng.uniform(-9, 5, 200000)).astype(np.float32)
+    h = rng.integers(0, 0x7BFF, 20000).astype(np.uint16).view(np.float16)
+    nxt = np.nextafter(h, np.float16(np.inf)).astype(np.float64)
+    mid = ((h.astype(np.float64) + nxt) / 2).astype(np.float32)  # exact fp16 ties
+    special = np.array([65504, 65519, 65520, 65535, 1e6, -1e6, np.inf, -np.inf, 0.0, -0.0,
+                        2.0 ** -24, 2.0 ** -25, 3 * 2.0 ** -26, 1e-30], np.float32)
+    v = np.concatenate([v, mid, special])
+    with np.errstate(over="ignore"):
+        want16 = v.astype(np.float16).astype(np.float32)
+    np.testing.assert_array_equal(oracle.round_t(v, "fp16"), want16)
+    want_bf = torch.from_numpy(v).to(torch.bfloat16).float().numpy()
+    np.testing.assert_array_equal(oracle.round_t(v, "bf16"), want_bf)
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+def test_hidden_rmsnorm_matches_torch_rms_norm(oracle, dtype):
+    rng = np.random.default_rng(41)
+    for rows, d in [(10, 128), (37, 1000), (8, 4096)]:
+        x = rand_t(rng, (rows, d), dtype, 3.0)
+        w = torch.from_numpy(rng.uniform(0.5, 1.5, d).astype(np.float32)).to(
+            RES_DTYPES[dtype]).float().numpy()
+        got = oracle.rmsnorm(x, w, 1e-6, dtype)
+        ref = torch.nn.functional.rms_norm(torch.from_numpy(x).double(), (d,),
+                                           torch.from_numpy(w).double(), 1e-6)
+        assert_within_ulp(got, ref.numpy(), dtype, f"rmsnorm {rows}x{d}")
+        # a dropped eps or a sum in place of the mean would be far outside one ulp
+        assert np.mean(got == oracle.round_t(ref.float().numpy(), dtype)) > 0.98
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+def test_hidden_rmsnorm_invariants(oracle, dtype):
+    rng = np.random.default_rng(42)
+    x = rand_t(rng, (16, 512), dtype)
+    w = rand_t(rng, (512,), dtype)
+    base = oracle.rmsnorm(x, w, 0.0, dtype)
+    # with eps = 0, power-of-two scalings commute with every rounding step
+    np.testing.assert_array_equal(oracle.rmsnorm(4.0 * x, w, 0.0, dtype), base)
+    np.testing.assert_array_equal(oracle.rmsnorm(x, 2.0 * w, 0.0, dtype), 2.0 * base)
+    # a constant row normalises to sign(c) * w
+    c = np.full((3, 512), -3.0, np.float32)
+    np.testing.assert_array_equal(oracle.rmsnorm(c, w, 0.0, dtype), np.broadcast_to(-w, c.shape))
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+def test_fused_add_rmsnorm_pins(oracle, dtype):
+    rng = np.random.default_rng(43)
+    x = rand_t(rng, (24, 2048), dtype)
+    r = rand_t(rng, (24, 2048), dtype, 4.0)
+    w = rand_t(rng, (2048,), dtype)
+    xo, ro = oracle.fused_add_rmsnorm(x, r, w, 1e-6, dtype)
+    # residual: one rounding of the fp32 sum (torch's add then cast)
+    want_r = (torch.from_numpy(x) + torch.from_numpy(r)).to(RES_DTYPES[dtype]).float().numpy()
+    np.testing.assert_array_equal(ro, want_r)
+    # the output normalises the unrounded sum
+    s = torch.from_numpy(x).double() + torch.from_numpy(r).double()
+    ref = torch.nn.functional.rms_norm(s, (2048,), torch.from_numpy(w).double(), 1e-6)
+    assert_within_ulp(xo, ref.numpy(), dtype, "fused add rmsnorm")
+    # zero residual reduces to the plain norm; the sum is symmetric
+    z = np.zeros_like(r)
+    xo0, ro0 = oracle.fused_add_rmsnorm(x, z, w, 1e-6, dtype)
+    np.testing.assert_array_equal(xo0, oracle.rmsnorm(x, w, 1e-6, dtype))
+    np.testing.assert_array_equal(ro0, x)
+    xs, rs = oracle.fused_add_rmsnorm(r, x, w, 1e-6, dtype)
+    np.testing.assert_array_equal(xs, xo)
+    np.testing.assert_array_equal(rs, ro)
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+@pytest.mark.parametrize("act", ["silu", "gelu"])
+def test_act_and_mul_matches_torch(oracle, dtype, act):
+    rng = np.random.default_rng(44)
+    d = 777
+    inp = rand_t(rng, (33, 2 * d), dtype, 3.0)
+    got = oracle.act_and_mul(inp, act, dtype)
+    x = torch.from_numpy(inp[:, :d]).double()
+    y = torch.from_numpy(inp[:, d:]).double()
+    a = torch.nn.functional.silu(x) if act == "silu" else \
+        torch.nn.functional.gelu(x, approximate="tanh")
+    ref = (a * y).numpy()
+    assert_within_ulp(got, ref, dtype, f"{act}_and_mul")
+    assert np.mean(got == oracle.round_t(ref.astype(np.float32), dtype)) > 0.99
+    # act(x) - act(-x) = x for both activations (y = 1)
+    xs = np.linspace(-8, 8, 257, dtype=np.float32)
+    xs = oracle.round_t(xs, dtype)
+    ones = np.ones_like(xs)
+    pos = oracle.act_and_mul(np.stack([np.concatenate([xs, ones])]), act, dtype)[0]
+    neg = oracle.act_and_mul(np.stack([np.concatenate([-xs, ones])]), act, dtype)[0]
+    slack = ULP[dtype] * (np.abs(pos) + np.abs(neg)) + 2 * ATOL_T[dtype]
+    assert np.all(np.abs(pos - neg - xs) <= slack)
+    assert pos[128] == 0.0  # act(0) = 0
