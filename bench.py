@@ -11,7 +11,8 @@ The other configs are reported under "extra" (and as their own lines with
 RoPE + qk-norm + KV store, cfg5 mixed 48-layer step replayed as a hipGraph;
 and the residual path around attention at the Qwen3-8B shape for an
 8192-token chunk: resid_norm (fused add + RMSNorm, hidden 4096) and
-resid_act (SiLU-and-mul, intermediate 12288).
+resid_act (SiLU-and-mul, intermediate 12288); and sampling (top-k + top-p
+draw for 256 rows over the Qwen3 vocabulary, as the Sampler runs it).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload cfgN]
                        [--no-extra] [--no-cpu]
@@ -43,7 +44,8 @@ def parse():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="cfg4",
-                    choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5", "resid_norm", "resid_act"])
+                    choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5", "resid_norm", "resid_act",
+                             "sampling"])
     ap.add_argument("--no-extra", action="store_true", help="headline workload only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--cfg5-layers", type=int, default=48)
@@ -338,8 +340,42 @@ def setup_resid(torch, capi, name, dev, seed=0):
     return step, 6 * T * d, {"tokens": T, "intermediate": d}
 
 
+SAMPLING_BATCH, QWEN3_VOCAB = 256, 151936
+
+
+def setup_sampling(torch, capi, dev, seed=0):
+    """Top-k + top-p draw as the reference's Sampler::sample runs it
+    (engine.cc:300-345): probs = softmax(logits / T) fp32 [256, 151936],
+    uniform [32, 256], per-row top_k int32 and top_p. Algorithmic bytes: one
+    read of probs (the rejection rounds re-read rows from L2)."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    B, V = SAMPLING_BATCH, QWEN3_VOCAB
+    logits = torch.randn((B, V), device=dev, generator=g) * 3
+    temp = torch.linspace(0.6, 1.2, B, device=dev).view(B, 1)
+    probs = torch.softmax(logits / temp, -1).contiguous()
+    del logits
+    u = torch.rand((32, B), device=dev, generator=g)
+    k = torch.full((B,), 50, dtype=torch.int32, device=dev)
+    tp = torch.full((B,), 0.9, dtype=torch.float32, device=dev)
+
+    def step():
+        capi.top_k_top_p_sampling_from_probs(probs, u, k, 0, tp, 0.0)
+
+    return step, B * V * 4 + 32 * B * 4 + B * 5, {"batch": B, "vocab": V, "top_k": 50,
+                                                  "top_p": 0.9}
+
+
 def run_workload(name, torch, capi, wl, dev, steps, warmup, cfg5_layers):
     timer = Timer(torch)
+    if name == "sampling":
+        step, nbytes, shape = setup_sampling(torch, capi, dev)
+        wall, ev = timer.run(step, steps, warmup)
+        rec = {"workload": f"sampling_top_k_top_p_b{SAMPLING_BATCH}_v{QWEN3_VOCAB}", **shape,
+               "ms_per_step": wall, "kernel_ms": ev, "bytes": nbytes,
+               "GB/s": nbytes / (wall * 1e-3) / 1e9,
+               "roofline": roofline_hbm(nbytes, ev, "sampling_top_k_top_p")}
+        return None, rec
     if name in ("resid_norm", "resid_act"):
         step, nbytes, shape = setup_resid(torch, capi, name, dev)
         wall, ev = timer.run(step, steps, warmup)
@@ -418,7 +454,8 @@ def main():
                            args.cfg5_layers)
     extra = {}
     if not args.no_extra:
-        for name in ("cfg1", "cfg2", "cfg3", "cfg4", "cfg5", "resid_norm", "resid_act"):
+        for name in ("cfg1", "cfg2", "cfg3", "cfg4", "cfg5", "resid_norm", "resid_act",
+                     "sampling"):
             if name == args.workload:
                 continue
             try:
@@ -445,7 +482,8 @@ def main():
         value, unit = head["decode_bytes"] / (head["ms_per_step"] * 1e-3) / 1e9, "GB/s"
     if w is None:
         config = {"workload": head["workload"], "parallelism": "single GPU",
-                  **{k: head[k] for k in ("tokens", "hidden", "intermediate") if k in head}}
+                  **{k: head[k] for k in ("tokens", "hidden", "intermediate", "batch", "vocab",
+                                          "top_k", "top_p") if k in head}}
     else:
         s = w.shape
         config = {"workload": head["workload"], "batch": w.batch.batch_size,

@@ -39,7 +39,7 @@ const char* sgl_status_string(int status);
 
 /* Library version, to check that the loaded .so matches this header. */
 int sgl_abi_version(void);
-#define SGL_ABI_VERSION 7
+#define SGL_ABI_VERSION 8
 
 /* ------------------------------------------------------------------ */
 /* KV-cache store                                                      */
@@ -303,6 +303,60 @@ int sgl_silu_and_mul(void* out, const void* input, int64_t tokens, int64_t d,
 int sgl_gelu_and_mul(void* out, const void* input, int64_t tokens, int64_t d,
                      int64_t in_stride_row, int64_t out_stride_row, int dtype,
                      void* stream);
+
+/* ------------------------------------------------------------------ */
+/* Sampling from probabilities                                         */
+/* ------------------------------------------------------------------ */
+
+/*
+ * probs: fp32 [batch_size, d], rows contiguous (the softmax of the
+ * temperature-scaled logits). out: int32 [batch_size]. The draw with
+ * uniform u is the first index i with probs[i] > 0 whose running sum of
+ * such probabilities exceeds u (d - 1 if rounding leaves none). uniform is
+ * fp32 [batch_size]. deterministic is accepted for the reference's
+ * signature; sums here always run in a fixed order.
+ * Replaces: flashinfer_sample_from_probs (src/engine/sampling.cu:65-84).
+ */
+int sgl_sampling_from_probs(const float* probs, const float* uniform, int32_t* out,
+                            int batch_size, int d, int deterministic, void* stream);
+
+/*
+ * Top-k draw by rejection rounds: round r draws from the probabilities
+ * above a pivot with u = uniform[r, row] * (their mass), the pivot rises to
+ * the drawn probability, and the draw is accepted once fewer than k
+ * probabilities exceed it. uniform: fp32 [max_rounds, batch_size]; k is
+ * top_k_arr[row] (fp32, as the reference passes it) or top_k_val when
+ * top_k_arr is NULL. success (bool bytes, optional) = accepted within
+ * max_rounds; out holds the last draw either way.
+ * Replaces: flashinfer_top_k_sample_from_probs (src/engine/sampling.cu:86-116).
+ */
+int sgl_top_k_sampling_from_probs(const float* probs, const float* uniform, int32_t* out,
+                                  uint8_t* success, const float* top_k_arr,
+                                  int batch_size, int top_k_val, int d, int max_rounds,
+                                  int deterministic, void* stream);
+
+/*
+ * As above, accepting once the mass above the pivot is below top_p
+ * (top_p_arr[row], or top_p_val when top_p_arr is NULL).
+ * Replaces: flashinfer_top_p_sample_from_probs (src/engine/sampling.cu:118-148).
+ */
+int sgl_top_p_sampling_from_probs(const float* probs, const float* uniform, int32_t* out,
+                                  uint8_t* success, const float* top_p_arr,
+                                  int batch_size, float top_p_val, int d, int max_rounds,
+                                  int deterministic, void* stream);
+
+/*
+ * Both filters: accepted once fewer than k probabilities exceed the pivot
+ * and their mass is below top_p. top_k_arr is int32 here, as the
+ * reference passes it.
+ * Replaces: flashinfer_top_k_top_p_sample_from_probs
+ *           (src/engine/sampling.cu:150-192).
+ */
+int sgl_top_k_top_p_sampling_from_probs(const float* probs, const float* uniform,
+                                        const int32_t* top_k_arr, const float* top_p_arr,
+                                        int32_t* out, uint8_t* success, int batch_size,
+                                        int top_k_val, float top_p_val, int d,
+                                        int max_rounds, int deterministic, void* stream);
 
 #ifdef __cplusplus
 }  /* extern "C" */

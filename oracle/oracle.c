@@ -381,3 +381,66 @@ void oracle_act_and_mul(const float* in, float* out, int64_t tokens, int64_t d, 
 void oracle_round_t(const float* in, float* out, int64_t n, int dtype) {
   for (int64_t i = 0; i < n; ++i) out[i] = round_t(in[i], dtype);
 }
+
+/* ---------- sampling from probabilities ----------
+ * src/engine/sampling.cu:65-194 (FlashInfer v0.2.0.post1's SamplingFromProb,
+ * TopK/TopP/TopKTopPSamplingFromProb, published algorithm): an inverse-CDF
+ * draw over the probabilities above a threshold, and rejection rounds with
+ * a rising pivot for the filtered draws. Running sums are kept in double:
+ * exact for inputs whose partial sums are exact in fp32 (the dyadic
+ * fixtures), and the true CDF otherwise; the fp32 kernels' sums differ
+ * from it by their summation error only. The target u * q is rounded to
+ * fp32, as the kernels compute it. */
+
+static int64_t draw_row(const float* p, int64_t d, float thr, float u) {
+  double agg = 0.0;
+  for (int64_t i = 0; i < d; ++i) {
+    if (p[i] > thr) {
+      agg += p[i];
+      if (agg > (double)u) return i;
+    }
+  }
+  return d - 1;
+}
+
+/* mode 0 plain (uniform [batch]), 1 top-k (k from top_k_f or top_k_val),
+ * 2 top-p, 3 top-k + top-p (k from top_k_i); uniform [rounds, batch]. */
+void oracle_sample(const float* probs, const float* uniform, int32_t* out, uint8_t* success,
+                   int64_t batch, int64_t d, int rounds, int mode, const float* top_k_f,
+                   const int32_t* top_k_i, int top_k_val, const float* top_p_arr,
+                   float top_p_val) {
+#pragma omp parallel for schedule(dynamic, 1)
+  for (int64_t b = 0; b < batch; ++b) {
+    const float* p = probs + b * d;
+    if (mode == 0) {
+      out[b] = (int32_t)draw_row(p, d, 0.f, uniform[b]);
+      continue;
+    }
+    int64_t k = top_k_val;
+    if (top_k_f) k = (int64_t)(uint32_t)top_k_f[b];
+    if (top_k_i) k = top_k_i[b];
+    const float top_p = top_p_arr ? top_p_arr[b] : top_p_val;
+    float pivot = 0.f, q = 1.f;
+    int64_t sampled = d - 1, count = 0;
+    int accepted = 0;
+    for (int r = 0; r < rounds; ++r) {
+      const float u = uniform[(int64_t)r * batch + b] * q;
+      sampled = draw_row(p, d, pivot, u);
+      if (p[sampled] > pivot) pivot = p[sampled];
+      double qd = 0.0;
+      count = 0;
+      for (int64_t i = 0; i < d; ++i)
+        if (p[i] > pivot) {
+          qd += p[i];
+          ++count;
+        }
+      q = (float)qd;
+      if (mode == 1) accepted = count < k;
+      else if (mode == 2) accepted = q < top_p;
+      else accepted = count < k && q < top_p;
+      if (accepted) break;
+    }
+    out[b] = (int32_t)sampled;
+    if (success) success[b] = (uint8_t)accepted;
+  }
+}

@@ -227,3 +227,26 @@ def round_t(x, dtype: str) -> np.ndarray:
     out = np.empty_like(x)
     lib().oracle_round_t(_p(x), _p(out), I64(x.size), ctypes.c_int(_DT[dtype]))
     return out
+
+
+# ---------------------------------------------------------------- sampling
+
+def sample(probs, uniform, mode: str, top_k=None, top_k_val: int = 0, top_p=None,
+           top_p_val: float = 0.0):
+    """src/engine/sampling.cu:65-194. probs fp32 [B, d]; uniform fp32 [B] (plain)
+    or [rounds, B]. top_k: fp32 [B] for "top_k", int32 [B] for "top_k_top_p".
+    Returns (samples int32 [B], success bool [B] or None)."""
+    probs = _f32c(probs)
+    uniform = _f32c(uniform)
+    B, d = probs.shape
+    m = {"plain": 0, "top_k": 1, "top_p": 2, "top_k_top_p": 3}[mode]
+    rounds = 1 if m == 0 else uniform.shape[0]
+    out = np.empty(B, np.int32)
+    succ = None if m == 0 else np.empty(B, np.uint8)
+    tkf = _f32c(top_k) if (top_k is not None and m == 1) else None
+    tki = np.ascontiguousarray(top_k, np.int32) if (top_k is not None and m == 3) else None
+    tp = _f32c(top_p) if top_p is not None else None
+    lib().oracle_sample(_p(probs), _p(uniform), _p(out), _p(succ), I64(B), I64(d),
+                        ctypes.c_int(rounds), ctypes.c_int(m), _p(tkf), _p(tki),
+                        ctypes.c_int(top_k_val), _p(tp), F32(top_p_val))
+    return out, (None if succ is None else succ.astype(bool))

@@ -36,7 +36,8 @@ HIP_FLAGS = [
     f"-I{REPO / 'include'}",
 ]
 
-SOURCES = ["kv_store.hip", "metadata.hip", "rope_norm.hip", "decode.hip", "prefill.hip", "residual.hip"]
+SOURCES = ["kv_store.hip", "metadata.hip", "rope_norm.hip", "decode.hip", "prefill.hip", "residual.hip",
+           "sampling.hip"]
 
 
 def _compile(src: Path, obj: Path) -> None:

@@ -25,7 +25,7 @@ SGL_INDEX_I32 = 0
 SGL_INDEX_I64 = 1
 SGL_DTYPE_BF16 = 0
 SGL_DTYPE_F16 = 1
-ABI_VERSION = 7
+ABI_VERSION = 8
 FUSED_NO_K_WRITEBACK = 1  # SGL_FUSED_NO_K_WRITEBACK
 
 
@@ -80,6 +80,13 @@ _SIGNATURES = {
     "sgl_fused_add_rmsnorm": ([_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i32, _f32, _vp], _i32),
     "sgl_silu_and_mul": ([_vp, _vp, _i64, _i64, _i64, _i64, _i32, _vp], _i32),
     "sgl_gelu_and_mul": ([_vp, _vp, _i64, _i64, _i64, _i64, _i32, _vp], _i32),
+    "sgl_sampling_from_probs": ([_vp, _vp, _vp, _i32, _i32, _i32, _vp], _i32),
+    "sgl_top_k_sampling_from_probs": ([_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32,
+                                       _vp], _i32),
+    "sgl_top_p_sampling_from_probs": ([_vp, _vp, _vp, _vp, _vp, _i32, _f32, _i32, _i32, _i32,
+                                       _vp], _i32),
+    "sgl_top_k_top_p_sampling_from_probs": ([_vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _f32, _i32,
+                                             _i32, _i32, _vp], _i32),
     "sgl_paged_prefill": ([_vp, _i64, _i64, _vp, _vp, _i64, _i64, _vp, _vp, _vp, _vp, _i32,
                            _i32, _i32, _i32, _i32, _f32, _vp, _i64, _i64, _vp], _i32),
 }
@@ -434,3 +441,87 @@ def paged_prefill(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                                    max_qo_len,
                                    hq, hkv, D, scale, _p(o), o.stride(0), o.stride(1),
                                    _stream(dev)), "sgl_paged_prefill")
+
+
+# ---------------------------------------------------------------- sampling
+
+def _check_probs(probs: torch.Tensor, uniform: torch.Tensor, dims: int) -> None:
+    if probs.dim() != 2 or not probs.is_contiguous() or probs.dtype != torch.float32:
+        raise ValueError("probs must be a contiguous float32 [batch, vocab] tensor")
+    if uniform.dtype != torch.float32 or not uniform.is_contiguous() or uniform.dim() != dims:
+        raise ValueError("uniform_samples must be contiguous float32 with "
+                         + ("shape [batch]" if dims == 1 else "shape [max_rounds, batch]"))
+    if uniform.shape[-1] != probs.shape[0]:
+        raise ValueError("uniform_samples must cover every row")
+
+
+def _opt(t: Optional[torch.Tensor], dtype, n: int, what: str):
+    if t is None:
+        return None
+    if t.dtype != dtype or not t.is_contiguous() or t.numel() != n:
+        raise ValueError(f"{what} must be a contiguous {dtype} tensor with shape [batch]")
+    return t
+
+
+def sampling_from_probs(probs: torch.Tensor, uniform_samples: torch.Tensor,
+                        deterministic: bool = False) -> torch.Tensor:
+    """flashinfer_sample_from_probs (src/engine/sampling.cu:65-84)."""
+    dev = _need_gpu(probs, uniform_samples)
+    _check_probs(probs, uniform_samples, 1)
+    out = torch.empty(probs.shape[0], dtype=torch.int32, device=dev)
+    _check(lib().sgl_sampling_from_probs(_p(probs), _p(uniform_samples), _p(out), probs.shape[0],
+                                         probs.shape[1], int(deterministic), _stream(dev)),
+           "sgl_sampling_from_probs")
+    return out
+
+
+def top_k_sampling_from_probs(probs, uniform_samples, top_k: Optional[torch.Tensor],
+                              top_k_value: int = 0, deterministic: bool = False):
+    """flashinfer_top_k_sample_from_probs (src/engine/sampling.cu:86-116): top_k is
+    float32 [batch] or None (then top_k_value). Returns (samples, success)."""
+    dev = _need_gpu(probs, uniform_samples, top_k)
+    _check_probs(probs, uniform_samples, 2)
+    B = probs.shape[0]
+    top_k = _opt(top_k, torch.float32, B, "top_k")
+    out = torch.empty(B, dtype=torch.int32, device=dev)
+    ok = torch.empty(B, dtype=torch.bool, device=dev)
+    _check(lib().sgl_top_k_sampling_from_probs(_p(probs), _p(uniform_samples), _p(out), _p(ok),
+                                               _p(top_k), B, int(top_k_value), probs.shape[1],
+                                               uniform_samples.shape[0], int(deterministic),
+                                               _stream(dev)), "sgl_top_k_sampling_from_probs")
+    return out, ok
+
+
+def top_p_sampling_from_probs(probs, uniform_samples, top_p: Optional[torch.Tensor],
+                              top_p_value: float = 0.0, deterministic: bool = False):
+    """flashinfer_top_p_sample_from_probs (src/engine/sampling.cu:118-148)."""
+    dev = _need_gpu(probs, uniform_samples, top_p)
+    _check_probs(probs, uniform_samples, 2)
+    B = probs.shape[0]
+    top_p = _opt(top_p, torch.float32, B, "top_p")
+    out = torch.empty(B, dtype=torch.int32, device=dev)
+    ok = torch.empty(B, dtype=torch.bool, device=dev)
+    _check(lib().sgl_top_p_sampling_from_probs(_p(probs), _p(uniform_samples), _p(out), _p(ok),
+                                               _p(top_p), B, float(top_p_value), probs.shape[1],
+                                               uniform_samples.shape[0], int(deterministic),
+                                               _stream(dev)), "sgl_top_p_sampling_from_probs")
+    return out, ok
+
+
+def top_k_top_p_sampling_from_probs(probs, uniform_samples, top_k: Optional[torch.Tensor],
+                                    top_k_value: int, top_p: Optional[torch.Tensor],
+                                    top_p_value: float, deterministic: bool = False):
+    """flashinfer_top_k_top_p_sample_from_probs (src/engine/sampling.cu:150-192):
+    top_k is int32 [batch] here, as the reference passes it."""
+    dev = _need_gpu(probs, uniform_samples, top_k, top_p)
+    _check_probs(probs, uniform_samples, 2)
+    B = probs.shape[0]
+    top_k = _opt(top_k, torch.int32, B, "top_k")
+    top_p = _opt(top_p, torch.float32, B, "top_p")
+    out = torch.empty(B, dtype=torch.int32, device=dev)
+    ok = torch.empty(B, dtype=torch.bool, device=dev)
+    _check(lib().sgl_top_k_top_p_sampling_from_probs(
+        _p(probs), _p(uniform_samples), _p(top_k), _p(top_p), _p(out), _p(ok), B,
+        int(top_k_value), float(top_p_value), probs.shape[1], uniform_samples.shape[0],
+        int(deterministic), _stream(dev)), "sgl_top_k_top_p_sampling_from_probs")
+    return out, ok

@@ -133,6 +133,29 @@ PYBIND11_MODULE(sgl_backend, m) {
         n.fused_add_forward_inplace(x, r);
       });
 
+  m.def("flashinfer_sample_from_probs", &flashinfer_sample_from_probs, py::arg("probs"),
+        py::arg("uniform_samples"), py::arg("deterministic") = false);
+  auto pair = [](const FlashInferSamplingResult& r) { return py::make_tuple(r.samples, r.success); };
+  m.def("flashinfer_top_k_sample_from_probs",
+        [pair](torch::Tensor p, torch::Tensor u, c10::optional<torch::Tensor> k, int64_t kv, bool det) {
+          return pair(flashinfer_top_k_sample_from_probs(p, u, k.value_or(torch::Tensor()), kv, det));
+        },
+        py::arg("probs"), py::arg("uniform_samples"), py::arg("top_k"), py::arg("top_k_value") = 0,
+        py::arg("deterministic") = false);
+  m.def("flashinfer_top_p_sample_from_probs",
+        [pair](torch::Tensor p, torch::Tensor u, c10::optional<torch::Tensor> t, double tv, bool det) {
+          return pair(flashinfer_top_p_sample_from_probs(p, u, t.value_or(torch::Tensor()), tv, det));
+        },
+        py::arg("probs"), py::arg("uniform_samples"), py::arg("top_p"), py::arg("top_p_value") = 0.0,
+        py::arg("deterministic") = false);
+  m.def("flashinfer_top_k_top_p_sample_from_probs",
+        [pair](torch::Tensor p, torch::Tensor u, c10::optional<torch::Tensor> k, double kv,
+               c10::optional<torch::Tensor> t, double tv, bool det) {
+          return pair(flashinfer_top_k_top_p_sample_from_probs(p, u, k.value_or(torch::Tensor()), kv,
+                                                               t.value_or(torch::Tensor()), tv, det));
+        },
+        py::arg("probs"), py::arg("uniform_samples"), py::arg("top_k"), py::arg("top_k_value"),
+        py::arg("top_p"), py::arg("top_p_value"), py::arg("deterministic") = false);
   m.def("silu_and_mul", [](torch::Tensor out, torch::Tensor input) { silu_and_mul(out, input); });
   m.def("gelu_and_mul", [](torch::Tensor out, torch::Tensor input) { gelu_and_mul(out, input); });
 

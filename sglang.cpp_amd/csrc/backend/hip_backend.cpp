@@ -549,6 +549,118 @@ static void act_and_mul(bool gelu, torch::Tensor& out, const torch::Tensor& inpu
 void silu_and_mul(torch::Tensor& out, const torch::Tensor& input) { act_and_mul(false, out, input); }
 void gelu_and_mul(torch::Tensor& out, const torch::Tensor& input) { act_and_mul(true, out, input); }
 
+// ---------------------------------------------------------------- sampling
+
+namespace {
+void check_probs(const torch::Tensor& probs) {
+  TORCH_CHECK(probs.defined(), "probs must be defined");
+  TORCH_CHECK(probs.is_cuda(), "sampling requires device probs");
+  TORCH_CHECK(probs.is_contiguous(), "sampling requires contiguous probs");
+  TORCH_CHECK(probs.scalar_type() == torch::kFloat32, "sampling expects float32 probs");
+  TORCH_CHECK(probs.dim() == 2, "probs must have shape [batch, vocab]");
+}
+
+void check_uniform(const torch::Tensor& probs, const torch::Tensor& u, int64_t dims) {
+  TORCH_CHECK(u.defined() && u.is_cuda() && u.is_contiguous() && u.scalar_type() == torch::kFloat32,
+              "uniform_samples must be a contiguous device float32 tensor");
+  TORCH_CHECK(u.device() == probs.device(), "uniform_samples must be on the same device as probs");
+  TORCH_CHECK(u.dim() == dims, "uniform_samples has unexpected dimensions");
+  TORCH_CHECK(u.size(dims - 1) == probs.size(0), dims == 1
+                  ? "uniform_samples must have shape [batch]"
+                  : "uniform_samples must have shape [max_rounds, batch]");
+}
+
+void check_row_arg(const torch::Tensor& t, const torch::Tensor& probs, c10::ScalarType st,
+                   const char* what) {
+  TORCH_CHECK(!t.defined() || (t.is_cuda() && t.is_contiguous() && t.scalar_type() == st &&
+                               t.device() == probs.device() && t.numel() == probs.size(0)),
+              what, " must be a contiguous device tensor of the documented dtype with shape [batch]");
+}
+
+FlashInferSamplingResult sampling_outputs(const torch::Tensor& probs) {
+  auto opts = probs.options();
+  return {torch::empty({probs.size(0)}, opts.dtype(torch::kInt32)),
+          torch::empty({probs.size(0)}, opts.dtype(torch::kBool))};
+}
+
+int32_t narrow_dim(int64_t v, const char* what) {
+  TORCH_CHECK(v >= 0 && v <= 0x7fffffff, what, " out of range");
+  return static_cast<int32_t>(v);
+}
+}  // namespace
+
+torch::Tensor flashinfer_sample_from_probs(const torch::Tensor& probs,
+                                           const torch::Tensor& uniform_samples, bool deterministic) {
+  check_probs(probs);
+  check_uniform(probs, uniform_samples, 1);
+  auto samples = torch::empty({probs.size(0)}, probs.options().dtype(torch::kInt32));
+  check_sgl(sgl_sampling_from_probs(probs.data_ptr<float>(), uniform_samples.data_ptr<float>(),
+                                    samples.data_ptr<int32_t>(), narrow_dim(probs.size(0), "batch"),
+                                    narrow_dim(probs.size(1), "vocab"), deterministic ? 1 : 0,
+                                    current_stream(probs.device())),
+            "sgl_sampling_from_probs");
+  return samples;
+}
+
+FlashInferSamplingResult flashinfer_top_k_sample_from_probs(const torch::Tensor& probs,
+                                                            const torch::Tensor& uniform_samples,
+                                                            const torch::Tensor& top_k,
+                                                            int64_t top_k_value, bool deterministic) {
+  check_probs(probs);
+  check_uniform(probs, uniform_samples, 2);
+  check_row_arg(top_k, probs, torch::kFloat32, "top_k");
+  auto r = sampling_outputs(probs);
+  check_sgl(sgl_top_k_sampling_from_probs(
+                probs.data_ptr<float>(), uniform_samples.data_ptr<float>(), r.samples.data_ptr<int32_t>(),
+                reinterpret_cast<uint8_t*>(r.success.data_ptr<bool>()),
+                top_k.defined() ? top_k.data_ptr<float>() : nullptr,
+                narrow_dim(probs.size(0), "batch"), static_cast<int>(top_k_value),
+                narrow_dim(probs.size(1), "vocab"), narrow_dim(uniform_samples.size(0), "rounds"),
+                deterministic ? 1 : 0, current_stream(probs.device())),
+            "sgl_top_k_sampling_from_probs");
+  return r;
+}
+
+FlashInferSamplingResult flashinfer_top_p_sample_from_probs(const torch::Tensor& probs,
+                                                            const torch::Tensor& uniform_samples,
+                                                            const torch::Tensor& top_p,
+                                                            double top_p_value, bool deterministic) {
+  check_probs(probs);
+  check_uniform(probs, uniform_samples, 2);
+  check_row_arg(top_p, probs, torch::kFloat32, "top_p");
+  auto r = sampling_outputs(probs);
+  check_sgl(sgl_top_p_sampling_from_probs(
+                probs.data_ptr<float>(), uniform_samples.data_ptr<float>(), r.samples.data_ptr<int32_t>(),
+                reinterpret_cast<uint8_t*>(r.success.data_ptr<bool>()),
+                top_p.defined() ? top_p.data_ptr<float>() : nullptr,
+                narrow_dim(probs.size(0), "batch"), static_cast<float>(top_p_value),
+                narrow_dim(probs.size(1), "vocab"), narrow_dim(uniform_samples.size(0), "rounds"),
+                deterministic ? 1 : 0, current_stream(probs.device())),
+            "sgl_top_p_sampling_from_probs");
+  return r;
+}
+
+FlashInferSamplingResult flashinfer_top_k_top_p_sample_from_probs(
+    const torch::Tensor& probs, const torch::Tensor& uniform_samples, const torch::Tensor& top_k,
+    double top_k_value, const torch::Tensor& top_p, double top_p_value, bool deterministic) {
+  check_probs(probs);
+  check_uniform(probs, uniform_samples, 2);
+  check_row_arg(top_k, probs, torch::kInt32, "top_k");
+  check_row_arg(top_p, probs, torch::kFloat32, "top_p");
+  auto r = sampling_outputs(probs);
+  check_sgl(sgl_top_k_top_p_sampling_from_probs(
+                probs.data_ptr<float>(), uniform_samples.data_ptr<float>(),
+                top_k.defined() ? top_k.data_ptr<int32_t>() : nullptr,
+                top_p.defined() ? top_p.data_ptr<float>() : nullptr, r.samples.data_ptr<int32_t>(),
+                reinterpret_cast<uint8_t*>(r.success.data_ptr<bool>()),
+                narrow_dim(probs.size(0), "batch"), static_cast<int>(top_k_value),
+                static_cast<float>(top_p_value), narrow_dim(probs.size(1), "vocab"),
+                narrow_dim(uniform_samples.size(0), "rounds"), deterministic ? 1 : 0,
+                current_stream(probs.device())),
+            "sgl_top_k_top_p_sampling_from_probs");
+  return r;
+}
+
 void fused_qk_rmsnorm_inplace_3d_strided(torch::Tensor& q, torch::Tensor& k, const RMSNorm& q_norm,
                                          const RMSNorm& k_norm) {
   TORCH_CHECK(q.is_cuda() && k.is_cuda(), "q and k must be device tensors");

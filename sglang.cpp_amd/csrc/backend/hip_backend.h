@@ -166,6 +166,27 @@ void fused_qk_rmsnorm_inplace_3d_strided(torch::Tensor& q, torch::Tensor& k, con
 void silu_and_mul(torch::Tensor& out, const torch::Tensor& input);
 void gelu_and_mul(torch::Tensor& out, const torch::Tensor& input);
 
+// Sampling from probabilities, the reference's Sampler kernels
+// (include/sglang/engine/sampling.h:7-36, src/engine/sampling.cu:65-194):
+// same names, arguments and checks; the HIP kernels replace FlashInfer's.
+struct FlashInferSamplingResult {
+  torch::Tensor samples;
+  torch::Tensor success;
+};
+torch::Tensor flashinfer_sample_from_probs(const torch::Tensor& probs,
+                                           const torch::Tensor& uniform_samples, bool deterministic);
+FlashInferSamplingResult flashinfer_top_k_sample_from_probs(const torch::Tensor& probs,
+                                                            const torch::Tensor& uniform_samples,
+                                                            const torch::Tensor& top_k,
+                                                            int64_t top_k_value, bool deterministic);
+FlashInferSamplingResult flashinfer_top_p_sample_from_probs(const torch::Tensor& probs,
+                                                            const torch::Tensor& uniform_samples,
+                                                            const torch::Tensor& top_p,
+                                                            double top_p_value, bool deterministic);
+FlashInferSamplingResult flashinfer_top_k_top_p_sample_from_probs(
+    const torch::Tensor& probs, const torch::Tensor& uniform_samples, const torch::Tensor& top_k,
+    double top_k_value, const torch::Tensor& top_p, double top_p_value, bool deterministic);
+
 // NeoX RoPE with a half-width fp32 cos/sin cache built on the device
 // (rotary_embedding.cu:75-94 builds the same table with LibTorch-CPU ops).
 class RotaryEmbedding {

@@ -30,7 +30,9 @@ def test_backend_module_surface(sb):
     """Loads on CPU too: every reference-named class is exported."""
     for name in ["Req", "Batch", "MHAKVCache", "HipAttnBackend", "RMSNorm", "RotaryEmbedding",
                  "AttentionLayer", "fused_qk_rmsnorm_inplace_3d_strided", "silu_and_mul",
-                 "gelu_and_mul"]:
+                 "gelu_and_mul", "flashinfer_sample_from_probs",
+                 "flashinfer_top_k_sample_from_probs", "flashinfer_top_p_sample_from_probs",
+                 "flashinfer_top_k_top_p_sample_from_probs"]:
         assert hasattr(sb, name), name
     r = sb.Req(3, 10, 25)
     assert (r.table_idx, r.cached_len, r.device_len(), r.extend_len()) == (3, 10, 25, 15)
@@ -372,4 +374,36 @@ def test_residual_modules_match_c_abi(dev, sb, dtype):
             fn(a, inp)
             cfn(b, inp)
             assert torch.equal(a, b)
+    torch.cuda.synchronize()
+
+
+@pytest.mark.gpu
+def test_sampling_functions_match_c_abi(dev, sb):
+    """The reference's sampling API (include/sglang/engine/sampling.h:7-36) as
+    the Sampler calls it (engine.cc:300-345: uniform [32, batch], top_k float32
+    for top-k, int32 for top-k + top-p) gives the C ABI's draws."""
+    from conftest import capi
+    note("sampling functions")
+    g = _gen(dev, 91)
+    B, V = 16, 151936
+    probs = torch.softmax(torch.randn((B, V), device=dev, generator=g) * 3, -1).contiguous()
+    u1 = torch.rand(B, device=dev, generator=g)
+    u = torch.rand((32, B), device=dev, generator=g)
+    k = torch.randint(1, 64, (B,), device=dev, generator=g)
+    tp = torch.rand(B, device=dev, generator=g) * 0.5 + 0.45
+    assert torch.equal(sb.flashinfer_sample_from_probs(probs, u1, False),
+                       capi.sampling_from_probs(probs, u1))
+    a = sb.flashinfer_top_k_sample_from_probs(probs, u, k.float(), 0, False)
+    b = capi.top_k_sampling_from_probs(probs, u, k.float())
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+    a = sb.flashinfer_top_p_sample_from_probs(probs, u, tp, 0.0, False)
+    b = capi.top_p_sampling_from_probs(probs, u, tp)
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+    a = sb.flashinfer_top_k_top_p_sample_from_probs(probs, u, k.int(), 0.0, tp, 0.0, False)
+    b = capi.top_k_top_p_sampling_from_probs(probs, u, k.int(), 0, tp, 0.0)
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+    a = sb.flashinfer_top_k_sample_from_probs(probs, u, None, 5, False)
+    assert bool(a[1].all())
+    with pytest.raises(Exception):
+        sb.flashinfer_top_k_top_p_sample_from_probs(probs, u, k.float(), 0.0, tp, 0.0, False)
     torch.cuda.synchronize()

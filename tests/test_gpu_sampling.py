@@ -1,0 +1,128 @@
+"""GPU parity of the sampling kernels (marked gpu) against the CPU oracle,
+through the C ABI: plain, top-k, top-p and top-k + top-p draws
+(src/engine/sampling.cu:65-194) with the reference's call shapes
+(uniform [32, batch] for the filtered draws, per-row top_k as float32 for
+top-k and int32 for top-k + top-p, engine.cc:300-345).
+
+Bars: on dyadic probabilities (k / 2^24, every partial sum exact in any
+order) samples and success flags are bit-exact. On softmax probabilities
+over the Qwen3 vocabulary the kernels' fp32 sums differ from the oracle's
+exact CDF by their summation error, so a draw may move where u falls that
+close to a boundary: every plain draw s must satisfy
+cdf(s - 1) <= u + 1e-5 and cdf(s) >= u - 1e-5 on the exact CDF, every draw
+is valid (a positive probability; inside the filtered set when accepted),
+and at least 90% of filtered draws equal the oracle's.
+"""
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import capi
+from test_oracle_pins import dyadic_probs
+
+pytestmark = pytest.mark.gpu
+
+QWEN3_VOCAB = 151936
+
+
+def note(msg):
+    print(f"[case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def in_filtered_set(row, s, mode, k, top_p):
+    """Whether index s may be accepted: fewer than k probabilities above it
+    (top-k), their mass below top_p (top-p), or both."""
+    gt = row > row[s]
+    ok = row[s] > 0
+    if mode in ("top_k", "top_k_top_p"):
+        ok &= gt.sum() < k
+    if mode in ("top_p", "top_k_top_p"):
+        ok &= row[gt].astype(np.float64).sum() < top_p
+    return bool(ok)
+
+
+def run_all(oracle, dev, p, u, k, tp, exact):
+    B = p.shape[0]
+    pt = torch.from_numpy(p).to(dev)
+    ut = torch.from_numpy(u).to(dev)
+    kf = torch.from_numpy(k.astype(np.float32)).to(dev)
+    ki = torch.from_numpy(k.astype(np.int32)).to(dev)
+    tpt = torch.from_numpy(tp).to(dev)
+    cases = {
+        "plain": (capi.sampling_from_probs(pt, ut[0].contiguous()),
+                  oracle.sample(p, u[0], "plain")),
+        "top_k": (capi.top_k_sampling_from_probs(pt, ut, kf),
+                  oracle.sample(p, u, "top_k", top_k=k.astype(np.float32))),
+        "top_k scalar": (capi.top_k_sampling_from_probs(pt, ut, None, 20),
+                         oracle.sample(p, u, "top_k", top_k_val=20)),
+        "top_p": (capi.top_p_sampling_from_probs(pt, ut, tpt),
+                  oracle.sample(p, u, "top_p", top_p=tp)),
+        "top_p scalar": (capi.top_p_sampling_from_probs(pt, ut, None, 0.8),
+                         oracle.sample(p, u, "top_p", top_p_val=0.8)),
+        "top_k_top_p": (capi.top_k_top_p_sampling_from_probs(pt, ut, ki, 0, tpt, 0.0),
+                        oracle.sample(p, u, "top_k_top_p", top_k=k.astype(np.int32), top_p=tp)),
+    }
+    torch.cuda.synchronize()
+    for name, (g, (want, want_ok)) in cases.items():
+        got = (g if isinstance(g, torch.Tensor) else g[0]).cpu().numpy()
+        got_ok = None if isinstance(g, torch.Tensor) else g[1].cpu().numpy()
+        assert ((got >= 0) & (got < p.shape[1])).all(), name
+        assert (p[np.arange(B), got] > 0).all(), name
+        if exact:
+            np.testing.assert_array_equal(got, want, err_msg=name)
+            if got_ok is not None:
+                np.testing.assert_array_equal(got_ok, want_ok, err_msg=name)
+        elif name == "plain":
+            for b in range(B):
+                cdf = np.cumsum(p[b].astype(np.float64))
+                lo = cdf[got[b] - 1] if got[b] > 0 else 0.0
+                assert lo <= u[0, b] + 1e-5 and cdf[got[b]] >= u[0, b] - 1e-5, (b, got[b], want[b])
+        else:
+            assert np.mean(got == want) >= 0.9, (name, np.mean(got == want))
+        if got_ok is not None and name != "plain":
+            mode = name.split(" ")[0]
+            for b in np.nonzero(got_ok)[0][:16]:
+                kk = 20 if name == "top_k scalar" else k[b]
+                pp = 0.8 if name == "top_p scalar" else tp[b]
+                assert in_filtered_set(p[b], got[b], mode, kk, pp), (name, b)
+
+
+@pytest.mark.parametrize("batch,d", [(64, QWEN3_VOCAB), (5, 1001), (3, 4096)])
+def test_sampling_dyadic_bit_exact(oracle, dev, batch, d):
+    note(f"sampling dyadic batch={batch} d={d}")
+    rng = np.random.default_rng(60 + d % 97)
+    p = dyadic_probs(rng, batch, d)
+    u = rng.random((32, batch)).astype(np.float32)
+    k = rng.integers(1, 50, batch)
+    tp = rng.uniform(0.3, 0.95, batch).astype(np.float32)
+    run_all(oracle, dev, p, u, k, tp, exact=True)
+
+
+def test_sampling_softmax_probs(oracle, dev):
+    note("sampling from softmax(logits / T), Qwen3 vocabulary")
+    g = torch.Generator(device=dev)
+    g.manual_seed(61)
+    B = 32
+    logits = torch.randn((B, QWEN3_VOCAB), device=dev, generator=g) * 4
+    temp = torch.linspace(0.5, 1.5, B, device=dev).view(B, 1)
+    probs = torch.softmax(logits / temp, -1).contiguous()
+    u = torch.rand((32, B), device=dev, generator=g)
+    rng = np.random.default_rng(62)
+    k = rng.integers(1, 100, B)
+    tp = rng.uniform(0.5, 0.95, B).astype(np.float32)
+    run_all(oracle, dev, probs.cpu().numpy(), u.cpu().numpy(), k, tp, exact=False)
+
+
+def test_sampling_rejects_bad_arguments(dev):
+    note("sampling argument checks")
+    p = torch.full((2, 8), 0.125, device=dev)
+    with pytest.raises(ValueError):
+        capi.sampling_from_probs(p.double(), torch.rand(2, device=dev))
+    with pytest.raises(ValueError):
+        capi.top_k_sampling_from_probs(p, torch.rand(2, device=dev), None, 3)  # needs [rounds, B]
+    with pytest.raises(ValueError):
+        capi.top_k_top_p_sampling_from_probs(p, torch.rand(4, 2, device=dev),
+                                             torch.ones(2, device=dev), 0, None, 0.5)

@@ -491,3 +491,87 @@ def test_act_and_mul_matches_torch(oracle, dtype, act):
     slack = ULP[dtype] * (np.abs(pos) + np.abs(neg)) + 2 * ATOL_T[dtype]
     assert np.all(np.abs(pos - neg - xs) <= slack)
     assert pos[128] == 0.0  # act(0) = 0
+
+
+# ------------------------------------------------------------------ sampling
+# src/engine/sampling.cu:65-194: inverse-CDF draws and rejection rounds.
+
+def dyadic_probs(rng, batch, d, zero_frac=0.2, bits=24):
+    """Rows of probabilities k / 2^bits summing to exactly 1: every partial sum
+    is exact in fp32, whatever the order."""
+    out = np.zeros((batch, d), np.float32)
+    total = 1 << bits
+    for b in range(batch):
+        w = rng.gamma(0.3, size=d) * (rng.random(d) > zero_frac)
+        n = np.floor(w / w.sum() * total).astype(np.int64)
+        n[np.argmax(n)] += total - n.sum()
+        out[b] = (n / total).astype(np.float32)
+    return out
+
+
+def test_sampling_plain_is_inverse_cdf(oracle):
+    rng = np.random.default_rng(50)
+    p = dyadic_probs(rng, 16, 3001)
+    u = rng.random((16,)).astype(np.float32)
+    u[0], u[1] = 0.0, np.nextafter(np.float32(1), np.float32(0))
+    got, _ = oracle.sample(p, u, "plain")
+    for b in range(16):
+        cdf = np.cumsum(p[b].astype(np.float64))
+        want = int(np.searchsorted(cdf, u[b], side="right"))  # first cdf > u
+        assert got[b] == want and p[b, got[b]] > 0
+
+
+def _filtered_set(p, mode, k, top_p):
+    """Indices a filtered draw may accept: fewer than k probabilities above
+    (top-k), mass above below top_p (top-p), or both."""
+    above_n = np.array([(p > x).sum() for x in p])
+    above_m = np.array([p[p > x].astype(np.float64).sum() for x in p])
+    ok = p > 0
+    if mode in ("top_k", "top_k_top_p"):
+        ok &= above_n < k
+    if mode in ("top_p", "top_k_top_p"):
+        ok &= above_m < top_p
+    return ok
+
+
+@pytest.mark.parametrize("mode", ["top_k", "top_p", "top_k_top_p"])
+def test_filtered_sampling_distribution(oracle, mode):
+    """Accepted draws are the renormalised filtered distribution (chi-square),
+    and every accepted index lies in the filtered set."""
+    rng = np.random.default_rng(51)
+    d, n = 12, 40000
+    base = dyadic_probs(rng, 1, d, zero_frac=0.0, bits=20)[0]
+    p = np.tile(base, (n, 1))
+    u = rng.random((32, n)).astype(np.float32)
+    k, tp = 4, 0.7
+    kw = {"top_k": dict(top_k=np.full(n, k, np.float32)), "top_p": dict(top_p_val=tp),
+          "top_k_top_p": dict(top_k=np.full(n, k, np.int32), top_p_val=tp)}[mode]
+    got, ok = oracle.sample(p, u, mode, **kw)
+    assert ok.all()
+    allowed = _filtered_set(base, mode, k, tp)
+    assert allowed[got].all()
+    expect = np.where(allowed, base, 0).astype(np.float64)
+    expect /= expect.sum()
+    counts = np.bincount(got, minlength=d)
+    m = expect > 0
+    chi2 = (((counts[m] - n * expect[m]) ** 2) / (n * expect[m])).sum()
+    assert chi2 < 40.0, (chi2, counts, expect * n)  # dof <= 11; p(chi2 > 40) < 1e-4
+
+
+def test_filtered_sampling_edge_cases(oracle):
+    rng = np.random.default_rng(52)
+    p = dyadic_probs(rng, 3, 257, zero_frac=0.5)
+    u = rng.random((32, 3)).astype(np.float32)
+    # top-k 1 and a tiny top-p both pick the (unique) largest probability
+    for b in range(3):
+        p[b, 7] = 0.0
+        p[b, 7] = np.float32(1.0) - p[b].astype(np.float64).sum()  # keep the sum 1
+    top = p.argmax(1)
+    got, ok = oracle.sample(p, u, "top_k", top_k_val=1)
+    assert ok.all() and (got == top).all()
+    got, ok = oracle.sample(p, u, "top_p", top_p_val=1e-6)
+    assert ok.all() and (got == top).all()
+    # k = vocab accepts the first draw: equals the plain draw with u[0]
+    got, ok = oracle.sample(p, u, "top_k", top_k_val=257)
+    plain, _ = oracle.sample(p, u[0], "plain")
+    assert ok.all() and (got == plain).all()
