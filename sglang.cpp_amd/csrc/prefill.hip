@@ -318,6 +318,7 @@ __device__ __forceinline__ void pv_steps(const LaneAddr& la, const bf16x8_t (&po
 template <int W, bool kPair>
 __global__ void __launch_bounds__(64 * W, 8 / W) paged_prefill_kernel(PrefillArgs a) {
   static_assert(!kPair || W == 8, "pairing splits 8 waves into two SIMD-sharing groups");
+  static_assert(W == 4 || W == 8, "gather lane bases assume 16 | 4 W (row % 16 fixed per lane)");
   constexpr int kGM = kPair ? 16 * W : 32 * W;  // rows per group tile
   const int n_items = gridDim.x;
   const int lin = blockIdx.x;
