@@ -240,6 +240,9 @@ __global__ void __launch_bounds__(128) rope_generic_kernel(
 // --- fused qk-norm + RoPE + KV store ---------------------------------------
 
 // Row jobs per token: [0, Hq) q rows, [Hq, Hq+Hkv) k rows, [Hq+Hkv, Hq+2Hkv) v rows.
+// Loads go out in two waves before any math: the row, slot and position,
+// then (once the position is in) the weight and the cos/sin row, so a lane
+// waits for two memory latencies (measured: 28.0 -> 26.7 us at config 3).
 template <int LPR>
 __global__ void __launch_bounds__(256) fused_qknorm_rope_store_kernel(
     uint16_t* __restrict__ qkv, int64_t qkv_st, uint16_t* __restrict__ k_cache,
@@ -250,6 +253,7 @@ __global__ void __launch_bounds__(256) fused_qknorm_rope_store_kernel(
     bool k_back) {
   constexpr int ROWS = 256 / LPR;
   constexpr int D = LPR * 8;
+  constexpr int HALF = LPR / 2;
   const int lane_in_row = threadIdx.x % LPR;
   const int rows_per_token = hq + 2 * hkv;
   const int64_t job = static_cast<int64_t>(blockIdx.x) * ROWS + threadIdx.x / LPR;
@@ -257,19 +261,56 @@ __global__ void __launch_bounds__(256) fused_qknorm_rope_store_kernel(
   const int64_t t = job / rows_per_token;
   const int r = static_cast<int>(job - t * rows_per_token);
   uint16_t* src = qkv + t * qkv_st + static_cast<int64_t>(r) * D + lane_in_row * 8;
+  const u32x4_t raw = ldg128(src);
   const int64_t slot = out_loc[t];
   if (r >= hq + hkv) {  // v row: raw copy into the cache
     const int h = r - hq - hkv;
-    stg128(v_cache + (slot * hkv + h) * D + lane_in_row * 8, ldg128(src));
+    stg128(v_cache + (slot * hkv + h) * D + lane_in_row * 8, raw);
     return;
   }
-  const bool is_q = r < hq;
-  float x[8];
-  unpack8(ldg128(src), x);
-  const uint16_t* w = is_q ? qw : kw;
-  if (w != nullptr) rmsnorm8<LPR>(x, w, lane_in_row, 1.0f / D, eps);
   const int64_t pos = positions[t];
-  rope8<LPR>(x, cos_cache + pos * (D / 2), sin_cache + pos * (D / 2), lane_in_row);
+  const bool is_q = r < hq;
+  const uint16_t* w = is_q ? qw : kw;
+  u32x4_t wv = {0, 0, 0, 0};
+  if (w != nullptr) wv = ldg128(w + lane_in_row * 8);
+  const bool first = lane_in_row < HALF;
+  const int jj = first ? lane_in_row : lane_in_row - HALF;
+  const float* cr = cos_cache + pos * (D / 2) + jj * 8;
+  const float* sr = sin_cache + pos * (D / 2) + jj * 8;
+  const f32x4_t c0 = *reinterpret_cast<const f32x4_t*>(cr);
+  const f32x4_t c1 = *reinterpret_cast<const f32x4_t*>(cr + 4);
+  const f32x4_t s0 = *reinterpret_cast<const f32x4_t*>(sr);
+  const f32x4_t s1 = *reinterpret_cast<const f32x4_t*>(sr + 4);
+
+  float x[8];
+  unpack8(raw, x);
+  if (w != nullptr) {  // rmsnorm8 with the weight already loaded
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ss += x[i] * x[i];
+    ss = group_sum<LPR>(ss);
+    const float scale = rsqrtf(ss * (1.0f / D) + eps);
+    float wf[8];
+    unpack8(wv, wf);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) x[i] = round_bf16((x[i] * scale) * wf[i]);
+  }
+  // rope8 with the cos/sin row already loaded: the partner half comes from
+  // lane ^ HALF as packed bf16 words (exact, x is bf16-valued).
+  float p[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t wd = pack_bf16x2(x[2 * i], x[2 * i + 1]);
+    uint32_t pw;
+    if constexpr (HALF == 8) pw = dpp_u32<0x128>(wd);  // lane ^ 8 inside the 16-lane row
+    else pw = static_cast<uint32_t>(__shfl_xor(static_cast<int>(wd), HALF, kWave));
+    p[2 * i] = bf16_lo(pw);
+    p[2 * i + 1] = bf16_hi(pw);
+  }
+  const float c[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
+  const float sn[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
+#pragma unroll
+  for (int i = 0; i < 8; ++i) x[i] = first ? (x[i] * c[i] - p[i] * sn[i]) : (x[i] * c[i] + p[i] * sn[i]);
   const u32x4_t packed = pack8(x);
   if (is_q || k_back) stg128(src, packed);
   if (!is_q) {
