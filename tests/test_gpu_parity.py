@@ -452,3 +452,24 @@ def test_prefill_wide_ragged(oracle, dev, hq, hkv, qo, prefix):
     b = wl.make_paged_batch(rng, prefix, [p + q for p, q in zip(prefix, qo)], page_size=16)
     check_prefill(oracle, dev, b, hq, hkv, 32, "prefill 8-wave ragged")
 
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2, 3, 4, 5])
+def test_prefill_random_batches(oracle, dev, seed):
+    """Seeded random ragged batches (lengths, prefixes, head groups, page
+    sizes) across the 4-wave, 8-wave and paired 8-wave launches; the seed
+    picks the shape, so each case names itself."""
+    rng = np.random.default_rng(100 + seed)
+    hq, hkv = [(32, 4), (32, 8), (32, 4), (64, 4), (64, 8), (32, 4)][seed]
+    B = int(rng.integers(1, 4))
+    big = seed % 2 == 0  # long chunks reach the 8-wave paths
+    qo = rng.integers(256 if big else 1, (2600 if big else 700) // max(1, hq // hkv // 4), B)
+    if seed == 2:  # one chunk of 2017..2048 tokens at G = 8: the paired launch
+        B, qo = 1, rng.integers(2017, 2049, 1)
+    prefix = rng.integers(0, 1500, B)
+    page = int(rng.choice([1, 16]))
+    note(f"prefill random seed={seed} hq={hq} hkv={hkv} qo={list(qo)} prefix={list(prefix)} "
+         f"page={page}")
+    b = wl.make_paged_batch(rng, [int(p) for p in prefix], [int(p + q) for p, q in zip(prefix, qo)],
+                            page_size=page)
+    check_prefill(oracle, dev, b, hq, hkv, 200 + seed, f"prefill random {seed}")
