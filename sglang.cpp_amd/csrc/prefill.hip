@@ -454,12 +454,14 @@ __global__ void __launch_bounds__(64 * W, 8 / W) paged_prefill_kernel(PrefillArg
   wait_gathers();
   __syncthreads();
 
-  f32x16_t s_cur[2], s_next[2];
+  // Scores of the current and next tile; the two arrays swap roles every
+  // step (the loop is unrolled by two), so no register copies move them.
+  f32x16_t s_a[2], s_b[2];
   bf16x8_t pop[4];
-  qk_tile<0>(la, qop, s_cur);
+  qk_tile<0>(la, qop, s_a);
   __syncthreads();  // every wave has read K(0) before K(2) overwrites it
 
-  auto step = [&](auto B, int t) {
+  auto step = [&](auto B, int t, f32x16_t(&s_cur)[2], f32x16_t(&s_next)[2]) {
     constexpr int buf = decltype(B)::value;  // t % 2
     if (t + 2 < ntiles) issue_half<W>(klane, ss_bytes, sl_k, tiles[buf].k, wave);
     if (t + 1 < ntiles) issue_half<W>(vlane, ss_bytes, sl_v, tiles[buf ^ 1].v, wave);
@@ -478,16 +480,14 @@ __global__ void __launch_bounds__(64 * W, 8 / W) paged_prefill_kernel(PrefillArg
       pv_steps<buf, 0, 2>(la, pop, vr, rs);
       softmax_exp_half<1>(a, s_cur, rs, pop);
       pv_steps<buf, 2, 4>(la, pop, vr, rs);
-#pragma unroll
-      for (int mb = 0; mb < 2; ++mb) s_cur[mb] = s_next[mb];
     }
     wait_gathers();
     __syncthreads();
   };
   for (int t = 0; t < ntiles; t += 2) {
-    step(std::integral_constant<int, 0>{}, t);
+    step(std::integral_constant<int, 0>{}, t, s_a, s_b);
     if (t + 1 >= ntiles) break;
-    step(std::integral_constant<int, 1>{}, t + 1);
+    step(std::integral_constant<int, 1>{}, t + 1, s_b, s_a);
   }
 
   float l = sum_xor32(rs.l);

@@ -20,17 +20,21 @@
 // and has no effect.
 //
 // MI355X layout: one 1024-thread workgroup (16 waves) per row. The row is
-// cut into blocks of 256 probabilities, one coalesced 16-byte load per lane
-// of a wave; waves take blocks round-robin. A sweep with a threshold
-// leaves in LDS the mass above it of every block (one wave reduction per
-// block) and the row's count above it. A draw scans the block masses
-// across the workgroup (each thread a run of consecutive blocks, then a
-// wave scan and the wave totals through LDS) to the block holding the
-// crossing, and one wave scans that block's 256 probabilities to the first
-// crossing index. A rejection round is one sweep: the sweep that counts the
-// probabilities above the new pivot also gives the next draw its block
-// masses. A vocabulary row (Qwen3: 151,936 x 4 B) comes from HBM on the
-// first sweep and from L2 afterwards.
+// cut into blocks of 1024 probabilities, four coalesced 16-byte loads per
+// lane of a wave; waves take blocks round-robin, two blocks in flight. A
+// sweep with a threshold leaves in LDS the mass above it of every block
+// (one wave reduction per block) and the row's mass and count above it. A
+// draw is wave 0's alone: each lane sums a run of block masses, a DPP wave
+// scan finds the lane whose run crosses u, that lane walks to the crossing
+// block, and the wave scans the block's probabilities in row order to the
+// first crossing index. A rejection round is one sweep: the sweep that
+// counts the probabilities above the new pivot also gives the next draw its
+// block masses. A vocabulary row (Qwen3: 151,936 x 4 B) comes from HBM on
+// the first sweep. That sweep also copies into LDS every probability above
+// 1/31,360 (at most 31,360 of them in a normalised row), so rounds whose
+// pivot clears that threshold sweep the copies instead of the row; when it
+// does not, the next sweep of the row copies what exceeds its pivot, space
+// allowing. Only the crossing block of a draw is read from the row then.
 #include <math.h>
 
 #include "common.h"
@@ -41,8 +45,20 @@ namespace {
 constexpr int kThreads = 1024;
 constexpr int kWaves = kThreads / kWave;
 constexpr int kVec = 4;
-constexpr int kBlock = kWave * kVec;  // probabilities per block
-constexpr int kMaxBlocks = 8192;      // rows up to 2M probabilities (32 KiB of block masses)
+constexpr int kSub = 4;                       // 16-byte loads per lane per block
+constexpr int kSpan = kWave * kVec;           // probabilities per wave load (1 KiB)
+constexpr int kBlock = kSpan * kSub;          // probabilities per block
+constexpr int kMaxBlocks = 2048;              // rows up to 2M probabilities
+// Candidate mode (rows of at most kCandBlocks blocks, 1M probabilities): a
+// sweep of the row also copies the probabilities above a threshold into
+// LDS, grouped by block, and later rounds whose pivot is at or above that
+// threshold sweep those copies instead of the row. The copies share one LDS
+// pool with the block masses, which then need only kCandBlocks entries.
+constexpr int kCandBlocks = 1024;              // one (start, count) word per block
+constexpr int kPool = 36864;                   // 144 KiB
+constexpr int kCandCap = kPool - kCandBlocks;  // 35,840 copies
+static_assert(kPool >= kMaxBlocks, "block masses of the longest rows fit the pool");
+static_assert(kCandCap < 65536 && kBlock < 65536, "segment words hold two 16-bit fields");
 
 struct SampleArgs {
   const float* probs;
@@ -60,187 +76,320 @@ struct SampleArgs {
 };
 
 struct Shared {
-  float blk[kMaxBlocks];  // mass above the current threshold, per block
+  // pool[b], b < nblk: mass above the current threshold of block b.
+  // pool[kCandBlocks + i]: candidate mode's copies, block by block.
+  float pool[kPool];
+  uint32_t seg[kCandBlocks];  // block b's copies: start | count << 16
+  int ncand;                  // copies written (beyond kCandCap: overflow)
   float wave_f[kWaves];
+  float wave_n[kWaves];
   int wave_i[kWaves];
   float wave_run[kWaves];  // draw: mass before the crossing block found by a wave
-  float total;            // row mass above the threshold
-  int count;              // row count above the threshold
-  int blk_star;
+  float total;             // row mass above the threshold
+  int count;               // row count above the threshold
   int sampled;
+  float sampled_p;
 };
-
-__device__ __forceinline__ void load4(const float* row, int e0, int d, bool vec, float (&p)[kVec]) {
-  if (vec && e0 + kVec <= d) {
-    const f32x4_t v = *reinterpret_cast<const f32x4_t*>(row + e0);
-#pragma unroll
-    for (int j = 0; j < kVec; ++j) p[j] = v[j];
-  } else {
-#pragma unroll
-    for (int j = 0; j < kVec; ++j) p[j] = e0 + j < d ? row[e0 + j] : 0.f;
-  }
-}
 
 __device__ __forceinline__ float wave_sum_f(float x) {
   return sum_xor32(sum_xor16(group_sum<16>(x)));
 }
-__device__ __forceinline__ int wave_sum_i(int x) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off, kWave);
+
+// DPP move with a row mask: rows left out of ROW_MASK, and lanes whose
+// source lies outside their row, read 0.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_rows(float x) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, ROW_MASK, 0xF, false));
+}
+
+// Inclusive scan within each row of 16 lanes (DPP row_shr 1, 2, 4, 8).
+__device__ __forceinline__ float row_scan(float x) {
+  x += dpp_rows<0x111, 0xF>(x);
+  x += dpp_rows<0x112, 0xF>(x);
+  x += dpp_rows<0x114, 0xF>(x);
+  x += dpp_rows<0x118, 0xF>(x);
   return x;
 }
 
-// Inclusive scan over the 64 lanes of a wave.
-__device__ __forceinline__ float wave_inclusive_scan(float x, int lane) {
-#pragma unroll
-  for (int off = 1; off < kWave; off <<= 1) {
-    const float y = __shfl_up(x, off, kWave);
-    if (lane >= off) x += y;
-  }
+// Inclusive scan over the 64 lanes: the row scans, then row_bcast:15 adds
+// row r's total to row r + 1 (rows 1 and 3) and row_bcast:31 the first two
+// rows' total to rows 2 and 3.
+__device__ __forceinline__ float wave_scan(float x) {
+  x = row_scan(x);
+  x += dpp_rows<0x142, 0xA>(x);
+  x += dpp_rows<0x143, 0xC>(x);
   return x;
+}
+
+template <typename T>
+__device__ __forceinline__ T read_lane(T x, int l) {
+  return __builtin_bit_cast(T, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), l));
+}
+
+// One block of a row: lane l holds probabilities kSpan s + kVec l + j
+// (s < kSub, j < kVec) of the block; bounds-checked when the block is the
+// row's last or the row is not 16-byte aligned.
+struct BlockVals {
+  f32x4_t v[kSub];
+};
+
+__device__ __forceinline__ void load_block(const float* __restrict__ row, int b, int d, bool full,
+                                           BlockVals& bv) {
+  const int lane = threadIdx.x & 63;
+  const int e0 = b * kBlock + kVec * lane;
+  if (full) {
+#pragma unroll
+    for (int s = 0; s < kSub; ++s) bv.v[s] = *reinterpret_cast<const f32x4_t*>(row + e0 + kSpan * s);
+  } else {
+#pragma unroll
+    for (int s = 0; s < kSub; ++s)
+#pragma unroll
+      for (int j = 0; j < kVec; ++j) {
+        const int e = e0 + kSpan * s + j;
+        bv.v[s][j] = e < d ? row[e] : 0.f;
+      }
+  }
+}
+
+// Row totals from the per-wave mass wm (wave-uniform) and per-lane counts
+// wn: wave sums, then wave 0 adds the 16 wave totals in a fixed DPP order.
+__device__ __forceinline__ void finish_totals(float wm, float wn, Shared& sh) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  wn = wave_sum_f(wn);
+  if (lane == 0) {
+    sh.wave_f[wave] = wm;
+    sh.wave_n[wave] = wn;
+  }
+  __syncthreads();
+  if (wave == 0) {
+    const float t = group_sum<16>(lane < kWaves ? sh.wave_f[lane] : 0.f);
+    const float c = group_sum<16>(lane < kWaves ? sh.wave_n[lane] : 0.f);
+    if (lane == 0) {
+      sh.total = t;
+      sh.count = static_cast<int>(c);
+    }
+  }
+  __syncthreads();
+}
+
+// Mass and count above thr of one block (mass wave-reduced into pool[b],
+// count per lane); kCompact: also the copies above cthr, each lane's after
+// those of lower lanes (a fixed order).
+template <bool kCompact>
+__device__ __forceinline__ void sweep_block(const BlockVals& bv, int b, float thr, float cthr,
+                                            float& wm, float& wn, Shared& sh) {
+  const int lane = threadIdx.x & 63;
+  float m = 0.f, n = 0.f;
+#pragma unroll
+  for (int s = 0; s < kSub; ++s)
+#pragma unroll
+    for (int j = 0; j < kVec; ++j) {
+      const float x = bv.v[s][j];
+      m += x > thr ? x : 0.f;
+      n += x > thr ? 1.f : 0.f;
+    }
+  wn += n;
+  m = wave_sum_f(m);
+  wm += m;
+  if (lane == 0) sh.pool[b] = m;
+  if constexpr (kCompact) {
+    float c = 0.f;
+#pragma unroll
+    for (int s = 0; s < kSub; ++s)
+#pragma unroll
+      for (int j = 0; j < kVec; ++j) c += bv.v[s][j] > cthr ? 1.f : 0.f;
+    const float incl = wave_scan(c);
+    const int tot = static_cast<int>(read_lane(incl, 63));
+    int base = 0;
+    if (tot > 0) {
+      if (lane == 0) base = atomicAdd(&sh.ncand, tot);
+      base = read_lane(base, 0);
+      if (base + tot <= kCandCap) {
+        int pos = kCandBlocks + base + static_cast<int>(incl - c);
+#pragma unroll
+        for (int s = 0; s < kSub; ++s)
+#pragma unroll
+          for (int j = 0; j < kVec; ++j)
+            if (bv.v[s][j] > cthr) sh.pool[pos++] = bv.v[s][j];
+      }
+    }
+    if (lane == 0) sh.seg[b] = static_cast<uint32_t>(base) | static_cast<uint32_t>(tot) << 16;
+  }
 }
 
 // Block masses, row mass and row count of the probabilities above thr.
-__device__ void sweep(const float* row, int d, bool vec, float thr, Shared& sh) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+// kCompact: also copy the probabilities above cthr (the caller has zeroed
+// sh.ncand; an overflow shows as sh.ncand > kCandCap). Waves take blocks
+// round-robin, two blocks (8 loads per lane) in flight.
+template <bool kCompact>
+__device__ __forceinline__ void sweep(const float* __restrict__ row, int d, bool vec, float thr,
+                                      float cthr, Shared& sh) {
+  const int wave = threadIdx.x >> 6;
   const int nblk = (d + kBlock - 1) / kBlock;
-  float wm = 0.f;
-  int wn = 0;
+  const int nfull = vec ? d / kBlock : 0;  // blocks loaded without bounds checks
+  float wm = 0.f, wn = 0.f;
   __syncthreads();  // the previous readers of sh are done
-  // Four blocks per iteration: their loads are in flight together.
-  constexpr int kUnroll = 4;
-  for (int b = wave; b < nblk; b += kWaves * kUnroll) {
-    float p[kUnroll][kVec];
-#pragma unroll
-    for (int x = 0; x < kUnroll; ++x) {
-      const int bx = b + x * kWaves;
-      if (bx < nblk) load4(row, bx * kBlock + lane * kVec, d, vec, p[x]);
-    }
-#pragma unroll
-    for (int x = 0; x < kUnroll; ++x) {
-      const int bx = b + x * kWaves;
-      if (bx >= nblk) break;
-      float m = 0.f;
-      int n = 0;
-#pragma unroll
-      for (int j = 0; j < kVec; ++j)
-        if (p[x][j] > thr) {
-          m += p[x][j];
-          ++n;
-        }
-      m = wave_sum_f(m);
-      wn += n;
-      wm += m;
-      if (lane == 0) sh.blk[bx] = m;
-    }
+  int b = wave;
+  for (; b + kWaves < nfull; b += 2 * kWaves) {
+    BlockVals x0, x1;
+    load_block(row, b, d, true, x0);
+    load_block(row, b + kWaves, d, true, x1);
+    sweep_block<kCompact>(x0, b, thr, cthr, wm, wn, sh);
+    sweep_block<kCompact>(x1, b + kWaves, thr, cthr, wm, wn, sh);
   }
-  wn = wave_sum_i(wn);
-  if (lane == 0) {
-    sh.wave_f[wave] = wm;
-    sh.wave_i[wave] = wn;
+  for (; b < nblk; b += kWaves) {
+    BlockVals x0;
+    load_block(row, b, d, b < nfull, x0);
+    sweep_block<kCompact>(x0, b, thr, cthr, wm, wn, sh);
   }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    float t = 0.f;
-    int c = 0;
-    for (int w = 0; w < kWaves; ++w) {
-      t += sh.wave_f[w];
-      c += sh.wave_i[w];
+  finish_totals(wm, wn, sh);
+}
+
+// The same sweep over the copies: each group of 16 lanes takes one block
+// (wave w, group g: blocks 4 w + g, 4 w + g + 64, ...) and its lanes the
+// block's copies.
+__device__ __forceinline__ void sweep_cand(int d, float thr, Shared& sh) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int sub = lane & 15;
+  const int nblk = (d + kBlock - 1) / kBlock;
+  float wm = 0.f, wn = 0.f;
+  // No leading barrier: only the draw, which ends with one, read the
+  // masses since the last sweep.
+  for (int b0 = 4 * wave; b0 < nblk; b0 += 4 * kWaves) {
+    const int b = b0 + (lane >> 4);
+    const uint32_t sg = b < nblk ? sh.seg[b] : 0u;
+    const int start = static_cast<int>(sg & 0xFFFF), n = static_cast<int>(sg >> 16);
+    float m = 0.f;
+    for (int i = sub; i < n; i += 16) {
+      const float x = sh.pool[kCandBlocks + start + i];
+      m += x > thr ? x : 0.f;
+      wn += x > thr ? 1.f : 0.f;
     }
-    sh.total = t;
-    sh.count = c;
+    m = group_sum<16>(m);
+    if (b < nblk && sub == 0) sh.pool[b] = m;
+    // wave-uniform partial of the four blocks, in group order
+    wm += read_lane(m, 0) + read_lane(m, 16) + read_lane(m, 32) + read_lane(m, 48);
   }
-  __syncthreads();
+  finish_totals(wm, wn, sh);
 }
 
 // The inverse-CDF draw over the probabilities above thr with target u,
-// from the block masses of the last sweep with the same threshold.
-__device__ int draw(const float* row, int d, bool vec, float thr, float u, Shared& sh) {
+// from the block masses of the last sweep with the same threshold, by wave
+// 0 alone (one barrier): lane l sums its run of block masses, a wave scan
+// finds the first lane whose run crosses u, that lane walks its run to the
+// crossing block, and the wave scans that block. Leaves the index in
+// sh.sampled and its probability in sh.sampled_p.
+__device__ __forceinline__ void draw(const float* __restrict__ row, int d, bool vec, float thr,
+                                     float u, Shared& sh) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int nblk = (d + kBlock - 1) / kBlock;
-  // Thread t owns blocks [t G, (t + 1) G).
-  const int G = (nblk + kThreads - 1) / kThreads;
-  const int b0 = min(nblk, static_cast<int>(threadIdx.x) * G), b1 = min(nblk, b0 + G);
-  float own = 0.f;
-  for (int b = b0; b < b1; ++b) own += sh.blk[b];
-  const float incl = wave_inclusive_scan(own, lane);
-  if (threadIdx.x == 0) {
-    sh.blk_star = nblk;
-    sh.sampled = d - 1;
-  }
-  if (lane == 63) sh.wave_f[wave] = incl;
-  __syncthreads();
-  float before = 0.f;
-  for (int w = 0; w < wave; ++w) before += sh.wave_f[w];
-  // The first thread whose run crosses u walks its run to the crossing block.
-  float run = before + (incl - own);
-  bool cross = run + own > u;
-  const uint64_t ballot = __ballot(cross);
-  const bool first_in_wave = cross && lane == __builtin_ctzll(ballot);
-  if (first_in_wave) {
-    int bs = b1 - 1;
-    for (int b = b0; b < b1; ++b) {
-      if (run + sh.blk[b] > u) {
-        bs = b;
-        break;
+  if (wave == 0) {
+    const int per = (nblk + kWave - 1) / kWave;
+    const int b0 = min(nblk, lane * per), b1 = min(nblk, b0 + per);
+    float own = 0.f;
+    for (int b = b0; b < b1; ++b) own += sh.pool[b];
+    const float incl = wave_scan(own);
+    const uint64_t cross = __ballot(incl > u);
+    int bs = nblk;
+    float base = 0.f;
+    if (cross) {
+      const int L = __builtin_ctzll(cross);
+      float run = incl - own;
+      int b = b1 - 1;
+      if (lane == L) {
+        for (int c = b0; c < b1; ++c) {
+          if (run + sh.pool[c] > u) {
+            b = c;
+            break;
+          }
+          run += sh.pool[c];
+        }
       }
-      run += sh.blk[b];
+      bs = read_lane(b, L);
+      base = read_lane(run, L);  // mass before block bs
     }
-    sh.wave_i[wave] = bs;
-    sh.wave_run[wave] = run;  // mass before block bs
-  } else if (lane == 0 && ballot == 0) {
-    sh.wave_i[wave] = nblk;
-  }
-  __syncthreads();
-  int bs = nblk;
-  float base = 0.f;
-  for (int w = 0; w < kWaves; ++w)
-    if (sh.wave_i[w] < nblk) {
-      bs = sh.wave_i[w];
-      base = sh.wave_run[w];
-      break;
-    }
-  // One wave scans the crossing block.
-  if (bs < nblk && wave == 0) {
-    const int e0 = bs * kBlock + lane * kVec;
-    float p[kVec], m[kVec];
-    load4(row, e0, d, vec, p);
-    float local = 0.f;
-#pragma unroll
-    for (int j = 0; j < kVec; ++j) {
-      m[j] = p[j] > thr ? p[j] : 0.f;
-      local += m[j];
-    }
-    const float cincl = wave_inclusive_scan(local, lane);
-    float cdf = base + (cincl - local);
     int first = d, last_valid = -1;
+    float first_p = 0.f, last_p = 0.f;
+    if (bs < nblk) {
+      // Lane l scans the block's probabilities [16 l, 16 l + 16) in row order.
+      constexpr int kPer = kBlock / kWave;
+      const int e0 = bs * kBlock + kPer * lane;
+      float p[kPer];
+      if (vec && e0 + kPer <= d) {
 #pragma unroll
-    for (int j = 0; j < kVec; ++j) {
-      cdf += m[j];
-      const bool valid = p[j] > thr && e0 + j < d;
-      if (valid) last_valid = e0 + j;
-      if (valid && cdf > u && first == d) first = e0 + j;
-    }
+        for (int s = 0; s < kPer / 4; ++s) {
+          const f32x4_t v = *reinterpret_cast<const f32x4_t*>(row + e0 + 4 * s);
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-      first = min(first, __shfl_xor(first, off, kWave));
-      last_valid = max(last_valid, __shfl_xor(last_valid, off, kWave));
+          for (int j = 0; j < 4; ++j) p[4 * s + j] = v[j];
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) p[i] = e0 + i < d ? row[e0 + i] : 0.f;
+      }
+      float local = 0.f;
+#pragma unroll
+      for (int i = 0; i < kPer; ++i) local += p[i] > thr ? p[i] : 0.f;
+      const float cincl = wave_scan(local);
+      float cdf = base + (cincl - local);
+#pragma unroll
+      for (int i = 0; i < kPer; ++i) {
+        const bool valid = p[i] > thr && e0 + i < d;
+        cdf += valid ? p[i] : 0.f;
+        if (valid) {
+          last_valid = e0 + i;
+          last_p = p[i];
+        }
+        if (valid && cdf > u && first == d) {
+          first = e0 + i;
+          first_p = p[i];
+        }
+      }
     }
-    // Rounding inside the block may miss u: then its last candidate.
-    if (lane == 0) sh.sampled = first < d ? first : (last_valid >= 0 ? last_valid : d - 1);
+    // The first crossing (lowest lane: lanes run in row order), else
+    // (rounding inside the block missed u) the block's last candidate,
+    // else d - 1.
+    const uint64_t has_first = __ballot(first < d);
+    const uint64_t has_last = __ballot(last_valid >= 0);
+    if (has_first) {
+      if (lane == __builtin_ctzll(has_first)) {
+        sh.sampled = first;
+        sh.sampled_p = first_p;
+      }
+    } else if (has_last) {
+      if (lane == 63 - __builtin_clzll(has_last)) {
+        sh.sampled = last_valid;
+        sh.sampled_p = last_p;
+      }
+    } else if (lane == 0) {
+      sh.sampled = d - 1;
+      sh.sampled_p = row[d - 1];
+    }
   }
   __syncthreads();
-  return sh.sampled;
 }
 
 __global__ void __launch_bounds__(kThreads) sampling_kernel(SampleArgs a) {
   __shared__ Shared sh;
   const int row_id = blockIdx.x;
-  const float* row = a.probs + static_cast<int64_t>(row_id) * a.d;
-  sweep(row, a.d, a.vec, 0.f, sh);
+  const float* __restrict__ row = a.probs + static_cast<int64_t>(row_id) * a.d;
+  const bool cand_ok = a.mode != 0 && (a.d + kBlock - 1) / kBlock <= kCandBlocks;
+  // The first sweep already copies the probabilities above cand_thr: at
+  // most 1 / cand_thr of them in a normalised row, so any pivot at or above
+  // cand_thr is served from LDS.
+  float cand_thr = 1.f / static_cast<float>(kCandCap - kCandCap / 8);
+  bool cand = false;  // the copies hold every probability above cand_thr
+  float u = a.uniform[row_id];
+  if (cand_ok) {
+    if (threadIdx.x == 0) sh.ncand = 0;
+    sweep<true>(row, a.d, a.vec, 0.f, cand_thr, sh);
+    cand = sh.ncand <= kCandCap;
+  } else {
+    sweep<false>(row, a.d, a.vec, 0.f, 0.f, sh);
+  }
   if (a.mode == 0) {
-    const int s = draw(row, a.d, a.vec, 0.f, a.uniform[row_id], sh);
-    if (threadIdx.x == 0) a.out[row_id] = s;
+    draw(row, a.d, a.vec, 0.f, u, sh);
+    if (threadIdx.x == 0) a.out[row_id] = sh.sampled;
     return;
   }
   int k = a.top_k_val;
@@ -251,12 +400,27 @@ __global__ void __launch_bounds__(kThreads) sampling_kernel(SampleArgs a) {
   int sampled = a.d - 1;
   bool accepted = false;
   for (int r = 0; r < a.rounds; ++r) {
-    const float u = a.uniform[static_cast<int64_t>(r) * a.batch + row_id] * q;
-    sampled = draw(row, a.d, a.vec, pivot, u, sh);
-    const float ps = row[sampled];
+    // The next round's uniform is loaded while this round runs.
+    const float u_next =
+        r + 1 < a.rounds ? a.uniform[static_cast<int64_t>(r + 1) * a.batch + row_id] : 0.f;
+    draw(row, a.d, a.vec, pivot, u * q, sh);
+    sampled = sh.sampled;
+    const float ps = sh.sampled_p;
     if (ps > pivot) {
+      // Masses above the new pivot: from the copies when they cover it,
+      // else from the row, copying what exceeds the pivot when no copies
+      // are held (they stay unused if they overflow).
       pivot = ps;
-      sweep(row, a.d, a.vec, pivot, sh);  // masses above the new pivot
+      if (cand && pivot >= cand_thr) {
+        sweep_cand(a.d, pivot, sh);
+      } else if (!cand && cand_ok) {
+        if (threadIdx.x == 0) sh.ncand = 0;
+        sweep<true>(row, a.d, a.vec, pivot, pivot, sh);
+        cand = sh.ncand <= kCandCap;
+        cand_thr = pivot;
+      } else {
+        sweep<false>(row, a.d, a.vec, pivot, 0.f, sh);
+      }
     }
     q = sh.total;
     const int count = sh.count;
@@ -264,6 +428,7 @@ __global__ void __launch_bounds__(kThreads) sampling_kernel(SampleArgs a) {
     else if (a.mode == 2) accepted = q < top_p;
     else accepted = count < k && q < top_p;
     if (accepted) break;
+    u = u_next;
   }
   if (threadIdx.x == 0) {
     a.out[row_id] = sampled;

@@ -90,7 +90,9 @@ def run_all(oracle, dev, p, u, k, tp, exact):
                 assert in_filtered_set(p[b], got[b], mode, kk, pp), (name, b)
 
 
-@pytest.mark.parametrize("batch,d", [(64, QWEN3_VOCAB), (5, 1001), (3, 4096)])
+@pytest.mark.parametrize("batch,d", [(64, QWEN3_VOCAB), (5, 1001), (3, 4096),
+                                     (4, 150001),    # odd length: bounds-checked loads
+                                     (2, 1 << 21)])  # longest rows (2,048 blocks, no LDS copies)
 def test_sampling_dyadic_bit_exact(oracle, dev, batch, d):
     note(f"sampling dyadic batch={batch} d={d}")
     rng = np.random.default_rng(60 + d % 97)
@@ -126,3 +128,34 @@ def test_sampling_rejects_bad_arguments(dev):
     with pytest.raises(ValueError):
         capi.top_k_top_p_sampling_from_probs(p, torch.rand(4, 2, device=dev),
                                              torch.ones(2, device=dev), 0, None, 0.5)
+    # rows longer than 2^21 probabilities are not supported
+    big = torch.full((1, (1 << 21) + 1), 1.0 / ((1 << 21) + 1), device=dev)
+    with pytest.raises(capi.SglError):
+        capi.sampling_from_probs(big, torch.rand(1, device=dev))
+
+
+def test_sampling_candidate_overflow(oracle, dev):
+    """Rows whose mass exceeds 1 (k / 2^20, 40,000 entries in [2^-13, 2^-12)
+    plus a tail; every partial sum still exact in fp32): the first rejection
+    round expects few candidates above the pivot (q = 1 in round 0), finds
+    more than LDS holds and falls back to sweeping the row; later rounds may
+    switch to the candidates. Bit-exact against the oracle."""
+    note("sampling: candidate overflow fallback, unnormalised dyadic rows")
+    rng = np.random.default_rng(63)
+    B, d = 8, QWEN3_VOCAB
+    n = np.zeros((B, d), np.int64)
+    for b in range(B):
+        pos = rng.permutation(d)
+        n[b, pos[:40000]] = rng.integers(128, 256, 40000)
+        n[b, pos[40000:60000]] = rng.integers(0, 16, 20000)
+    p = (n / float(1 << 20)).astype(np.float32)
+    u = rng.random((32, B)).astype(np.float32)
+    k = np.full(B, 3)
+    tp = np.full(B, 0.5, np.float32)
+    pt = torch.from_numpy(p).to(dev)
+    ut = torch.from_numpy(u).to(dev)
+    got, ok = capi.top_k_sampling_from_probs(pt, ut, torch.from_numpy(k.astype(np.float32)).to(dev))
+    torch.cuda.synchronize()
+    want, want_ok = oracle.sample(p, u, "top_k", top_k=k.astype(np.float32))
+    np.testing.assert_array_equal(got.cpu().numpy(), want)
+    np.testing.assert_array_equal(ok.cpu().numpy(), want_ok)
