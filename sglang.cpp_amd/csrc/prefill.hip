@@ -373,18 +373,6 @@ __global__ void __launch_bounds__(64 * W, 8 / W) paged_prefill_kernel(PrefillArg
   const int qhead = h * G + (row_ok ? prow - (prow / G) * G : 0);
   const int allow = row_ok ? qtok + off : kv_len - 1;  // last visible kv token
 
-  // Q^T operand: q[qtok][qhead][16 s + 8 hl .. +8], s < 8.
-  bf16x8_t qop[8];
-  {
-    const uint16_t* qp =
-        a.q + static_cast<int64_t>(qo_beg + qtok) * a.q_st + static_cast<int64_t>(qhead) * a.q_sh;
-#pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      u32x4_t v = row_ok ? ldg128(qp + 16 * s + 8 * hl) : u32x4_t{0, 0, 0, 0};
-      qop[s] = as_bf16x8(v);
-    }
-  }
-
   // kv tiles a group needs: up to its last row's visible token. The
   // workgroup gathers group 0's range, which contains group 1's.
   auto tiles_for = [&](int r0) {
@@ -444,13 +432,30 @@ __global__ void __launch_bounds__(64 * W, 8 / W) paged_prefill_kernel(PrefillArg
   // tiles: during iteration t the gathers of K(t + 2) and V(t + 1) are in
   // flight. Tile j's K and V use buffer j % 2. Slot indices of tile t + 2
   // serve K(t + 2) now and V(t + 2) in the next iteration.
+  // The slots of tiles 0 and 1 are waited for together before any gather
+  // is issued (a gather between them would make the wait for the later
+  // slots wait for the gather too: loads complete in order).
   int32_t sl_k[16 / W], sl_v[16 / W];
-  load_slots<W>(idx, 0, kv_len, sl_v);
-  issue_half<W>(klane, ss_bytes, sl_v, tiles[0].k, wave);
-  issue_half<W>(vlane, ss_bytes, sl_v, tiles[0].v, wave);
+  load_slots<W>(idx, 0, kv_len, sl_k);
   load_slots<W>(idx, kBN, kv_len, sl_v);
+  wait_gathers();
+  issue_half<W>(klane, ss_bytes, sl_k, tiles[0].k, wave);
+  issue_half<W>(vlane, ss_bytes, sl_k, tiles[0].v, wave);
   issue_half<W>(klane, ss_bytes, sl_v, tiles[1].k, wave);
   load_slots<W>(idx, 2 * kBN, kv_len, sl_k);
+  // Q^T operand: q[qtok][qhead][16 s + 8 hl .. +8], s < 8. Loaded after
+  // the first gathers are issued: loads complete in order, so Q issued
+  // earlier would delay the slot indices the gathers wait for.
+  bf16x8_t qop[8];
+  {
+    const uint16_t* qp =
+        a.q + static_cast<int64_t>(qo_beg + qtok) * a.q_st + static_cast<int64_t>(qhead) * a.q_sh;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      u32x4_t v = row_ok ? ldg128(qp + 16 * s + 8 * hl) : u32x4_t{0, 0, 0, 0};
+      qop[s] = as_bf16x8(v);
+    }
+  }
   wait_gathers();
   __syncthreads();
 
