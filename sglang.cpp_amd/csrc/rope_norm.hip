@@ -240,82 +240,109 @@ __global__ void __launch_bounds__(128) rope_generic_kernel(
 // --- fused qk-norm + RoPE + KV store ---------------------------------------
 
 // Row jobs per token: [0, Hq) q rows, [Hq, Hq+Hkv) k rows, [Hq+Hkv, Hq+2Hkv) v rows.
-// Loads go out in two waves before any math: the row, slot and position,
-// then (once the position is in) the weight and the cos/sin row, so a lane
-// waits for two memory latencies (measured: 28.0 -> 26.7 us at config 3).
+// blocks_per_token consecutive blocks cover the rows of kFusedTokensPerBlock
+// consecutive tokens (the last block's spare rows idle), so the token index
+// is one scalar division; a thread takes the same row of each of those
+// tokens. Loads go out in two waves before any math: every token's row,
+// slot and position, then (once the positions are in) the weight and the
+// cos/sin rows, so a lane waits for two memory latencies for all its rows
+// (measured at config 3: 28.0 -> 26.7 us for the two waves, 25.9 -> 24.9 us
+// for the scalar token index and one rounding per pair, 24.9 -> 23.3 us for
+// two tokens per thread; four measured slower).
+constexpr int kFusedTokensPerBlock = 2;
+
 template <int LPR>
 __global__ void __launch_bounds__(256) fused_qknorm_rope_store_kernel(
     uint16_t* __restrict__ qkv, int64_t qkv_st, uint16_t* __restrict__ k_cache,
     uint16_t* __restrict__ v_cache, const uint16_t* __restrict__ qw,
     const uint16_t* __restrict__ kw, const float* __restrict__ cos_cache,
     const float* __restrict__ sin_cache, const int32_t* __restrict__ positions,
-    const int32_t* __restrict__ out_loc, int64_t num_tokens, int hq, int hkv, float eps,
-    bool k_back) {
+    const int32_t* __restrict__ out_loc, int hq, int hkv, int blocks_per_token, float eps,
+    bool k_back, int64_t num_tokens) {
   constexpr int ROWS = 256 / LPR;
   constexpr int D = LPR * 8;
   constexpr int HALF = LPR / 2;
+  constexpr int NT = kFusedTokensPerBlock;
   const int lane_in_row = threadIdx.x % LPR;
   const int rows_per_token = hq + 2 * hkv;
-  const int64_t job = static_cast<int64_t>(blockIdx.x) * ROWS + threadIdx.x / LPR;
-  if (job >= num_tokens * rows_per_token) return;
-  const int64_t t = job / rows_per_token;
-  const int r = static_cast<int>(job - t * rows_per_token);
-  uint16_t* src = qkv + t * qkv_st + static_cast<int64_t>(r) * D + lane_in_row * 8;
-  const u32x4_t raw = ldg128(src);
-  const int64_t slot = out_loc[t];
-  if (r >= hq + hkv) {  // v row: raw copy into the cache
-    const int h = r - hq - hkv;
-    stg128(v_cache + (slot * hkv + h) * D + lane_in_row * 8, raw);
-    return;
-  }
-  const int64_t pos = positions[t];
+  const int64_t tb = blockIdx.x / static_cast<uint32_t>(blocks_per_token);
+  const int r = static_cast<int>(blockIdx.x - tb * blocks_per_token) * ROWS + threadIdx.x / LPR;
+  if (r >= rows_per_token) return;
+  const bool is_v = r >= hq + hkv;
   const bool is_q = r < hq;
   const uint16_t* w = is_q ? qw : kw;
+  u32x4_t raw[NT];
+  int64_t slot[NT], pos[NT];
+  uint16_t* src[NT];
+#pragma unroll
+  for (int k = 0; k < NT; ++k) {
+    const int64_t t = min(tb * NT + k, num_tokens - 1);
+    src[k] = qkv + t * qkv_st + static_cast<int64_t>(r) * D + lane_in_row * 8;
+    raw[k] = ldg128(src[k]);
+    slot[k] = out_loc[t];
+    pos[k] = positions[t];
+  }
+  if (is_v) {  // v row: raw copy into the cache
+    const int h = r - hq - hkv;
+#pragma unroll
+    for (int k = 0; k < NT; ++k)
+      if (tb * NT + k < num_tokens) stg128(v_cache + (slot[k] * hkv + h) * D + lane_in_row * 8, raw[k]);
+    return;
+  }
   u32x4_t wv = {0, 0, 0, 0};
   if (w != nullptr) wv = ldg128(w + lane_in_row * 8);
   const bool first = lane_in_row < HALF;
   const int jj = first ? lane_in_row : lane_in_row - HALF;
-  const float* cr = cos_cache + pos * (D / 2) + jj * 8;
-  const float* sr = sin_cache + pos * (D / 2) + jj * 8;
-  const f32x4_t c0 = *reinterpret_cast<const f32x4_t*>(cr);
-  const f32x4_t c1 = *reinterpret_cast<const f32x4_t*>(cr + 4);
-  const f32x4_t s0 = *reinterpret_cast<const f32x4_t*>(sr);
-  const f32x4_t s1 = *reinterpret_cast<const f32x4_t*>(sr + 4);
-
-  float x[8];
-  unpack8(raw, x);
-  if (w != nullptr) {  // rmsnorm8 with the weight already loaded
-    float ss = 0.f;
+  f32x4_t c0[NT], c1[NT], s0[NT], s1[NT];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) ss += x[i] * x[i];
-    ss = group_sum<LPR>(ss);
-    const float scale = rsqrtf(ss * (1.0f / D) + eps);
-    float wf[8];
-    unpack8(wv, wf);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) x[i] = round_bf16((x[i] * scale) * wf[i]);
+  for (int k = 0; k < NT; ++k) {
+    const float* cr = cos_cache + pos[k] * (D / 2) + jj * 8;
+    const float* sr = sin_cache + pos[k] * (D / 2) + jj * 8;
+    c0[k] = *reinterpret_cast<const f32x4_t*>(cr);
+    c1[k] = *reinterpret_cast<const f32x4_t*>(cr + 4);
+    s0[k] = *reinterpret_cast<const f32x4_t*>(sr);
+    s1[k] = *reinterpret_cast<const f32x4_t*>(sr + 4);
   }
-  // rope8 with the cos/sin row already loaded: the partner half comes from
-  // lane ^ HALF as packed bf16 words (exact, x is bf16-valued).
-  float p[8];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t wd = pack_bf16x2(x[2 * i], x[2 * i + 1]);
-    uint32_t pw;
-    if constexpr (HALF == 8) pw = dpp_u32<0x128>(wd);  // lane ^ 8 inside the 16-lane row
-    else pw = static_cast<uint32_t>(__shfl_xor(static_cast<int>(wd), HALF, kWave));
-    p[2 * i] = bf16_lo(pw);
-    p[2 * i + 1] = bf16_hi(pw);
-  }
-  const float c[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
-  const float sn[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
+  for (int k = 0; k < NT; ++k) {
+    float x[8];
+    unpack8(raw[k], x);
+    u32x4_t words = raw[k];
+    if (w != nullptr) {
+      float ss = 0.f;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) x[i] = first ? (x[i] * c[i] - p[i] * sn[i]) : (x[i] * c[i] + p[i] * sn[i]);
-  const u32x4_t packed = pack8(x);
-  if (is_q || k_back) stg128(src, packed);
-  if (!is_q) {
-    const int h = r - hq;
-    stg128(k_cache + (slot * hkv + h) * D + lane_in_row * 8, packed);
+      for (int i = 0; i < 8; ++i) ss += x[i] * x[i];
+      ss = group_sum<LPR>(ss);
+      const float scale = rsqrtf(ss * (1.0f / D) + eps);
+      float wf[8];
+      unpack8(wv, wf);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        words[i] = pack_bf16x2((x[2 * i] * scale) * wf[2 * i], (x[2 * i + 1] * scale) * wf[2 * i + 1]);
+      unpack8(words, x);
+    }
+    float p[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t wd = words[i];
+      uint32_t pw;
+      if constexpr (HALF == 8) pw = dpp_u32<0x128>(wd);
+      else pw = static_cast<uint32_t>(__shfl_xor(static_cast<int>(wd), HALF, kWave));
+      p[2 * i] = bf16_lo(pw);
+      p[2 * i + 1] = bf16_hi(pw);
+    }
+    const float c[8] = {c0[k][0], c0[k][1], c0[k][2], c0[k][3], c1[k][0], c1[k][1], c1[k][2], c1[k][3]};
+    const float sn[8] = {s0[k][0], s0[k][1], s0[k][2], s0[k][3], s1[k][0], s1[k][1], s1[k][2], s1[k][3]};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) x[i] = first ? (x[i] * c[i] - p[i] * sn[i]) : (x[i] * c[i] + p[i] * sn[i]);
+    const u32x4_t packed = pack8(x);
+    if (tb * NT + k < num_tokens) {
+      if (is_q || k_back) stg128(src[k], packed);
+      if (!is_q) {
+        const int h = r - hq;
+        stg128(k_cache + (slot[k] * hkv + h) * D + lane_in_row * 8, packed);
+      }
+    }
   }
 }
 
@@ -443,19 +470,23 @@ extern "C" int sgl_fused_qknorm_rope_store(void* qkv, int64_t qkv_stride_token, 
       !aligned16(v_cache) || !aligned16(cos_cache) || !aligned16(sin_cache) ||
       (q_weight && (!aligned16(q_weight) || !aligned16(k_weight))))
     return SGL_ERR_ALIGNMENT;
-  const int64_t jobs = num_tokens * rows;
   hipStream_t s = static_cast<hipStream_t>(stream);
   auto* base = static_cast<uint16_t*>(qkv);
   auto* kc = static_cast<uint16_t*>(k_cache);
   auto* vc = static_cast<uint16_t*>(v_cache);
   auto* qw = static_cast<const uint16_t*>(q_weight);
   auto* kw = static_cast<const uint16_t*>(k_weight);
-#define SGL_FUSED_CASE(LPR_)                                                                  \
-  hipLaunchKernelGGL(fused_qknorm_rope_store_kernel<LPR_>, dim3(blocks_for(jobs, 256 / LPR_)), \
-                     dim3(256), 0, s, base, qkv_stride_token, kc, vc, qw, kw, cos_cache,      \
-                     sin_cache, positions, out_loc, num_tokens, num_qo_heads, num_kv_heads,   \
-                     eps, (flags & SGL_FUSED_NO_K_WRITEBACK) == 0);                           \
-  return launch_status();
+#define SGL_FUSED_CASE(LPR_)                                                                   \
+  {                                                                                            \
+    const int64_t bpt = blocks_for(rows, 256 / LPR_);                                          \
+    if (num_tokens * bpt > 0x7fffffff) return SGL_ERR_UNSUPPORTED;                             \
+    hipLaunchKernelGGL(fused_qknorm_rope_store_kernel<LPR_>, dim3((num_tokens + kFusedTokensPerBlock - 1) / kFusedTokensPerBlock * bpt), \
+                       dim3(256), \
+                       0, s, base, qkv_stride_token, kc, vc, qw, kw, cos_cache, sin_cache,      \
+                       positions, out_loc, num_qo_heads, num_kv_heads, static_cast<int>(bpt),   \
+                       eps, (flags & SGL_FUSED_NO_K_WRITEBACK) == 0, num_tokens);               \
+    return launch_status();                                                                    \
+  }
   switch (head_dim) {
     case 64: SGL_FUSED_CASE(8)
     case 128: SGL_FUSED_CASE(16)
