@@ -314,7 +314,9 @@ int sgl_gelu_and_mul(void* out, const void* input, int64_t tokens, int64_t d,
  * uniform u is the first index i with probs[i] > 0 whose running sum of
  * such probabilities exceeds u (d - 1 if rounding leaves none). uniform is
  * fp32 [batch_size]. deterministic is accepted for the reference's
- * signature; sums here always run in a fixed order.
+ * signature; sums here always run in a fixed order. Rows of up to 2^21
+ * probabilities (SGL_ERR_UNSUPPORTED beyond). One 1024-thread workgroup
+ * per row, about 148 KiB of LDS; nothing is allocated.
  * Replaces: flashinfer_sample_from_probs (src/engine/sampling.cu:65-84).
  */
 int sgl_sampling_from_probs(const float* probs, const float* uniform, int32_t* out,
