@@ -197,7 +197,8 @@ def _fused_inputs(dev, T, hq, hkv, d, seed, slots=None):
 
 
 @pytest.mark.parametrize("k_back", [True, False])
-@pytest.mark.parametrize("T,hq,hkv,d", [(8192, 16, 8, 128), (100, 32, 4, 128), (77, 8, 2, 64)])
+@pytest.mark.parametrize("T,hq,hkv,d", [(8192, 16, 8, 128), (100, 32, 4, 128), (77, 8, 2, 64),
+                                      (1, 16, 8, 128), (2, 64, 4, 128)])
 def test_fused_qknorm_rope_store(oracle, dev, T, hq, hkv, d, k_back):
     note(f"fused qknorm+rope+store T={T} hq={hq} hkv={hkv} d={d} k_back={k_back}")
     qkv, kc, vc, qw, kw, pos, loc, cos, sin = _fused_inputs(dev, T, hq, hkv, d, 8)
