@@ -159,3 +159,29 @@ def test_sampling_candidate_overflow(oracle, dev):
     want, want_ok = oracle.sample(p, u, "top_k", top_k=k.astype(np.float32))
     np.testing.assert_array_equal(got.cpu().numpy(), want)
     np.testing.assert_array_equal(ok.cpu().numpy(), want_ok)
+
+
+def test_sampling_low_first_pivot(oracle, dev):
+    """Normalised dyadic rows with a heavy flat bulk (60,000 probabilities of
+    2^-17, below the copy threshold of the first sweep) beside 2,000 larger
+    ones: first draws often land in the bulk, so a round sweeps the row
+    again with copies held, and later rounds return to the copies.
+    Bit-exact against the oracle."""
+    note("sampling: first pivot below the copy threshold")
+    rng = np.random.default_rng(64)
+    B, d = 16, QWEN3_VOCAB
+    total = 1 << 24
+    p = np.zeros((B, d), np.float32)
+    for b in range(B):
+        n = np.zeros(d, np.int64)
+        pos = rng.permutation(d)
+        n[pos[:60000]] = 128
+        n[pos[60000:61000]] = 8192
+        n[pos[61000:62000]] = rng.integers(600, 1200, 1000)
+        n[pos[61000]] += total - n.sum()
+        assert n.min() >= 0 and n.sum() == total
+        p[b] = (n / total).astype(np.float32)
+    u = rng.random((32, B)).astype(np.float32)
+    k = rng.integers(1, 50, B)
+    tp = rng.uniform(0.3, 0.95, B).astype(np.float32)
+    run_all(oracle, dev, p, u, k, tp, exact=True)
