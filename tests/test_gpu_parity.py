@@ -279,7 +279,8 @@ def run_decode(dev, batch, hq, hkv, d, seed, q_indptr=None, rows=None, plan=None
     return q, kc, vc, o, scale, plan
 
 
-@pytest.mark.parametrize("hq,hkv", [(16, 8), (32, 8), (32, 4), (8, 8), (64, 4)])
+@pytest.mark.parametrize("hq,hkv", [(16, 8), (32, 8), (32, 4), (8, 8), (64, 4),
+                                     (40, 8), (16, 16), (8, 1), (14, 2)])
 @pytest.mark.parametrize("lens", [[512] * 4, [1, 2, 31, 32, 33, 127, 128, 129],
                                   [4096, 1, 700, 3000, 257]])
 def test_decode_parity(oracle, dev, hq, hkv, lens):
@@ -393,7 +394,8 @@ def test_prefill_cfg2(oracle, dev):
     check_prefill(oracle, dev, w.batch, w.shape.num_qo_heads, w.shape.num_kv_heads, 20, w.name)
 
 
-@pytest.mark.parametrize("hq,hkv", [(16, 8), (32, 4), (8, 8), (32, 8), (12, 4)])
+@pytest.mark.parametrize("hq,hkv", [(16, 8), (32, 4), (8, 8), (32, 8), (12, 4),
+                                     (40, 8), (16, 16), (8, 1), (64, 8)])
 def test_prefill_ragged(oracle, dev, hq, hkv):
     note(f"prefill ragged hq={hq} hkv={hkv}")
     rng = np.random.default_rng(21)
