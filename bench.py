@@ -8,8 +8,9 @@ kernel plus its split merge) over the whole batch, inputs resident in HBM.
 
 The other configs are reported under "extra" (and as their own lines with
 --workload): cfg1 small decode, cfg2 prefill with prefix hits, cfg3 fused
-RoPE + qk-norm + KV store, cfg5 mixed 48-layer step replayed as a hipGraph;
-and the residual path around attention at the Qwen3-8B shape for an
+RoPE + qk-norm + KV store, cfg5 mixed 48-layer step replayed as a hipGraph,
+prefill_chunk (cfg5's 2048-token prefill chunk on its 4096-token prefix, one
+layer, alone: the prefill kernel's MFMA fraction); and the residual path around attention at the Qwen3-8B shape for an
 8192-token chunk: resid_norm (fused add + RMSNorm, hidden 4096) and
 resid_act (SiLU-and-mul, intermediate 12288); and sampling (top-k + top-p
 draw for 256 rows over the Qwen3 vocabulary, as the Sampler runs it).
@@ -44,8 +45,8 @@ def parse():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="cfg4",
-                    choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5", "resid_norm", "resid_act",
-                             "sampling"])
+                    choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5", "prefill_chunk", "resid_norm",
+                             "resid_act", "sampling"])
     ap.add_argument("--no-extra", action="store_true", help="headline workload only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--cfg5-layers", type=int, default=48)
@@ -392,14 +393,15 @@ def run_workload(name, torch, capi, wl, dev, steps, warmup, cfg5_layers):
                "GB/s": nbytes / (wall * 1e-3) / 1e9,
                "roofline": roofline_hbm(nbytes, ev, "paged_decode_" + name)}
         return w, rec
-    if name == "cfg2":
-        w = wl.cfg2_prefill_prefix()
+    if name in ("cfg2", "prefill_chunk"):
+        w = wl.cfg2_prefill_prefix() if name == "cfg2" else wl.cfg5_prefill_chunk()
+        key = "paged_prefill_cfg2" if name == "cfg2" else "paged_prefill_cfg5_chunk"
         step, nbytes, flops = setup_prefill(torch, capi, wl, w, dev)
         wall, ev = timer.run(step, steps, warmup)
         rec = {"workload": w.name, "ms_per_step": wall, "kernel_ms": ev, "flops": flops,
                "bytes": nbytes, "TFLOP/s": flops / (wall * 1e-3) / 1e12,
                "GB/s": nbytes / (wall * 1e-3) / 1e9,
-               "roofline": roofline_mfma(flops, ev, "paged_prefill_cfg2"),
+               "roofline": roofline_mfma(flops, ev, key),
                "roofline_hbm": roofline_hbm(nbytes, ev, None)}
         return w, rec
     if name == "cfg3":
@@ -454,8 +456,8 @@ def main():
                            args.cfg5_layers)
     extra = {}
     if not args.no_extra:
-        for name in ("cfg1", "cfg2", "cfg3", "cfg4", "cfg5", "resid_norm", "resid_act",
-                     "sampling"):
+        for name in ("cfg1", "cfg2", "cfg3", "cfg4", "cfg5", "prefill_chunk", "resid_norm",
+                     "resid_act", "sampling"):
             if name == args.workload:
                 continue
             try:

@@ -179,6 +179,14 @@ def cfg5_mixed(seed: int = 0, layers: int = 48, decode_reqs: int = 64) -> Worklo
                     QWEN3_30B_A3B, b, layers=layers)
 
 
+def cfg5_prefill_chunk(seed: int = 0) -> Workload:
+    """The prefill part of config 5 on its own: one 2048-token chunk on a
+    4096-token cached prefix, 32q/4kv, page_size 16 (one layer)."""
+    rng = np.random.default_rng(seed)
+    b = make_paged_batch(rng, [4096], [4096 + 2048], page_size=16)
+    return Workload("cfg5_prefill_chunk_qwen3_30b_a3b_2048_on4096_p16", QWEN3_30B_A3B, b)
+
+
 def attention_bytes(shape: AttnShape, qo_lens, kv_lens, page_size: int) -> int:
     """Algorithmic HBM bytes: K+V bf16 once, Q in + O out bf16, one int32 index per page."""
     kv = np.asarray(kv_lens, dtype=np.int64)
