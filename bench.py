@@ -165,7 +165,7 @@ def setup_fused(torch, capi, wl, w, dev, seed=0):
 
     def step():
         # The pass as the attention layer runs it: k goes to the pool only
-        # (the survey's byte count has no k write-back into qkv).
+        # (the algorithmic byte count has no k write-back into qkv).
         capi.fused_qknorm_rope_store(qkv, kc, vc, qw, kw, cos, sin, pos, loc, hq, hkv, D, eps,
                                      write_k_back=False)
 

@@ -1,9 +1,9 @@
 """The measurement contract of bench.py, checked on the CPU.
 
-The algorithmic work behind every roofline figure is pinned to the
-figures the survey of the reference derives for the benchmark
-configurations (bytes and flops per launch), so a wrong term in a formula
-shows up here rather than as a plausible-looking fraction. The per-kernel
+The algorithmic work behind every roofline figure is pinned to figures
+derived by hand for the benchmark configurations (bytes and flops per
+launch, the derivation in each test's comments), so a wrong term in a
+formula shows up here rather than as a plausible-looking fraction. The per-kernel
 HBM traffic keys bench.py reads must exist in profiles/traffic.json, each
 with its rocprof summary, and a multi-GPU request must be refused.
 """
