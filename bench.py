@@ -16,7 +16,11 @@ resid_act (SiLU-and-mul, intermediate 12288); and sampling (top-k + top-p
 draw for 256 rows over the Qwen3 vocabulary, as the Sampler runs it).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload cfgN]
-                       [--no-extra] [--no-cpu]
+                       [--no-extra] [--no-cpu] [--min-warm-seconds S]
+
+Each workload is warmed for W steps and then until at least S seconds
+(default 0.5) have passed, because the GPU clock ramps under sustained
+load; the timed region is exactly K steps.
 """
 from __future__ import annotations
 
@@ -44,6 +48,9 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--min-warm-seconds", type=float, default=0.5,
+                    help="keep warming each workload until this much time has passed "
+                         "(after the W warm-up steps; the timed region is still K steps)")
     ap.add_argument("--workload", default="cfg4",
                     choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5", "prefill_chunk", "resid_norm",
                              "resid_act", "sampling"])
@@ -64,15 +71,25 @@ class Timer:
     run on, bracketing the same K steps (per-step event pairs would add a
     queue barrier between steps)."""
 
-    def __init__(self, torch):
+    def __init__(self, torch, min_warm_s=0.0):
         self.torch = torch
+        self.min_warm_s = min_warm_s
 
     def run(self, fn, steps, warmup):
+        """W warm-up steps, continued (in batches of 8) until at least
+        min_warm_s seconds have passed: the GPU clock ramps under sustained
+        load, and a few warm-up steps leave a short kernel timed below its
+        steady-state clock. Then exactly K timed steps."""
         torch = self.torch
         stream = torch.cuda.current_stream()
+        w0 = time.perf_counter()
         for _ in range(warmup):
             fn()
         torch.cuda.synchronize()
+        while time.perf_counter() - w0 < self.min_warm_s:
+            for _ in range(8):
+                fn()
+            torch.cuda.synchronize()
         start = torch.cuda.Event(enable_timing=True)
         end = torch.cuda.Event(enable_timing=True)
         t0 = time.perf_counter()
@@ -367,8 +384,8 @@ def setup_sampling(torch, capi, dev, seed=0):
                                                   "top_p": 0.9}
 
 
-def run_workload(name, torch, capi, wl, dev, steps, warmup, cfg5_layers):
-    timer = Timer(torch)
+def run_workload(name, torch, capi, wl, dev, steps, warmup, cfg5_layers, min_warm_s=0.0):
+    timer = Timer(torch, min_warm_s)
     if name == "sampling":
         step, nbytes, shape = setup_sampling(torch, capi, dev)
         wall, ev = timer.run(step, steps, warmup)
@@ -453,7 +470,7 @@ def main():
         return
 
     w, head = run_workload(args.workload, torch, capi, wl, dev, args.steps, args.warmup,
-                           args.cfg5_layers)
+                           args.cfg5_layers, args.min_warm_seconds)
     extra = {}
     if not args.no_extra:
         for name in ("cfg1", "cfg2", "cfg3", "cfg4", "cfg5", "prefill_chunk", "resid_norm",
@@ -462,7 +479,7 @@ def main():
                 continue
             try:
                 _, rec = run_workload(name, torch, capi, wl, dev, args.steps, args.warmup,
-                                      args.cfg5_layers)
+                                      args.cfg5_layers, args.min_warm_seconds)
                 extra[name] = rec
             except Exception as e:  # report, keep the headline line
                 extra[name] = {"error": repr(e)}
@@ -499,6 +516,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "min_warm_seconds": args.min_warm_seconds,
         "ms_per_step": round(head["ms_per_step"], 5),
         "higher_is_better": True,
         "scaling": "weak",
