@@ -39,7 +39,7 @@ const char* sgl_status_string(int status);
 
 /* Library version, to check that the loaded .so matches this header. */
 int sgl_abi_version(void);
-#define SGL_ABI_VERSION 8
+#define SGL_ABI_VERSION 9
 
 /* ------------------------------------------------------------------ */
 /* KV-cache store                                                      */
@@ -178,29 +178,29 @@ int sgl_fused_qknorm_rope_store(void* qkv, int64_t qkv_stride_token,
 
 /* Split-KV decode plan (host). */
 typedef struct {
-  int32_t kv_chunk_size;  /* W_max: largest unit in tokens (multiple of 16, <= 2048) */
-  int32_t min_chunk_size; /* W_min: smallest unit (bounds pieces per request) */
-  int32_t max_chunks;     /* partial slots per request (pieces a request may span) */
-  int32_t split_kv;       /* 1 when a request of the planned batch spans units */
+  int32_t kv_chunk_size;  /* W_max: largest unit in tokens (multiple of 16, <= 8192) */
+  int32_t min_chunk_size; /* W_min: smallest unit (64) */
   int32_t num_units;      /* work units = workgroups launched */
-  int32_t batch_size;
+  int32_t split_kv;       /* 1 when a request of the planned batch spans units */
+  int32_t batch_size;     /* largest batch the plan serves */
   int32_t num_qo_heads;
   int32_t num_kv_heads;
   int32_t head_dim;
-  int64_t workspace_bytes; /* fp32 split partials + log2-sum-exp */
+  int64_t max_total_tokens; /* capacity: num_units * kv_chunk_size tokens per call */
+  int64_t workspace_bytes;  /* 256-byte header (status word) + fp32 partials, two per unit */
 } sgl_decode_plan_t;
 
 /*
- * Token-balanced schedule from the host copy of kv_indptr: the batch's
- * flattened token stream is cut into num_units equal units, one per
- * resident workgroup (the count comes from the device's CU count, 256 when
- * no device is visible). The launch picks the unit size on the device,
- * clamp(ceil(total / num_units), min_chunk_size, kv_chunk_size) rounded to
- * 16 tokens, from kv_indptr[batch], so a plan built from a kv_indptr with
- * every request at its maximum length stays valid and balanced for any batch
- * of at most batch_size requests whose per-request and total lengths are no
- * larger (graph capture / replay without re-planning). The workspace holds
- * the partials of requests that span units.
+ * Token-balanced schedule from the host copy of kv_indptr (kv_indptr[0] must
+ * be 0): the batch's flattened token stream is cut into num_units equal
+ * units, one per resident workgroup (the count comes from the device's CU
+ * count, 256 when no device is visible). The launch picks the unit size on
+ * the device, clamp(ceil(total / num_units), min_chunk_size, kv_chunk_size)
+ * rounded to 16 tokens, from kv_indptr[batch], so a plan built from a
+ * kv_indptr with every request at its maximum length stays valid and
+ * balanced for any batch of at most batch_size requests and at most
+ * max_total_tokens tokens, whatever the per-request lengths (graph capture /
+ * replay without re-planning).
  * Replaces: FlashInfer DecodePlan as called from
  *           FlashInferBackend::initialize_decode_metadata_once
  *           (src/attention/flashinfer_backend.cu:354-397).
@@ -209,19 +209,32 @@ int sgl_decode_plan(const int32_t* kv_indptr_host, int batch_size,
                     int num_qo_heads, int num_kv_heads, int head_dim,
                     sgl_decode_plan_t* plan);
 
+/*
+ * Host-side check that a batch (host kv_indptr, batch_size requests) fits a
+ * plan: SGL_OK, or SGL_ERR_CAPACITY when it has more requests than
+ * plan->batch_size or more tokens than plan->max_total_tokens.
+ * Replaces: the batch-size / length checks of
+ *           FlashInferBackend::prepare_for_replay (src/attention/flashinfer_backend.cu:267-352).
+ */
+int sgl_decode_plan_check(const sgl_decode_plan_t* plan, const int32_t* kv_indptr_host,
+                          int batch_size);
 
 /*
  * Paged decode: for request r (rows q[q_row(r)], q_row(r) = r, or
  * q_indptr[r] when q_indptr is non-NULL) and q head h,
  * o[q_row, h] = softmax_j(q.K[indices[kv_indptr[r] + j], h / G] * sm_scale)
  *               . V[indices[...], h / G]
- * over j < kv_indptr[r+1] - kv_indptr[r]. G = Hq / Hkv. q is strided
- * (q_stride_token, q_stride_head), o likewise; k_cache/v_cache are one
- * layer's [slots, Hkv, D] (slot stride kv_stride_slot, head stride
- * kv_stride_head). workspace holds split partials (plan->workspace_bytes);
- * a request longer than one chunk is merged by a second kernel on the same
- * stream. kv_len must not exceed plan->max_chunks * plan->kv_chunk_size.
- * Calls that share one workspace must be stream-ordered.
+ * over j < kv_indptr[r+1] - kv_indptr[r]; an empty request gets a zero row.
+ * G = Hq / Hkv. q is strided (q_stride_token, q_stride_head), o likewise
+ * (strides multiples of 8 elements); k_cache/v_cache are one layer's
+ * [slots, Hkv, D] (slot stride kv_stride_slot, head stride kv_stride_head).
+ * workspace (plan->workspace_bytes, 16-byte aligned) holds the split
+ * partials and, at offset 0, an int32 status word: each call clears it, and
+ * when the device kv_indptr[batch] exceeds plan->max_total_tokens the rows
+ * of every request reaching past the capacity are written as NaN and the
+ * word is set to SGL_ERR_CAPACITY (read it with sgl_decode_status). Two
+ * kernels run on the stream (decode, then merge). Calls that share one
+ * workspace must be stream-ordered.
  * Replaces: BatchDecodeWithPagedKVCacheDispatched call in
  *           FlashInferBackend::forward (src/attention/flashinfer_backend.cu:553-595).
  */
@@ -235,6 +248,14 @@ int sgl_paged_decode(const sgl_decode_plan_t* plan, const void* q,
                      float sm_scale, void* o, int64_t o_stride_token,
                      int64_t o_stride_head, void* workspace,
                      int64_t workspace_bytes, void* stream);
+
+/*
+ * Reads the status word a decode call left in its workspace (waits for the
+ * stream): SGL_OK, or SGL_ERR_CAPACITY when the batch exceeded its plan.
+ * Replaces: no device-side counterpart in the reference (FlashInfer's plan
+ *           is host-side); pairs with sgl_paged_decode.
+ */
+int sgl_decode_status(const void* workspace, int32_t* status, void* stream);
 
 /*
  * Paged causal prefill over ragged requests: query i (0-based inside

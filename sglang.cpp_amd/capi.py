@@ -25,7 +25,7 @@ SGL_INDEX_I32 = 0
 SGL_INDEX_I64 = 1
 SGL_DTYPE_BF16 = 0
 SGL_DTYPE_F16 = 1
-ABI_VERSION = 8
+ABI_VERSION = 9
 FUSED_NO_K_WRITEBACK = 1  # SGL_FUSED_NO_K_WRITEBACK
 
 
@@ -39,13 +39,13 @@ class DecodePlan(ctypes.Structure):
     _fields_ = [
         ("kv_chunk_size", ctypes.c_int32),
         ("min_chunk_size", ctypes.c_int32),
-        ("max_chunks", ctypes.c_int32),
-        ("split_kv", ctypes.c_int32),
         ("num_units", ctypes.c_int32),
+        ("split_kv", ctypes.c_int32),
         ("batch_size", ctypes.c_int32),
         ("num_qo_heads", ctypes.c_int32),
         ("num_kv_heads", ctypes.c_int32),
         ("head_dim", ctypes.c_int32),
+        ("max_total_tokens", ctypes.c_int64),
         ("workspace_bytes", ctypes.c_int64),
     ]
 
@@ -73,6 +73,8 @@ _SIGNATURES = {
     "sgl_fused_qknorm_rope_store": ([_vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64,
                                      _i32, _i32, _i32, _f32, _i32, _vp], _i32),
     "sgl_decode_plan": ([_vp, _i32, _i32, _i32, _i32, ctypes.POINTER(DecodePlan)], _i32),
+    "sgl_decode_plan_check": ([ctypes.POINTER(DecodePlan), _vp, _i32], _i32),
+    "sgl_decode_status": ([_vp, _vp, _vp], _i32),
     "sgl_paged_decode": ([ctypes.POINTER(DecodePlan), _vp, _i64, _i64, _vp, _vp, _i64, _i64,
                           _vp, _vp, _vp, _i32, _i32, _i32, _i32, _f32, _vp, _i64, _i64, _vp,
                           _i64, _vp], _i32),
@@ -388,9 +390,25 @@ def decode_plan(kv_indptr_host: Sequence[int], num_qo_heads: int, num_kv_heads: 
     return plan
 
 
+def decode_plan_check(plan: DecodePlan, kv_indptr_host: Sequence[int]) -> int:
+    """SGL_OK (0) when the batch fits the plan, SGL_ERR_CAPACITY (-3) when not."""
+    arr = (ctypes.c_int32 * len(kv_indptr_host))(*[int(x) for x in kv_indptr_host])
+    return lib().sgl_decode_plan_check(ctypes.byref(plan), ctypes.cast(arr, ctypes.c_void_p),
+                                       len(kv_indptr_host) - 1)
+
+
 def decode_workspace(plan: DecodePlan, device: torch.device) -> torch.Tensor:
     """Allocates the split-KV workspace a plan needs."""
-    return torch.empty(max(int(plan.workspace_bytes), 256), dtype=torch.uint8, device=device)
+    return torch.empty(int(plan.workspace_bytes), dtype=torch.uint8, device=device)
+
+
+def decode_status(workspace: torch.Tensor) -> int:
+    """Status word of the last decode call on this workspace (waits for the stream)."""
+    dev = _need_gpu(workspace)
+    st = ctypes.c_int32(-100)
+    _check(lib().sgl_decode_status(_p(workspace), ctypes.byref(st), _stream(dev)),
+           "sgl_decode_status")
+    return st.value
 
 
 def _kv_strides(k_cache: torch.Tensor):

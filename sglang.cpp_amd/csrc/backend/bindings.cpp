@@ -30,7 +30,7 @@ py::dict plan_dict(const sgl_decode_plan_t& p) {
   py::dict d;
   d["kv_chunk_size"] = p.kv_chunk_size;
   d["min_chunk_size"] = p.min_chunk_size;
-  d["max_chunks"] = p.max_chunks;
+  d["max_total_tokens"] = p.max_total_tokens;
   d["split_kv"] = p.split_kv;
   d["num_units"] = p.num_units;
   d["batch_size"] = p.batch_size;
@@ -114,6 +114,9 @@ PYBIND11_MODULE(sgl_backend, m) {
       .def("attend", &HipAttnBackend::attend, py::arg("q"), py::arg("layer_id"), py::arg("batch"))
       .def("init_capture_graph", &HipAttnBackend::init_capture_graph, py::arg("max_seq_len"),
            py::arg("bs_list"))
+      .def("init_mixed_capture_graph", &HipAttnBackend::init_mixed_capture_graph,
+           py::arg("max_seq_len"), py::arg("max_decode_rows"), py::arg("max_prefill_reqs"),
+           py::arg("max_prefill_qo"))
       .def("prepare_for_capture", &HipAttnBackend::prepare_for_capture)
       .def("prepare_for_replay", &HipAttnBackend::prepare_for_replay);
 

@@ -148,6 +148,10 @@ void HipAttnBackend::set_page_table(const torch::Tensor& page_table) {
 
 torch::Tensor& HipAttnBackend::workspace(int64_t bytes) {
   if (!workspace_.defined() || workspace_.numel() < bytes) {
+    if (workspace_captured_ && workspace_.defined()) {
+      retired_workspaces_.push_back(workspace_);
+      workspace_captured_ = false;
+    }
     workspace_ = torch::empty({std::max<int64_t>(bytes, 256)},
                               torch::TensorOptions().dtype(torch::kUInt8).device(
                                   kv_cache_->device()));
@@ -323,9 +327,17 @@ torch::Tensor HipAttnBackend::attend(const torch::Tensor& q_in, int layer_id, Ba
   }
   if (meta->num_decode > 0) {
     // Graph-captured launches use the capture workspace, whose address never
-    // changes; eager launches use the growable one.
-    torch::Tensor& ws = meta->use_capture_buffers ? capture_->workspace
-                                                  : workspace(meta->dec_plan.workspace_bytes);
+    // changes; eager launches use the growable one, which is kept alive if a
+    // graph records it anyway (capture of eagerly prepared metadata).
+    torch::Tensor& ws = !meta->use_capture_buffers ? workspace(meta->dec_plan.workspace_bytes)
+                        : meta->is_prefill         ? mixed_->workspace
+                                                   : capture_->workspace;
+    if (!meta->use_capture_buffers) {
+      hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+      check_hip(hipStreamIsCapturing(static_cast<hipStream_t>(stream), &cs),
+                "hipStreamIsCapturing");
+      if (cs != hipStreamCaptureStatusNone) workspace_captured_ = true;
+    }
     TORCH_CHECK(ws.numel() >= meta->dec_plan.workspace_bytes, "decode workspace too small");
     check_sgl(sgl_paged_decode(&meta->dec_plan, q.data_ptr(), q.stride(0), q.stride(1),
                                kc.data_ptr(), vc.data_ptr(), kc.stride(0), kc.stride(1),
@@ -392,7 +404,10 @@ void HipAttnBackend::init_capture_graph(int max_seq_len, const std::vector<int>&
 }
 
 void HipAttnBackend::prepare_for_capture(Batch& batch) {
-  TORCH_CHECK(batch.is_decode(), "HipAttnBackend capture only supports decode batches");
+  if (batch.is_prefill()) {
+    prepare_mixed_for_capture(batch);
+    return;
+  }
   TORCH_CHECK(capture_, "Decode capture state is not initialized");
   TORCH_CHECK(page_table_.defined(), "HipAttnBackend: set_page_table() first");
   const int bs = batch.padded_size();
@@ -425,7 +440,10 @@ void HipAttnBackend::prepare_for_capture(Batch& batch) {
 }
 
 void HipAttnBackend::prepare_for_replay(Batch& batch) {
-  TORCH_CHECK(batch.is_decode(), "HipAttnBackend replay only supports decode batches");
+  if (batch.is_prefill()) {
+    prepare_mixed_for_replay(batch);
+    return;
+  }
   TORCH_CHECK(capture_, "Decode capture state is not initialized");
   auto meta = metadata_of(batch);
   const int bs = batch.padded_size();
@@ -438,12 +456,170 @@ void HipAttnBackend::prepare_for_replay(Batch& batch) {
     TORCH_CHECK(meta->kv_indptr_host[i + 1] - meta->kv_indptr_host[i] <= capture_->max_seq_len,
                 "request longer than the captured max_seq_len");
   }
+  check_sgl(sgl_decode_plan_check(&cap->dec_plan, meta->kv_indptr_host.data(), bs),
+            "sgl_decode_plan_check");
   const int64_t total = meta->kv_indptr_host[bs];
   cap->dec_kv_indptr.copy_(meta->dec_kv_indptr, /*non_blocking=*/true);
   if (total > 0)
     cap->dec_indices.slice(0, 0, total).copy_(meta->dec_indices.slice(0, 0, total),
                                               /*non_blocking=*/true);
   cap->kv_indptr_host = meta->kv_indptr_host;
+  batch.attn_metadata = cap;
+}
+
+
+// Mixed steps. The reference captures decode batches only
+// (flashinfer_backend.cu:193-219,267-352); the same contract -- fixed
+// addresses sized at init, replay rewrites contents only -- is extended here
+// to prefill-phase batches whose qo_len == 1 rows go to the split-KV decode
+// kernel and whose chunks go to the prefill kernel. Capture metadata is keyed
+// by (decode rows, prefill requests); the decode rows use a worst-case plan
+// (every row at max_seq_len, units sized on the device at replay) and the
+// prefill launch is sized for max_prefill_qo (tiles past a request's rows
+// exit at once), so both launches stay valid for any replayed lengths.
+
+void HipAttnBackend::init_mixed_capture_graph(int max_seq_len, int max_decode_rows,
+                                              int max_prefill_reqs, int max_prefill_qo) {
+  mixed_.reset();
+  TORCH_CHECK(max_seq_len > 0 && max_decode_rows >= 0 && max_prefill_reqs > 0 &&
+                  max_prefill_qo > 1 && max_prefill_qo <= max_seq_len,
+              "init_mixed_capture_graph: need max_seq_len > 0, max_decode_rows >= 0, "
+              "max_prefill_reqs > 0 and 1 < max_prefill_qo <= max_seq_len");
+  auto m = std::make_unique<MixedCapture>();
+  m->max_seq_len = max_seq_len;
+  m->max_dec = max_decode_rows;
+  m->max_pre = max_prefill_reqs;
+  m->max_qo = max_prefill_qo;
+  const auto dev = kI32.device(kv_cache_->device());
+  const int64_t L = max_seq_len;
+  m->qo_indptr = torch::zeros({max_decode_rows + max_prefill_reqs + 1}, dev);
+  m->dec_kv_indptr = torch::zeros({max_decode_rows + 1}, dev);
+  m->dec_indices = torch::zeros({std::max<int64_t>(max_decode_rows * L, 1)}, dev);
+  m->dec_q_rows = torch::zeros({std::max(max_decode_rows, 1)}, dev);
+  m->pre_qo_indptr = torch::zeros({max_prefill_reqs + 1}, dev);
+  m->pre_kv_indptr = torch::zeros({max_prefill_reqs + 1}, dev);
+  m->pre_q_start = torch::zeros({max_prefill_reqs}, dev);
+  m->pre_indices = torch::zeros({max_prefill_reqs * L}, dev);
+  // Workspace for the largest worst-case decode plan of any row count.
+  int64_t ws_bytes = 256;
+  std::vector<int32_t> worst(1, 0);
+  for (int n = 1; n <= max_decode_rows; ++n) {
+    worst.push_back(static_cast<int32_t>(n * L));
+    sgl_decode_plan_t plan;
+    check_sgl(sgl_decode_plan(worst.data(), n, num_qo_heads_, num_kv_heads_, head_dim_, &plan),
+              "sgl_decode_plan");
+    ws_bytes = std::max<int64_t>(ws_bytes, plan.workspace_bytes);
+  }
+  m->workspace = torch::empty({ws_bytes}, torch::TensorOptions().dtype(torch::kUInt8).device(
+                                              kv_cache_->device()));
+  mixed_ = std::move(m);
+}
+
+void HipAttnBackend::check_mixed_capacity(const HipAttnMetadata& m) const {
+  TORCH_CHECK(m.num_decode <= mixed_->max_dec, "mixed step has ", m.num_decode,
+              " decode rows; capture capacity is ", mixed_->max_dec);
+  TORCH_CHECK(m.num_prefill <= mixed_->max_pre, "mixed step has ", m.num_prefill,
+              " prefill requests; capture capacity is ", mixed_->max_pre);
+  TORCH_CHECK(m.max_qo_len <= mixed_->max_qo, "prefill chunk of ", m.max_qo_len,
+              " tokens exceeds the captured max_prefill_qo ", mixed_->max_qo);
+  for (size_t i = 0; i + 1 < m.kv_indptr_host.size(); ++i)
+    TORCH_CHECK(m.kv_indptr_host[i + 1] - m.kv_indptr_host[i] <= mixed_->max_seq_len,
+                "request longer than the captured max_seq_len");
+}
+
+// Device-to-device copy of a batch's metadata contents into capture buffers.
+void HipAttnBackend::copy_contents(HipAttnMetadata& dst, const HipAttnMetadata& src) {
+  const int bs = static_cast<int>(src.qo_indptr_host.size()) - 1;
+  dst.indptr.slice(0, 0, bs + 1).copy_(src.indptr.slice(0, 0, bs + 1), true);
+  if (src.num_decode > 0) {
+    const int n = src.num_decode;
+    dst.dec_kv_indptr.slice(0, 0, n + 1).copy_(src.dec_kv_indptr.slice(0, 0, n + 1), true);
+    dst.dec_q_rows.slice(0, 0, n).copy_(src.dec_q_rows.slice(0, 0, n), true);
+    const int64_t total = src.dec_indices.numel();
+    dst.dec_indices.slice(0, 0, total).copy_(src.dec_indices, true);
+  }
+  if (src.num_prefill > 0) {
+    const int n = src.num_prefill;
+    dst.pre_qo_indptr.slice(0, 0, n + 1).copy_(src.pre_qo_indptr.slice(0, 0, n + 1), true);
+    dst.pre_kv_indptr.slice(0, 0, n + 1).copy_(src.pre_kv_indptr.slice(0, 0, n + 1), true);
+    dst.pre_q_start.slice(0, 0, n).copy_(src.pre_q_start.slice(0, 0, n), true);
+    const int64_t total = src.pre_indices.numel();
+    dst.pre_indices.slice(0, 0, total).copy_(src.pre_indices, true);
+  }
+  dst.seq_lens = src.seq_lens;
+  dst.cached_lens = src.cached_lens;
+  dst.qo_indptr_host = src.qo_indptr_host;
+  dst.kv_indptr_host = src.kv_indptr_host;
+}
+
+void HipAttnBackend::prepare_mixed_for_capture(Batch& batch) {
+  TORCH_CHECK(mixed_, "prefill-phase capture needs init_mixed_capture_graph() first");
+  prepare_metadata(batch);  // this batch's contents, then moved into the fixed buffers
+  auto src = metadata_of(batch);
+  check_mixed_capacity(*src);
+  const int bs = batch.padded_size();
+  const int n_dec = src->num_decode, n_pre = src->num_prefill;
+  const int64_t L = mixed_->max_seq_len;
+  auto meta = std::make_shared<HipAttnMetadata>();
+  meta->is_prefill = true;
+  meta->use_capture_buffers = true;
+  meta->indptr = mixed_->qo_indptr.slice(0, 0, bs + 1);
+  meta->num_decode = n_dec;
+  if (n_dec > 0) {
+    std::vector<int32_t> worst(n_dec + 1);
+    for (int i = 0; i <= n_dec; ++i) worst[i] = static_cast<int32_t>(i * L);
+    check_sgl(sgl_decode_plan(worst.data(), n_dec, num_qo_heads_, num_kv_heads_, head_dim_,
+                              &meta->dec_plan),
+              "sgl_decode_plan");
+    TORCH_CHECK(meta->dec_plan.workspace_bytes <= mixed_->workspace.numel(),
+                "mixed capture workspace too small");
+    meta->dec_kv_indptr = mixed_->dec_kv_indptr.slice(0, 0, n_dec + 1);
+    meta->dec_indices = mixed_->dec_indices.slice(0, 0, n_dec * L);
+    meta->dec_q_rows = mixed_->dec_q_rows.slice(0, 0, n_dec);
+  }
+  meta->num_prefill = n_pre;
+  meta->max_qo_len = mixed_->max_qo;
+  if (n_pre > 0) {
+    meta->pre_qo_indptr = mixed_->pre_qo_indptr.slice(0, 0, n_pre + 1);
+    meta->pre_kv_indptr = mixed_->pre_kv_indptr.slice(0, 0, n_pre + 1);
+    meta->pre_q_start = mixed_->pre_q_start.slice(0, 0, n_pre);
+    meta->pre_indices = mixed_->pre_indices.slice(0, 0, n_pre * L);
+  }
+  copy_contents(*meta, *src);
+  meta->capture_tokens = src->qo_indptr_host[bs];
+  meta->host_staging = src->host_staging;  // pending H2D copies of the source stay alive
+  mixed_->metadata[{n_dec, n_pre}] = meta;
+  batch.attn_metadata = meta;
+}
+
+void HipAttnBackend::prepare_mixed_for_replay(Batch& batch) {
+  TORCH_CHECK(mixed_, "prefill-phase replay needs init_mixed_capture_graph() first");
+  auto src = metadata_of(batch);
+  TORCH_CHECK(!src->use_capture_buffers, "prepare_for_replay expects prepare_metadata() first");
+  auto it = mixed_->metadata.find({src->num_decode, src->num_prefill});
+  TORCH_CHECK(it != mixed_->metadata.end(), "no captured mixed step with ", src->num_decode,
+              " decode rows and ", src->num_prefill, " prefill requests");
+  auto& cap = it->second;
+  check_mixed_capacity(*src);
+  const int bs = batch.padded_size();
+  TORCH_CHECK(static_cast<int>(cap->indptr.numel()) == bs + 1,
+              "replayed batch size differs from the captured one");
+  TORCH_CHECK(src->qo_indptr_host[bs] <= cap->capture_tokens, "replayed step has ",
+              src->qo_indptr_host[bs], " query rows; the graph was captured with ",
+              cap->capture_tokens);
+  if (src->num_decode > 0) {
+    std::vector<int32_t> dec_ip(src->num_decode + 1, 0);
+    int i = 0;
+    for (int r = 0; r < bs; ++r)
+      if (src->qo_indptr_host[r + 1] - src->qo_indptr_host[r] == 1) {
+        dec_ip[i + 1] = dec_ip[i] + (src->kv_indptr_host[r + 1] - src->kv_indptr_host[r]);
+        ++i;
+      }
+    check_sgl(sgl_decode_plan_check(&cap->dec_plan, dec_ip.data(), src->num_decode),
+              "sgl_decode_plan_check");
+  }
+  copy_contents(*cap, *src);
+  cap->host_staging = src->host_staging;
   batch.attn_metadata = cap;
 }
 

@@ -68,6 +68,7 @@ struct HipAttnMetadata : public BaseAttnMetadata {
   torch::Tensor pre_qo_indptr, pre_kv_indptr, pre_indices, pre_q_start, pre_table_idx;
 
   bool use_capture_buffers = false;
+  int64_t capture_tokens = 0;  // query rows of the captured step (replays may use fewer)
   std::vector<torch::Tensor> host_staging;  // pinned buffers of pending H2D copies
 
   torch::Tensor get_last_indices(int bs) const override;
@@ -92,6 +93,15 @@ class HipAttnBackend : public BaseAttnBackend {
   torch::Tensor forward(const torch::Tensor& q, const torch::Tensor& k, const torch::Tensor& v,
                         int layer_id, Batch& batch) override;
   void init_capture_graph(int max_seq_len, const std::vector<int>& bs_list) override;
+  // Fixed-address buffers for capturing mixed steps (prefill-phase batches:
+  // qo_len == 1 rows beside chunked-prefill requests): up to max_decode_rows
+  // decode rows and max_prefill_reqs prefill requests of at most
+  // max_prefill_qo new tokens, every request at most max_seq_len long. After
+  // this, prepare_for_capture / prepare_for_replay accept prefill-phase
+  // batches; a graph replays any batch with the captured (decode rows,
+  // prefill requests) counts and no more query rows than it was captured with.
+  void init_mixed_capture_graph(int max_seq_len, int max_decode_rows, int max_prefill_reqs,
+                                int max_prefill_qo);
   void prepare_for_capture(Batch& batch) override;
   void prepare_for_replay(Batch& batch) override;
 
@@ -117,6 +127,21 @@ class HipAttnBackend : public BaseAttnBackend {
   void build_decode_rows(HipAttnMetadata& meta, const std::vector<int>& reqs,
                          const std::vector<int32_t>& q_rows, const Batch& batch);
 
+  void prepare_mixed_for_capture(Batch& batch);
+  void prepare_mixed_for_replay(Batch& batch);
+  void check_mixed_capacity(const HipAttnMetadata& m) const;
+  static void copy_contents(HipAttnMetadata& dst, const HipAttnMetadata& src);
+
+  struct MixedCapture {
+    int max_seq_len = 0, max_dec = 0, max_pre = 0, max_qo = 0;
+    torch::Tensor qo_indptr;                                  // [max_dec + max_pre + 1]
+    torch::Tensor dec_kv_indptr, dec_indices, dec_q_rows;     // decode rows
+    torch::Tensor pre_qo_indptr, pre_kv_indptr, pre_q_start, pre_indices;  // prefill rows
+    torch::Tensor workspace;  // decode split workspace of the largest plan
+    std::map<std::pair<int, int>, std::shared_ptr<HipAttnMetadata>> metadata;
+  };
+  std::unique_ptr<MixedCapture> mixed_;
+
   struct CaptureState {
     int max_seq_len = 0;
     int max_bs = 0;
@@ -132,6 +157,10 @@ class HipAttnBackend : public BaseAttnBackend {
   int num_qo_heads_, num_kv_heads_, head_dim_;
   torch::Tensor page_table_;
   torch::Tensor workspace_;
+  // Set once the growable workspace has been recorded into a graph: growing
+  // it then keeps the old buffer alive (a graph may still write to it).
+  bool workspace_captured_ = false;
+  std::vector<torch::Tensor> retired_workspaces_;
   std::unique_ptr<CaptureState> capture_;
   // Side stream and fork/join events for mixed batches (created on first use).
   void* side_stream();

@@ -6,30 +6,33 @@
 //             . V[indices[kv_indptr[r] + j], h / G]
 // with the page table token-granular (page_size 1), no window, no soft-cap.
 //
-// Design rule (measured on MI355X): HBM gather bandwidth is set by how many
-// waves each CU keeps in flight, not by how many bytes one wave has
-// outstanding — 8 waves/CU top out near 3.4 TB/s, 24 waves/CU reach ~5.9 TB/s
-// on random 256-byte rows. So this kernel is built to stay under 80 VGPRs
-// (6 waves per SIMD):
-//   * Work: one workgroup per (request, KV chunk), one wave per kv head, so
-//     a workgroup streams whole [Hkv, D] slot rows. All G query heads of a kv
-//     head share each K/V byte, which is read from HBM once per step.
-//   * 16-token steps. S^T[tok, head] = K . Q^T runs on the matrix cores
-//     (v_mfma_f32_16x16x32_bf16; K operand straight from HBM, 16 rows x 64 B
-//     per load; the Q^T operand is re-read from a per-wave LDS copy instead
-//     of pinning 16 registers). P.V runs on the vector ALUs with each lane
-//     owning two head-dim columns for all G heads (2G accumulators instead of
-//     the 32 a 16-wide MFMA tile would need); V arrives as one 256-byte row
-//     per load instruction at a wave-uniform address, so slot indices come
-//     through scalar loads. P and the rescale factors are broadcast through a
-//     per-wave LDS scratch.
-//   * Rolling prefetch: K of step t+1 is issued as soon as the QK products of
-//     step t have read their operands, V of step t+1 right after the P.V of
-//     step t, so each wave keeps ~8 KiB in flight with no second buffer.
-// A request longer than one chunk writes fp32 partials plus a log2-sum-exp,
-// combined by a second, short kernel. (Merging inside the decode launch would
-// need an agent-scope release per workgroup, which on a multi-XCD part is an
-// L2 write-back per workgroup; the kernel boundary is far cheaper.)
+// Schedule: persistent and token balanced. The batch's flattened KV token
+// stream (request r owns [kv_indptr[r], kv_indptr[r+1])) is cut into
+// num_units units of W tokens, one per resident workgroup, so every
+// workgroup streams the same number of tokens to the end instead of a few
+// long requests leaving a tail. W is picked on the device from
+// kv_indptr[batch], which keeps a plan built for a worst-case batch (graph
+// capture) valid and balanced for any shorter batch replayed with it.
+//   * One wave per kv head: each K/V byte is read from HBM once and feeds all
+//     G query heads of that kv head (GQA sharing).
+//   * 16-token steps on the matrix cores: S^T = K . Q^T on
+//     v_mfma_f32_16x16x32_bf16 (K straight from HBM into VGPRs, Q^T from a
+//     per-wave LDS copy), O^T += V^T . P^T on v_mfma_f32_16x16x16bf16_1k fed
+//     from the S^T accumulators; the online softmax is lane-local plus two
+//     lane exchanges.
+//   * K and V of step t+1 are issued before the products of step t.
+// A request that spans units is written as fp32 partials (normalised output
+// plus log2-sum-exp) into two slots per unit -- slot 2u for the piece of the
+// request running into unit u from before it, slot 2u+1 for the piece of the
+// request that starts inside u and runs past it -- and folded by a second,
+// short kernel. Merging inside the decode launch would need an agent-scope
+// release per workgroup, which on this multi-XCD part is an L2 write-back per
+// workgroup; the kernel boundary is cheaper.
+//
+// A batch whose tokens exceed the plan's capacity (num_units * W_max) is not
+// processed silently wrong: the merge kernel writes NaN to the rows of every
+// request reaching past the capacity and sets the workspace's status word to
+// SGL_ERR_CAPACITY (cleared by every launch).
 #include <math.h>
 
 #include "common.h"
@@ -42,7 +45,7 @@ constexpr int kStep = 16;       // tokens per pipeline step
 constexpr int kTile = 32;       // chunk granularity (tokens)
 constexpr int kMaxKvHeads = 16; // kv heads per workgroup (one wave each)
 constexpr int kMaxGroup = 16;
-constexpr int kMaxChunks = 128; // bound on splits per request (merge table)
+constexpr int kMinUnit = 64;    // smallest unit: keeps per-unit set-up small next to the stream
 constexpr int kMaxChunkTokens = 8192;  // slot indices of a chunk staged in LDS (32 KiB)
 constexpr int kQPitch = kD + 8; // LDS row pitch (bf16) of the Q^T copy
 // Word 3 of a raw buffer resource on gfx9-class parts: 32-bit data format,
@@ -62,11 +65,11 @@ struct DecodeArgs {
   float scale_log2;  // sm_scale * log2(e)
   uint16_t* o;
   int64_t o_st, o_sh;
-  float* part_o;     // [B, max_chunks, hq, D]
-  float* part_lse;   // [B, max_chunks, hq]
+  float* part_o;     // [2 num_units, hq, D]
+  float* part_lse;   // [2 num_units, hq]
+  int32_t* status;   // workspace status word
   int chunk;         // W_max: largest unit (LDS staging capacity)
-  int chunk_min;     // W_min: smallest unit (bounds the pieces per request)
-  int max_chunks;    // partial slots per request (max pieces)
+  int chunk_min;     // W_min: smallest unit
   int batch;
   int num_units;     // workgroups of the decode launch
 };
@@ -86,17 +89,19 @@ struct WaveLds {
   uint16_t q[16 * kQPitch];  // Q rows of the wave's G heads (zero rows past G)
 };
 
-// Workspace carve-up shared by the plan and the launch.
+// Workspace carve-up shared by the plan and the launch: a 256-byte header
+// (int32 status word at offset 0), then the partial outputs and their
+// log2-sum-exp, two slots per unit.
 struct WorkspaceLayout {
   int64_t part_o_off, part_lse_off, total;
 };
 
-inline WorkspaceLayout workspace_layout(int batch, int max_chunks, int hq) {
+inline WorkspaceLayout workspace_layout(int num_units, int hq) {
   WorkspaceLayout w;
-  const int64_t npart = static_cast<int64_t>(batch) * max_chunks * hq;
+  const int64_t npart = 2 * static_cast<int64_t>(num_units) * hq;
   auto align = [](int64_t x) { return (x + 255) / 256 * 256; };
-  w.part_o_off = 0;
-  w.part_lse_off = align(npart * kD * 4);
+  w.part_o_off = 256;
+  w.part_lse_off = w.part_o_off + align(npart * kD * 4);
   w.total = w.part_lse_off + align(npart * 4);
   return w;
 }
@@ -155,9 +160,9 @@ __device__ __forceinline__ bf16x4_t v_operand(const u32x4_t (&vr)[4]) {
   acc[nb] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(v_operand<nb>(vr), pop, acc[nb], \
                                                       0, 0, 0)
 
-// One wave: kv head h of request r over the `len` tokens whose slots are
-// sidx[0, len); c is the partial slot of this piece of request r, nch == 1
-// when the piece is the whole request.
+// One wave: kv head h over the `len` tokens whose slots are sidx[0, len)
+// (one piece of a request). whole: the piece is the whole request (output
+// written directly); otherwise it goes to partial slot pslot.
 //
 // Per 16-token step (v_mfma, lane l, n = l % 16, j = l / 16):
 //   S^T[tok, head] = K . Q^T          4 x 16x16x32: rows tok, columns head
@@ -167,7 +172,7 @@ __device__ __forceinline__ bf16x4_t v_operand(const u32x4_t (&vr)[4]) {
 // on the lane's column, so max, sum and the rescale of O are lane-local apart
 // from one exchange across the four lane groups.
 __device__ __forceinline__ void decode_head(const DecodeArgs& a, WaveLds& L, const int32_t* sidx,
-                                            int r, int c, int nch, int h, int len, int qrow,
+                                            int pslot, bool whole, int h, int len, int qrow,
                                             int lane) {
   const int n = lane & 15;
   const int j = lane >> 4;
@@ -250,7 +255,7 @@ __device__ __forceinline__ void decode_head(const DecodeArgs& a, WaveLds& L, con
   const float inv = l > 0.f ? 1.0f / l : 0.f;
   const int head = h * G + n;
   // Lane holds O[head n][d = 32 j + 8 i + nb] in acc[nb][i].
-  if (nch == 1) {
+  if (whole) {
     uint16_t* op = a.o + static_cast<int64_t>(qrow) * a.o_st + static_cast<int64_t>(head) * a.o_sh;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -260,11 +265,7 @@ __device__ __forceinline__ void decode_head(const DecodeArgs& a, WaveLds& L, con
       stg128(op + 32 * j + 8 * i, pack8(v));
     }
   } else {
-    // A batch longer than its plan allows (pieces beyond max_chunks) would
-    // write past the workspace: drop those pieces instead (the host-side
-    // checks keep a correct caller from getting here).
-    if (c >= a.max_chunks) return;
-    const int64_t pidx = (static_cast<int64_t>(r) * a.max_chunks + c) * a.hq + head;
+    const int64_t pidx = static_cast<int64_t>(pslot) * a.hq + head;
     float* pp = a.part_o + pidx * kD;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -292,14 +293,9 @@ __device__ __forceinline__ void zero_row(const DecodeArgs& a, int qrow) {
   }
 }
 
-// Persistent, token-balanced schedule: the flattened token stream of the
-// batch (request r owns [kv_indptr[r], kv_indptr[r+1])) is cut into units of
-// W tokens; workgroup u takes unit u, i.e. the tokens [u W, (u+1) W), which
-// may cover the tail of one request, whole requests and the head of another.
-// Every workgroup gets the same number of tokens, so all stay resident until
-// the end instead of leaving a tail of long requests. A request that spans
-// several units is written as partials (piece p = unit - first unit of the
-// request) and merged by decode_merge_kernel. Waves take the kv heads.
+// Persistent, token-balanced schedule: workgroup u takes the tokens
+// [u W, (u+1) W) of the flattened stream, which may cover the tail of one
+// request, whole requests and the head of another. Waves take the kv heads.
 // Budget 128 VGPRs (up to 4 waves per SIMD, above the ~2 the schedule keeps
 // resident): a tighter budget spills, and scratch traffic in the step loop
 // costs ~9%.
@@ -314,6 +310,9 @@ __global__ void __launch_bounds__(kMaxKvHeads * kWave)
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform per wave
   const bool last_unit = tok1 == total;
+  // The merge kernel, stream-ordered after this launch, reports capacity
+  // overflows; every launch starts from a clear status.
+  if (u == 0 && threadIdx.x == 0) *a.status = SGL_OK;
 
   if (tok0 >= tok1) {
     // Past the end of the token stream: only an all-empty batch needs work.
@@ -350,65 +349,65 @@ __global__ void __launch_bounds__(kMaxKvHeads * kWave)
     const int s0 = max(rb, tok0);
     const int s1 = min(re, tok1);
     if (s1 <= s0) continue;
-    const int first_unit = rb / W;
-    const int pieces = (re - 1) / W - first_unit + 1;
-    decode_head(a, L, sidx + (s0 - tok0), r, u - first_unit, pieces, wave, s1 - s0, qrow, lane);
+    const bool whole = rb >= tok0 && re <= tok1;
+    const int pslot = 2 * u + (rb > tok0 ? 1 : 0);
+    decode_head(a, L, sidx + (s0 - tok0), pslot, whole, wave, s1 - s0, qrow, lane);
   }
 }
 
-// Combines the chunk partials of every split request: one workgroup per
-// (request, kv head) handles its G heads. The chunk lse values are fetched
-// in parallel into LDS and turned into weights; then each thread owns 4
-// consecutive d of one head and streams the chunk partials (16-byte loads,
-// several in flight).
+// Folds the partials of every split request: one workgroup per (kv head,
+// request) handles its G heads; each thread owns 4 consecutive d of one head
+// and runs an online log-sum-exp merge over the request's pieces in order
+// (any number of pieces, 16-byte loads, several in flight). Requests reaching
+// past the plan's token capacity get NaN rows and the CAPACITY status.
 __global__ void __launch_bounds__(256) decode_merge_kernel(DecodeArgs a) {
   const int h = blockIdx.x;
   const int r = blockIdx.y;
   const int rb = a.kv_indptr[r];
   const int re = a.kv_indptr[r + 1];
-  if (re <= rb) return;
-  const int W = unit_tokens(a, a.kv_indptr[a.batch]);
-  // Pieces of request r (never more than the workspace holds).
-  const int nch = min((re - 1) / W - rb / W + 1, a.max_chunks);
-  if (nch <= 1) return;
-  __shared__ float sh_w[kMaxChunks][kMaxGroup];
   const int G = a.group;
   const int qrow = a.q_indptr ? a.q_indptr[r] : r;
-  const int64_t base = static_cast<int64_t>(r) * a.max_chunks * a.hq + h * G;
-  for (int e = threadIdx.x; e < nch * G; e += blockDim.x) {
-    const int cc = e / G;
-    const int g = e - cc * G;
-    sh_w[cc][g] = a.part_lse[base + cc * a.hq + g];
-  }
-  __syncthreads();
-  if (threadIdx.x < G) {
-    const int g = threadIdx.x;
-    float mx = -INFINITY;
-    for (int cc = 0; cc < nch; ++cc) mx = fmaxf(mx, sh_w[cc][g]);
-    float den = 0.f;
-    for (int cc = 0; cc < nch; ++cc) {
-      const float lse = sh_w[cc][g];
-      const float w = lse == -INFINITY ? 0.f : exp2f(lse - mx);
-      sh_w[cc][g] = w;
-      den += w;
+  const int W = unit_tokens(a, a.kv_indptr[a.batch]);
+  if (static_cast<int64_t>(re) > static_cast<int64_t>(a.num_units) * W) {
+    for (int e = threadIdx.x; e < G * (kD / 4); e += blockDim.x) {
+      const int g = e / (kD / 4);
+      const int d4 = (e - g * (kD / 4)) * 4;
+      uint16_t* op = a.o + static_cast<int64_t>(qrow) * a.o_st +
+                     static_cast<int64_t>(h * G + g) * a.o_sh + d4;
+      *reinterpret_cast<u32x2_t*>(op) = u32x2_t{0x7fc07fc0u, 0x7fc07fc0u};  // bf16 NaN
     }
-    const float inv = den > 0.f ? 1.0f / den : 0.f;
-    for (int cc = 0; cc < nch; ++cc) sh_w[cc][g] *= inv;
+    if (threadIdx.x == 0) *a.status = SGL_ERR_CAPACITY;  // same value from every writer
+    return;
   }
-  __syncthreads();
+  if (re <= rb) return;
+  const int u0 = rb / W;
+  const int u1 = (re - 1) / W;
+  if (u0 == u1) return;  // whole request, written by the decode kernel
   for (int e = threadIdx.x; e < G * (kD / 4); e += blockDim.x) {
     const int g = e / (kD / 4);
     const int d4 = (e - g * (kD / 4)) * 4;
+    const int head = h * G + g;
+    float m = -INFINITY, den = 0.f;
     f32x4_t accm = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 8
-    for (int cc = 0; cc < nch; ++cc) {
-      const f32x4_t v =
-          *reinterpret_cast<const f32x4_t*>(a.part_o + (base + cc * a.hq + g) * kD + d4);
-      accm += v * sh_w[cc][g];
+#pragma unroll 4
+    for (int u = u0; u <= u1; ++u) {
+      const int slot = 2 * u + (u == u0 && rb > u0 * W ? 1 : 0);
+      const int64_t pidx = static_cast<int64_t>(slot) * a.hq + head;
+      const float lse = a.part_lse[pidx];
+      const f32x4_t v = *reinterpret_cast<const f32x4_t*>(a.part_o + pidx * kD + d4);
+      if (lse == -INFINITY) continue;
+      const float mn = fmaxf(m, lse);
+      const float so = exp2f(m - mn);   // 0 on the first piece (m = -inf)
+      const float sn = exp2f(lse - mn);
+      den = den * so + sn;
+      accm = accm * so + v * sn;
+      m = mn;
     }
+    const float inv = den > 0.f ? 1.0f / den : 0.f;
     uint16_t* op = a.o + static_cast<int64_t>(qrow) * a.o_st +
-                   static_cast<int64_t>(h * G + g) * a.o_sh + d4;
-    u32x2_t packed = {pack_bf16x2(accm[0], accm[1]), pack_bf16x2(accm[2], accm[3])};
+                   static_cast<int64_t>(head) * a.o_sh + d4;
+    u32x2_t packed = {pack_bf16x2(accm[0] * inv, accm[1] * inv),
+                      pack_bf16x2(accm[2] * inv, accm[3] * inv)};
     *reinterpret_cast<u32x2_t*>(op) = packed;
   }
 }
@@ -443,13 +442,12 @@ extern "C" int sgl_decode_plan(const int32_t* kv_indptr_host, int batch_size, in
   const int group = num_qo_heads / num_kv_heads;
   if (head_dim != kD || group > kMaxGroup || num_kv_heads > kMaxKvHeads)
     return SGL_ERR_UNSUPPORTED;
+  if (kv_indptr_host[0] != 0) return SGL_ERR_INVALID_ARG;
   int64_t total = 0;
-  int max_len = 0;
   for (int r = 0; r < batch_size; ++r) {
     const int len = kv_indptr_host[r + 1] - kv_indptr_host[r];
-    if (len < 0 || kv_indptr_host[r] < 0) return SGL_ERR_INVALID_ARG;
+    if (len < 0) return SGL_ERR_INVALID_ARG;
     total += len;
-    max_len = len > max_len ? len : max_len;
   }
   if (total > 0x7fffffff) return SGL_ERR_UNSUPPORTED;
   // One work unit per resident workgroup (one wave per kv head), about 8
@@ -459,76 +457,85 @@ extern "C" int sgl_decode_plan(const int32_t* kv_indptr_host, int batch_size, in
   // hiding), and 4 starve long contexts.
   int units_per_cu = 8 / num_kv_heads > 1 ? 8 / num_kv_heads : 1;
   const int64_t units_target = static_cast<int64_t>(device_cu_count()) * units_per_cu;
-  constexpr int64_t kMinUnit = 64;  // keeps per-unit set-up small next to the stream
   auto round16 = [](int64_t x) { return (x + kStep - 1) / kStep * kStep; };
-  // W_min bounds the pieces of the longest request: ceil(L / W) + 1 <= kMaxChunks.
-  int64_t w_min = round16((static_cast<int64_t>(max_len) + kMaxChunks - 2) / (kMaxChunks - 1));
-  if (w_min < kMinUnit) w_min = kMinUnit;
-  if (w_min > kMaxChunkTokens) return SGL_ERR_UNSUPPORTED;
   int64_t W = round16((total + units_target - 1) / units_target);
-  if (W < w_min) W = w_min;
+  if (W < kMinUnit) W = kMinUnit;
   if (W > kMaxChunkTokens) W = kMaxChunkTokens;
   const int64_t units = total > 0 ? (total + W - 1) / W : 1;
-  // The device picks w = clamp(round16(ceil(total / units)), w_min, W) <= W.
+  if (units > 0x7fffffff / 2) return SGL_ERR_UNSUPPORTED;
+  // The device picks w = clamp(round16(ceil(total / units)), W_min, W) <= W.
   int64_t w_dev = round16((total + units - 1) / units);
-  if (w_dev < w_min) w_dev = w_min;
+  if (w_dev < kMinUnit) w_dev = kMinUnit;
   if (w_dev > W) w_dev = W;
-  int max_pieces = 1;
-  for (int r = 0; r < batch_size; ++r) {
+  int split = 0;
+  for (int r = 0; r < batch_size && !split; ++r) {
     const int rb = kv_indptr_host[r], re = kv_indptr_host[r + 1];
-    if (re > rb) {
-      const int pieces = static_cast<int>((re - 1) / w_dev - rb / w_dev + 1);
-      max_pieces = pieces > max_pieces ? pieces : max_pieces;
-    }
+    if (re > rb && (re - 1) / w_dev != rb / w_dev) split = 1;
   }
-  // Capacity for any batch no longer than this one (any unit size >= w_min).
-  const int cap_pieces =
-      max_len > 0 ? static_cast<int>((max_len + w_min - 1) / w_min) + 1 : 1;
   plan->kv_chunk_size = static_cast<int32_t>(W);
-  plan->min_chunk_size = static_cast<int32_t>(w_min);
-  plan->max_chunks = cap_pieces;
-  plan->split_kv = max_pieces > 1 ? 1 : 0;
+  plan->min_chunk_size = kMinUnit;
   plan->num_units = static_cast<int32_t>(units);
+  plan->split_kv = split;
   plan->batch_size = batch_size;
   plan->num_qo_heads = num_qo_heads;
   plan->num_kv_heads = num_kv_heads;
   plan->head_dim = head_dim;
-  plan->workspace_bytes =
-      plan->max_chunks > 1 ? workspace_layout(batch_size, plan->max_chunks, num_qo_heads).total : 0;
+  plan->max_total_tokens = units * W;
+  plan->workspace_bytes = workspace_layout(static_cast<int>(units), num_qo_heads).total;
   return SGL_OK;
 }
 
-extern "C" int sgl_paged_decode(const sgl_decode_plan_t* plan, const void* q,
-                                int64_t q_stride_token, int64_t q_stride_head,
-                                const void* k_cache, const void* v_cache, int64_t kv_stride_slot,
-                                int64_t kv_stride_head, const int32_t* indices,
-                                const int32_t* kv_indptr, const int32_t* q_indptr,
-                                int batch_size, int num_qo_heads, int num_kv_heads, int head_dim,
-                                float sm_scale, void* o, int64_t o_stride_token,
-                                int64_t o_stride_head, void* workspace, int64_t workspace_bytes,
-                                void* stream) {
+extern "C" int sgl_decode_plan_check(const sgl_decode_plan_t* plan,
+                                     const int32_t* kv_indptr_host, int batch_size) {
+  if (!plan || !kv_indptr_host || batch_size < 0) return SGL_ERR_INVALID_ARG;
+  if (batch_size > plan->batch_size) return SGL_ERR_CAPACITY;
+  if (kv_indptr_host[0] != 0) return SGL_ERR_INVALID_ARG;
+  for (int r = 0; r < batch_size; ++r)
+    if (kv_indptr_host[r + 1] < kv_indptr_host[r]) return SGL_ERR_INVALID_ARG;
+  if (static_cast<int64_t>(kv_indptr_host[batch_size]) > plan->max_total_tokens)
+    return SGL_ERR_CAPACITY;
+  return SGL_OK;
+}
+
+extern "C" int sgl_decode_status(const void* workspace, int32_t* status, void* stream) {
+  if (!workspace || !status) return SGL_ERR_INVALID_ARG;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t e = hipMemcpyAsync(status, workspace, sizeof(int32_t), hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  return e == hipSuccess ? SGL_OK : static_cast<int>(e);
+}
+
+namespace {
+
+// Checks shared by the decode entry points; fills the kernel arguments
+// except the workspace pointers.
+int decode_args(const sgl_decode_plan_t* plan, const void* q, int64_t q_stride_token,
+                int64_t q_stride_head, const void* k_cache, const void* v_cache,
+                int64_t kv_stride_slot, int64_t kv_stride_head, const int32_t* indices,
+                const int32_t* kv_indptr, const int32_t* q_indptr, int batch_size,
+                int num_qo_heads, int num_kv_heads, int head_dim, float sm_scale, void* o,
+                int64_t o_stride_token, int64_t o_stride_head, DecodeArgs& a) {
   if (!plan || batch_size < 0 || num_qo_heads <= 0 || num_kv_heads <= 0)
     return SGL_ERR_INVALID_ARG;
-  if (batch_size == 0) return SGL_OK;
   if (!q || !k_cache || !v_cache || !indices || !kv_indptr || !o) return SGL_ERR_INVALID_ARG;
   if (num_qo_heads % num_kv_heads != 0) return SGL_ERR_INVALID_ARG;
   const int group = num_qo_heads / num_kv_heads;
   if (head_dim != kD || group > kMaxGroup || num_kv_heads > kMaxKvHeads) return SGL_ERR_UNSUPPORTED;
   if (plan->kv_chunk_size <= 0 || plan->kv_chunk_size % kStep != 0 ||
       plan->min_chunk_size <= 0 || plan->min_chunk_size > plan->kv_chunk_size ||
-      plan->kv_chunk_size > kMaxChunkTokens || plan->max_chunks <= 0 ||
-      plan->max_chunks > kMaxChunks)
+      plan->kv_chunk_size > kMaxChunkTokens || plan->num_units <= 0 ||
+      plan->num_units > 0x7fffffff / 2 ||
+      plan->max_total_tokens != static_cast<int64_t>(plan->num_units) * plan->kv_chunk_size ||
+      plan->workspace_bytes != workspace_layout(plan->num_units, plan->num_qo_heads).total)
     return SGL_ERR_INVALID_ARG;
   if (batch_size > plan->batch_size || num_qo_heads != plan->num_qo_heads ||
       num_kv_heads != plan->num_kv_heads)
     return SGL_ERR_CAPACITY;
-  if (plan->max_chunks > 1 && (workspace == nullptr || workspace_bytes < plan->workspace_bytes))
-    return SGL_ERR_CAPACITY;
+  // Output rows are written with 16-byte stores (whole requests).
   if (q_stride_head % 8 || q_stride_token % 8 || kv_stride_slot % 8 || kv_stride_head % 8 ||
-      o_stride_token % 8 || o_stride_head % 4 || !aligned16(q) || !aligned16(k_cache) ||
-      !aligned16(v_cache) || !aligned16(o) || (workspace && !aligned16(workspace)))
+      o_stride_token % 8 || o_stride_head % 8 || !aligned16(q) || !aligned16(k_cache) ||
+      !aligned16(v_cache) || !aligned16(o))
     return SGL_ERR_ALIGNMENT;
-  DecodeArgs a;
   a.q = static_cast<const uint16_t*>(q);
   a.q_st = q_stride_token;
   a.q_sh = q_stride_head;
@@ -548,27 +555,55 @@ extern "C" int sgl_paged_decode(const sgl_decode_plan_t* plan, const void* q,
   a.o_sh = o_stride_head;
   a.chunk = plan->kv_chunk_size;
   a.chunk_min = plan->min_chunk_size;
-  a.max_chunks = plan->max_chunks;
   a.batch = batch_size;
   a.num_units = plan->num_units;
-  if (plan->max_chunks > 1) {
-    const WorkspaceLayout w = workspace_layout(plan->batch_size, plan->max_chunks, num_qo_heads);
-    char* base = static_cast<char*>(workspace);
-    a.part_o = reinterpret_cast<float*>(base + w.part_o_off);
-    a.part_lse = reinterpret_cast<float*>(base + w.part_lse_off);
-  } else {
-    a.part_o = nullptr;
-    a.part_lse = nullptr;
-  }
-  hipStream_t s = static_cast<hipStream_t>(stream);
+  return SGL_OK;
+}
+
+// Points the kernel arguments at a workspace of the plan's layout.
+void bind_workspace(DecodeArgs& a, const sgl_decode_plan_t* plan, void* workspace) {
+  const WorkspaceLayout w = workspace_layout(plan->num_units, plan->num_qo_heads);
+  char* base = static_cast<char*>(workspace);
+  a.status = reinterpret_cast<int32_t*>(base);
+  a.part_o = reinterpret_cast<float*>(base + w.part_o_off);
+  a.part_lse = reinterpret_cast<float*>(base + w.part_lse_off);
+}
+
+// Decode launch + merge launch on one stream.
+int launch_decode(const DecodeArgs& a, const sgl_decode_plan_t* plan, hipStream_t s) {
   const dim3 grid(plan->num_units);
-  const dim3 block(num_kv_heads * kWave);
-  const size_t lds = static_cast<size_t>(num_kv_heads) * sizeof(WaveLds) +
-                    static_cast<size_t>(plan->kv_chunk_size) * sizeof(int32_t);
-  if (plan->num_units <= 0) return SGL_ERR_INVALID_ARG;
+  const dim3 block(a.hkv * kWave);
+  const size_t lds = static_cast<size_t>(a.hkv) * sizeof(WaveLds) +
+                     static_cast<size_t>(plan->kv_chunk_size) * sizeof(int32_t);
   hipLaunchKernelGGL(paged_decode_kernel, grid, block, lds, s, a);
   int st = launch_status();
-  if (st != SGL_OK || plan->max_chunks <= 1) return st;
-  hipLaunchKernelGGL(decode_merge_kernel, dim3(num_kv_heads, batch_size), dim3(256), 0, s, a);
+  if (st != SGL_OK) return st;
+  // Always launched: besides folding split requests it is what reports a
+  // batch that exceeds the plan.
+  hipLaunchKernelGGL(decode_merge_kernel, dim3(a.hkv, a.batch), dim3(256), 0, s, a);
   return launch_status();
+}
+
+}  // namespace
+
+extern "C" int sgl_paged_decode(const sgl_decode_plan_t* plan, const void* q,
+                                int64_t q_stride_token, int64_t q_stride_head,
+                                const void* k_cache, const void* v_cache, int64_t kv_stride_slot,
+                                int64_t kv_stride_head, const int32_t* indices,
+                                const int32_t* kv_indptr, const int32_t* q_indptr,
+                                int batch_size, int num_qo_heads, int num_kv_heads, int head_dim,
+                                float sm_scale, void* o, int64_t o_stride_token,
+                                int64_t o_stride_head, void* workspace, int64_t workspace_bytes,
+                                void* stream) {
+  if (!plan || batch_size < 0) return SGL_ERR_INVALID_ARG;
+  if (batch_size == 0) return SGL_OK;
+  DecodeArgs a;
+  int st = decode_args(plan, q, q_stride_token, q_stride_head, k_cache, v_cache, kv_stride_slot,
+                       kv_stride_head, indices, kv_indptr, q_indptr, batch_size, num_qo_heads,
+                       num_kv_heads, head_dim, sm_scale, o, o_stride_token, o_stride_head, a);
+  if (st != SGL_OK) return st;
+  if (workspace == nullptr || workspace_bytes < plan->workspace_bytes) return SGL_ERR_CAPACITY;
+  if (!aligned16(workspace)) return SGL_ERR_ALIGNMENT;
+  bind_workspace(a, plan, workspace);
+  return launch_decode(a, plan, static_cast<hipStream_t>(stream));
 }

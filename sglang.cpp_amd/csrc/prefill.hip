@@ -340,7 +340,21 @@ __global__ void __launch_bounds__(64 * W, 8 / W) paged_prefill_kernel(PrefillArg
   const int kv_len = a.kv_indptr[r + 1] - kv_beg;
   const int G = a.group;
   const int rows = qo_len * G;
-  if (kv_len <= 0) return;
+  if (kv_len <= 0) {
+    // No visible token: zero output rows, as the decode path writes for an
+    // empty request. The item at position 0 of each (request, kv head)
+    // writes the G heads of that kv head for every query token.
+    if (pos == 0)
+      for (int e = threadIdx.x; e < rows * (kD / 8); e += blockDim.x) {
+        const int prow = e / (kD / 8);
+        const int tok = prow / G;
+        const int head = h * G + (prow - tok * G);
+        stg128(a.o + static_cast<int64_t>(qo_beg + tok) * a.o_st +
+                   static_cast<int64_t>(head) * a.o_sh + (e - prow * (kD / 8)) * 8,
+               u32x4_t{0, 0, 0, 0});
+      }
+    return;
+  }
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int c = lane & 31;

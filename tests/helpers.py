@@ -54,3 +54,25 @@ def assert_bf16_close(got: np.ndarray, ref: np.ndarray, atol=1e-6, what: str = "
         raise AssertionError(f"{what}: {int(bad.sum())} of {bad.size} elements differ by more "
                              f"than {max_ulp} bf16 ulp and {atol}; worst at {i}: got "
                              f"{bf16_f32(got)[i]}, ref {bf16_f32(ref)[i]}")
+
+
+def decode_ws_bytes(units: int, hq: int) -> int:
+    """Decode workspace layout: a 256-byte header (status word), then fp32
+    partial outputs [2 units, hq, 128] and log2-sum-exp [2 units, hq], each
+    padded to 256 bytes."""
+    npart = 2 * units * hq
+    return 256 + -(-npart * 512 // 256) * 256 + -(-npart * 4 // 256) * 256
+
+
+def forced_plan(capi, kv_indptr, hq, hkv, unit):
+    """A decode plan with a forced unit size (every unit `unit` tokens), so
+    small batches exercise many split pieces."""
+    plan = capi.decode_plan(kv_indptr, hq, hkv, 128)
+    total = int(kv_indptr[-1])
+    plan.kv_chunk_size = unit
+    plan.min_chunk_size = unit
+    plan.num_units = max(1, -(-total // unit))
+    plan.max_total_tokens = plan.num_units * unit
+    plan.split_kv = 1
+    plan.workspace_bytes = decode_ws_bytes(plan.num_units, hq)
+    return plan

@@ -68,6 +68,12 @@ def test_argument_checks_reject_before_launch():
                                  ctypes.c_float(0.1), 16, 0, 0, None) == -2  # head_dim 64
 
 
+def ws_bytes(units, hq):
+    """Workspace layout: 256-byte header, then fp32 partial o and lse, two slots per unit."""
+    npart = 2 * units * hq
+    return 256 + -(-npart * 512 // 256) * 256 + -(-npart * 4 // 256) * 256
+
+
 def test_decode_plan_host_logic():
     # config 4 shape: 32q / 8kv, ragged lengths
     import numpy as np
@@ -77,30 +83,60 @@ def test_decode_plan_host_logic():
     plan = capi.decode_plan(ip, 32, 8, 128)
     assert plan.kv_chunk_size % 16 == 0 and plan.kv_chunk_size >= 64
     W = plan.kv_chunk_size
-    assert plan.min_chunk_size <= W and plan.min_chunk_size % 16 == 0
+    assert plan.min_chunk_size == 64
     # units cover the token stream exactly
     assert plan.num_units == -(-int(kv.sum()) // W)
-    # the unit size the device picks, and the pieces per request it implies
+    assert plan.max_total_tokens == plan.num_units * W >= int(kv.sum())
+    # the unit size the device picks, and whether some request spans units
     w = min(W, max(plan.min_chunk_size, -(-(-(-int(kv.sum()) // plan.num_units)) // 16) * 16))
     pieces = [(ip[r + 1] - 1) // w - ip[r] // w + 1 for r in range(256)]
-    assert plan.max_chunks >= max(pieces)
-    assert plan.max_chunks == -(-int(kv.max()) // plan.min_chunk_size) + 1 <= 128
     assert plan.split_kv == (max(pieces) > 1)
-    npart = 256 * plan.max_chunks * 32
-    assert plan.workspace_bytes == -(-npart * 512 // 256) * 256 + -(-npart * 4 // 256) * 256
+    # partials: two slots per unit, independent of request lengths
+    assert plan.workspace_bytes == ws_bytes(plan.num_units, 32)
+    assert plan.workspace_bytes < 16 << 20
     # one unit per resident workgroup: 1 per CU at 8 kv heads on 256 CUs
     assert 250 <= plan.num_units <= 260
     # a batch shorter than one unit is a single unit; a request inside it is whole
     plan = capi.decode_plan([0, 20, 52], 16, 8, 128)
     assert plan.num_units == 1 and plan.split_kv == 0
-    # graph-capture style plan: every request at the capture max length; any
-    # shorter replay batch fits its piece capacity
+    # graph-capture style plan: every request at the capture max length
     plan = capi.decode_plan(list(range(0, 8 * 32768 + 1, 32768)), 32, 8, 128)
-    assert (plan.max_chunks - 1) * plan.min_chunk_size >= 32768
-    assert plan.max_chunks <= 128
+    assert plan.max_total_tokens >= 8 * 32768
     with pytest.raises(capi.SglError):
         capi.decode_plan([0, 10], 48, 2, 128)  # group 24 > 16
     with pytest.raises(capi.SglError):
         capi.decode_plan([0, 10], 16, 8, 96)   # head_dim not built
     with pytest.raises(capi.SglError):
         capi.decode_plan([0, 10, 5], 16, 8, 128)  # negative length
+    with pytest.raises(capi.SglError):
+        capi.decode_plan([3, 10], 16, 8, 128)  # kv_indptr[0] != 0
+
+
+def test_decode_plan_check_host():
+    """A plan serves any batch with at most batch_size requests and
+    max_total_tokens tokens, whatever the per-request lengths; beyond it the
+    host check says CAPACITY."""
+    plan = capi.decode_plan([0, 1000, 2000, 3000, 4000], 32, 4, 128)
+    cap = plan.max_total_tokens
+    assert capi.decode_plan_check(plan, [0, 1000, 2000, 3000, 4000]) == 0
+    assert capi.decode_plan_check(plan, [0, cap]) == 0          # one request, all tokens
+    assert capi.decode_plan_check(plan, [0, 1, 2, 3]) == 0
+    assert capi.decode_plan_check(plan, [0, cap + 1]) == -3
+    assert capi.decode_plan_check(plan, [0] * 6) == -3            # 5 requests > 4
+    assert capi.decode_plan_check(plan, [0, 5, 4]) == -1          # negative length
+
+
+def test_paged_decode_rejects_inconsistent_plan():
+    """The launch validates the plan's derived fields before touching the GPU."""
+    plan = capi.decode_plan([0, 100, 300], 16, 8, 128)
+    bad = capi.DecodePlan.from_buffer_copy(plan)
+    bad.max_total_tokens += 16
+    lib = capi.lib()
+    args = lambda pl, ws_bytes, ostride_h=128: (  # noqa: E731
+        ctypes.byref(pl), 16, 16 * 128, 128, 16, 16, 8 * 128, 128, 16, 16, None, 2, 16, 8, 128,
+        ctypes.c_float(0.1), 16, 16 * 128, ostride_h, 16, ws_bytes, None)
+    assert lib.sgl_paged_decode(*args(bad, plan.workspace_bytes)) == -1
+    # workspace smaller than the plan's
+    assert lib.sgl_paged_decode(*args(plan, plan.workspace_bytes - 1)) == -3
+    # output head stride not a multiple of 8 elements (16-byte row stores)
+    assert lib.sgl_paged_decode(*args(plan, plan.workspace_bytes, 132)) == -4

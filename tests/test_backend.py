@@ -337,6 +337,22 @@ def test_backend_mixed_batch_overlap_and_graph_replay(oracle, dev, sb):
         o_eager = s.backend.forward(s.q, s.k, s.v, 0, s.batch)
         torch.cuda.synchronize()
         assert torch.equal(o_graph.view(torch.int16), o_eager.view(torch.int16)), f"replay {it}"
+    # An eager decode batch whose plan needs a larger split workspace than the
+    # one the graph recorded: the backend grows its workspace, and the graph's
+    # buffer must stay alive and private to it.
+    big = sb.Batch(False, [sb.Req(1, 2999, 3000) for _ in range(200)],
+                   torch.full((200,), 2999, dtype=torch.int32, device=dev),
+                   torch.zeros(200, dtype=torch.int32, device=dev))
+    s.backend.prepare_metadata(big)
+    assert big.decode_plan()["num_units"] > 100
+    g = _gen(dev, 55)
+    s.backend.attend(_randn((200, 32 * D), dev, g), 0, big)
+    torch.cuda.synchronize()
+    o_graph.zero_()
+    graph.replay()
+    o_eager = s.backend.forward(s.q, s.k, s.v, 0, s.batch)
+    torch.cuda.synchronize()
+    assert torch.equal(o_graph.view(torch.int16), o_eager.view(torch.int16)), "after growth"
 
 
 @pytest.mark.gpu

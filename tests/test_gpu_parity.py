@@ -14,8 +14,8 @@ import pytest
 import torch
 
 from conftest import capi, wl
-from helpers import (assert_attn_close, assert_bf16_close, bf16_f32, bf16_ulp_dist, from_u16,
-                     u16)
+from helpers import (assert_attn_close, assert_bf16_close, bf16_f32, bf16_ulp_dist,
+                     forced_plan, from_u16, u16)
 
 pytestmark = pytest.mark.gpu
 
@@ -308,15 +308,10 @@ def test_decode_forced_split_and_q_indptr(oracle, dev):
     rng = np.random.default_rng(12)
     lens = [1000, 64, 1]
     b = wl.make_paged_batch(rng, [x - 1 for x in lens], lens, page_size=1, decode=True)
-    plan = capi.decode_plan(b.kv_indptr, 16, 8, 128)
-    # 128-token units: ceil(1065 / 128) = 9 units; a 1000-token request spans
-    # at most ceil(1000 / 128) + 1 = 9 pieces.
-    plan.kv_chunk_size = 128
-    plan.min_chunk_size = 128
-    plan.num_units = 9
-    plan.max_chunks = 9
-    plan.split_kv = 1
-    plan.workspace_bytes = 3 * 9 * 16 * (128 + 1) * 4 + 4096  # partial o and lse, padding
+    # 128-token units: ceil(1065 / 128) = 9 units; the 1000-token request
+    # spans 9 of them.
+    plan = forced_plan(capi, b.kv_indptr, 16, 8, 128)
+    assert plan.num_units == 9
     qip = np.array([4, 0, 2], np.int32)
     q, kc, vc, o, scale, _ = run_decode(dev, b, 16, 8, 128, 13, q_indptr=qip, rows=5, plan=plan)
     ref = oracle.decode(u16(q).copy(), u16(kc), u16(vc), b.indices, b.kv_indptr, scale,
@@ -342,6 +337,76 @@ def test_decode_cfg4_full_size(oracle, dev):
     ref = oracle.decode(u16(q[sample]).copy(), u16(kc), u16(vc), idx, ip, scale)
     assert_attn_close(o[sample].float().cpu().numpy(), ref, what=w.name)
     assert torch.isfinite(o.float()).all()
+
+
+@pytest.mark.parametrize("hq,hkv", [(32, 4), (32, 8)])
+def test_decode_long_context(oracle, dev, hq, hkv):
+    """Config 5's decode lengths: requests of 8K, 16K and 32K tokens beside
+    short ones, so a 32K request spans dozens of units and the merge folds
+    that many pieces."""
+    note(f"decode long context hq={hq} hkv={hkv}")
+    rng = np.random.default_rng(18)
+    lens = [32768, 16384, 8192, 1, 1024, 32768, 77, 20000]
+    b = wl.make_paged_batch(rng, [x - 1 for x in lens], lens, page_size=16, decode=True)
+    q, kc, vc, o, scale, plan = run_decode(dev, b, hq, hkv, 128, 19)
+    assert plan.split_kv
+    W = plan.kv_chunk_size
+    assert -(-32768 // W) >= 16, "a 32K request must span many units"
+    ref = oracle.decode(u16(q).copy(), u16(kc), u16(vc), b.indices, b.kv_indptr, scale)
+    assert_attn_close(o.float().cpu().numpy(), ref, what=f"long decode W={W}")
+
+
+def test_decode_many_pieces(oracle, dev):
+    """64-token units on 32K and 16K requests: 512 + 256 pieces folded by the merge."""
+    note("decode 512-piece merge")
+    rng = np.random.default_rng(20)
+    lens = [32768, 100, 16384, 64, 65]
+    b = wl.make_paged_batch(rng, [x - 1 for x in lens], lens, page_size=16, decode=True)
+    plan = forced_plan(capi, b.kv_indptr, 32, 4, 64)
+    q, kc, vc, o, scale, _ = run_decode(dev, b, 32, 4, 128, 21, plan=plan)
+    ref = oracle.decode(u16(q).copy(), u16(kc), u16(vc), b.indices, b.kv_indptr, scale)
+    assert_attn_close(o.float().cpu().numpy(), ref, what="512-piece merge")
+
+
+def test_decode_plan_exceeded_reports_capacity(oracle, dev):
+    """A plan reused for a longer batch: requests reaching past the plan's
+    token capacity come back as NaN rows with the CAPACITY status, the others
+    are correct; the next call that fits clears the status."""
+    note("decode plan exceeded")
+    rng = np.random.default_rng(22)
+    lens = [100, 40, 500, 30]
+    b = wl.make_paged_batch(rng, [x - 1 for x in lens], lens, page_size=16, decode=True)
+    plan = capi.decode_plan(np.array([0, 100, 200, 300, 400], np.int32), 16, 8, 128)
+    cap = plan.max_total_tokens
+    assert b.kv_indptr[2] <= cap < b.kv_indptr[3]  # requests 2 and 3 reach past it
+    assert capi.decode_plan_check(plan, b.kv_indptr) == -3
+    kc, vc = _pool(dev, b.num_slots, 8, 128, 23)
+    g = gen(dev, 24)
+    q = randn_bf16((4, 16, 128), dev, g)
+    o = torch.zeros((4, 16, 128), device=dev, dtype=torch.bfloat16)
+    ws = capi.decode_workspace(plan, dev)
+    idx = torch.from_numpy(b.indices).to(dev)
+    kvp = torch.from_numpy(b.kv_indptr).to(dev)
+    capi.paged_decode(plan, q, kc, vc, idx, kvp, o, ws)
+    assert capi.decode_status(ws) == -3
+    scale = 1 / math.sqrt(128)
+    ref = oracle.decode(u16(q).copy(), u16(kc), u16(vc), b.indices, b.kv_indptr, scale)
+    got = o.float().cpu().numpy()
+    for r in range(4):
+        if b.kv_indptr[r + 1] > cap:
+            assert np.isnan(got[r]).all(), f"request {r} past capacity must be NaN"
+        else:
+            assert_attn_close(got[r], ref[r], what=f"request {r} within capacity")
+    # more requests than the plan serves: refused on the host
+    plan3 = capi.decode_plan(np.array([0, 100, 200, 300], np.int32), 16, 8, 128)
+    with pytest.raises(capi.SglError):
+        capi.paged_decode(plan3, q, kc, vc, idx, kvp, o, capi.decode_workspace(plan3, dev))
+    # a fitting batch on the same workspace: status cleared, results correct
+    fit = np.array([0, 100, 200, 300, 400], np.int32)
+    capi.paged_decode(plan, q, kc, vc, idx, torch.from_numpy(fit).to(dev), o, ws)
+    assert capi.decode_status(ws) == 0
+    ref = oracle.decode(u16(q).copy(), u16(kc), u16(vc), b.indices, fit, scale)
+    assert_attn_close(o.float().cpu().numpy(), ref, what="fitting batch after overflow")
 
 
 def test_decode_page_permutation_invariance(dev):
@@ -476,3 +541,27 @@ def test_prefill_random_batches(oracle, dev, seed):
     b = wl.make_paged_batch(rng, [int(p) for p in prefix], [int(p + q) for p, q in zip(prefix, qo)],
                             page_size=page)
     check_prefill(oracle, dev, b, hq, hkv, 200 + seed, f"prefill random {seed}")
+
+
+def test_prefill_empty_kv_rows_are_zero(oracle, dev):
+    """A request with no visible kv token gets zero rows (as decode writes for
+    an empty request); its neighbours are unaffected."""
+    note("prefill empty-kv request")
+    rng = np.random.default_rng(60)
+    b = wl.make_paged_batch(rng, [0, 10], [300, 90], page_size=16)
+    hq, hkv = 16, 8
+    kc, vc = _pool(dev, b.num_slots, hkv, 128, 61)
+    g = gen(dev, 62)
+    # request 1 is given 5 query rows and kv_len 0
+    qo = np.array([0, 300, 305], np.int32)
+    kvp = np.array([0, 300, 300], np.int32)
+    q = randn_bf16((305, hq, 128), dev, g)
+    o = torch.full((305, hq, 128), float("nan"), device=dev, dtype=torch.bfloat16)
+    capi.paged_prefill(q, kc, vc, torch.from_numpy(b.indices).to(dev),
+                       torch.from_numpy(qo).to(dev), torch.from_numpy(kvp).to(dev), 300, o)
+    torch.cuda.synchronize()
+    got = o.float().cpu().numpy()
+    assert (got[300:] == 0).all()
+    ref = oracle.prefill(u16(q[:300]).copy(), u16(kc), u16(vc), b.indices[:300], qo[:2], kvp[:2],
+                         1 / math.sqrt(128))
+    assert_attn_close(got[:300], ref, what="neighbour of the empty request")
