@@ -250,6 +250,30 @@ int sgl_paged_decode(const sgl_decode_plan_t* plan, const void* q,
                      int64_t workspace_bytes, void* stream);
 
 /*
+ * sgl_paged_decode without a workspace argument, for callers that cannot
+ * allocate device memory (code under graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). The split partials live in a file-scope
+ * device array of SGL_DECODE_SCRATCH_BYTES (32 MiB) that each GPU holds
+ * until the process ends; plans with workspace_bytes above it get
+ * SGL_ERR_CAPACITY. Nothing is allocated. Calls on one GPU share the array
+ * and must be stream-ordered: calls that overlap on one GPU race. A batch
+ * past the plan's capacity gets NaN rows as in sgl_paged_decode (the status
+ * word is not readable here; check batches with sgl_decode_plan_check).
+ * Replaces: no counterpart in the reference; it exists for callers that
+ *           cannot allocate.
+ */
+int sgl_paged_decode_noalloc(const sgl_decode_plan_t* plan, const void* q,
+                             int64_t q_stride_token, int64_t q_stride_head,
+                             const void* k_cache, const void* v_cache,
+                             int64_t kv_stride_slot, int64_t kv_stride_head,
+                             const int32_t* indices, const int32_t* kv_indptr,
+                             const int32_t* q_indptr, int batch_size,
+                             int num_qo_heads, int num_kv_heads, int head_dim,
+                             float sm_scale, void* o, int64_t o_stride_token,
+                             int64_t o_stride_head, void* stream);
+#define SGL_DECODE_SCRATCH_BYTES (32ll << 20)
+
+/*
  * Reads the status word a decode call left in its workspace (waits for the
  * stream): SGL_OK, or SGL_ERR_CAPACITY when the batch exceeded its plan.
  * Replaces: no device-side counterpart in the reference (FlashInfer's plan

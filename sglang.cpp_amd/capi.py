@@ -75,6 +75,9 @@ _SIGNATURES = {
     "sgl_decode_plan": ([_vp, _i32, _i32, _i32, _i32, ctypes.POINTER(DecodePlan)], _i32),
     "sgl_decode_plan_check": ([ctypes.POINTER(DecodePlan), _vp, _i32], _i32),
     "sgl_decode_status": ([_vp, _vp, _vp], _i32),
+    "sgl_paged_decode_noalloc": ([ctypes.POINTER(DecodePlan), _vp, _i64, _i64, _vp, _vp, _i64,
+                                  _i64, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _f32, _vp, _i64,
+                                  _i64, _vp], _i32),
     "sgl_paged_decode": ([ctypes.POINTER(DecodePlan), _vp, _i64, _i64, _vp, _vp, _i64, _i64,
                           _vp, _vp, _vp, _i32, _i32, _i32, _i32, _f32, _vp, _i64, _i64, _vp,
                           _i64, _vp], _i32),
@@ -438,6 +441,31 @@ def paged_decode(plan: DecodePlan, q: torch.Tensor, k_cache: torch.Tensor,
                                   _p(q_indptr), B, hq, hkv, D, scale, _p(o), o.stride(0),
                                   o.stride(1), _p(workspace), ws_bytes, _stream(dev)),
            "sgl_paged_decode")
+
+
+DECODE_SCRATCH_BYTES = 32 << 20  # SGL_DECODE_SCRATCH_BYTES
+
+
+def paged_decode_noalloc(plan: DecodePlan, q: torch.Tensor, k_cache: torch.Tensor,
+                         v_cache: torch.Tensor, indices: torch.Tensor, kv_indptr: torch.Tensor,
+                         o: torch.Tensor, sm_scale: Optional[float] = None,
+                         q_indptr: Optional[torch.Tensor] = None) -> None:
+    """sgl_paged_decode with the library's own device scratch (no workspace)."""
+    dev = _need_gpu(q, k_cache, v_cache, indices, kv_indptr, o, q_indptr)
+    if q.dtype != torch.bfloat16 or k_cache.dtype != torch.bfloat16 or o.dtype != torch.bfloat16:
+        raise ValueError("decode supports bf16 q / KV / o only")
+    hq, D = q.shape[1], q.shape[2]
+    hkv = k_cache.shape[1]
+    ss, sh = _kv_strides(k_cache)
+    if v_cache.stride() != k_cache.stride():
+        raise ValueError("K and V caches must share strides")
+    B = kv_indptr.shape[0] - 1
+    scale = 1.0 / math.sqrt(D) if sm_scale is None else sm_scale
+    _check(lib().sgl_paged_decode_noalloc(ctypes.byref(plan), _p(q), q.stride(0), q.stride(1),
+                                          _p(k_cache), _p(v_cache), ss, sh, _p(indices),
+                                          _p(kv_indptr), _p(q_indptr), B, hq, hkv, D, scale,
+                                          _p(o), o.stride(0), o.stride(1), _stream(dev)),
+           "sgl_paged_decode_noalloc")
 
 
 def paged_prefill(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,

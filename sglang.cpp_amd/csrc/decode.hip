@@ -35,6 +35,8 @@
 // SGL_ERR_CAPACITY (cleared by every launch).
 #include <math.h>
 
+#include <mutex>
+
 #include "common.h"
 
 namespace sgl {
@@ -605,5 +607,75 @@ extern "C" int sgl_paged_decode(const sgl_decode_plan_t* plan, const void* q,
   if (workspace == nullptr || workspace_bytes < plan->workspace_bytes) return SGL_ERR_CAPACITY;
   if (!aligned16(workspace)) return SGL_ERR_ALIGNMENT;
   bind_workspace(a, plan, workspace);
+  return launch_decode(a, plan, static_cast<hipStream_t>(stream));
+}
+
+// ------------------------------------------------------------------ no-alloc variant
+//
+// Callers that cannot allocate (code under graph capture, tight serving
+// loops) get the decode with its split workspace in a file-scope device
+// array. Each GPU holds its own copy of the array for the life of the
+// process; its device address is looked up once per device and used for
+// every launch (the array's name is only a host-side stand-in). All calls on
+// one GPU share the array: calls that overlap on one GPU (different streams
+// without ordering) race on it.
+
+namespace {
+constexpr int64_t kScratchBytes = 32ll << 20;
+constexpr int kMaxDevices = 64;
+}  // namespace
+
+static __device__ __align__(256) char scratch[kScratchBytes];
+
+static void* g_scratch_ptr[kMaxDevices];
+static std::mutex g_scratch_mu;
+
+// Device address of `scratch` on the current device (looked up on first
+// use with that device current); nullptr with *status set on failure.
+static void* scratch_on_current_device(int* status) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    *status = static_cast<int>(e);
+    return nullptr;
+  }
+  if (dev < 0 || dev >= kMaxDevices) {
+    *status = SGL_ERR_UNSUPPORTED;
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr) {
+      *status = e != hipSuccess ? static_cast<int>(e) : SGL_ERR_INVALID_ARG;
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = ptr;
+  }
+  *status = SGL_OK;
+  return g_scratch_ptr[dev];
+}
+
+extern "C" int sgl_paged_decode_noalloc(const sgl_decode_plan_t* plan, const void* q,
+                                        int64_t q_stride_token, int64_t q_stride_head,
+                                        const void* k_cache, const void* v_cache,
+                                        int64_t kv_stride_slot, int64_t kv_stride_head,
+                                        const int32_t* indices, const int32_t* kv_indptr,
+                                        const int32_t* q_indptr, int batch_size,
+                                        int num_qo_heads, int num_kv_heads, int head_dim,
+                                        float sm_scale, void* o, int64_t o_stride_token,
+                                        int64_t o_stride_head, void* stream) {
+  if (!plan || batch_size < 0) return SGL_ERR_INVALID_ARG;
+  if (batch_size == 0) return SGL_OK;
+  DecodeArgs a;
+  int st = decode_args(plan, q, q_stride_token, q_stride_head, k_cache, v_cache, kv_stride_slot,
+                       kv_stride_head, indices, kv_indptr, q_indptr, batch_size, num_qo_heads,
+                       num_kv_heads, head_dim, sm_scale, o, o_stride_token, o_stride_head, a);
+  if (st != SGL_OK) return st;
+  if (plan->workspace_bytes > kScratchBytes) return SGL_ERR_CAPACITY;
+  void* ws = scratch_on_current_device(&st);
+  if (!ws) return st;
+  bind_workspace(a, plan, ws);
   return launch_decode(a, plan, static_cast<hipStream_t>(stream));
 }
