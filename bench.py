@@ -268,63 +268,112 @@ def setup_mixed(torch, wl, w, dev, layers, seed=0):
 
 # ------------------------------------------------------------------ CPU baseline
 
-def cpu_baseline_decode(wl, w, budget_s=12.0):
-    """The CPU oracle (C, OpenMP) on a bounded sample of the same workload:
-    the first requests of the batch, repeated until ~budget_s of CPU work."""
-    from oracle import oracle as orc
+def _cpu_threads(torch):
+    """LibTorch threads for the CPU legs: the host's CPU share (OMP_NUM_THREADS
+    when set, else the process's CPU affinity)."""
+    n = int(os.environ.get("OMP_NUM_THREADS") or len(os.sched_getaffinity(0)))
+    torch.set_num_threads(max(1, n))
+    return torch.get_num_threads()
+
+
+def _cpu_pool(torch, slots, hkv, D, seed):
+    g = torch.Generator()
+    g.manual_seed(seed)
+    kc = torch.randn((slots, hkv, D), generator=g).to(torch.bfloat16)
+    vc = torch.randn((slots, hkv, D), generator=g).to(torch.bfloat16)
+    return kc, vc, g
+
+
+def cpu_baseline_decode(torch, wl, w, target_s=1.0):
+    """LibTorch-CPU fp32 decode (oracle/torch_cpu.py) on the first n requests
+    of the same workload, n grown until one run takes about target_s;
+    median of 5 runs after a warm-up."""
+    from oracle import torch_cpu as tc
     b, s = w.batch, w.shape
-    rng = np.random.default_rng(1)
-    n = min(16, b.batch_size)
-    lens = b.kv_lens[:n]
-    ip = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
-    slots = int(ip[-1])
-    idx = rng.permutation(slots).astype(np.int32)
+    threads = _cpu_threads(torch)
     hkv, hq, D = s.num_kv_heads, s.num_qo_heads, s.head_dim
-    kc = orc.f32_to_bf16(rng.standard_normal((slots, hkv, D), dtype=np.float32))
-    vc = orc.f32_to_bf16(rng.standard_normal((slots, hkv, D), dtype=np.float32))
-    q = orc.f32_to_bf16(rng.standard_normal((n, hq, D), dtype=np.float32))
     scale = 1.0 / math.sqrt(D)
-    orc.decode(q, kc, vc, idx, ip, scale)  # warm
-    reps, t0 = 0, time.perf_counter()
+    lens_all = b.kv_lens.astype(np.int64)
+    n = min(32, b.batch_size)
     while True:
-        orc.decode(q, kc, vc, idx, ip, scale)
-        reps += 1
+        lens = lens_all[:n]
+        ip = torch.from_numpy(np.concatenate([[0], np.cumsum(lens)]))
+        slots = int(ip[-1])
+        kc, vc, g = _cpu_pool(torch, slots, hkv, D, 3)
+        idx = torch.randperm(slots, generator=g)
+        q = torch.randn((n, hq, D), generator=g).to(torch.bfloat16)
+        t0 = time.perf_counter()
+        tc.decode(q, kc, vc, idx, ip, scale)
         el = time.perf_counter() - t0
-        if el >= budget_s or reps >= 1000:
+        if el >= target_s / 2 or n == b.batch_size:
             break
+        n = min(b.batch_size, max(n + 1, int(n * target_s / max(el, 1e-3))))
+    med, runs = tc.median_time(lambda: tc.decode(q, kc, vc, idx, ip, scale))
     nbytes = wl.attention_bytes(s, np.ones(n, np.int64), lens, b.page_size)
-    return {"value": round(nbytes * reps / el / 1e9, 3), "unit": "GB/s",
-            "cores": orc.threads(), "kind": "port",
-            "sample": f"oracle_decode on the first {n} requests of {w.name} "
-                      f"(sum kv {slots} tokens), {reps} repetitions in {el:.1f} s"}
+    info = tc.host_info()
+    return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "kind": "port", "cpu_model": info["cpu_model"], "median_s": round(med, 4),
+            "runs_s": [round(t, 4) for t in runs],
+            "sample": f"LibTorch-CPU fp32 decode (oracle/torch_cpu.py) on the first {n} of "
+                      f"{b.batch_size} requests of {w.name} (sum kv {slots} tokens), median "
+                      f"of 5 runs after 1 warm-up, {threads} threads"}
 
 
-def cpu_baseline_prefill(wl, w, budget_s=10.0):
-    from oracle import oracle as orc
+def cpu_baseline_prefill(torch, wl, w):
+    """LibTorch-CPU fp32 causal prefill on the whole workload, median of 5."""
+    from oracle import torch_cpu as tc
     b, s = w.batch, w.shape
-    rng = np.random.default_rng(2)
-    n = min(2, b.batch_size)
-    qo, kv = b.qo_lens[:n], b.kv_lens[:n]
-    qip = np.concatenate([[0], np.cumsum(qo)]).astype(np.int32)
-    kip = np.concatenate([[0], np.cumsum(kv)]).astype(np.int32)
-    slots = int(kip[-1])
-    idx = rng.permutation(slots).astype(np.int32)
+    threads = _cpu_threads(torch)
     hkv, hq, D = s.num_kv_heads, s.num_qo_heads, s.head_dim
-    kc = orc.f32_to_bf16(rng.standard_normal((slots, hkv, D), dtype=np.float32))
-    vc = orc.f32_to_bf16(rng.standard_normal((slots, hkv, D), dtype=np.float32))
-    q = orc.f32_to_bf16(rng.standard_normal((int(qip[-1]), hq, D), dtype=np.float32))
+    kc, vc, g = _cpu_pool(torch, b.num_slots, hkv, D, 4)
+    q = torch.randn((int(b.qo_indptr[-1]), hq, D), generator=g).to(torch.bfloat16)
+    idx = torch.from_numpy(b.indices.astype(np.int64))
+    qip, kip = b.qo_indptr.astype(np.int64), b.kv_indptr.astype(np.int64)
     scale = 1.0 / math.sqrt(D)
-    reps, t0 = 0, time.perf_counter()
-    while True:
-        orc.prefill(q, kc, vc, idx, qip, kip, scale)
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= budget_s or reps >= 1000:
-            break
-    flops = wl.attention_flops(s, qo, kv, causal=True)
-    return {"value": round(flops * reps / el / 1e12, 5), "unit": "TFLOP/s",
-            "cores": orc.threads(), "kind": "port",
-            "sample": f"oracle_prefill on {n} requests of {w.name}, {reps} reps in {el:.1f} s"}
+    med, runs = tc.median_time(lambda: tc.prefill(q, kc, vc, idx, qip, kip, scale))
+    flops = wl.attention_flops(s, b.qo_lens, b.kv_lens, causal=True)
+    return {"value": round(flops / med / 1e12, 5), "unit": "TFLOP/s", "cores": threads,
+            "kind": "port", "cpu_model": tc.host_info()["cpu_model"], "median_s": round(med, 4),
+            "runs_s": [round(t, 4) for t in runs],
+            "sample": f"LibTorch-CPU fp32 causal prefill (oracle/torch_cpu.py), all of {w.name}, "
+                      f"median of 5 runs after 1 warm-up, {threads} threads"}
+
+
+def cpu_baseline_mixed(torch, wl, w):
+    """Config 5 on the CPU: ONE layer (the 64 decode rows and the 2048-token
+    chunk, LibTorch-CPU fp32), median of 5, scaled x layers as stated."""
+    from oracle import torch_cpu as tc
+    b, s = w.batch, w.shape
+    threads = _cpu_threads(torch)
+    hkv, hq, D = s.num_kv_heads, s.num_qo_heads, s.head_dim
+    kc, vc, g = _cpu_pool(torch, b.num_slots, hkv, D, 5)
+    rows = int(b.qo_indptr[-1])
+    q = torch.randn((rows, hq, D), generator=g).to(torch.bfloat16)
+    qo, kvl = b.qo_lens, b.kv_lens
+    dec = np.nonzero(qo == 1)[0]
+    pre = np.nonzero(qo > 1)[0]
+    idx = torch.from_numpy(b.indices.astype(np.int64))
+    kip = b.kv_indptr.astype(np.int64)
+    scale = 1.0 / math.sqrt(D)
+    # decode rows keep their own kv ranges; the chunk is a one-request prefill
+    dec_ip = np.concatenate([[0], np.cumsum(kvl[dec])]).astype(np.int64)
+    dec_idx = torch.cat([idx[kip[r]:kip[r + 1]] for r in dec])
+    dec_q = q[torch.from_numpy(b.qo_indptr[dec].astype(np.int64))]
+    pre_rows = [(int(b.qo_indptr[r]), int(b.qo_indptr[r + 1])) for r in pre]
+
+    def layer():
+        tc.decode(dec_q, kc, vc, dec_idx, dec_ip, scale)
+        for (q0, q1), r in zip(pre_rows, pre):
+            tc.prefill(q[q0:q1], kc, vc, idx[kip[r]:kip[r + 1]], np.array([0, q1 - q0]),
+                       np.array([0, kvl[r]]), scale)
+
+    med, runs = tc.median_time(layer)
+    return {"ms_per_step": round(med * 1e3 * w.layers, 2), "unit": "ms per 48-layer step",
+            "ms_per_layer": round(med * 1e3, 2), "cores": threads, "kind": "port",
+            "cpu_model": tc.host_info()["cpu_model"], "runs_s": [round(t, 4) for t in runs],
+            "sample": f"LibTorch-CPU fp32, one layer of {w.name} (64 decode rows + the "
+                      f"2048-token chunk), median of 5 runs after 1 warm-up, scaled x{w.layers} "
+                      f"layers, {threads} threads"}
 
 
 # ------------------------------------------------------------------ main
@@ -507,9 +556,24 @@ def main():
     cpu = None
     if not args.no_cpu:
         if args.workload in ("cfg1", "cfg4"):
-            cpu = cpu_baseline_decode(wl, w)
+            cpu = cpu_baseline_decode(torch, wl, w)
         elif args.workload == "cfg2":
-            cpu = cpu_baseline_prefill(wl, w)
+            cpu = cpu_baseline_prefill(torch, wl, w)
+        elif args.workload == "cfg5":
+            cpu = cpu_baseline_mixed(torch, wl, w)
+        if args.workload == "cfg4" and not args.no_extra:
+            # the other CPU legs of the plan, beside their GPU lines in extra
+            for name, fn in (("cfg2", lambda: cpu_baseline_prefill(torch, wl,
+                                                                   wl.cfg2_prefill_prefix())),
+                             ("cfg5", lambda: cpu_baseline_mixed(torch, wl,
+                                                                 wl.cfg5_mixed(layers=48)))):
+                try:
+                    rec = fn()
+                except Exception as e:  # report, keep the headline line
+                    rec = {"error": repr(e)}
+                if name in extra:
+                    extra[name]["cpu_baseline"] = rec
+                print(f"[bench] cpu {name}: {json.dumps(rec)}", file=sys.stderr, flush=True)
 
     if "GB/s" in head and args.workload != "cfg2":
         value, unit = head["GB/s"], "GB/s"

@@ -100,6 +100,26 @@ int sgl_write_token_pool(int32_t* pool, int64_t rows, int64_t stride,
                          int64_t count, void* stream);
 
 /*
+ * Page allocation -> token-granular page table, on the device. The
+ * allocations alloc_info[a] = (table_idx, first_page, last_page), int32
+ * [num_allocs, 3], take consecutive entries of page_starts (the slot of each
+ * allocated page's first token, num_pages of them, in allocation order);
+ * page p of allocation a writes
+ *   page_table[table_idx * stride + p * page_size + i] = page_start + i,
+ * i < page_size, skipping out-of-range rows and columns as
+ * sgl_write_token_pool does. Pages beyond what the allocations take are
+ * ignored; the caller keeps sum(last_page - first_page) == num_pages, as the
+ * reference checks on the host. At most 8192 allocations per call.
+ * Replaces: CacheManager::write_page_table + pages_to_tokens
+ *           (src/scheduler/prefill.cc:144-187, :103-119): the host expansion
+ *           loop and its three token-sized H2D copies.
+ */
+int sgl_write_page_table(int32_t* page_table, int64_t rows, int64_t stride,
+                         int64_t cols, const int32_t* page_starts, int64_t num_pages,
+                         const int32_t* alloc_info, int num_allocs, int page_size,
+                         void* stream);
+
+/*
  * out[i] = table[req_indices[i] * stride + positions[i]] (0 when out of range).
  * Replaces: gather_int32_2d (src/kernels/token_pool.cu:95-133, kernel :31-49).
  */

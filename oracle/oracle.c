@@ -118,6 +118,32 @@ void oracle_pages_to_tokens(const int32_t* page_starts, int64_t npages, int page
     for (int i = 0; i < page_size; ++i) tokens[p * page_size + i] = page_starts[p] + i;
 }
 
+/* CacheManager::write_page_table (src/scheduler/prefill.cc:144-187): the
+ * allocations, in order, take consecutive entries of page_starts; page p of
+ * allocation (table_idx, first_page, last_page) writes positions
+ * p*P .. p*P+P-1 of row table_idx with page_start + 0 .. P-1, through the
+ * token-pool write (out-of-range rows / columns skipped, token_pool.cu:10-29).
+ * Returns the number of page starts consumed (the reference checks that it
+ * equals npages).                                                         */
+int64_t oracle_write_page_table(int32_t* table, int64_t rows, int64_t stride, int64_t cols,
+                                const int32_t* page_starts, int64_t npages,
+                                const int32_t* alloc, int64_t nalloc, int page_size) {
+  int64_t used = 0;
+  for (int64_t a = 0; a < nalloc; ++a) {
+    const int32_t row = alloc[3 * a], first = alloc[3 * a + 1], last = alloc[3 * a + 2];
+    for (int32_t page = first; page < last; ++page) {
+      if (used >= npages) return -1;
+      const int32_t start = page_starts[used++];
+      for (int i = 0; i < page_size; ++i) {
+        const int32_t tok = start + i;
+        const int32_t pos = page * page_size + i;
+        oracle_write_token_pool(table, rows, stride, cols, &row, &pos, &tok, 1);
+      }
+    }
+  }
+  return used;
+}
+
 /* ---------- RoPE cache: src/layers/rotary_embedding.cu:75-94 ---------- */
 
 void oracle_cos_sin_cache(float* cos_cache, float* sin_cache, int64_t max_pos, int rotary_dim,

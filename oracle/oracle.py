@@ -116,6 +116,17 @@ def gather_int32_2d(table, req, pos) -> np.ndarray:
     return out
 
 
+def write_page_table(table, page_starts, alloc, page_size: int) -> int:
+    """In place on the int32 [rows, cols] table; alloc is [n, 3] (table_idx,
+    first_page, last_page). Returns the page starts consumed (-1 if short)."""
+    ps = np.ascontiguousarray(page_starts, np.int32)
+    al = np.ascontiguousarray(np.asarray(alloc, np.int32).reshape(-1, 3))
+    fn = lib().oracle_write_page_table
+    fn.restype = ctypes.c_int64
+    return fn(_p(table), I64(table.shape[0]), I64(table.shape[1]), I64(table.shape[1]), _p(ps),
+              I64(len(ps)), _p(al), I64(al.shape[0]), ctypes.c_int(page_size))
+
+
 def pages_to_tokens(page_starts, page_size: int) -> np.ndarray:
     ps = np.ascontiguousarray(page_starts, np.int32)
     out = np.empty(len(ps) * page_size, np.int32)

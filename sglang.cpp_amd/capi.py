@@ -64,6 +64,7 @@ _SIGNATURES = {
     "sgl_build_decode_indices": ([_vp, _i64, _i64, _i64, _vp, _vp, _vp, _i32, _vp], _i32),
     "sgl_build_prefill_indices": ([_vp, _i64, _i64, _i64, _vp, _vp, _vp, _i32, _vp], _i32),
     "sgl_write_token_pool": ([_vp, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _vp], _i32),
+    "sgl_write_page_table": ([_vp, _i64, _i64, _i64, _vp, _i64, _vp, _i32, _i32, _vp], _i32),
     "sgl_gather_int32_2d": ([_vp, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _vp], _i32),
     "sgl_rope_cos_sin_cache": ([_vp, _vp, _i64, _i32, _f32, _vp], _i32),
     "sgl_qk_rmsnorm": ([_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
@@ -228,6 +229,21 @@ def write_token_pool(pool: torch.Tensor, req_indices: torch.Tensor, positions: t
     _check(lib().sgl_write_token_pool(_p(pool), rows, stride, cols, _p(req_indices),
                                       _p(positions), _p(tokens), tokens.numel(), _stream(dev)),
            "sgl_write_token_pool")
+
+
+def write_page_table(page_table: torch.Tensor, page_starts: torch.Tensor,
+                     alloc_info: torch.Tensor, page_size: int) -> None:
+    """CacheManager::write_page_table on the device (src/scheduler/prefill.cc:144-187).
+    alloc_info: int32 [n, 3] (table_idx, first_page, last_page)."""
+    dev = _need_gpu(page_table, page_starts, alloc_info)
+    rows, stride, cols = _table_args(page_table)
+    if page_starts.dtype != torch.int32 or alloc_info.dtype != torch.int32:
+        raise ValueError("page_starts and alloc_info must be int32")
+    if not alloc_info.is_contiguous() or alloc_info.dim() != 2 or alloc_info.shape[1] != 3:
+        raise ValueError("alloc_info must be a contiguous [n, 3] int32 tensor")
+    _check(lib().sgl_write_page_table(_p(page_table), rows, stride, cols, _p(page_starts),
+                                      page_starts.numel(), _p(alloc_info), alloc_info.shape[0],
+                                      page_size, _stream(dev)), "sgl_write_page_table")
 
 
 def gather_int32_2d(table: torch.Tensor, req_indices: torch.Tensor,

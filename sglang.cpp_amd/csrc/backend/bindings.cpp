@@ -120,6 +120,10 @@ PYBIND11_MODULE(sgl_backend, m) {
       .def("prepare_for_capture", &HipAttnBackend::prepare_for_capture)
       .def("prepare_for_replay", &HipAttnBackend::prepare_for_replay);
 
+  m.def("write_page_table", &write_page_table, py::arg("page_table"),
+        py::arg("allocated_pages"), py::arg("allocation_info"), py::arg("page_size"),
+        "CacheManager::write_page_table (prefill.cc:144-187) on the device");
+
   py::class_<RMSNorm, std::shared_ptr<RMSNorm>>(m, "RMSNorm")
       .def(py::init([](int size, float eps, int device) {
              return std::make_shared<RMSNorm>(size, eps, cuda(device));

@@ -623,6 +623,42 @@ void HipAttnBackend::prepare_mixed_for_replay(Batch& batch) {
   batch.attn_metadata = cap;
 }
 
+// ---------------------------------------------------------------- page table
+
+void write_page_table(const torch::Tensor& page_table, const std::vector<int32_t>& allocated_pages,
+                      const std::vector<std::tuple<int, int, int>>& allocation_info,
+                      int page_size) {
+  if (allocated_pages.empty()) return;
+  TORCH_CHECK(page_size > 0, "page_size must be positive");
+  TORCH_CHECK(page_table.is_cuda() && page_table.dim() == 2 &&
+                  page_table.scalar_type() == torch::kInt32 && page_table.stride(1) == 1,
+              "page table must be a 2-D int32 device tensor with unit column stride");
+  const int64_t npages = static_cast<int64_t>(allocated_pages.size());
+  const int64_t nalloc = static_cast<int64_t>(allocation_info.size());
+  int64_t taken = 0;
+  for (const auto& [table_idx, first_page, last_page] : allocation_info) {
+    (void)table_idx;
+    if (last_page > first_page) taken += last_page - first_page;
+  }
+  TORCH_CHECK(taken == npages, "Allocated page count mismatch");
+  auto staging = torch::empty({npages + 3 * nalloc}, kI32.pinned_memory(true));
+  int32_t* h = staging.data_ptr<int32_t>();
+  std::memcpy(h, allocated_pages.data(), sizeof(int32_t) * npages);
+  int32_t* ai = h + npages;
+  for (const auto& [table_idx, first_page, last_page] : allocation_info) {
+    *ai++ = table_idx;
+    *ai++ = first_page;
+    *ai++ = last_page;
+  }
+  auto dev = staging.to(page_table.device(), /*non_blocking=*/true);
+  check_sgl(sgl_write_page_table(page_table.data_ptr<int32_t>(), page_table.size(0),
+                                 page_table.stride(0), page_table.size(1),
+                                 dev.data_ptr<int32_t>(), npages, dev.data_ptr<int32_t>() + npages,
+                                 static_cast<int>(nalloc), page_size,
+                                 current_stream(page_table.device())),
+            "sgl_write_page_table");
+}
+
 // ---------------------------------------------------------------- layers
 
 RMSNorm::RMSNorm(int size, float eps, torch::Device device) : eps_(eps) {

@@ -14,6 +14,7 @@
 #include <torch/torch.h>
 
 #include <map>
+#include <tuple>
 #include <memory>
 #include <vector>
 
@@ -169,6 +170,16 @@ class HipAttnBackend : public BaseAttnBackend {
   hipEvent_t fork_event_ = nullptr;
   hipEvent_t join_event_ = nullptr;
 };
+
+// CacheManager::write_page_table (src/scheduler/prefill.cc:144-187): the
+// scheduler's host list of allocated page starts and (table_idx, first_page,
+// last_page) tuples go up in one pinned copy of num_pages + 3 n ints, and the
+// device expands pages to token slots (sgl_write_page_table) -- instead of
+// the reference's host loop and three token-sized copies. Same checks: the
+// allocations take exactly the pages given.
+void write_page_table(const torch::Tensor& page_table, const std::vector<int32_t>& allocated_pages,
+                      const std::vector<std::tuple<int, int, int>>& allocation_info,
+                      int page_size);
 
 // RMSNorm module (weight [size], bf16 by default; fp16 weights serve fp16
 // activations). The q/k path is bf16 only.

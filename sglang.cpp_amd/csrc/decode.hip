@@ -359,8 +359,8 @@ __global__ void __launch_bounds__(kMaxKvHeads * kWave)
 
 // Folds the partials of every split request: one workgroup per (kv head,
 // request) handles its G heads; each thread owns 4 consecutive d of one head
-// and runs an online log-sum-exp merge over the request's pieces in order
-// (any number of pieces, 16-byte loads, several in flight). Requests reaching
+// and folds the request's pieces (any number of them) with log-sum-exp
+// weights, 16-byte loads, several in flight. Requests reaching
 // past the plan's token capacity get NaN rows and the CAPACITY status.
 __global__ void __launch_bounds__(256) decode_merge_kernel(DecodeArgs a) {
   const int h = blockIdx.x;
@@ -389,21 +389,26 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(DecodeArgs a) {
     const int g = e / (kD / 4);
     const int d4 = (e - g * (kD / 4)) * 4;
     const int head = h * G + g;
-    float m = -INFINITY, den = 0.f;
-    f32x4_t accm = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 4
+    const int s0 = 2 * u0 + (rb > u0 * W ? 1 : 0);  // slot of the first piece
+    // Two passes with independent loads (no rescale chain between pieces):
+    // the largest log2-sum-exp, then the weighted sum.
+    float m = -INFINITY;
+#pragma unroll 8
     for (int u = u0; u <= u1; ++u) {
-      const int slot = 2 * u + (u == u0 && rb > u0 * W ? 1 : 0);
+      const int slot = u == u0 ? s0 : 2 * u;
+      m = fmaxf(m, a.part_lse[static_cast<int64_t>(slot) * a.hq + head]);
+    }
+    float den = 0.f;
+    f32x4_t accm = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 8
+    for (int u = u0; u <= u1; ++u) {
+      const int slot = u == u0 ? s0 : 2 * u;
       const int64_t pidx = static_cast<int64_t>(slot) * a.hq + head;
       const float lse = a.part_lse[pidx];
       const f32x4_t v = *reinterpret_cast<const f32x4_t*>(a.part_o + pidx * kD + d4);
-      if (lse == -INFINITY) continue;
-      const float mn = fmaxf(m, lse);
-      const float so = exp2f(m - mn);   // 0 on the first piece (m = -inf)
-      const float sn = exp2f(lse - mn);
-      den = den * so + sn;
-      accm = accm * so + v * sn;
-      m = mn;
+      const float wgt = lse == -INFINITY ? 0.f : exp2f(lse - m);
+      den += wgt;
+      accm += v * wgt;
     }
     const float inv = den > 0.f ? 1.0f / den : 0.f;
     uint16_t* op = a.o + static_cast<int64_t>(qrow) * a.o_st +

@@ -4,6 +4,8 @@
 // write_token_pool_kernel / gather_int32_2d_kernel (src/kernels/token_pool.cu:10-49).
 // The page table is token-granular: row r, column p holds the pool slot of
 // request r's p-th token.
+#include <algorithm>
+
 #include "common.h"
 
 namespace sgl {
@@ -65,6 +67,64 @@ __global__ void __launch_bounds__(256) gather_int32_2d_kernel(
   out[i] = (r >= 0 && r < rows && p >= 0 && p < cols) ? table[r * stride + p] : 0;
 }
 
+// Page allocation -> token-granular page table. Allocation a = (row,
+// first_page, last_page) takes page starts [pre[a], pre[a+1]) of the batch's
+// allocated pages, pre the exclusive prefix sum of last - first. Each block
+// rebuilds pre in LDS (a few hundred allocations at most per scheduler
+// step), then each thread takes one token of the flattened page list: page
+// k = t / P of allocation a (binary search on pre) writes slot
+// page_starts[k] + t % P at column (first_page + k - pre[a]) * P + t % P of
+// its row -- P consecutive columns per page, so a wave writes whole pages.
+constexpr int kMaxAllocs = 8192;
+
+__global__ void __launch_bounds__(256) write_page_table_kernel(
+    int32_t* __restrict__ table, int64_t rows, int64_t stride, int64_t cols,
+    const int32_t* __restrict__ page_starts, int64_t num_pages,
+    const int32_t* __restrict__ alloc, int n_alloc, int page_size) {
+  __shared__ int32_t pre[kMaxAllocs + 1];
+  __shared__ int32_t part[256];
+  const int t = threadIdx.x;
+  // Per-thread runs of allocations, then a serial scan of the 256 run sums.
+  const int per = (n_alloc + 255) / 256;
+  const int a0 = min(n_alloc, t * per), a1 = min(n_alloc, a0 + per);
+  int32_t run = 0;
+  for (int a = a0; a < a1; ++a) run += max(0, alloc[3 * a + 2] - alloc[3 * a + 1]);
+  part[t] = run;
+  __syncthreads();
+  if (t == 0) {
+    int32_t acc = 0;
+    for (int i = 0; i < 256; ++i) {
+      const int32_t v = part[i];
+      part[i] = acc;
+      acc += v;
+    }
+    pre[n_alloc] = acc;
+  }
+  __syncthreads();
+  run = part[t];
+  for (int a = a0; a < a1; ++a) {
+    pre[a] = run;
+    run += max(0, alloc[3 * a + 2] - alloc[3 * a + 1]);
+  }
+  __syncthreads();
+  const int64_t count = num_pages * page_size;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + t; i < count;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t k = i / page_size;
+    const int off = static_cast<int>(i - k * page_size);
+    if (k >= pre[n_alloc]) continue;  // more page starts than the allocations take
+    int lo = 0, hi = n_alloc - 1;     // last a with pre[a] <= k
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (pre[mid] <= k) lo = mid; else hi = mid - 1;
+    }
+    const int64_t r = alloc[3 * lo];
+    const int64_t col = (static_cast<int64_t>(alloc[3 * lo + 1]) + (k - pre[lo])) * page_size + off;
+    if (r < 0 || r >= rows || col < 0 || col >= cols) continue;
+    table[r * stride + col] = page_starts[k] + off;
+  }
+}
+
 int launch_build_indices(const int32_t* page_table, int64_t rows, int64_t stride, int64_t cols,
                          const int32_t* table_indices, const int32_t* kv_indptr,
                          int32_t* indices, int batch_size, void* stream) {
@@ -121,6 +181,25 @@ extern "C" int sgl_gather_int32_2d(const int32_t* table, int64_t rows, int64_t s
   hipLaunchKernelGGL(sgl::gather_int32_2d_kernel, dim3(blocks), dim3(256), 0,
                      static_cast<hipStream_t>(stream), table, rows, stride, cols, req_indices,
                      positions, out, count);
+  return sgl::launch_status();
+}
+
+extern "C" int sgl_write_page_table(int32_t* page_table, int64_t rows, int64_t stride,
+                                    int64_t cols, const int32_t* page_starts, int64_t num_pages,
+                                    const int32_t* alloc_info, int num_allocs, int page_size,
+                                    void* stream) {
+  if (num_pages < 0 || num_allocs < 0 || page_size <= 0 || rows < 0 || cols < 0 ||
+      stride < cols)
+    return SGL_ERR_INVALID_ARG;
+  if (num_pages == 0 || num_allocs == 0) return SGL_OK;
+  if (!page_table || !page_starts || !alloc_info) return SGL_ERR_INVALID_ARG;
+  if (num_allocs > sgl::kMaxAllocs) return SGL_ERR_UNSUPPORTED;
+  const int64_t count = num_pages * page_size;
+  if (count > (int64_t{1} << 40)) return SGL_ERR_INVALID_ARG;
+  const int64_t blocks = std::min<int64_t>((count + 255) / 256, 4096);
+  hipLaunchKernelGGL(sgl::write_page_table_kernel, dim3(static_cast<uint32_t>(blocks)),
+                     dim3(256), 0, static_cast<hipStream_t>(stream), page_table, rows, stride,
+                     cols, page_starts, num_pages, alloc_info, num_allocs, page_size);
   return sgl::launch_status();
 }
 

@@ -32,7 +32,7 @@ def test_backend_module_surface(sb):
                  "AttentionLayer", "fused_qk_rmsnorm_inplace_3d_strided", "silu_and_mul",
                  "gelu_and_mul", "flashinfer_sample_from_probs",
                  "flashinfer_top_k_sample_from_probs", "flashinfer_top_p_sample_from_probs",
-                 "flashinfer_top_k_top_p_sample_from_probs"]:
+                 "flashinfer_top_k_top_p_sample_from_probs", "write_page_table"]:
         assert hasattr(sb, name), name
     r = sb.Req(3, 10, 25)
     assert (r.table_idx, r.cached_len, r.device_len(), r.extend_len()) == (3, 10, 25, 15)
@@ -423,3 +423,24 @@ def test_sampling_functions_match_c_abi(dev, sb):
     with pytest.raises(Exception):
         sb.flashinfer_top_k_top_p_sample_from_probs(probs, u, k.float(), 0.0, tp, 0.0, False)
     torch.cuda.synchronize()
+
+
+@pytest.mark.gpu
+def test_write_page_table_module(oracle, dev, sb):
+    """The reference's CacheManager::write_page_table call (host page list and
+    (table_idx, first_page, last_page) tuples, prefill.cc:144-187) writes what
+    the oracle writes, and refuses a page count that does not match."""
+    note("backend write_page_table")
+    rng = np.random.default_rng(95)
+    P = 16
+    table = torch.zeros((9, 64 * P), dtype=torch.int32, device=dev)
+    alloc = [(0, 0, 64), (3, 10, 12), (8, 5, 6)]
+    n = sum(b - a for _, a, b in alloc)
+    pages = [int(x) * P for x in rng.permutation(5000)[:n]]
+    sb.write_page_table(table, pages, alloc, P)
+    torch.cuda.synchronize()
+    want = np.zeros((9, 64 * P), np.int32)
+    assert oracle.write_page_table(want, np.array(pages, np.int32), alloc, P) == n
+    np.testing.assert_array_equal(table.cpu().numpy(), want)
+    with pytest.raises(RuntimeError, match="page count mismatch"):
+        sb.write_page_table(table, pages[:-1], alloc, P)

@@ -116,6 +116,54 @@ def test_token_pool_bit_exact(oracle, dev):
     np.testing.assert_array_equal(got.cpu().numpy(), oracle.gather_int32_2d(want, req, pos))
 
 
+@pytest.mark.parametrize("P", [1, 16])
+def test_write_page_table_bit_exact(oracle, dev, P):
+    """Device page-table write vs the oracle: a scheduler step's worth of
+    allocations (prefix-hit requests taking their new pages, a 2048-page
+    chunk, decode requests crossing into a new page) plus allocations on
+    rows or columns outside the table, which write nothing."""
+    note(f"write_page_table P={P}")
+    rng = np.random.default_rng(6 + P)
+    rows, cols = 40, 2100 * P
+    alloc = [[0, 0, 2048], [5, 3, 4], [7, 0, 1], [rows + 2, 0, 3], [9, 2099, 2103], [-1, 0, 2]]
+    for r in range(10, 38):
+        first = int(rng.integers(0, 100))
+        alloc.append([r, first, first + int(rng.integers(0, 40))])
+    n = sum(b - a for _, a, b in alloc)
+    pages = (rng.permutation(200000)[:n] * P).astype(np.int32)
+    table = rng.integers(0, 1 << 20, (rows, cols)).astype(np.int32)
+    want = table.copy()
+    assert oracle.write_page_table(want, pages, alloc, P) == n
+    d = torch.from_numpy(table).to(dev)
+    capi.write_page_table(d, torch.from_numpy(pages).to(dev),
+                          torch.tensor(alloc, dtype=torch.int32, device=dev), P)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(d.cpu().numpy(), want)
+
+
+def test_write_page_table_then_decode_indices(dev):
+    """Pages written on the device give the same decode indices as the
+    workload generator's host-expanded page table (the scheduler's path)."""
+    note("write_page_table -> build_decode_indices")
+    rng = np.random.default_rng(9)
+    lens = [1, 16, 17, 500, 4096]
+    b = wl.make_paged_batch(rng, [x - 1 for x in lens], lens, page_size=16, decode=True)
+    pt = b.page_table
+    alloc, pages = [], []
+    for r, n in enumerate(lens):
+        npg = -(-n // 16)
+        alloc.append([r, 0, npg])
+        pages += [int(pt[r, 16 * i]) for i in range(npg)]
+    d = torch.zeros(pt.shape, dtype=torch.int32, device=dev)
+    capi.write_page_table(d, torch.tensor(pages, dtype=torch.int32, device=dev),
+                          torch.tensor(alloc, dtype=torch.int32, device=dev), 16)
+    out = torch.empty(int(b.kv_indptr[-1]), dtype=torch.int32, device=dev)
+    capi.build_decode_indices(d, torch.from_numpy(b.table_idx).to(dev),
+                              torch.from_numpy(b.kv_indptr).to(dev), out)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(out.cpu().numpy(), b.indices)
+
+
 # ------------------------------------------------------------------ RoPE / norm
 
 def test_cos_sin_cache(oracle, dev):

@@ -16,6 +16,7 @@ import numpy as np
 import pytest
 import torch
 
+from conftest import wl
 from helpers import bf16_f32, bf16_ulp_dist
 
 GOLDEN = Path(__file__).resolve().parent / "golden"
@@ -86,6 +87,49 @@ def test_metadata_golden(oracle):
     for case in g["pages_to_tokens"]:
         got = oracle.pages_to_tokens(case["page_starts"], case["page_size"])
         np.testing.assert_array_equal(got, np.array(case["expected"], np.int32))
+
+
+def test_write_page_table_kat(oracle):
+    """Hand-derived: page_size 4, allocations (row 2, pages 1..2) then (row 0,
+    page 0) take the page starts 8, 20, 4 in that order; an allocation on a
+    row past the table and a page past the columns write nothing."""
+    table = np.zeros((3, 12), np.int32)
+    used = oracle.write_page_table(table, [8, 20, 4, 40, 44],
+                                   [[2, 1, 3], [0, 0, 1], [7, 0, 1], [1, 3, 4]], 4)
+    want = np.zeros((3, 12), np.int32)
+    want[2, 4:8] = [8, 9, 10, 11]
+    want[2, 8:12] = [20, 21, 22, 23]
+    want[0, 0:4] = [4, 5, 6, 7]
+    assert used == 5
+    np.testing.assert_array_equal(table, want)
+    # fewer page starts than the allocations take: reported as -1
+    assert oracle.write_page_table(np.zeros((3, 12), np.int32), [8], [[2, 1, 3]], 4) == -1
+
+
+def test_write_page_table_is_pages_to_tokens_then_token_pool(oracle):
+    """The page-table write equals the reference's two steps composed:
+    expand the pages (pages_to_tokens, prefill.cc:103-119), then one
+    write_token_pool of (table_idx, page * P + i, token) (prefill.cc:160-186)."""
+    rng = np.random.default_rng(5)
+    for P in (1, 4, 16):
+        rows, cols = 6, 40 * P
+        alloc = []
+        for _ in range(9):
+            first = int(rng.integers(0, 42))
+            alloc.append([int(rng.integers(-1, rows + 1)), first, first + int(rng.integers(0, 5))])
+        n = sum(b - a for _, a, b in alloc)
+        pages = (rng.permutation(1000)[:n] * P).astype(np.int32)
+        table = rng.integers(0, 99, (rows, cols)).astype(np.int32)
+        want = table.copy()
+        toks = oracle.pages_to_tokens(pages, P)
+        req, pos = [], []
+        for r, a, b in alloc:
+            for page in range(a, b):
+                req += [r] * P
+                pos += [page * P + i for i in range(P)]
+        oracle.write_token_pool(want, np.array(req, np.int32), np.array(pos, np.int32), toks)
+        assert oracle.write_page_table(table, pages, alloc, P) == n
+        np.testing.assert_array_equal(table, want)
 
 
 def test_build_indices_brute_force(oracle):
@@ -575,3 +619,27 @@ def test_filtered_sampling_edge_cases(oracle):
     got, ok = oracle.sample(p, u, "top_k", top_k_val=257)
     plain, _ = oracle.sample(p, u[0], "plain")
     assert ok.all() and (got == plain).all()
+
+
+def test_torch_cpu_baseline_matches_oracle(oracle):
+    """The LibTorch-CPU baseline leg (oracle/torch_cpu.py) computes what the C
+    oracle computes: decode and causal prefill with prefix hits, ragged, GQA."""
+    import torch
+    from oracle import torch_cpu as tc
+    rng = np.random.default_rng(11)
+    b = wl.make_paged_batch(rng, [0, 30, 200, 5], [40, 100, 260, 5], page_size=16)
+    hq, hkv, D = 8, 2, 128
+    kc = oracle.f32_to_bf16(rng.standard_normal((b.num_slots, hkv, D), dtype=np.float32))
+    vc = oracle.f32_to_bf16(rng.standard_normal((b.num_slots, hkv, D), dtype=np.float32))
+    T = int(b.qo_indptr[-1])
+    q = oracle.f32_to_bf16(rng.standard_normal((T, hq, D), dtype=np.float32))
+    t = lambda a: torch.from_numpy(a.view(np.int16)).view(torch.bfloat16)  # noqa: E731
+    scale = 1 / np.sqrt(D)
+    idx = torch.from_numpy(b.indices.astype(np.int64))
+    got = tc.prefill(t(q), t(kc), t(vc), idx, b.qo_indptr, b.kv_indptr, scale).numpy()
+    want = oracle.prefill(q, kc, vc, b.indices, b.qo_indptr, b.kv_indptr, scale)
+    np.testing.assert_allclose(got, want, atol=2e-5, rtol=1e-4)
+    qd = q[:4].copy()
+    got = tc.decode(t(qd), t(kc), t(vc), idx, b.kv_indptr, scale).numpy()
+    want = oracle.decode(qd, kc, vc, b.indices, b.kv_indptr, scale)
+    np.testing.assert_allclose(got, want, atol=2e-5, rtol=1e-4)
