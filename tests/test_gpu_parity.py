@@ -404,6 +404,19 @@ def test_decode_long_context(oracle, dev, hq, hkv):
     assert_attn_close(o.float().cpu().numpy(), ref, what=f"long decode W={W}")
 
 
+def test_decode_large_batch(oracle, dev):
+    """700 requests (past the 512 kv_indptr entries a wave keeps in registers:
+    the unit's first request comes from a binary search over memory)."""
+    note("decode batch 700")
+    rng = np.random.default_rng(25)
+    lens = [int(x) for x in rng.integers(0, 300, 700)]
+    b = wl.make_paged_batch(rng, [max(x - 1, 0) for x in lens], lens, page_size=16,
+                            decode=True)
+    q, kc, vc, o, scale, plan = run_decode(dev, b, 32, 8, 128, 26)
+    ref = oracle.decode(u16(q).copy(), u16(kc), u16(vc), b.indices, b.kv_indptr, scale)
+    assert_attn_close(o.float().cpu().numpy(), ref, what="decode batch 700")
+
+
 def test_decode_many_pieces(oracle, dev):
     """64-token units on 32K and 16K requests: 512 + 256 pieces folded by the merge."""
     note("decode 512-piece merge")

@@ -9,9 +9,16 @@ order) samples and success flags are bit-exact. On softmax probabilities
 over the Qwen3 vocabulary the kernels' fp32 sums differ from the oracle's
 exact CDF by their summation error, so a draw may move where u falls that
 close to a boundary: every plain draw s must satisfy
-cdf(s - 1) <= u + 1e-5 and cdf(s) >= u - 1e-5 on the exact CDF, every draw
-is valid (a positive probability; inside the filtered set when accepted),
-and at least 90% of filtered draws equal the oracle's.
+cdf(s - 1) <= u + 1e-5 and cdf(s) >= u - 1e-5 on the exact CDF, and every
+draw is valid (a positive probability; inside the filtered set when
+accepted). A filtered draw may differ from the oracle's only on a row whose
+rejection trajectory (replayed in float64) comes within SUM_TOL of a
+decision boundary at some round up to its end: the target u * q within
+SUM_TOL of a CDF step, or the mass above the pivot within SUM_TOL of top_p.
+Every other row must give the oracle's sample and success flag exactly.
+SUM_TOL = 2e-5 bounds the kernel's fp32 fixed-order sums of up to 151,936
+probabilities of total mass <= 1 (block sums of 1024, then a sum over
+blocks: well under 1e-5), plus the same error carried into u * q.
 """
 import sys
 
@@ -25,6 +32,7 @@ from test_oracle_pins import dyadic_probs
 pytestmark = pytest.mark.gpu
 
 QWEN3_VOCAB = 151936
+SUM_TOL = 2e-5
 
 
 def note(msg):
@@ -42,6 +50,44 @@ def in_filtered_set(row, s, mode, k, top_p):
     if mode in ("top_p", "top_k_top_p"):
         ok &= row[gt].astype(np.float64).sum() < top_p
     return bool(ok)
+
+
+def trajectory_margin(row, u, mode, k, top_p):
+    """Replays the rejection rounds (the oracle's algorithm, float64 sums) for
+    one row; returns (sample, accepted, smallest distance to a decision
+    boundary over the rounds taken)."""
+    d = len(row)
+    pivot, q = np.float32(0), np.float32(1)
+    margin = np.inf
+    sampled, accepted = d - 1, False
+    for r in range(u.shape[0]):
+        target = np.float64(np.float32(u[r] * q))
+        idx = np.nonzero(row > pivot)[0]
+        cdf = np.cumsum(row[idx].astype(np.float64))
+        j = int(np.searchsorted(cdf, target, side="right"))
+        if j < len(idx):
+            sampled = int(idx[j])
+            margin = min(margin, cdf[j] - target, target - (cdf[j - 1] if j > 0 else 0.0))
+        else:
+            sampled = d - 1
+            margin = min(margin, target - (cdf[-1] if len(cdf) else 0.0))
+        if row[sampled] > pivot:
+            pivot = row[sampled]
+        above = row > pivot
+        qd = row[above].astype(np.float64).sum()
+        q = np.float32(qd)
+        count = int(above.sum())
+        if mode in ("top_p", "top_k_top_p"):
+            margin = min(margin, abs(qd - top_p))
+        if mode == "top_k":
+            accepted = count < k
+        elif mode == "top_p":
+            accepted = q < top_p
+        else:
+            accepted = count < k and q < top_p
+        if accepted:
+            break
+    return sampled, accepted, margin
 
 
 def run_all(oracle, dev, p, u, k, tp, exact):
@@ -81,7 +127,20 @@ def run_all(oracle, dev, p, u, k, tp, exact):
                 lo = cdf[got[b] - 1] if got[b] > 0 else 0.0
                 assert lo <= u[0, b] + 1e-5 and cdf[got[b]] >= u[0, b] - 1e-5, (b, got[b], want[b])
         else:
-            assert np.mean(got == want) >= 0.9, (name, np.mean(got == want))
+            mode = name.split(" ")[0]
+            near = 0
+            for b in range(B):
+                kk = 20 if name == "top_k scalar" else int(k[b])
+                pp = np.float32(0.8) if name == "top_p scalar" else tp[b]
+                s_ref, ok_ref, margin = trajectory_margin(p[b], u[:, b], mode, kk, pp)
+                # the float64 replay is the oracle's algorithm
+                assert (s_ref, ok_ref) == (int(want[b]), bool(want_ok[b])), (name, b)
+                if margin > SUM_TOL:
+                    assert (int(got[b]), bool(got_ok[b])) == (s_ref, ok_ref), \
+                        (name, b, int(got[b]), s_ref, margin)
+                else:
+                    near += 1
+            assert near <= B // 4, (name, near)  # the bound is not vacuous
         if got_ok is not None and name != "plain":
             mode = name.split(" ")[0]
             for b in np.nonzero(got_ok)[0][:16]:
