@@ -124,15 +124,16 @@ struct Tile {
   uint16_t v[kBN * kD];
 };
 
-// Slot indices of one 64-token tile for this thread's rows: with W waves a
-// wave instruction covers 4 rows, so thread (wave, lane) takes rows
-// 4 W u + 4 wave + lane / 16, u < 16 / W, i.e. (threadIdx.x + 64 W u) / 16.
+// Slot indices of one 64-token tile for this thread's rows: with W waves
+// gathering a tile, a wave instruction covers 4 rows, so thread (wave, lane)
+// of the gathering group takes rows 4 W u + 4 wave + lane / 16, u < 16 / W,
+// i.e. (tid + 64 W u) / 16 with tid = 64 wave + lane.
 template <int W>
-__device__ __forceinline__ void load_slots(const int32_t* idx, int tile0, int kv_len,
+__device__ __forceinline__ void load_slots(const int32_t* idx, int tile0, int kv_len, int tid,
                                            int32_t (&sl)[16 / W]) {
 #pragma unroll
   for (int u = 0; u < 16 / W; ++u) {
-    const int tok = (threadIdx.x + 64 * W * u) >> 4;
+    const int tok = (tid + 64 * W * u) >> 4;
     sl[u] = idx[min(tile0 + tok, kv_len - 1)];
   }
 }
@@ -141,17 +142,19 @@ __device__ __forceinline__ void load_slots(const int32_t* idx, int tile0, int kv
 // lane i of a wave writes LDS bytes [16 i, 16 i + 16) after the wave's
 // base), so the prefetch holds no registers. Lane i takes physical chunk
 // i % 16 of its row and therefore loads logical chunk (i % 16) ^ swz(row);
-// row % 16 = 4 wave + i / 16 for every u, so lane_base (the head's row 0
-// plus that chunk) is fixed and each address is one 32 x 32 -> 64-bit
-// multiply-add of the slot.
+// row % 16 = 4 W u + 4 wave + i / 16 (mod 16) takes one value for every u
+// when 4 | W and two (u even, u odd) when W = 2, so lane_base[0 or 1] (the
+// head's row 0 plus that chunk) is fixed per u parity and each address is
+// one 32 x 32 -> 64-bit multiply-add of the slot.
 template <int W>
-__device__ __forceinline__ void issue_half(const char* lane_base, uint32_t ss_bytes,
+__device__ __forceinline__ void issue_half(const char* const (&lane_base)[2], uint32_t ss_bytes,
                                            const int32_t (&sl)[16 / W], uint16_t* dst, int wave) {
 #pragma unroll
   for (int u = 0; u < 16 / W; ++u) {
     const int lds_row = 4 * W * u + 4 * wave;  // wave-uniform destination base
     __builtin_amdgcn_global_load_lds(
-        lane_base + static_cast<uint64_t>(static_cast<uint32_t>(sl[u])) * ss_bytes,
+        lane_base[W == 2 ? (u & 1) : 0] +
+            static_cast<uint64_t>(static_cast<uint32_t>(sl[u])) * ss_bytes,
         (__attribute__((address_space(3))) void*)(dst + lds_row * kD), 16, 0, 0);
   }
 }
@@ -315,11 +318,21 @@ __device__ __forceinline__ void pv_steps(const LaneAddr& la, const bf16x8_t (&po
 // carries the same work and each SIMD holds one heavy and one light wave.
 // Both groups share each gathered K/V tile; a group whose rows can no
 // longer see the current tile skips its compute for that step.
-template <int W, bool kPair>
+//
+// KS = 2 (W = 4, for launches that would leave CUs idle): each item is a
+// 32 GW-row tile (GW = W / KS = 2 waves) and the workgroup holds KS groups of
+// GW waves on the same rows, group g taking the g-th share of the item's kv
+// tiles through its own LDS ring; twice the items of a 4-wave launch with
+// half the kv tiles each, so small launches reach every CU. The other
+// groups' softmax states are folded into group 0's through LDS at the end.
+template <int W, bool kPair, int KS>
 __global__ void __launch_bounds__(64 * W, 8 / W) paged_prefill_kernel(PrefillArgs a) {
-  static_assert(!kPair || W == 8, "pairing splits 8 waves into two SIMD-sharing groups");
-  static_assert(W == 4 || W == 8, "gather lane bases assume 16 | 4 W (row % 16 fixed per lane)");
-  constexpr int kGM = kPair ? 16 * W : 32 * W;  // rows per group tile
+  static_assert(!kPair || (W == 8 && KS == 1),
+                "pairing splits 8 waves into two SIMD-sharing groups");
+  constexpr int GW = W / KS;  // waves per group (gathering a group's tiles)
+  static_assert(GW * KS == W && (GW == 2 || GW == 4 || GW == 8),
+                "gather lane bases need row % 16 to take at most two values per lane");
+  constexpr int kGM = kPair ? 16 * W : 32 * GW;  // rows per group tile
   const int n_items = gridDim.x;
   const int lin = blockIdx.x;
   int w = lin;
@@ -356,7 +369,10 @@ __global__ void __launch_bounds__(64 * W, 8 / W) paged_prefill_kernel(PrefillArg
     return;
   }
   const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wave_all = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int split = KS == 1 ? 0 : wave_all / GW;  // kv share of this wave's group
+  const int wave = KS == 1 ? wave_all : wave_all - split * GW;
+  const int tid = threadIdx.x - split * 64 * GW;  // thread index inside the group
   const int c = lane & 31;
   const int hl = lane >> 5;
   // Tile of group 0 (the whole workgroup without pairing) and this wave's
@@ -398,21 +414,37 @@ __global__ void __launch_bounds__(64 * W, 8 / W) paged_prefill_kernel(PrefillArg
   // First token index at which some row of the group may be masked.
   const int first_masked = row0 / G + off + 1;
 
-  // Two K/V buffers; the loop is unrolled by two so each read names its
-  // buffer by a compile-time offset.
-  __shared__ Tile tiles[2];
+  // Two K/V buffers per group; the loop is unrolled by two so each read
+  // names its buffer by a compile-time offset. With KS > 1 the same memory
+  // then carries the other groups' softmax states to group 0.
+  constexpr int kRingBytes = KS * 2 * kTileBytes;
+  constexpr int kXchBytes = (KS - 1) * 66 * 64 * GW * 4;
+  __shared__ __attribute__((aligned(16)))
+      char lds_raw[kRingBytes > kXchBytes ? kRingBytes : kXchBytes];
+  Tile* tiles = reinterpret_cast<Tile*>(lds_raw) + 2 * split;
+  // This group's kv tiles [tb, te) and the steps every group runs (equal,
+  // so the workgroup-wide barriers match).
+  const int share = (ntiles + KS - 1) / KS;
+  const int tb = min(ntiles, split * share);
+  const int te = min(ntiles, tb + share);
+  const int nsteps = share;
 
   const uint16_t* kbase = a.kc + static_cast<int64_t>(h) * a.kv_sh;
   const uint16_t* vbase = a.vc + static_cast<int64_t>(h) * a.kv_sh;
   const int32_t* idx = a.indices + kv_beg;
   const uint32_t ss_bytes = static_cast<uint32_t>(a.kv_ss * 2);
-  const int lch = (lane & 15) ^ swz(4 * wave + (lane >> 4));
-  const char* klane = reinterpret_cast<const char*>(kbase) + lch * 16;
-  const char* vlane = reinterpret_cast<const char*>(vbase) + lch * 16;
+  // Lane bases for rows r and r + 8 (r = 4 wave + lane / 16; the second is
+  // used on odd u when GW = 2).
+  const int lch0 = (lane & 15) ^ swz(4 * wave + (lane >> 4));
+  const int lch1 = (lane & 15) ^ swz((4 * wave + (lane >> 4) + 8) & 15);
+  const char* const klane[2] = {reinterpret_cast<const char*>(kbase) + lch0 * 16,
+                                reinterpret_cast<const char*>(kbase) + lch1 * 16};
+  const char* const vlane[2] = {reinterpret_cast<const char*>(vbase) + lch0 * 16,
+                                reinterpret_cast<const char*>(vbase) + lch1 * 16};
 
   LaneAddr la;
   {
-    const uint32_t base = lds_addr(&tiles[0]);
+    const uint32_t base = lds_addr(tiles);
     const int sw = swz(c);
 #pragma unroll
     for (int s = 0; s < 8; ++s) la.k[s] = base + c * kD * 2 + ((2 * s + hl) ^ sw) * 16;
@@ -449,14 +481,16 @@ __global__ void __launch_bounds__(64 * W, 8 / W) paged_prefill_kernel(PrefillArg
   // The slots of tiles 0 and 1 are waited for together before any gather
   // is issued (a gather between them would make the wait for the later
   // slots wait for the gather too: loads complete in order).
-  int32_t sl_k[16 / W], sl_v[16 / W];
-  load_slots<W>(idx, 0, kv_len, sl_k);
-  load_slots<W>(idx, kBN, kv_len, sl_v);
+  int32_t sl_k[16 / GW], sl_v[16 / GW];
+  load_slots<GW>(idx, tb * kBN, kv_len, tid, sl_k);
+  load_slots<GW>(idx, (tb + 1) * kBN, kv_len, tid, sl_v);
   wait_gathers();
-  issue_half<W>(klane, ss_bytes, sl_k, tiles[0].k, wave);
-  issue_half<W>(vlane, ss_bytes, sl_k, tiles[0].v, wave);
-  issue_half<W>(klane, ss_bytes, sl_v, tiles[1].k, wave);
-  load_slots<W>(idx, 2 * kBN, kv_len, sl_k);
+  if (tb < te) {
+    issue_half<GW>(klane, ss_bytes, sl_k, tiles[0].k, wave);
+    issue_half<GW>(vlane, ss_bytes, sl_k, tiles[0].v, wave);
+  }
+  if (tb + 1 < te) issue_half<GW>(klane, ss_bytes, sl_v, tiles[1].k, wave);
+  load_slots<GW>(idx, (tb + 2) * kBN, kv_len, tid, sl_k);
   // Q^T operand: q[qtok][qhead][16 s + 8 hl .. +8], s < 8. Loaded after
   // the first gathers are issued: loads complete in order, so Q issued
   // earlier would delay the slot indices the gathers wait for.
@@ -481,13 +515,13 @@ __global__ void __launch_bounds__(64 * W, 8 / W) paged_prefill_kernel(PrefillArg
   __syncthreads();  // every wave has read K(0) before K(2) overwrites it
 
   auto step = [&](auto B, int t, f32x16_t(&s_cur)[2], f32x16_t(&s_next)[2]) {
-    constexpr int buf = decltype(B)::value;  // t % 2
-    if (t + 2 < ntiles) issue_half<W>(klane, ss_bytes, sl_k, tiles[buf].k, wave);
-    if (t + 1 < ntiles) issue_half<W>(vlane, ss_bytes, sl_v, tiles[buf ^ 1].v, wave);
+    constexpr int buf = decltype(B)::value;  // (t - tb) % 2
+    if (t + 2 < te) issue_half<GW>(klane, ss_bytes, sl_k, tiles[buf].k, wave);
+    if (t + 1 < te) issue_half<GW>(vlane, ss_bytes, sl_v, tiles[buf ^ 1].v, wave);
 #pragma unroll
-    for (int u = 0; u < 16 / W; ++u) sl_v[u] = sl_k[u];
-    load_slots<W>(idx, (t + 3) * kBN, kv_len, sl_k);
-    if (!kPair || t < my_tiles) {
+    for (int u = 0; u < 16 / GW; ++u) sl_v[u] = sl_k[u];
+    load_slots<GW>(idx, (t + 3) * kBN, kv_len, tid, sl_k);
+    if (t < te && (!kPair || t < my_tiles)) {
       softmax_head(a, s_cur, rs, t * kBN, first_masked, allow, kv_len, hl);
       // The VALU work of P(t) is split so each half runs beside MFMAs: the
       // first half beside S(t + 1), the second beside the first half of
@@ -503,10 +537,46 @@ __global__ void __launch_bounds__(64 * W, 8 / W) paged_prefill_kernel(PrefillArg
     wait_gathers();
     __syncthreads();
   };
-  for (int t = 0; t < ntiles; t += 2) {
-    step(std::integral_constant<int, 0>{}, t, s_a, s_b);
-    if (t + 1 >= ntiles) break;
-    step(std::integral_constant<int, 1>{}, t + 1, s_b, s_a);
+  for (int i = 0; i < nsteps; i += 2) {
+    step(std::integral_constant<int, 0>{}, tb + i, s_a, s_b);
+    if (i + 1 >= nsteps) break;
+    step(std::integral_constant<int, 1>{}, tb + i + 1, s_b, s_a);
+  }
+
+  if constexpr (KS > 1) {
+    // Fold groups 1 .. KS-1 into group 0: each writes its (O, m, l) lane-major
+    // ([group][value][wave][lane], conflict-free), group 0 reads the entries
+    // of its own wave and lane (same rows, same accumulator slots) and
+    // rescales every state to the largest reference point. The rings are
+    // free once every wave is past its loop.
+    float* xch = reinterpret_cast<float*>(lds_raw);
+    auto at = [&](int g, int v) -> float& {
+      return xch[((g - 1) * 66 + v) * 64 * GW + wave * 64 + lane];
+    };
+    __syncthreads();
+    if (split > 0) {
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) at(split, 16 * db + v) = rs.acc[db][v];
+      at(split, 64) = rs.m;
+      at(split, 65) = rs.l;
+    }
+    __syncthreads();
+    if (split > 0) return;
+#pragma unroll
+    for (int g = 1; g < KS; ++g) {
+      const float mg = at(g, 64);
+      const float mn = fmaxf(rs.m, mg);
+      const float w0 = rs.m == -INFINITY ? 0.f : exp2f(rs.m - mn);
+      const float wg = mg == -INFINITY ? 0.f : exp2f(mg - mn);
+      rs.l = rs.l * w0 + at(g, 65) * wg;
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) rs.acc[db][v] = rs.acc[db][v] * w0 + at(g, 16 * db + v) * wg;
+      rs.m = mn;
+    }
   }
 
   float l = sum_xor32(rs.l);
@@ -574,7 +644,12 @@ extern "C" int sgl_paged_prefill(const void* q, int64_t q_stride_token, int64_t 
   // workgroups per CU, heavy-first dispatch balances better.
   const int64_t pairs = ((rows_max + 127) / 128 + 1) / 2;
   const bool pair = wide && pairs * num_kv_heads * batch_size <= static_cast<int64_t>(device_cus());
-  const int bm = wide ? 256 : 128;
+  // Launches that would leave CUs idle even with 64-row items split each
+  // item's kv tiles between two 2-wave groups (KS = 2): 64-row items reach
+  // twice the CUs, each group streaming half the kv tiles.
+  const bool split_kv = !wide && ((rows_max + 63) / 64) * num_kv_heads * batch_size <=
+                                     static_cast<int64_t>(device_cus());
+  const int bm = wide ? 256 : split_kv ? 64 : 128;
   const int64_t tiles = pair ? pairs : (rows_max + bm - 1) / bm;
   const int64_t items = tiles * num_kv_heads * batch_size;
   if (items > 0x7fffffff) return SGL_ERR_INVALID_ARG;
@@ -600,10 +675,12 @@ extern "C" int sgl_paged_prefill(const void* q, int64_t q_stride_token, int64_t 
   const dim3 grid(static_cast<uint32_t>(items));
   const hipStream_t s = static_cast<hipStream_t>(stream);
   if (pair)
-    hipLaunchKernelGGL((paged_prefill_kernel<8, true>), grid, dim3(512), 0, s, a);
+    hipLaunchKernelGGL((paged_prefill_kernel<8, true, 1>), grid, dim3(512), 0, s, a);
   else if (wide)
-    hipLaunchKernelGGL((paged_prefill_kernel<8, false>), grid, dim3(512), 0, s, a);
+    hipLaunchKernelGGL((paged_prefill_kernel<8, false, 1>), grid, dim3(512), 0, s, a);
+  else if (split_kv)
+    hipLaunchKernelGGL((paged_prefill_kernel<4, false, 2>), grid, dim3(256), 0, s, a);
   else
-    hipLaunchKernelGGL((paged_prefill_kernel<4, false>), grid, dim3(256), 0, s, a);
+    hipLaunchKernelGGL((paged_prefill_kernel<4, false, 1>), grid, dim3(256), 0, s, a);
   return launch_status();
 }
