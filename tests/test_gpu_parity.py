@@ -521,7 +521,7 @@ def test_prefill_cfg2(oracle, dev):
 
 
 @pytest.mark.parametrize("hq,hkv", [(16, 8), (32, 4), (8, 8), (32, 8), (12, 4),
-                                     (40, 8), (16, 16), (8, 1), (64, 8)])
+                                     (40, 8), (16, 16), (8, 1), (64, 8), (32, 2), (16, 1)])
 def test_prefill_ragged(oracle, dev, hq, hkv):
     note(f"prefill ragged hq={hq} hkv={hkv}")
     rng = np.random.default_rng(21)
