@@ -253,8 +253,9 @@ int sgl_decode_plan_check(const sgl_decode_plan_t* plan, const int32_t* kv_indpt
  * when the device kv_indptr[batch] exceeds plan->max_total_tokens the rows
  * of every request reaching past the capacity are written as NaN and the
  * word is set to SGL_ERR_CAPACITY (read it with sgl_decode_status). Two
- * kernels run on the stream (decode, then merge). Calls that share one
- * workspace must be stream-ordered.
+ * kernels run on the stream (decode, then merge), or one for small batches
+ * (plans at the 64-token minimum unit with batch_size x Hkv workgroups at
+ * most the CU count). Calls that share one workspace must be stream-ordered.
  * Replaces: BatchDecodeWithPagedKVCacheDispatched call in
  *           FlashInferBackend::forward (src/attention/flashinfer_backend.cu:553-595).
  */

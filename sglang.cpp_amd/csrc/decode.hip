@@ -162,9 +162,18 @@ __device__ __forceinline__ bf16x4_t v_operand(const u32x4_t (&vr)[4]) {
   acc[nb] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(v_operand<nb>(vr), pop, acc[nb], \
                                                       0, 0, 0)
 
+// Softmax state of one wave's piece (lane (n, j): head n, d = 32 j + 8 i + nb
+// in acc[nb][i]), for the small-batch kernel's in-workgroup fold.
+struct HeadState {
+  float m, l;
+  f32x4_t acc[8];
+};
+
 // One wave: kv head h over the `len` tokens whose slots are sidx[0, len)
 // (one piece of a request). whole: the piece is the whole request (output
-// written directly); otherwise it goes to partial slot pslot.
+// written directly); otherwise it goes to partial slot pslot. kState: leave
+// the state in *st instead (no output), with no per-step workgroup barrier
+// (the waves of the small-batch kernel take pieces of different lengths).
 //
 // Per 16-token step (v_mfma, lane l, n = l % 16, j = l / 16):
 //   S^T[tok, head] = K . Q^T          4 x 16x16x32: rows tok, columns head
@@ -173,9 +182,10 @@ __device__ __forceinline__ bf16x4_t v_operand(const u32x4_t (&vr)[4]) {
 // exactly the B operand P^T the second product needs, and both put the head
 // on the lane's column, so max, sum and the rescale of O are lane-local apart
 // from one exchange across the four lane groups.
+template <bool kState>
 __device__ __forceinline__ void decode_head(const DecodeArgs& a, WaveLds& L, const int32_t* sidx,
                                             int pslot, bool whole, int h, int len, int qrow,
-                                            int lane) {
+                                            int lane, HeadState* st = nullptr) {
   const int n = lane & 15;
   const int j = lane >> 4;
   const int G = a.group;
@@ -213,7 +223,7 @@ __device__ __forceinline__ void decode_head(const DecodeArgs& a, WaveLds& L, con
     // Keep the workgroup's waves (one per kv head) in step: together they
     // read each token's whole [Hkv, D] row, which DRAM serves better as one
     // burst than as per-head pieces spread over time.
-    __builtin_amdgcn_s_barrier();
+    if constexpr (!kState) __builtin_amdgcn_s_barrier();
     const int tn = t + kStep;
     const int kslot_next = sidx[min(tn + n, len - 1)];
     f32x4_t sacc = {0.f, 0.f, 0.f, 0.f};
@@ -253,6 +263,13 @@ __device__ __forceinline__ void decode_head(const DecodeArgs& a, WaveLds& L, con
     __builtin_amdgcn_sched_barrier(0);
   }
   l = sum_xor32(sum_xor16(l));
+  if constexpr (kState) {
+    st->m = m;
+    st->l = l;
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb) st->acc[nb] = acc[nb];
+    return;
+  }
   if (!head_ok) return;
   const float inv = l > 0.f ? 1.0f / l : 0.f;
   const int head = h * G + n;
@@ -353,7 +370,105 @@ __global__ void __launch_bounds__(kMaxKvHeads * kWave)
     if (s1 <= s0) continue;
     const bool whole = rb >= tok0 && re <= tok1;
     const int pslot = 2 * u + (rb > tok0 ? 1 : 0);
-    decode_head(a, L, sidx + (s0 - tok0), pslot, whole, wave, s1 - s0, qrow, lane);
+    decode_head<false>(a, L, sidx + (s0 - tok0), pslot, whole, wave, s1 - s0, qrow, lane);
+  }
+}
+
+
+// Small batches (every unit at the 64-token minimum and at most one
+// workgroup per CU for each (request, kv head)): one 8-wave workgroup per
+// (kv head, request), the request's tokens cut into 8 contiguous pieces, one
+// per wave, and the waves' softmax states folded through LDS by wave 0 --
+// one launch instead of decode + merge, which is what such a call is bound
+// by. The plan's capacity contract is kept: requests reaching past
+// num_units * W_max tokens get NaN rows, and workgroup (0, 0) sets the status
+// word from kv_indptr[batch] (a request reaches past the capacity exactly
+// when the batch's total does), so no other workgroup writes it.
+constexpr int kSmallWaves = 8;
+constexpr int kSmallStage = 8192;  // slot indices staged in LDS (longer requests read them from HBM)
+
+__global__ void __launch_bounds__(kSmallWaves * kWave) paged_decode_small_kernel(DecodeArgs a) {
+  __shared__ WaveLds ql[kSmallWaves];
+  __shared__ int32_t slots[kSmallStage];
+  __shared__ float xch[34][kSmallWaves][kWave];
+  const int h = blockIdx.x;
+  const int r = blockIdx.y;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int G = a.group;
+  const int total = a.kv_indptr[a.batch];
+  const int W = unit_tokens(a, total);
+  const int64_t cover = static_cast<int64_t>(a.num_units) * W;
+  if (h == 0 && r == 0 && threadIdx.x == 0)
+    *a.status = static_cast<int64_t>(total) > cover ? SGL_ERR_CAPACITY : SGL_OK;
+  const int rb = a.kv_indptr[r];
+  const int re = a.kv_indptr[r + 1];
+  const int qrow = a.q_indptr ? a.q_indptr[r] : r;
+  const int len = re - rb;
+  if (static_cast<int64_t>(re) > cover || len <= 0) {
+    // Past the capacity: NaN rows; empty request: zero rows (G heads of h).
+    const uint32_t fill = len <= 0 ? 0u : 0x7fc07fc0u;
+    for (int e = threadIdx.x; e < G * (kD / 8); e += blockDim.x) {
+      const int g = e / (kD / 8);
+      stg128(a.o + static_cast<int64_t>(qrow) * a.o_st + static_cast<int64_t>(h * G + g) * a.o_sh +
+                 (e - g * (kD / 8)) * 8,
+             u32x4_t{fill, fill, fill, fill});
+    }
+    return;
+  }
+  const int32_t* sp = a.indices + rb;
+  if (len <= kSmallStage) {
+    for (int e = threadIdx.x; e < len; e += blockDim.x) slots[e] = sp[e];
+    __syncthreads();
+    sp = slots;
+  }
+  const int per = ((len + kSmallWaves - 1) / kSmallWaves + kStep - 1) / kStep * kStep;
+  const int t0 = min(len, wave * per);
+  const int t1 = min(len, t0 + per);
+  HeadState st;
+  st.m = -INFINITY;
+  st.l = 0.f;
+#pragma unroll
+  for (int nb = 0; nb < 8; ++nb) st.acc[nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  if (t0 < t1) decode_head<true>(a, ql[wave], sp + t0, 0, false, h, t1 - t0, qrow, lane, &st);
+#pragma unroll
+  for (int nb = 0; nb < 8; ++nb)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) xch[4 * nb + i][wave][lane] = st.acc[nb][i];
+  xch[32][wave][lane] = st.m;
+  xch[33][wave][lane] = st.l;
+  __syncthreads();
+  if (wave != 0) return;
+  // Wave 0 folds the pieces in wave order (the largest log2-sum-exp first,
+  // then the weighted sums), as the merge kernel folds units.
+  const int n = lane & 15;
+  const int j = lane >> 4;
+  if (n >= G) return;
+  float mx = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < kSmallWaves; ++w) mx = fmaxf(mx, xch[32][w][lane]);
+  float den = 0.f;
+  f32x4_t acc[8];
+#pragma unroll
+  for (int nb = 0; nb < 8; ++nb) acc[nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int w = 0; w < kSmallWaves; ++w) {
+    const float mw = xch[32][w][lane];
+    const float wgt = mw == -INFINITY ? 0.f : exp2f(mw - mx);
+    den += xch[33][w][lane] * wgt;
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[nb][i] += xch[4 * nb + i][w][lane] * wgt;
+  }
+  const float inv = den > 0.f ? 1.0f / den : 0.f;
+  uint16_t* op = a.o + static_cast<int64_t>(qrow) * a.o_st + static_cast<int64_t>(h * G + n) * a.o_sh;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float v[8];
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb) v[nb] = acc[nb][i] * inv;
+    stg128(op + 32 * j + 8 * i, pack8(v));
   }
 }
 
@@ -576,8 +691,14 @@ void bind_workspace(DecodeArgs& a, const sgl_decode_plan_t* plan, void* workspac
   a.part_lse = reinterpret_cast<float*>(base + w.part_lse_off);
 }
 
-// Decode launch + merge launch on one stream.
+// Decode launch + merge launch on one stream (or the small-batch kernel alone).
 int launch_decode(const DecodeArgs& a, const sgl_decode_plan_t* plan, hipStream_t s) {
+  if (plan->kv_chunk_size <= kMinUnit &&
+      static_cast<int64_t>(a.batch) * a.hkv <= static_cast<int64_t>(device_cu_count())) {
+    hipLaunchKernelGGL(paged_decode_small_kernel, dim3(a.hkv, a.batch), dim3(kSmallWaves * kWave),
+                       0, s, a);
+    return launch_status();
+  }
   const dim3 grid(plan->num_units);
   const dim3 block(a.hkv * kWave);
   const size_t lds = static_cast<size_t>(a.hkv) * sizeof(WaveLds) +

@@ -418,15 +418,33 @@ def test_decode_large_batch(oracle, dev):
 
 
 def test_decode_many_pieces(oracle, dev):
-    """64-token units on 32K and 16K requests: 512 + 256 pieces folded by the merge."""
-    note("decode 512-piece merge")
+    """80-token units on 32K and 16K requests: 410 + 205 pieces folded by the merge."""
+    note("decode 410-piece merge")
     rng = np.random.default_rng(20)
     lens = [32768, 100, 16384, 64, 65]
     b = wl.make_paged_batch(rng, [x - 1 for x in lens], lens, page_size=16, decode=True)
-    plan = forced_plan(capi, b.kv_indptr, 32, 4, 64)
+    plan = forced_plan(capi, b.kv_indptr, 32, 4, 80)
     q, kc, vc, o, scale, _ = run_decode(dev, b, 32, 4, 128, 21, plan=plan)
     ref = oracle.decode(u16(q).copy(), u16(kc), u16(vc), b.indices, b.kv_indptr, scale)
-    assert_attn_close(o.float().cpu().numpy(), ref, what="512-piece merge")
+    assert_attn_close(o.float().cpu().numpy(), ref, what="410-piece merge")
+
+
+@pytest.mark.parametrize("hq,hkv,lens", [
+    (16, 8, [512] * 4),                       # config 1's shape
+    (32, 4, [10000, 20, 0, 1]),               # a request past the LDS slot stage, empty, one token
+    (64, 4, [7, 8, 9, 15, 16, 17, 129]),      # G = 16, pieces shorter than a step
+    (8, 1, [3000, 2999]),                     # one kv head
+])
+def test_decode_small_batch_kernel(oracle, dev, hq, hkv, lens):
+    """Small batches (units at the 64-token minimum, batch x kv heads <= CUs)
+    run one workgroup per (request, kv head) whose waves fold through LDS."""
+    note(f"decode small-batch kernel hq={hq} hkv={hkv} lens={lens}")
+    rng = np.random.default_rng(27)
+    b = wl.make_paged_batch(rng, [max(x - 1, 0) for x in lens], lens, page_size=16, decode=True)
+    q, kc, vc, o, scale, plan = run_decode(dev, b, hq, hkv, 128, 28)
+    assert plan.kv_chunk_size == 64 and plan.batch_size * hkv <= 256
+    ref = oracle.decode(u16(q).copy(), u16(kc), u16(vc), b.indices, b.kv_indptr, scale)
+    assert_attn_close(o.float().cpu().numpy(), ref, what="small-batch decode")
 
 
 def test_decode_plan_exceeded_reports_capacity(oracle, dev):
