@@ -36,6 +36,7 @@ constexpr int kD = 128;
 constexpr int kBN = 64;    // kv tokens per LDS tile
 constexpr int kXcds = 8;  // MI355X: 8 XCDs, each with its own L2
 constexpr float kRescaleSlack = 8.f;  // log2 units: p <= 256 between rescales
+constexpr int kKAhead = 4;            // K operand reads in flight ahead of their MFMA (6 measured the same)
 
 struct PrefillArgs {
   const uint16_t* q;
@@ -182,27 +183,42 @@ static_assert(sizeof(Tile) == kTileBytes, "tile buffers are addressed by fixed o
 // S^T = K Q^T for one 64-token tile from LDS buffer BUF: tokens
 // [32 mb, 32 mb + 32) in st[mb]. MFMA i uses mb = i % 2, s = i / 2 (the two
 // accumulation chains alternate); its K operand is read four MFMAs ahead.
+template <int BUF, int I>
+__device__ __forceinline__ void k_read(const LaneAddr& la, u32x4_t (&kb)[16]) {
+  kb[I] = lds_read_b128<BUF * kTileBytes + (I & 1) * 32 * kD * 2>(la.k[I >> 1]);
+}
+
+// The first four K operand reads of S = K Q^T on buffer BUF, issued ahead of
+// qk_tile_run (the caller's work in between hides their latency).
 template <int BUF>
-__device__ __forceinline__ void qk_tile(const LaneAddr& la, const bf16x8_t (&qop)[8],
-                                        f32x16_t (&st)[2]) {
+__device__ __forceinline__ void qk_tile_prefetch(const LaneAddr& la, u32x4_t (&kb)[16]) {
+  static_for<0, kKAhead>([&](auto I) { k_read<BUF, decltype(I)::value>(la, kb); });
+}
+
+template <int BUF>
+__device__ __forceinline__ void qk_tile_run(const LaneAddr& la, const bf16x8_t (&qop)[8],
+                                            f32x16_t (&st)[2], u32x4_t (&kb)[16]) {
 #pragma unroll
   for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
     for (int v = 0; v < 16; ++v) st[mb][v] = 0.f;
-  u32x4_t kb[16];
-  auto kread = [&](auto I) {
-    constexpr int i = decltype(I)::value;
-    kb[i] = lds_read_b128<BUF * kTileBytes + (i & 1) * 32 * kD * 2>(la.k[i >> 1]);
-  };
-  static_for<0, 4>(kread);
+  auto kread = [&](auto I) { k_read<BUF, decltype(I)::value>(la, kb); };
   static_for<0, 16>([&](auto I) {
     constexpr int i = decltype(I)::value;
-    constexpr int younger = (15 - i) < 3 ? (15 - i) : 3;
+    constexpr int younger = (15 - i) < kKAhead - 1 ? (15 - i) : kKAhead - 1;
     lgkm_wait<younger>(kb[i]);
     st[i & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(kb[i]), qop[i >> 1], st[i & 1],
                                                         0, 0, 0);
-    if constexpr (i + 4 < 16) kread(std::integral_constant<int, i + 4>{});
+    if constexpr (i + kKAhead < 16) kread(std::integral_constant<int, i + kKAhead>{});
   });
+}
+
+template <int BUF>
+__device__ __forceinline__ void qk_tile(const LaneAddr& la, const bf16x8_t (&qop)[8],
+                                        f32x16_t (&st)[2]) {
+  u32x4_t kb[16];
+  qk_tile_prefetch<BUF>(la, kb);
+  qk_tile_run<BUF>(la, qop, st, kb);
 }
 
 // Mask, running max and (lazy) rescale of the scores of the tile at tile0.
@@ -522,12 +538,20 @@ __global__ void __launch_bounds__(64 * W, 8 / W) paged_prefill_kernel(PrefillArg
     for (int u = 0; u < 16 / GW; ++u) sl_v[u] = sl_k[u];
     load_slots<GW>(idx, (t + 3) * kBN, kv_len, tid, sl_k);
     if (t < te && (!kPair || t < my_tiles)) {
+      // S(t + 1)'s first K operand reads go out before the mask / max of
+      // S(t), which hides their LDS latency (K(t + 1) landed and became
+      // visible at the previous step's barrier). The full wait after the
+      // VALU work keeps the counted waits exact whatever the compiler
+      // placed in between.
+      u32x4_t kb[16];
+      qk_tile_prefetch<buf ^ 1>(la, kb);
       softmax_head(a, s_cur, rs, t * kBN, first_masked, allow, kv_len, hl);
+      lgkm_wait<0>(kb[kKAhead - 1]);
       // The VALU work of P(t) is split so each half runs beside MFMAs: the
       // first half beside S(t + 1), the second beside the first half of
       // O += P(t) V(t).
       u32x2_t vr[4][8];
-      qk_tile<buf ^ 1>(la, qop, s_next);  // S(t + 1); unused after the last tile
+      qk_tile_run<buf ^ 1>(la, qop, s_next, kb);  // S(t + 1); unused after the last tile
       softmax_exp_half<0>(a, s_cur, rs, pop);
       pv_reads<buf, 0>(la, vr[0]);
       pv_steps<buf, 0, 2>(la, pop, vr, rs);
