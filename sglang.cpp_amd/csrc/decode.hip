@@ -50,9 +50,7 @@ constexpr int kMaxGroup = 16;
 constexpr int kMinUnit = 64;    // smallest unit: keeps per-unit set-up small next to the stream
 constexpr int kMaxChunkTokens = 8192;  // slot indices of a chunk staged in LDS (32 KiB)
 constexpr int kQPitch = kD + 8; // LDS row pitch (bf16) of the Q^T copy
-// Word 3 of a raw buffer resource on gfx9-class parts: 32-bit data format,
-// no swizzle, no index stride.
-constexpr int kBufferRsrcWord3 = 0x00020000;
+constexpr float kRescaleSlack = 8.f;  // log2 units: p <= 256 between rescales
 
 struct DecodeArgs {
   const uint16_t* q;
@@ -120,19 +118,28 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// K operand of a 16-token step: lane (n, j) holds K[tok n][32 s + 8 j .. + 8].
-__device__ __forceinline__ void load_k_step(const uint16_t* kbase, int64_t kv_ss, int slot, int j,
+// Row addresses are a lane base plus the slot times the slot stride in
+// bytes, one 32 x 32 -> 64-bit multiply-add (the stride is < 2^31 bytes and
+// slots are non-negative int32).
+__device__ __forceinline__ const char* slot_row(const char* lane_base, int slot, uint32_t ss_bytes) {
+  return lane_base + static_cast<uint64_t>(static_cast<uint32_t>(slot)) * ss_bytes;
+}
+
+// K operand of a 16-token step: lane (n, j) holds K[tok n][32 s + 8 j .. + 8]
+// (klane: the head's row 0 plus 8 j elements).
+__device__ __forceinline__ void load_k_step(const char* klane, uint32_t ss_bytes, int slot,
                                             u32x4_t (&kr)[4]) {
-  const uint16_t* row = kbase + static_cast<int64_t>(slot) * kv_ss + 8 * j;
+  const char* row = slot_row(klane, slot, ss_bytes);
 #pragma unroll
-  for (int s = 0; s < 4; ++s) kr[s] = ldg128(row + 32 * s);
+  for (int s = 0; s < 4; ++s) kr[s] = ldg128(reinterpret_cast<const uint16_t*>(row) + 32 * s);
 }
 
 // V rows of a 16-token step: lane (n, j) holds V[tok 4 j + e][8 n .. 8 n + 7]
-// for e < 4, so each load instruction reads four whole 256-byte rows.
-// Tokens at or past `len` re-read the last valid row (an L2 hit).
-__device__ __forceinline__ void load_v_step(const uint16_t* vbase, int64_t kv_ss,
-                                            const int32_t* sidx, int tb, int len, int n, int j,
+// for e < 4, so each load instruction reads four whole 256-byte rows
+// (vlane: the head's row 0 plus 8 n elements). Tokens at or past `len`
+// re-read the last valid row (an L2 hit).
+__device__ __forceinline__ void load_v_step(const char* vlane, uint32_t ss_bytes,
+                                            const int32_t* sidx, int tb, int len, int j,
                                             u32x4_t (&vr)[4]) {
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
@@ -142,7 +149,7 @@ __device__ __forceinline__ void load_v_step(const uint16_t* vbase, int64_t kv_ss
     // their 64-byte halves come from two instructions and the second one
     // hits the line the first brought into L2.
     vr[e] = __builtin_nontemporal_load(
-        reinterpret_cast<const u32x4_t*>(vbase + static_cast<int64_t>(sidx[tok]) * kv_ss + 8 * n));
+        reinterpret_cast<const u32x4_t*>(slot_row(vlane, sidx[tok], ss_bytes)));
   }
 }
 
@@ -190,8 +197,9 @@ __device__ __forceinline__ void decode_head(const DecodeArgs& a, WaveLds& L, con
   const int j = lane >> 4;
   const int G = a.group;
   const bool head_ok = n < G;
-  const uint16_t* kbase = a.kc + static_cast<int64_t>(h) * a.kv_sh;
-  const uint16_t* vbase = a.vc + static_cast<int64_t>(h) * a.kv_sh;
+  const char* klane = reinterpret_cast<const char*>(a.kc + static_cast<int64_t>(h) * a.kv_sh + 8 * j);
+  const char* vlane = reinterpret_cast<const char*>(a.vc + static_cast<int64_t>(h) * a.kv_sh + 8 * n);
+  const uint32_t ss_bytes = static_cast<uint32_t>(a.kv_ss * 2);
 
   // Q rows of this kv head's G query heads -> LDS (16 rows x 16 chunks).
 #pragma unroll
@@ -208,9 +216,9 @@ __device__ __forceinline__ void decode_head(const DecodeArgs& a, WaveLds& L, con
   // Prologue: K and V rows of the first step in flight, K issued first as
   // inside the loop (the loop-head wait counts merge both paths).
   u32x4_t kr[4], vr[4];
-  load_k_step(kbase, a.kv_ss, sidx[min(n, len - 1)], j, kr);
+  load_k_step(klane, ss_bytes, sidx[min(n, len - 1)], kr);
   __builtin_amdgcn_sched_barrier(0);
-  load_v_step(vbase, a.kv_ss, sidx, 0, len, n, j, vr);
+  load_v_step(vlane, ss_bytes, sidx, 0, len, j, vr);
   __builtin_amdgcn_sched_barrier(0);
 
   float m = -INFINITY;  // running max of head n (replicated over j)
@@ -233,33 +241,43 @@ __device__ __forceinline__ void decode_head(const DecodeArgs& a, WaveLds& L, con
       sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kr[s]), qop, sacc, 0, 0, 0);
     }
     __builtin_amdgcn_sched_barrier(0);
-    load_k_step(kbase, a.kv_ss, kslot_next, j, kr);  // K of the next step
+    load_k_step(klane, ss_bytes, kslot_next, kr);  // K of the next step
     __builtin_amdgcn_sched_barrier(0);
 
+    // Online softmax in the log2 domain with a lazy reference point: m only
+    // moves when a head's step maximum exceeds it by more than
+    // kRescaleSlack, so most steps skip the rescale of O. Exact: p and l of
+    // a head always use the same m, and p <= 2^kRescaleSlack.
     const int last = len - t - 1;
     float sc[4];
     float mt = -INFINITY;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      sc[i] = (4 * j + i <= last) ? sacc[i] * a.scale_log2 : -INFINITY;
+      sc[i] = (4 * j + i <= last) ? sacc[i] : -INFINITY;
       mt = fmaxf(mt, sc[i]);
     }
-    mt = max_xor32(max_xor16(mt));
-    const float mn = fmaxf(m, mt);
-    const float alpha = exp2f(m - mn);
+    mt = max_xor32(max_xor16(mt)) * a.scale_log2;
+    const bool move = mt > m + kRescaleSlack;
+    if (__builtin_amdgcn_ballot_w64(move) != 0) {
+      const float mn = move ? mt : m;
+      const float alpha = __builtin_amdgcn_exp2f(m - mn);  // 0 on the first step
+      l *= alpha;
+      m = mn;
+#pragma unroll
+      for (int nb = 0; nb < 8; ++nb) acc[nb] *= alpha;
+    }
+    // v_exp_f32 directly: arguments are <= kRescaleSlack, and results below
+    // 2^-126 flush to zero, which a bf16 weight could not hold anyway.
     float p[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) p[i] = exp2f(sc[i] - mn);
-    l = l * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
-    m = mn;
+    for (int i = 0; i < 4; ++i) p[i] = __builtin_amdgcn_exp2f(fmaf(sc[i], a.scale_log2, -m));
+    l += (p[0] + p[1]) + (p[2] + p[3]);
     u32x2_t pw = {pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3])};
     const bf16x4_t pop = __builtin_bit_cast(bf16x4_t, pw);
-#pragma unroll
-    for (int nb = 0; nb < 8; ++nb) acc[nb] *= alpha;
     SGL_PV(0); SGL_PV(1); SGL_PV(2); SGL_PV(3);
     SGL_PV(4); SGL_PV(5); SGL_PV(6); SGL_PV(7);
     __builtin_amdgcn_sched_barrier(0);
-    load_v_step(vbase, a.kv_ss, sidx, tn, len, n, j, vr);  // V of the next step
+    load_v_step(vlane, ss_bytes, sidx, tn, len, j, vr);  // V of the next step
     __builtin_amdgcn_sched_barrier(0);
   }
   l = sum_xor32(sum_xor16(l));
@@ -653,6 +671,8 @@ int decode_args(const sgl_decode_plan_t* plan, const void* q, int64_t q_stride_t
   if (batch_size > plan->batch_size || num_qo_heads != plan->num_qo_heads ||
       num_kv_heads != plan->num_kv_heads)
     return SGL_ERR_CAPACITY;
+  // Row addresses use 32-bit slot byte strides.
+  if (kv_stride_slot <= 0 || kv_stride_slot > 0x7fffffff) return SGL_ERR_UNSUPPORTED;
   // Output rows are written with 16-byte stores (whole requests).
   if (q_stride_head % 8 || q_stride_token % 8 || kv_stride_slot % 8 || kv_stride_head % 8 ||
       o_stride_token % 8 || o_stride_head % 8 || !aligned16(q) || !aligned16(k_cache) ||
