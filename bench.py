@@ -339,6 +339,39 @@ def cpu_baseline_prefill(torch, wl, w):
                       f"median of 5 runs after 1 warm-up, {threads} threads"}
 
 
+def cpu_baseline_fused(torch, wl, w):
+    """LibTorch-CPU fused qk-norm + RoPE + KV store (oracle/torch_cpu.py) on the
+    whole config 3 workload, median of 5 runs after a warm-up."""
+    from oracle import torch_cpu as tc
+    b, s = w.batch, w.shape
+    threads = _cpu_threads(torch)
+    hq, hkv, D = s.num_qo_heads, s.num_kv_heads, s.head_dim
+    T = int(b.qo_indptr[-1])
+    g = torch.Generator()
+    g.manual_seed(6)
+    qkv = torch.randn((T, s.qkv_width), generator=g).to(torch.bfloat16)
+    kc = torch.zeros((T, hkv, D), dtype=torch.bfloat16)
+    vc = torch.zeros_like(kc)
+    qw = (torch.rand(D, generator=g) + 0.5).to(torch.bfloat16)
+    kw = (torch.rand(D, generator=g) + 0.5).to(torch.bfloat16)
+    # the reference's table (rotary_embedding.cu:80-93), built once, not timed
+    inv_freq = 1.0 / (w.extra["theta"] ** (torch.arange(0, D, 2, dtype=torch.float32) / D))
+    freqs = torch.outer(torch.arange(w.extra["max_pos"], dtype=torch.float32), inv_freq)
+    cos, sin = freqs.cos(), freqs.sin()
+    pos = torch.from_numpy(b.positions.astype(np.int64))
+    loc = torch.from_numpy(b.out_loc.astype(np.int64))
+    eps = w.extra["eps"]
+    med, runs = tc.median_time(lambda: tc.fused_qknorm_rope_store(qkv, kc, vc, qw, kw, cos, sin,
+                                                                   pos, loc, hq, hkv, eps))
+    nbytes = wl.fused_store_bytes(s, T)
+    return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "kind": "port", "cpu_model": tc.host_info()["cpu_model"], "median_s": round(med, 4),
+            "runs_s": [round(t, 4) for t in runs],
+            "sample": f"LibTorch-CPU fused qk-norm + RoPE + KV store (oracle/torch_cpu.py), all "
+                      f"{T} tokens of {w.name}, median of 5 runs after 1 warm-up, "
+                      f"{threads} threads"}
+
+
 def cpu_baseline_mixed(torch, wl, w):
     """Config 5 on the CPU: ONE layer (the 64 decode rows and the 2048-token
     chunk, LibTorch-CPU fp32), median of 5, scaled x layers as stated."""
@@ -559,12 +592,15 @@ def main():
             cpu = cpu_baseline_decode(torch, wl, w)
         elif args.workload == "cfg2":
             cpu = cpu_baseline_prefill(torch, wl, w)
+        elif args.workload == "cfg3":
+            cpu = cpu_baseline_fused(torch, wl, w)
         elif args.workload == "cfg5":
             cpu = cpu_baseline_mixed(torch, wl, w)
         if args.workload == "cfg4" and not args.no_extra:
             # the other CPU legs of the plan, beside their GPU lines in extra
             for name, fn in (("cfg2", lambda: cpu_baseline_prefill(torch, wl,
                                                                    wl.cfg2_prefill_prefix())),
+                             ("cfg3", lambda: cpu_baseline_fused(torch, wl, wl.cfg3_fused_store())),
                              ("cfg5", lambda: cpu_baseline_mixed(torch, wl,
                                                                  wl.cfg5_mixed(layers=48)))):
                 try:

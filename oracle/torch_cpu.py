@@ -6,6 +6,10 @@ and per kv-head group, gather the request's K/V rows from the pool, then
 matmul -> (causal-masked) softmax -> matmul (the semantics of
 src/attention/flashinfer_backend.cu:553-595 for decode and :596-679 for
 causal prefill, bottom-right aligned). PyTorch's CPU operators are LibTorch's.
+The fused store is the same elementwise operations plus index_put_: q/k
+RMSNorm (src/layers/normalization.cu:138-170, bf16-rounded), NeoX RoPE
+(src/layers/rotary_embedding.cu:50-66, half-width cos/sin table), then the
+K/V store (src/kvcache/mha_kvcache.cu:13-41).
 Only bench.py's cpu_baseline leg and tests/ use this module, never the
 product path. Tensors are CPU torch tensors: q [rows, Hq, D] bf16, caches
 [slots, Hkv, D] bf16, index arrays int64.
@@ -72,6 +76,35 @@ def prefill(q, k_cache, v_cache, indices, qo_indptr, kv_indptr, sm_scale, out=No
             o = torch.matmul(p, v).view(hkv, n, G, D).permute(1, 0, 2, 3)
             out[q0 + t0:q0 + t1] = o.reshape(n, hq, D)
     return out
+
+
+def fused_qknorm_rope_store(qkv, k_cache, v_cache, q_weight, k_weight, cos, sin, positions,
+                            out_loc, num_qo_heads, num_kv_heads, eps):
+    """In place: q part of qkv [T, (Hq + 2 Hkv) D] bf16 normalised and rotated;
+    k normalised, rotated and stored at k_cache[out_loc]; v stored raw at
+    v_cache[out_loc]. cos/sin fp32 [max_pos, D/2]; positions, out_loc int64."""
+    T = qkv.shape[0]
+    D = q_weight.shape[0]
+    hq, hkv = num_qo_heads, num_kv_heads
+    q = qkv[:, :hq * D].view(T, hq, D)
+    k = qkv[:, hq * D:(hq + hkv) * D].view(T, hkv, D)
+    v = qkv[:, (hq + hkv) * D:].view(T, hkv, D)
+    c = cos.index_select(0, positions).unsqueeze(1)
+    s = sin.index_select(0, positions).unsqueeze(1)
+
+    def norm(x, w):
+        xf = x.float()
+        r = torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
+        return (xf * r * w.float()).to(torch.bfloat16)
+
+    def rope(x):
+        xf = x.float()
+        x1, x2 = xf[..., :D // 2], xf[..., D // 2:]
+        return torch.cat([x1 * c - x2 * s, x2 * c + x1 * s], -1).to(torch.bfloat16)
+
+    q.copy_(rope(norm(q, q_weight)))
+    k_cache.index_put_((out_loc,), rope(norm(k, k_weight)))
+    v_cache.index_put_((out_loc,), v)
 
 
 def host_info() -> dict:

@@ -643,3 +643,55 @@ def test_torch_cpu_baseline_matches_oracle(oracle):
     got = tc.decode(t(qd), t(kc), t(vc), idx, b.kv_indptr, scale).numpy()
     want = oracle.decode(qd, kc, vc, b.indices, b.kv_indptr, scale)
     np.testing.assert_allclose(got, want, atol=2e-5, rtol=1e-4)
+
+
+def test_torch_cpu_fused_store_matches_oracle(oracle):
+    """The LibTorch-CPU leg of the fused qk-norm + RoPE + store
+    (oracle/torch_cpu.py) against the C oracle's norm -> rope -> store: V
+    placement bit-exact, q and the stored k within two bf16 ulps (two chained
+    roundings) or the norm's rounding carried through the rotation."""
+    import torch
+    from oracle import torch_cpu as tc
+    rng = np.random.default_rng(12)
+    T, hq, hkv, D, slots = 37, 8, 2, 128, 64
+    qkv = oracle.f32_to_bf16(rng.standard_normal((T, (hq + 2 * hkv) * D), dtype=np.float32))
+    qw = oracle.f32_to_bf16(rng.uniform(0.5, 1.5, D).astype(np.float32))
+    kw = oracle.f32_to_bf16(rng.uniform(0.5, 1.5, D).astype(np.float32))
+    cos, sin = oracle.cos_sin_cache(512, D, 1e6)
+    pos = rng.integers(0, 512, T).astype(np.int32)
+    loc = rng.permutation(slots)[:T].astype(np.int32)
+    kc0 = oracle.f32_to_bf16(rng.standard_normal((slots, hkv * D), dtype=np.float32))
+    vc0 = oracle.f32_to_bf16(rng.standard_normal((slots, hkv * D), dtype=np.float32))
+    # C oracle
+    qh = qkv[:, :hq * D].reshape(T, hq, D).copy()
+    kh = qkv[:, hq * D:(hq + hkv) * D].reshape(T, hkv, D).copy()
+    vh = qkv[:, (hq + hkv) * D:].reshape(T, hkv * D).copy()
+    oracle.qk_rmsnorm(qh, kh, qw, kw, 1e-6)
+    oracle.rope(qh, kh, cos, sin, pos)
+    kc_ref, vc_ref = kc0.copy(), vc0.copy()
+    oracle.store_kv(kc_ref, vc_ref, kh.reshape(T, -1), vh, loc)
+    # LibTorch CPU
+    t = lambda a: torch.from_numpy(a.copy().view(np.int16)).view(torch.bfloat16)  # noqa: E731
+    qkv_t, kc_t, vc_t = t(qkv), t(kc0).view(slots, hkv, D), t(vc0).view(slots, hkv, D)
+    tc.fused_qknorm_rope_store(qkv_t, kc_t, vc_t, t(qw), t(kw), torch.from_numpy(cos),
+                               torch.from_numpy(sin), torch.from_numpy(pos.astype(np.int64)),
+                               torch.from_numpy(loc.astype(np.int64)), hq, hkv, 1e-6)
+    u = lambda x: x.contiguous().view(torch.int16).numpy().view(np.uint16)  # noqa: E731
+    np.testing.assert_array_equal(u(vc_t).reshape(slots, -1), vc_ref)
+    np.testing.assert_array_equal(u(qkv_t)[:, hq * D:], qkv[:, hq * D:])  # k, v of qkv untouched
+    f = lambda x: oracle.bf16_to_f32(x).astype(np.float64)  # noqa: E731
+
+    def close(got, want, pre):
+        # two chained roundings: <= 2 ulps of the output, or one ulp of the
+        # normalised input pair carried through the rotation
+        x = np.abs(f(pre))
+        tol = np.maximum(2.0 ** -6 * np.abs(f(want)), 2.0 ** -7 * (x + np.roll(x, D // 2, -1)))
+        assert np.all(np.abs(f(got) - f(want)) <= tol + 1e-6)
+
+    qn = qkv[:, :hq * D].reshape(T, hq, D).copy()
+    kn = qkv[:, hq * D:(hq + hkv) * D].reshape(T, hkv, D).copy()
+    oracle.qk_rmsnorm(qn, kn, qw, kw, 1e-6)
+    close(u(qkv_t)[:, :hq * D].reshape(T, hq, D), qh, qn)
+    close(u(kc_t).reshape(slots, hkv, D)[loc], kc_ref.reshape(slots, hkv, D)[loc], kn)
+    untouched = np.setdiff1d(np.arange(slots), loc)
+    np.testing.assert_array_equal(u(kc_t).reshape(slots, -1)[untouched], kc0[untouched])
