@@ -165,10 +165,6 @@ __device__ __forceinline__ bf16x4_t v_operand(const u32x4_t (&vr)[4]) {
   return __builtin_bit_cast(bf16x4_t, out);
 }
 
-#define SGL_PV(nb)                                                                   \
-  acc[nb] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(v_operand<nb>(vr), pop, acc[nb], \
-                                                      0, 0, 0)
-
 // Softmax state of one wave's piece (lane (n, j): head n, d = 32 j + 8 i + nb
 // in acc[nb][i]), for the small-batch kernel's in-workgroup fold.
 struct HeadState {
@@ -189,6 +185,9 @@ struct HeadState {
 // exactly the B operand P^T the second product needs, and both put the head
 // on the lane's column, so max, sum and the rescale of O are lane-local apart
 // from one exchange across the four lane groups.
+//
+// K and V of step t + 1 are in flight during step t; the Q rows are loaded
+// first and the first step's K/V rows issued before Q is waited for.
 template <bool kState>
 __device__ __forceinline__ void decode_head(const DecodeArgs& a, WaveLds& L, const int32_t* sidx,
                                             int pslot, bool whole, int h, int len, int qrow,
@@ -201,53 +200,50 @@ __device__ __forceinline__ void decode_head(const DecodeArgs& a, WaveLds& L, con
   const char* vlane = reinterpret_cast<const char*>(a.vc + static_cast<int64_t>(h) * a.kv_sh + 8 * n);
   const uint32_t ss_bytes = static_cast<uint32_t>(a.kv_ss * 2);
 
-  // Q rows of this kv head's G query heads -> LDS (16 rows x 16 chunks).
+  // Q rows of this kv head's G query heads (16 rows x 16 chunks), for LDS.
+  u32x4_t qv[4];
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
     const int row = u * 4 + j;
-    u32x4_t v = {0, 0, 0, 0};
+    qv[u] = u32x4_t{0, 0, 0, 0};
     if (row < G)
-      v = ldg128(a.q + static_cast<int64_t>(qrow) * a.q_st +
-                 static_cast<int64_t>(h * G + row) * a.q_sh + n * 8);
-    *reinterpret_cast<u32x4_t*>(L.q + row * kQPitch + n * 8) = v;
+      qv[u] = ldg128(a.q + static_cast<int64_t>(qrow) * a.q_st +
+                     static_cast<int64_t>(h * G + row) * a.q_sh + n * 8);
   }
-  wave_lds_sync();
 
-  // Prologue: K and V rows of the first step in flight, K issued first as
-  // inside the loop (the loop-head wait counts merge both paths).
+  // K and V rows of the first step in flight, K issued first as inside the
+  // loop (the loop-head wait counts merge both paths).
   u32x4_t kr[4], vr[4];
   load_k_step(klane, ss_bytes, sidx[min(n, len - 1)], kr);
   __builtin_amdgcn_sched_barrier(0);
   load_v_step(vlane, ss_bytes, sidx, 0, len, j, vr);
   __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int u = 0; u < 4; ++u) *reinterpret_cast<u32x4_t*>(L.q + (u * 4 + j) * kQPitch + n * 8) = qv[u];
+  wave_lds_sync();
 
-  float m = -INFINITY;  // running max of head n (replicated over j)
+  float m = -INFINITY;  // running reference point of head n (replicated over j)
   float l = 0.f;        // partial sum over this lane's tokens of head n
   f32x4_t acc[8];
 #pragma unroll
   for (int nb = 0; nb < 8; ++nb) acc[nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  for (int t = 0; t < len; t += kStep) {
-    // Keep the workgroup's waves (one per kv head) in step: together they
-    // read each token's whole [Hkv, D] row, which DRAM serves better as one
-    // burst than as per-head pieces spread over time.
-    if constexpr (!kState) __builtin_amdgcn_s_barrier();
-    const int tn = t + kStep;
-    const int kslot_next = sidx[min(tn + n, len - 1)];
+  // S^T of one step.
+  auto qk = [&](const u32x4_t (&k)[4]) {
     f32x4_t sacc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       const bf16x8_t qop = *reinterpret_cast<const bf16x8_t*>(L.q + n * kQPitch + 32 * s + 8 * j);
-      sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kr[s]), qop, sacc, 0, 0, 0);
+      sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(k[s]), qop, sacc, 0, 0, 0);
     }
-    __builtin_amdgcn_sched_barrier(0);
-    load_k_step(klane, ss_bytes, kslot_next, kr);  // K of the next step
-    __builtin_amdgcn_sched_barrier(0);
-
-    // Online softmax in the log2 domain with a lazy reference point: m only
-    // moves when a head's step maximum exceeds it by more than
-    // kRescaleSlack, so most steps skip the rescale of O. Exact: p and l of
-    // a head always use the same m, and p <= 2^kRescaleSlack.
+    return sacc;
+  };
+  // Online softmax of the step starting at token t, then O^T += V^T P^T.
+  auto softmax_pv = [&](const f32x4_t& sacc, const u32x4_t (&vv)[4], int t) {
+    // Log2 domain with a lazy reference point: m only moves when a head's
+    // step maximum exceeds it by more than kRescaleSlack, so most steps skip
+    // the rescale of O. Exact: p and l of a head always use the same m, and
+    // p <= 2^kRescaleSlack.
     const int last = len - t - 1;
     float sc[4];
     float mt = -INFINITY;
@@ -274,8 +270,24 @@ __device__ __forceinline__ void decode_head(const DecodeArgs& a, WaveLds& L, con
     l += (p[0] + p[1]) + (p[2] + p[3]);
     u32x2_t pw = {pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3])};
     const bf16x4_t pop = __builtin_bit_cast(bf16x4_t, pw);
-    SGL_PV(0); SGL_PV(1); SGL_PV(2); SGL_PV(3);
-    SGL_PV(4); SGL_PV(5); SGL_PV(6); SGL_PV(7);
+    static_for<0, 8>([&](auto NB) {
+      constexpr int nb = decltype(NB)::value;
+      acc[nb] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(v_operand<nb>(vv), pop, acc[nb], 0, 0, 0);
+    });
+  };
+
+  for (int t = 0; t < len; t += kStep) {
+    // Keep the workgroup's waves (one per kv head) in step: together they
+    // read each token's whole [Hkv, D] row, which DRAM serves better as one
+    // burst than as per-head pieces spread over time.
+    if constexpr (!kState) __builtin_amdgcn_s_barrier();
+    const int tn = t + kStep;
+    const int kslot_next = sidx[min(tn + n, len - 1)];
+    const f32x4_t sacc = qk(kr);
+    __builtin_amdgcn_sched_barrier(0);
+    load_k_step(klane, ss_bytes, kslot_next, kr);  // K of the next step
+    __builtin_amdgcn_sched_barrier(0);
+    softmax_pv(sacc, vr, t);
     __builtin_amdgcn_sched_barrier(0);
     load_v_step(vlane, ss_bytes, sidx, tn, len, j, vr);  // V of the next step
     __builtin_amdgcn_sched_barrier(0);
@@ -318,7 +330,6 @@ __device__ __forceinline__ void decode_head(const DecodeArgs& a, WaveLds& L, con
     if (j == 0) a.part_lse[pidx] = l > 0.f ? m + log2f(l) : -INFINITY;
   }
 }
-#undef SGL_PV
 
 // Zero output row of an empty request (kv_len 0).
 __device__ __forceinline__ void zero_row(const DecodeArgs& a, int qrow) {
