@@ -292,7 +292,9 @@ void HipAttnBackend::prepare_metadata(Batch& batch) {
 torch::Tensor HipAttnBackend::forward(const torch::Tensor& q, const torch::Tensor& k,
                                       const torch::Tensor& v, int layer_id, Batch& batch) {
   // Reference: FlashInferBackend::forward (flashinfer_backend.cu:522-681):
-  // store the new tokens' K/V, then paged attention over the pool.
+  // store the new tokens' K/V, then paged attention over the pool. A batch
+  // without metadata is refused before the store.
+  metadata_of(batch);
   auto k_3d = k.dim() == 2 ? k.view({-1, num_kv_heads_, head_dim_}) : k;
   auto v_3d = v.dim() == 2 ? v.view({-1, num_kv_heads_, head_dim_}) : v;
   kv_cache_->store_kv(k_3d, v_3d, batch.out_loc, layer_id);
@@ -938,6 +940,10 @@ AttentionLayer::AttentionLayer(int layer_id, int num_qo_heads, int num_kv_heads,
 
 torch::Tensor AttentionLayer::forward(const torch::Tensor& qkv, const torch::Tensor& positions,
                                       Batch& batch) {
+  // Missing context fails before anything is written (the reference's
+  // layer throws on a missing context, tests/layers/test_attention_layer.cpp:7-22).
+  TORCH_CHECK(batch.attn_metadata,
+              "AttentionLayer: the batch has no attention metadata (call prepare_metadata first)");
   TORCH_CHECK(qkv.dim() == 2 && qkv.stride(1) == 1, "qkv must be [T, (Hq + 2 Hkv) D]");
   check_bf16(qkv, "qkv");
   TORCH_CHECK(qkv.size(1) == (num_qo_heads_ + 2 * num_kv_heads_) * head_dim_,

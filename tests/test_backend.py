@@ -195,6 +195,34 @@ def test_attention_layer_matches_unfused_modules(dev, sb):
 
 
 @pytest.mark.gpu
+def test_missing_context_raises_without_side_effects(dev, sb):
+    """The reference's layer test expects a throw when the context is missing
+    (tests/layers/test_attention_layer.cpp:7-22): here a backend without a page
+    table refuses prepare_metadata, and a layer or backend forward on a batch
+    without metadata raises before anything reaches the pool."""
+    note("missing context")
+    rng = np.random.default_rng(53)
+    hq, hkv = 16, 8
+    b = wl.make_paged_batch(rng, [3, 0], [4, 20], page_size=16)
+    s = Setup(sb, dev, b, hq, hkv, 54)
+    bare = sb.HipAttnBackend(s.cache, hq, hkv, D)
+    with pytest.raises(RuntimeError, match="set_page_table"):
+        bare.prepare_metadata(s.batch)
+    rot = sb.RotaryEmbedding(D, D, 8192, 1e6, 0)
+    layer = sb.AttentionLayer(0, hq, hkv, D, s.backend, rot, None, None)
+    qkv = torch.cat([s.q, s.k, s.v], dim=1)
+    qkv_before = qkv.clone()
+    pool_before = s.cache.buffer().clone()
+    with pytest.raises(RuntimeError, match="prepare_metadata"):
+        layer.forward(qkv, s.batch.positions, s.batch)
+    with pytest.raises(RuntimeError, match="prepare_metadata"):
+        s.backend.forward(s.q, s.k, s.v, 0, s.batch)
+    torch.cuda.synchronize()
+    assert torch.equal(qkv.view(torch.int16), qkv_before.view(torch.int16))
+    assert torch.equal(s.cache.buffer().view(torch.int16), pool_before.view(torch.int16))
+
+
+@pytest.mark.gpu
 def test_backend_decode_graph_capture_replay(oracle, dev, sb):
     """Capture forward once at the worst case, replay on batches of new lengths;
     every replay matches the oracle and the eager forward of the same batch."""
