@@ -31,7 +31,7 @@ extern "C" {
 #define SGL_INDEX_I32 0
 #define SGL_INDEX_I64 1
 
-#define SGL_DTYPE_BF16 0  /* 16-bit element types of the residual-path kernels */
+#define SGL_DTYPE_BF16 0  /* 16-bit element types (norm, RoPE and residual-path kernels) */
 #define SGL_DTYPE_F16 1
 
 /* Human-readable text for a status code (static storage). */
@@ -39,7 +39,7 @@ const char* sgl_status_string(int status);
 
 /* Library version, to check that the loaded .so matches this header. */
 int sgl_abi_version(void);
-#define SGL_ABI_VERSION 9
+#define SGL_ABI_VERSION 10
 
 /* ------------------------------------------------------------------ */
 /* KV-cache store                                                      */
@@ -143,7 +143,9 @@ int sgl_rope_cos_sin_cache(float* cos_cache, float* sin_cache, int64_t max_pos,
 /*
  * In-place per-(token, head) RMSNorm of q [tokens, q_heads, d] and
  * k [tokens, k_heads, d] (strided views, last dim contiguous):
- * x <- bf16(x * rsqrt(mean(x^2) + eps) * w), fp32 accumulation.
+ * x <- T(x * rsqrt(mean(x^2) + eps) * w), fp32 accumulation, T = bf16 or
+ * fp16 (dtype SGL_DTYPE_*; q, k and the weights share it, as the reference
+ * dispatches both at :346-372).
  * Pass k = NULL / k_heads = 0 to normalise q only.
  * Replaces: fused_qk_rmsnorm_inplace_3d_strided (src/layers/normalization.cu:318-384)
  *           and RMSNorm::forward_inplace_3d_strided (:271-316).
@@ -152,13 +154,15 @@ int sgl_qk_rmsnorm(void* q, void* k, const void* q_weight,
                    const void* k_weight, int64_t tokens, int64_t q_heads,
                    int64_t k_heads, int64_t d, int64_t q_stride_token,
                    int64_t q_stride_head, int64_t k_stride_token,
-                   int64_t k_stride_head, float eps, void* stream);
+                   int64_t k_stride_head, float eps, int dtype, void* stream);
 
 /*
  * In-place NeoX (rotate-half) RoPE of q [nnz, q_heads, head_dim] and
  * k [nnz, kv_heads, head_dim] at positions[t] (int32), using fp32 cos/sin
  * caches of width cos_width (rotary_dim/2 or rotary_dim). Elements at
- * index >= rotary_dim pass through.
+ * index >= rotary_dim pass through. q and k are bf16 or fp16 (dtype
+ * SGL_DTYPE_*, the reference dispatches both at :124-168); fp32 math, one
+ * rounding per element.
  * Replaces: RotaryEmbedding::forward_inplace (src/layers/rotary_embedding.cu:96-178;
  *           formula :50-66).
  */
@@ -166,7 +170,7 @@ int sgl_rope(void* q, void* k, const float* cos_cache, const float* sin_cache,
              const int32_t* positions, int64_t nnz, int64_t q_heads,
              int64_t kv_heads, int64_t rotary_dim, int64_t head_dim,
              int64_t cos_width, int64_t q_stride_token, int64_t q_stride_head,
-             int64_t k_stride_token, int64_t k_stride_head, void* stream);
+             int64_t k_stride_token, int64_t k_stride_head, int dtype, void* stream);
 
 /*
  * One pass over the qkv activation [T, (Hq + 2 Hkv) * D] (row stride

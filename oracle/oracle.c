@@ -160,33 +160,72 @@ void oracle_cos_sin_cache(float* cos_cache, float* sin_cache, int64_t max_pos, i
   }
 }
 
+/* ---------- fp16 bit patterns (IEEE binary16) ---------- */
+
+static float round_t(float x, int dtype);
+
+static inline float f16_to_f32(uint16_t h) {
+  const int sign = (h >> 15) & 1, e = (h >> 10) & 0x1f, m = h & 0x3ff;
+  float v;
+  if (e == 0) v = ldexpf((float)m, -24);                 /* zero / subnormal */
+  else if (e == 31) v = m ? NAN : INFINITY;
+  else v = ldexpf((float)(m | 0x400), e - 25);
+  return sign ? -v : v;
+}
+
+/* Round to nearest even (round_t), then encode. */
+static inline uint16_t f32_to_f16(float x) {
+  const float r = round_t(x, 1);
+  const uint16_t sign = signbit(r) ? 0x8000 : 0;
+  if (isnan(r)) return 0x7e00;
+  const float a = fabsf(r);
+  if (isinf(a)) return sign | 0x7c00;
+  if (a < 6.103515625e-05f) return sign | (uint16_t)(a * 16777216.0f); /* subnormal: a / 2^-24 */
+  int e;
+  const float m = frexpf(a, &e);               /* a = m 2^e, m in [0.5, 1) */
+  const int field = e - 1 + 15;
+  const uint16_t man = (uint16_t)((m * 2.0f - 1.0f) * 1024.0f);
+  return sign | (uint16_t)(field << 10) | man;
+}
+
+/* 16-bit element load / store: dtype 0 = bf16, 1 = fp16. */
+static inline float ld16(uint16_t b, int dtype) { return dtype ? f16_to_f32(b) : bf16_to_f32(b); }
+static inline uint16_t st16(float x, int dtype) { return dtype ? f32_to_f16(x) : f32_to_bf16(x); }
+
+void oracle_f16_bits(const float* in, uint16_t* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = f32_to_f16(in[i]);
+}
+void oracle_f16_values(const uint16_t* in, float* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = f16_to_f32(in[i]);
+}
+
 /* ---------- q/k RMSNorm: src/layers/normalization.cu:99-170 ---------- */
 
-static void rmsnorm_row(uint16_t* row, const uint16_t* w, int64_t d, float eps) {
+static void rmsnorm_row(uint16_t* row, const uint16_t* w, int64_t d, float eps, int dtype) {
   float ss = 0.f;
   for (int64_t i = 0; i < d; ++i) {
-    const float x = bf16_to_f32(row[i]);
+    const float x = ld16(row[i], dtype);
     ss += x * x;
   }
   const float scale = 1.0f / sqrtf(ss / (float)d + eps);
   for (int64_t i = 0; i < d; ++i)
-    row[i] = f32_to_bf16((bf16_to_f32(row[i]) * scale) * bf16_to_f32(w[i]));
+    row[i] = st16((ld16(row[i], dtype) * scale) * ld16(w[i], dtype), dtype);
 }
 
 void oracle_qk_rmsnorm(uint16_t* q, uint16_t* k, const uint16_t* qw, const uint16_t* kw,
                        int64_t tokens, int64_t qh, int64_t kh, int64_t d, int64_t q_st,
-                       int64_t q_sh, int64_t k_st, int64_t k_sh, float eps) {
+                       int64_t q_sh, int64_t k_st, int64_t k_sh, float eps, int dtype) {
   for (int64_t t = 0; t < tokens; ++t) {
-    for (int64_t h = 0; h < qh; ++h) rmsnorm_row(q + t * q_st + h * q_sh, qw, d, eps);
+    for (int64_t h = 0; h < qh; ++h) rmsnorm_row(q + t * q_st + h * q_sh, qw, d, eps, dtype);
     if (k)
-      for (int64_t h = 0; h < kh; ++h) rmsnorm_row(k + t * k_st + h * k_sh, kw, d, eps);
+      for (int64_t h = 0; h < kh; ++h) rmsnorm_row(k + t * k_st + h * k_sh, kw, d, eps, dtype);
   }
 }
 
 /* ---------- RoPE: src/layers/rotary_embedding.cu:50-66 (NeoX rotate-half) ---------- */
 
 static void rope_row(uint16_t* row, const float* cos_row, const float* sin_row,
-                     int64_t rotary_dim, int64_t cos_width) {
+                     int64_t rotary_dim, int64_t cos_width, int dtype) {
   const int64_t half = rotary_dim / 2;
   float buf[4096];
   for (int64_t i = 0; i < rotary_dim; ++i) {
@@ -194,25 +233,27 @@ static void rope_row(uint16_t* row, const float* cos_row, const float* sin_row,
     const int64_t pair = first ? i : i - half;
     const int64_t other = first ? i + half : i - half;
     const int64_t ci = cos_width == rotary_dim ? i : pair;
-    const float v = bf16_to_f32(row[i]);
-    const float o = bf16_to_f32(row[other]);
+    const float v = ld16(row[i], dtype);
+    const float o = ld16(row[other], dtype);
     const float c = cos_row[ci], s = sin_row[ci];
     buf[i] = first ? (v * c - o * s) : (v * c + o * s);
   }
-  for (int64_t i = 0; i < rotary_dim; ++i) row[i] = f32_to_bf16(buf[i]);
+  for (int64_t i = 0; i < rotary_dim; ++i) row[i] = st16(buf[i], dtype);
 }
 
 int oracle_rope(uint16_t* q, uint16_t* k, const float* cos_cache, const float* sin_cache,
                 const int32_t* positions, int64_t nnz, int64_t qh, int64_t kh,
                 int64_t rotary_dim, int64_t cos_width, int64_t q_st, int64_t q_sh,
-                int64_t k_st, int64_t k_sh) {
+                int64_t k_st, int64_t k_sh, int dtype) {
   if (rotary_dim > 4096) return -1;
   for (int64_t t = 0; t < nnz; ++t) {
     const int64_t p = positions[t];
     const float* cr = cos_cache + p * cos_width;
     const float* sr = sin_cache + p * cos_width;
-    for (int64_t h = 0; h < qh; ++h) rope_row(q + t * q_st + h * q_sh, cr, sr, rotary_dim, cos_width);
-    for (int64_t h = 0; h < kh; ++h) rope_row(k + t * k_st + h * k_sh, cr, sr, rotary_dim, cos_width);
+    for (int64_t h = 0; h < qh; ++h)
+      rope_row(q + t * q_st + h * q_sh, cr, sr, rotary_dim, cos_width, dtype);
+    for (int64_t h = 0; h < kh; ++h)
+      rope_row(k + t * k_st + h * k_sh, cr, sr, rotary_dim, cos_width, dtype);
   }
   return 0;
 }

@@ -141,22 +141,40 @@ def cos_sin_cache(max_pos: int, rotary_dim: int, base: float):
     return cos, sin
 
 
-def qk_rmsnorm(q, k, qw, kw, eps: float) -> None:
-    """In place on uint16 arrays q [T, Hq, D], k [T, Hk, D] (contiguous)."""
+def qk_rmsnorm(q, k, qw, kw, eps: float, dtype: str = "bf16") -> None:
+    """In place on uint16 bit patterns (bf16 or fp16) q [T, Hq, D], k [T, Hk, D]
+    (contiguous)."""
     T, qh, d = q.shape
     kh = 0 if k is None else k.shape[1]
     lib().oracle_qk_rmsnorm(_p(q), _p(k), _p(qw), _p(kw), I64(T), I64(qh), I64(kh), I64(d),
-                            I64(qh * d), I64(d), I64(kh * d), I64(d), F32(eps))
+                            I64(qh * d), I64(d), I64(kh * d), I64(d), F32(eps),
+                            ctypes.c_int(_DT[dtype]))
 
 
-def rope(q, k, cos, sin, positions, rotary_dim: int | None = None) -> None:
+def rope(q, k, cos, sin, positions, rotary_dim: int | None = None, dtype: str = "bf16") -> None:
     T, qh, d = q.shape
     kh = k.shape[1]
     rd = d if rotary_dim is None else rotary_dim
     pos = np.ascontiguousarray(positions, np.int32)
     rc = lib().oracle_rope(_p(q), _p(k), _p(cos), _p(sin), _p(pos), I64(T), I64(qh), I64(kh),
-                           I64(rd), I64(cos.shape[1]), I64(qh * d), I64(d), I64(kh * d), I64(d))
+                           I64(rd), I64(cos.shape[1]), I64(qh * d), I64(d), I64(kh * d), I64(d),
+                           ctypes.c_int(_DT[dtype]))
     assert rc == 0
+
+
+def f32_to_f16_bits(x: np.ndarray) -> np.ndarray:
+    """fp32 -> IEEE binary16 bit patterns (round to nearest even), the oracle's encoding."""
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty(x.shape, np.uint16)
+    lib().oracle_f16_bits(_p(x), _p(out), I64(x.size))
+    return out
+
+
+def f16_bits_to_f32(b: np.ndarray) -> np.ndarray:
+    b = np.ascontiguousarray(b, np.uint16)
+    out = np.empty(b.shape, np.float32)
+    lib().oracle_f16_values(_p(b), _p(out), I64(b.size))
+    return out
 
 
 def decode(q, k_cache, v_cache, indices, kv_indptr, sm_scale: float, q_indptr=None) -> np.ndarray:

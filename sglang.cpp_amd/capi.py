@@ -25,7 +25,7 @@ SGL_INDEX_I32 = 0
 SGL_INDEX_I64 = 1
 SGL_DTYPE_BF16 = 0
 SGL_DTYPE_F16 = 1
-ABI_VERSION = 9
+ABI_VERSION = 10
 FUSED_NO_K_WRITEBACK = 1  # SGL_FUSED_NO_K_WRITEBACK
 
 
@@ -68,9 +68,9 @@ _SIGNATURES = {
     "sgl_gather_int32_2d": ([_vp, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _vp], _i32),
     "sgl_rope_cos_sin_cache": ([_vp, _vp, _i64, _i32, _f32, _vp], _i32),
     "sgl_qk_rmsnorm": ([_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
-                        _f32, _vp], _i32),
+                        _f32, _i32, _vp], _i32),
     "sgl_rope": ([_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
-                  _i64, _i64, _vp], _i32),
+                  _i64, _i64, _i32, _vp], _i32),
     "sgl_fused_qknorm_rope_store": ([_vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64,
                                      _i32, _i32, _i32, _f32, _i32, _vp], _i32),
     "sgl_decode_plan": ([_vp, _i32, _i32, _i32, _i32, ctypes.POINTER(DecodePlan)], _i32),
@@ -277,14 +277,13 @@ def qk_rmsnorm(q: torch.Tensor, k: Optional[torch.Tensor], q_weight: torch.Tenso
     dev = _need_gpu(q, k, q_weight, k_weight)
     if q.dim() != 3 or q.stride(2) != 1 or (k is not None and (k.dim() != 3 or k.stride(2) != 1)):
         raise ValueError("q/k must be rank-3 with a contiguous last dimension")
-    if q.dtype != torch.bfloat16 or (k is not None and k.dtype != torch.bfloat16):
-        raise ValueError("q/k must be bf16")
+    dt = _dtype_code(*[t for t in (q, k, q_weight, k_weight) if t is not None])
     d = q.shape[2]
     kh = 0 if k is None else k.shape[1]
     _check(lib().sgl_qk_rmsnorm(_p(q), _p(k), _p(q_weight), _p(k_weight), q.shape[0], q.shape[1],
                                 kh, d, q.stride(0), q.stride(1),
                                 0 if k is None else k.stride(0), 0 if k is None else k.stride(1),
-                                eps, _stream(dev)), "sgl_qk_rmsnorm")
+                                eps, dt, _stream(dev)), "sgl_qk_rmsnorm")
 
 
 # ---------------------------------------------------------------- residual path
@@ -297,7 +296,7 @@ def _dtype_code(*ts: torch.Tensor) -> int:
         return SGL_DTYPE_BF16
     if dt == torch.float16:
         return SGL_DTYPE_F16
-    raise ValueError("residual-path kernels take bf16 or fp16")
+    raise ValueError("the 16-bit kernels take bf16 or fp16")
 
 
 def _rows2d(t: torch.Tensor, what: str) -> tuple[int, int, int]:
@@ -371,10 +370,11 @@ def rope(positions: torch.Tensor, q: torch.Tensor, k: torch.Tensor, cos_cache: t
     rd = head_dim if rotary_dim is None else rotary_dim
     if positions.dtype != torch.int32:
         raise ValueError("positions must be int32")
+    dt = _dtype_code(q, k)
     _check(lib().sgl_rope(_p(q), _p(k), _p(cos_cache), _p(sin_cache), _p(positions),
                           positions.shape[0], q.shape[1], k.shape[1], rd, head_dim,
                           cos_cache.shape[1], q.stride(0), q.stride(1), k.stride(0), k.stride(1),
-                          _stream(dev)), "sgl_rope")
+                          dt, _stream(dev)), "sgl_rope")
 
 
 def fused_qknorm_rope_store(qkv: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,

@@ -663,6 +663,21 @@ void write_page_table(const torch::Tensor& page_table, const std::vector<int32_t
 
 // ---------------------------------------------------------------- layers
 
+namespace {
+// SGL_DTYPE_* of a 16-bit floating tensor; the reference's kernels take
+// fp16 and bf16 (normalization.cu:253-268,346-372, activation.cu:25-44,
+// rotary_embedding.cu:124-168).
+int half_dtype(const torch::Tensor& t, const char* what) {
+  if (t.scalar_type() == torch::kBFloat16) return SGL_DTYPE_BF16;
+  TORCH_CHECK(t.scalar_type() == torch::kFloat16, what, " must be bf16 or fp16");
+  return SGL_DTYPE_F16;
+}
+
+void check_same_dtype(const torch::Tensor& a, const torch::Tensor& b, const char* what) {
+  TORCH_CHECK(a.scalar_type() == b.scalar_type(), what, " must share one dtype");
+}
+}  // namespace
+
 RMSNorm::RMSNorm(int size, float eps, torch::Device device) : eps_(eps) {
   weight = torch::ones({size}, torch::TensorOptions().dtype(torch::kBFloat16).device(device));
 }
@@ -670,23 +685,16 @@ RMSNorm::RMSNorm(int size, float eps, torch::Device device) : eps_(eps) {
 void RMSNorm::forward_inplace_3d_strided(torch::Tensor& x) const {
   TORCH_CHECK(x.is_cuda() && x.dim() == 3 && x.stride(2) == 1,
               "Strided RMSNorm expects a rank-3 device tensor with a contiguous last dim");
-  check_bf16(x, "x");
+  const int dt = half_dtype(x, "x");
+  check_same_dtype(x, weight, "x and the RMSNorm weight");
   TORCH_CHECK(weight.size(0) == x.size(2), "RMSNorm weight size must match last dimension");
   check_sgl(sgl_qk_rmsnorm(x.data_ptr(), nullptr, weight.data_ptr(), nullptr, x.size(0), x.size(1),
-                           0, x.size(2), x.stride(0), x.stride(1), 0, 0, eps_,
+                           0, x.size(2), x.stride(0), x.stride(1), 0, 0, eps_, dt,
                            current_stream(x.device())),
             "sgl_qk_rmsnorm");
 }
 
 namespace {
-// SGL_DTYPE_* of a 16-bit floating tensor; the reference's kernels take
-// fp16 and bf16 (normalization.cu:253-268, activation.cu:25-44).
-int half_dtype(const torch::Tensor& t, const char* what) {
-  if (t.scalar_type() == torch::kBFloat16) return SGL_DTYPE_BF16;
-  TORCH_CHECK(t.scalar_type() == torch::kFloat16, what, " must be bf16 or fp16");
-  return SGL_DTYPE_F16;
-}
-
 // [rows, d] view of a tensor whose rows are contiguous: rank 2 with any row
 // stride, or a contiguous tensor of higher rank.
 void rows_view(const torch::Tensor& t, int64_t& rows, int64_t& d, int64_t& stride,
@@ -882,11 +890,13 @@ void fused_qk_rmsnorm_inplace_3d_strided(torch::Tensor& q, torch::Tensor& k, con
   TORCH_CHECK(q.stride(2) == 1 && k.stride(2) == 1, "Last dimension must be contiguous");
   TORCH_CHECK(q.size(0) == k.size(0) && q.size(2) == k.size(2), "q / k shapes must agree");
   TORCH_CHECK(q_norm.eps() == k_norm.eps(), "Q and K RMSNorm eps must match");
-  check_bf16(q, "q");
-  check_bf16(k, "k");
+  const int dt = half_dtype(q, "q");
+  check_same_dtype(q, k, "q and k");
+  check_same_dtype(q, q_norm.weight, "q and the q-norm weight");
+  check_same_dtype(q, k_norm.weight, "q and the k-norm weight");
   check_sgl(sgl_qk_rmsnorm(q.data_ptr(), k.data_ptr(), q_norm.weight.data_ptr(),
                            k_norm.weight.data_ptr(), q.size(0), q.size(1), k.size(1), q.size(2),
-                           q.stride(0), q.stride(1), k.stride(0), k.stride(1), q_norm.eps(),
+                           q.stride(0), q.stride(1), k.stride(0), k.stride(1), q_norm.eps(), dt,
                            current_stream(q.device())),
             "sgl_qk_rmsnorm");
 }
@@ -910,13 +920,13 @@ void RotaryEmbedding::forward_inplace(const torch::Tensor& positions, torch::Ten
   TORCH_CHECK(query.is_cuda() && key.is_cuda() && positions.is_cuda(),
               "Inputs must be device tensors");
   TORCH_CHECK(positions.scalar_type() == torch::kInt32, "positions must be int32");
-  check_bf16(query, "query");
-  check_bf16(key, "key");
+  const int dt = half_dtype(query, "query");
+  check_same_dtype(query, key, "query and key");
   check_sgl(sgl_rope(query.data_ptr(), key.data_ptr(), cos_cache_.data_ptr<float>(),
                      sin_cache_.data_ptr<float>(), positions.data_ptr<int32_t>(),
                      positions.size(0), query.size(1), key.size(1), rotary_dim_, query.size(2),
                      cos_cache_.size(1), query.stride(0), query.stride(1), key.stride(0),
-                     key.stride(1), current_stream(query.device())),
+                     key.stride(1), dt, current_stream(query.device())),
             "sgl_rope");
 }
 

@@ -74,6 +74,48 @@ __device__ __forceinline__ u32x4_t pack8(const float* f) {
   return v;
 }
 
+// 16-bit element types carried as bit patterns: DT = SGL_DTYPE_BF16 or
+// SGL_DTYPE_F16 (fp32 arithmetic, one round-to-nearest-even per store).
+typedef _Float16 f16_t;
+
+template <int DT>
+__device__ __forceinline__ float to_f32(uint32_t bits16) {
+  if constexpr (DT == SGL_DTYPE_BF16) return __uint_as_float(bits16 << 16);
+  else return static_cast<float>(__builtin_bit_cast(f16_t, static_cast<uint16_t>(bits16)));
+}
+template <int DT>
+__device__ __forceinline__ uint32_t from_f32(float x) {
+  // Round to nearest even in both cases (v_cvt_f16_f32 / the bf16 cast).
+  if constexpr (DT == SGL_DTYPE_BF16) return f32_to_bf16_bits(x);
+  else return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<f16_t>(x)));
+}
+template <int DT>
+__device__ __forceinline__ float round_t(float x) {
+  return to_f32<DT>(from_f32<DT>(x));
+}
+// Two values packed into one word (a in the low half), exact when both are
+// DT-representable.
+template <int DT>
+__device__ __forceinline__ uint32_t pack2_t(float a, float b) {
+  if constexpr (DT == SGL_DTYPE_BF16) return pack_bf16x2(a, b);
+  else return from_f32<DT>(a) | (from_f32<DT>(b) << 16);
+}
+template <int DT>
+__device__ __forceinline__ void unpack8_t(const u32x4_t& v, float (&f)[8]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = to_f32<DT>(v[i] & 0xffffu);
+    f[2 * i + 1] = to_f32<DT>(v[i] >> 16);
+  }
+}
+template <int DT>
+__device__ __forceinline__ u32x4_t pack8_t(const float (&f)[8]) {
+  u32x4_t v;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = pack2_t<DT>(f[2 * i], f[2 * i + 1]);
+  return v;
+}
+
 __device__ __forceinline__ u32x4_t ldg128(const void* p) {
   return *reinterpret_cast<const u32x4_t*>(p);
 }

@@ -21,39 +21,6 @@
 namespace sgl {
 namespace {
 
-typedef _Float16 f16_t;
-
-// Element type helpers: DT 0 = bf16, 1 = fp16, carried as 16-bit patterns.
-template <int DT>
-__device__ __forceinline__ float to_f32(uint32_t bits16) {
-  if constexpr (DT == SGL_DTYPE_BF16) return __uint_as_float(bits16 << 16);
-  else return static_cast<float>(__builtin_bit_cast(f16_t, static_cast<uint16_t>(bits16)));
-}
-template <int DT>
-__device__ __forceinline__ uint32_t from_f32(float x) {
-  // Round to nearest even in both cases (v_cvt_f16_f32 / the bf16 cast).
-  if constexpr (DT == SGL_DTYPE_BF16) return f32_to_bf16_bits(x);
-  else return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<f16_t>(x)));
-}
-template <int DT>
-__device__ __forceinline__ void unpack8_t(const u32x4_t& v, float (&f)[8]) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    f[2 * i] = to_f32<DT>(v[i] & 0xffffu);
-    f[2 * i + 1] = to_f32<DT>(v[i] >> 16);
-  }
-}
-template <int DT>
-__device__ __forceinline__ u32x4_t pack8_t(const float (&f)[8]) {
-  u32x4_t v;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    if constexpr (DT == SGL_DTYPE_BF16) v[i] = pack_bf16x2(f[2 * i], f[2 * i + 1]);
-    else v[i] = from_f32<DT>(f[2 * i]) | (from_f32<DT>(f[2 * i + 1]) << 16);
-  }
-  return v;
-}
-
 // Eight consecutive elements starting at e0 of a row of d elements: one
 // 16-byte access when the row allows it (VEC), element by element with a
 // bound check otherwise (elements past d read as 0 and are not written).

@@ -26,7 +26,10 @@ namespace {
 
 // --- per-row building blocks (LPR = lanes per row = D / 8) ------------------
 
-template <int LPR>
+// DT: the 16-bit element type of the rows (SGL_DTYPE_BF16 / SGL_DTYPE_F16),
+// as the reference dispatches both (normalization.cu:346-372,
+// rotary_embedding.cu:124-168).
+template <int LPR, int DT>
 __device__ __forceinline__ void rmsnorm8(float (&x)[8], const uint16_t* __restrict__ w,
                                          int lane_in_row, float inv_d, float eps) {
   float ss = 0.f;
@@ -35,31 +38,31 @@ __device__ __forceinline__ void rmsnorm8(float (&x)[8], const uint16_t* __restri
   ss = group_sum<LPR>(ss);
   const float scale = rsqrtf(ss * inv_d + eps);
   float wf[8];
-  unpack8(ldg128(w + lane_in_row * 8), wf);
+  unpack8_t<DT>(ldg128(w + lane_in_row * 8), wf);
 #pragma unroll
-  for (int i = 0; i < 8; ++i) x[i] = round_bf16((x[i] * scale) * wf[i]);
+  for (int i = 0; i < 8; ++i) x[i] = round_t<DT>((x[i] * scale) * wf[i]);
 }
 
-// Rotate-half RoPE of the 8 values this lane holds; x must hold bf16 values.
-template <int LPR>
+// Rotate-half RoPE of the 8 values this lane holds; x must hold DT values.
+template <int LPR, int DT>
 __device__ __forceinline__ void rope8(float (&x)[8], const float* __restrict__ cos_row,
                                       const float* __restrict__ sin_row, int lane_in_row) {
   constexpr int HALF = LPR / 2;
   const bool first = lane_in_row < HALF;
   const int j = first ? lane_in_row : lane_in_row - HALF;
-  // Partner values: exchange packed bf16 words (exact, x is bf16-valued).
+  // Partner values: exchange packed 16-bit words (exact, x is DT-valued).
   float p[8];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const uint32_t w = pack_bf16x2(x[2 * i], x[2 * i + 1]);
+    const uint32_t w = pack2_t<DT>(x[2 * i], x[2 * i + 1]);
     uint32_t pw;
     if constexpr (HALF == 8) {
       pw = dpp_u32<0x128>(w);  // lane ^ 8 inside the 16-lane row
     } else {
       pw = static_cast<uint32_t>(__shfl_xor(static_cast<int>(w), HALF, kWave));
     }
-    p[2 * i] = bf16_lo(pw);
-    p[2 * i + 1] = bf16_hi(pw);
+    p[2 * i] = to_f32<DT>(pw & 0xffffu);
+    p[2 * i + 1] = to_f32<DT>(pw >> 16);
   }
   const f32x4_t c0 = *reinterpret_cast<const f32x4_t*>(cos_row + j * 8);
   const f32x4_t c1 = *reinterpret_cast<const f32x4_t*>(cos_row + j * 8 + 4);
@@ -98,7 +101,7 @@ __global__ void __launch_bounds__(256) cos_sin_cache_kernel(float* __restrict__ 
 
 // --- standalone qk RMSNorm --------------------------------------------------
 
-template <int LPR>
+template <int LPR, int DT>
 __global__ void __launch_bounds__(256) qk_rmsnorm_kernel(
     uint16_t* __restrict__ q, uint16_t* __restrict__ k, const uint16_t* __restrict__ qw,
     const uint16_t* __restrict__ kw, int64_t tokens, int64_t q_heads, int64_t k_heads,
@@ -123,12 +126,13 @@ __global__ void __launch_bounds__(256) qk_rmsnorm_kernel(
     w = kw;
   }
   float x[8];
-  unpack8(ldg128(row + lane_in_row * 8), x);
-  rmsnorm8<LPR>(x, w, lane_in_row, inv_d, eps);
-  stg128(row + lane_in_row * 8, pack8(x));
+  unpack8_t<DT>(ldg128(row + lane_in_row * 8), x);
+  rmsnorm8<LPR, DT>(x, w, lane_in_row, inv_d, eps);
+  stg128(row + lane_in_row * 8, pack8_t<DT>(x));
 }
 
 // Any d: one wave per row, scalar element loop.
+template <int DT>
 __global__ void __launch_bounds__(256) qk_rmsnorm_generic_kernel(
     uint16_t* __restrict__ q, uint16_t* __restrict__ k, const uint16_t* __restrict__ qw,
     const uint16_t* __restrict__ kw, int64_t tokens, int64_t q_heads, int64_t k_heads,
@@ -152,20 +156,20 @@ __global__ void __launch_bounds__(256) qk_rmsnorm_generic_kernel(
   }
   float ss = 0.f;
   for (int64_t i = lane; i < d; i += kWave) {
-    const float v = bf16_bits_to_f32(row[i]);
+    const float v = to_f32<DT>(row[i]);
     ss += v * v;
   }
   ss = group_sum<kWave>(ss);
   const float scale = rsqrtf(ss / static_cast<float>(d) + eps);
   for (int64_t i = lane; i < d; i += kWave) {
-    const float v = bf16_bits_to_f32(row[i]);
-    row[i] = static_cast<uint16_t>(f32_to_bf16_bits((v * scale) * bf16_bits_to_f32(w[i])));
+    const float v = to_f32<DT>(row[i]);
+    row[i] = static_cast<uint16_t>(from_f32<DT>((v * scale) * to_f32<DT>(w[i])));
   }
 }
 
 // --- standalone RoPE --------------------------------------------------------
 
-template <int LPR>
+template <int LPR, int DT>
 __global__ void __launch_bounds__(256) rope_kernel(
     uint16_t* __restrict__ q, uint16_t* __restrict__ k, const float* __restrict__ cos_cache,
     const float* __restrict__ sin_cache, const int32_t* __restrict__ positions, int64_t nnz,
@@ -189,14 +193,15 @@ __global__ void __launch_bounds__(256) rope_kernel(
   }
   const int64_t pos = positions[t];
   float x[8];
-  unpack8(ldg128(row + lane_in_row * 8), x);
-  rope8<LPR>(x, cos_cache + pos * (D / 2), sin_cache + pos * (D / 2), lane_in_row);
-  stg128(row + lane_in_row * 8, pack8(x));
+  unpack8_t<DT>(ldg128(row + lane_in_row * 8), x);
+  rope8<LPR, DT>(x, cos_cache + pos * (D / 2), sin_cache + pos * (D / 2), lane_in_row);
+  stg128(row + lane_in_row * 8, pack8_t<DT>(x));
 }
 
 // Any head_dim / rotary_dim / cache width: one workgroup per row, as the
 // reference fallback kernel (src/layers/rotary_embedding.cu:9-67). All reads
 // of the row finish before any write (barrier), so the update is in place.
+template <int DT>
 __global__ void __launch_bounds__(128) rope_generic_kernel(
     uint16_t* __restrict__ q, uint16_t* __restrict__ k, const float* __restrict__ cos_cache,
     const float* __restrict__ sin_cache, const int32_t* __restrict__ positions, int64_t nnz,
@@ -224,8 +229,8 @@ __global__ void __launch_bounds__(128) rope_generic_kernel(
     const int64_t pair = first ? i : i - half;
     const int64_t other = first ? i + half : i - half;
     const int64_t ci = cos_width == rotary_dim ? i : pair;
-    const float v = bf16_bits_to_f32(row[i]);
-    const float o = bf16_bits_to_f32(row[other]);
+    const float v = to_f32<DT>(row[i]);
+    const float o = to_f32<DT>(row[other]);
     const float c = cos_cache[pos * cos_width + ci];
     const float s = sin_cache[pos * cos_width + ci];
     out[n] = first ? (v * c - o * s) : (v * c + o * s);
@@ -233,7 +238,7 @@ __global__ void __launch_bounds__(128) rope_generic_kernel(
   __syncthreads();
   n = 0;
   for (int64_t i = threadIdx.x; i < rotary_dim && n < kMaxPerThread; i += blockDim.x, ++n) {
-    row[i] = static_cast<uint16_t>(f32_to_bf16_bits(out[n]));
+    row[i] = static_cast<uint16_t>(from_f32<DT>(out[n]));
   }
 }
 
@@ -375,8 +380,9 @@ extern "C" int sgl_rope_cos_sin_cache(float* cos_cache, float* sin_cache, int64_
 extern "C" int sgl_qk_rmsnorm(void* q, void* k, const void* q_weight, const void* k_weight,
                               int64_t tokens, int64_t q_heads, int64_t k_heads, int64_t d,
                               int64_t q_st, int64_t q_sh, int64_t k_st, int64_t k_sh, float eps,
-                              void* stream) {
+                              int dtype, void* stream) {
   if (tokens < 0 || q_heads < 0 || k_heads < 0 || d <= 0) return SGL_ERR_INVALID_ARG;
+  if (dtype != SGL_DTYPE_BF16 && dtype != SGL_DTYPE_F16) return SGL_ERR_UNSUPPORTED;
   if (k == nullptr) k_heads = 0;
   const int64_t total = tokens * (q_heads + k_heads);
   if (total == 0) return SGL_OK;
@@ -391,10 +397,15 @@ extern "C" int sgl_qk_rmsnorm(void* q, void* k, const void* q_weight, const void
                       aligned16(q) && (k == nullptr || aligned16(k)) &&
                       (qw == nullptr || aligned16(qw)) && (kw == nullptr || aligned16(kw));
   const float inv_d = 1.0f / static_cast<float>(d);
-#define SGL_NORM_CASE(LPR_)                                                                    \
-  hipLaunchKernelGGL(qk_rmsnorm_kernel<LPR_>, dim3(blocks_for(total, 256 / LPR_)), dim3(256), 0, \
-                     s, qp, kp, qw, kw, tokens, q_heads, k_heads, q_st, q_sh, k_st, k_sh,      \
-                     inv_d, eps);                                                              \
+#define SGL_NORM_CASE(LPR_)                                                                  \
+  if (dtype == SGL_DTYPE_BF16)                                                               \
+    hipLaunchKernelGGL((qk_rmsnorm_kernel<LPR_, SGL_DTYPE_BF16>),                            \
+                       dim3(blocks_for(total, 256 / LPR_)), dim3(256), 0, s, qp, kp, qw, kw, \
+                       tokens, q_heads, k_heads, q_st, q_sh, k_st, k_sh, inv_d, eps);        \
+  else                                                                                       \
+    hipLaunchKernelGGL((qk_rmsnorm_kernel<LPR_, SGL_DTYPE_F16>),                             \
+                       dim3(blocks_for(total, 256 / LPR_)), dim3(256), 0, s, qp, kp, qw, kw, \
+                       tokens, q_heads, k_heads, q_st, q_sh, k_st, k_sh, inv_d, eps);        \
   return launch_status();
   if (vec_ok) {
     switch (d) {
@@ -406,16 +417,23 @@ extern "C" int sgl_qk_rmsnorm(void* q, void* k, const void* q_weight, const void
     }
   }
 #undef SGL_NORM_CASE
-  hipLaunchKernelGGL(qk_rmsnorm_generic_kernel, dim3(blocks_for(total, 4)), dim3(256), 0, s, qp,
-                     kp, qw, kw, tokens, q_heads, k_heads, d, q_st, q_sh, k_st, k_sh, eps);
+  if (dtype == SGL_DTYPE_BF16)
+    hipLaunchKernelGGL(qk_rmsnorm_generic_kernel<SGL_DTYPE_BF16>, dim3(blocks_for(total, 4)),
+                       dim3(256), 0, s, qp, kp, qw, kw, tokens, q_heads, k_heads, d, q_st, q_sh,
+                       k_st, k_sh, eps);
+  else
+    hipLaunchKernelGGL(qk_rmsnorm_generic_kernel<SGL_DTYPE_F16>, dim3(blocks_for(total, 4)),
+                       dim3(256), 0, s, qp, kp, qw, kw, tokens, q_heads, k_heads, d, q_st, q_sh,
+                       k_st, k_sh, eps);
   return launch_status();
 }
 
 extern "C" int sgl_rope(void* q, void* k, const float* cos_cache, const float* sin_cache,
                         const int32_t* positions, int64_t nnz, int64_t q_heads, int64_t kv_heads,
                         int64_t rotary_dim, int64_t head_dim, int64_t cos_width, int64_t q_st,
-                        int64_t q_sh, int64_t k_st, int64_t k_sh, void* stream) {
+                        int64_t q_sh, int64_t k_st, int64_t k_sh, int dtype, void* stream) {
   if (nnz < 0 || q_heads < 0 || kv_heads < 0 || head_dim <= 0) return SGL_ERR_INVALID_ARG;
+  if (dtype != SGL_DTYPE_BF16 && dtype != SGL_DTYPE_F16) return SGL_ERR_UNSUPPORTED;
   if (rotary_dim <= 0 || (rotary_dim & 1) || rotary_dim > head_dim) return SGL_ERR_INVALID_ARG;
   if (cos_width != rotary_dim && cos_width != rotary_dim / 2) return SGL_ERR_INVALID_ARG;
   const int64_t total = nnz * (q_heads + kv_heads);
@@ -430,9 +448,14 @@ extern "C" int sgl_rope(void* q, void* k, const float* cos_cache, const float* s
                       (q == nullptr || aligned16(q)) && (k == nullptr || aligned16(k)) &&
                       aligned16(cos_cache) && aligned16(sin_cache);
 #define SGL_ROPE_CASE(LPR_)                                                                   \
-  hipLaunchKernelGGL(rope_kernel<LPR_>, dim3(blocks_for(total, 256 / LPR_)), dim3(256), 0, s,  \
-                     qp, kp, cos_cache, sin_cache, positions, nnz, q_heads, kv_heads, q_st,   \
-                     q_sh, k_st, k_sh);                                                       \
+  if (dtype == SGL_DTYPE_BF16)                                                                \
+    hipLaunchKernelGGL((rope_kernel<LPR_, SGL_DTYPE_BF16>), dim3(blocks_for(total, 256 / LPR_)), \
+                       dim3(256), 0, s, qp, kp, cos_cache, sin_cache, positions, nnz, q_heads, \
+                       kv_heads, q_st, q_sh, k_st, k_sh);                                     \
+  else                                                                                        \
+    hipLaunchKernelGGL((rope_kernel<LPR_, SGL_DTYPE_F16>), dim3(blocks_for(total, 256 / LPR_)), \
+                       dim3(256), 0, s, qp, kp, cos_cache, sin_cache, positions, nnz, q_heads, \
+                       kv_heads, q_st, q_sh, k_st, k_sh);                                     \
   return launch_status();
   if (vec_ok) {
     switch (head_dim) {
@@ -445,9 +468,14 @@ extern "C" int sgl_rope(void* q, void* k, const float* cos_cache, const float* s
   }
 #undef SGL_ROPE_CASE
   if (rotary_dim > 128 * 8) return SGL_ERR_UNSUPPORTED;
-  hipLaunchKernelGGL(rope_generic_kernel, dim3(total), dim3(128), 0, s, qp, kp, cos_cache,
-                     sin_cache, positions, nnz, q_heads, kv_heads, rotary_dim, head_dim,
-                     cos_width, q_st, q_sh, k_st, k_sh);
+  if (dtype == SGL_DTYPE_BF16)
+    hipLaunchKernelGGL(rope_generic_kernel<SGL_DTYPE_BF16>, dim3(total), dim3(128), 0, s, qp, kp,
+                       cos_cache, sin_cache, positions, nnz, q_heads, kv_heads, rotary_dim,
+                       head_dim, cos_width, q_st, q_sh, k_st, k_sh);
+  else
+    hipLaunchKernelGGL(rope_generic_kernel<SGL_DTYPE_F16>, dim3(total), dim3(128), 0, s, qp, kp,
+                       cos_cache, sin_cache, positions, nnz, q_heads, kv_heads, rotary_dim,
+                       head_dim, cos_width, q_st, q_sh, k_st, k_sh);
   return launch_status();
 }
 

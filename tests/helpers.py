@@ -21,7 +21,8 @@ def bf16_f32(a: np.ndarray) -> np.ndarray:
 
 
 def bf16_ulp_dist(a: np.ndarray, b: np.ndarray) -> np.ndarray:
-    """Distance in bf16 ulps between two uint16 bf16 arrays (sign-magnitude aware)."""
+    """Distance in ulps between two uint16 arrays of bf16 (or fp16: the same
+    sign-magnitude ordering) bit patterns."""
     def key(x):
         x = x.astype(np.int32)
         return np.where(x & 0x8000, -(x & 0x7FFF), x & 0x7FFF)
@@ -40,20 +41,22 @@ def assert_attn_close(got: np.ndarray, ref: np.ndarray, atol=ATOL, rtol=RTOL, wh
 
 
 def assert_bf16_close(got: np.ndarray, ref: np.ndarray, atol=1e-6, what: str = "",
-                      max_ulp: int = 1):
+                      max_ulp: int = 1, dtype: str = "bf16"):
     """bf16 results of fp32 math with the same rounding points: within one bf16
     ulp of the oracle, or within atol absolute where the fp32 result sits near
     zero after cancellation (x c - y s), where one fp32 ulp of difference in the
     inputs (fused multiply-add vs separate rounding) spans many bf16 ulps.
-    atol may be an array (a per-element bound) broadcastable to ref."""
+    atol may be an array (a per-element bound) broadcastable to ref. dtype
+    "fp16": the same for fp16 bit patterns (ulps of fp16)."""
+    val = bf16_f32 if dtype == "bf16" else (lambda x: x.view(np.float16).astype(np.float32))
     dist = bf16_ulp_dist(got, ref)
-    diff = np.abs(bf16_f32(got).astype(np.float64) - bf16_f32(ref).astype(np.float64))
+    diff = np.abs(val(got).astype(np.float64) - val(ref).astype(np.float64))
     bad = (dist > max_ulp) & (diff > atol)
     if bad.any():
         i = np.unravel_index(np.argmax(np.where(bad, diff, 0)), diff.shape)
         raise AssertionError(f"{what}: {int(bad.sum())} of {bad.size} elements differ by more "
-                             f"than {max_ulp} bf16 ulp and {atol}; worst at {i}: got "
-                             f"{bf16_f32(got)[i]}, ref {bf16_f32(ref)[i]}")
+                             f"than {max_ulp} {dtype} ulp and {atol}; worst at {i}: got "
+                             f"{val(got)[i]}, ref {val(ref)[i]}")
 
 
 def decode_ws_bytes(units: int, hq: int) -> int:

@@ -52,9 +52,13 @@ def test_argument_checks_reject_before_launch():
     assert lib.sgl_build_decode_indices(None, 4, 8, 8, None, None, None, 0, None) == 0
     assert lib.sgl_gather_int32_2d(None, 4, 2, 8, None, None, None, 3, None) == -1  # stride < cols
     assert lib.sgl_qk_rmsnorm(None, None, None, None, 3, 2, 1, 128, 0, 0, 0, 0,
-                              ctypes.c_float(1e-6), None) == -1
+                              ctypes.c_float(1e-6), 0, None) == -1
+    assert lib.sgl_qk_rmsnorm(None, None, None, None, 3, 2, 1, 128, 0, 0, 0, 0,
+                              ctypes.c_float(1e-6), 2, None) == -2  # dtype not built
     assert lib.sgl_rope(None, None, None, None, None, 3, 2, 1, 7, 128, 7, 0, 0, 0, 0,
-                        None) == -1  # odd rotary_dim
+                        0, None) == -1  # odd rotary_dim
+    assert lib.sgl_rope(None, None, None, None, None, 3, 2, 1, 8, 128, 4, 0, 0, 0, 0,
+                        2, None) == -2  # dtype not built
     # fused: head_dim not built
     assert lib.sgl_fused_qknorm_rope_store(16, 96 * 5, 16, 16, None, None, 16, 16, 16, 16, 4, 1,
                                            2, 96, ctypes.c_float(1e-6), 0, None) == -2

@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 import torch
 
-from conftest import pkg, wl
+from conftest import capi, pkg, wl
 from helpers import assert_attn_close, u16
 
 D = 128
@@ -192,6 +192,37 @@ def test_attention_layer_matches_unfused_modules(dev, sb):
     torch.cuda.synchronize()
     assert torch.equal(o1.view(torch.int16), o2.view(torch.int16))
     assert torch.equal(s1.cache.buffer().view(torch.int16), s2.cache.buffer().view(torch.int16))
+
+
+@pytest.mark.gpu
+def test_norm_and_rope_modules_fp16(dev, sb):
+    """The reference's RMSNorm / fused qk-norm / RotaryEmbedding dispatch fp16
+    as well as bf16 (normalization.cu:346-372, rotary_embedding.cu:124-168):
+    the modules on fp16 tensors equal the C ABI calls (pinned to the oracle in
+    test_gpu_parity), bit for bit, and mixed dtypes are refused."""
+    note("fp16 norm / rope modules")
+    g = _gen(dev, 55)
+    T, hq, hkv = 9, 16, 8
+    q = (torch.randn((T, hq, D), device=dev, generator=g)).to(torch.float16)
+    k = (torch.randn((T, hkv, D), device=dev, generator=g)).to(torch.float16)
+    qn, kn = sb.RMSNorm(D, 1e-6, 0), sb.RMSNorm(D, 1e-6, 0)
+    qn.weight = (torch.rand(D, device=dev, generator=g) + 0.5).to(torch.float16)
+    kn.weight = (torch.rand(D, device=dev, generator=g) + 0.5).to(torch.float16)
+    rot = sb.RotaryEmbedding(D, D, 4096, 1e6, 0)
+    pos = torch.randint(0, 4096, (T,), device=dev, generator=g, dtype=torch.int32)
+    q1, k1, q2, k2 = q.clone(), k.clone(), q.clone(), k.clone()
+    sb.fused_qk_rmsnorm_inplace_3d_strided(q1, k1, qn, kn)
+    rot.forward_inplace(pos, q1, k1)
+    capi.qk_rmsnorm(q2, k2, qn.weight, kn.weight, 1e-6)
+    capi.rope(pos, q2, k2, rot.cos_cache(), rot.sin_cache())
+    torch.cuda.synchronize()
+    assert torch.equal(q1.view(torch.int16), q2.view(torch.int16))
+    assert torch.equal(k1.view(torch.int16), k2.view(torch.int16))
+    assert not torch.equal(q1.view(torch.int16), q.view(torch.int16))
+    with pytest.raises(RuntimeError, match="share one dtype"):
+        sb.fused_qk_rmsnorm_inplace_3d_strided(q1, k1.to(torch.bfloat16), qn, kn)
+    with pytest.raises(RuntimeError, match="share one dtype"):
+        rot.forward_inplace(pos, q1, k1.to(torch.bfloat16))
 
 
 @pytest.mark.gpu

@@ -175,31 +175,40 @@ def test_cos_sin_cache(oracle, dev):
     assert np.abs(sin.cpu().numpy() - rs).max() <= 2e-6
 
 
+TORCH_DT = {"bf16": torch.bfloat16, "fp16": torch.float16}
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
 @pytest.mark.parametrize("d", [64, 128, 256, 96])
-def test_qk_rmsnorm(oracle, dev, d):
-    note(f"qk_rmsnorm d={d}")
+def test_qk_rmsnorm(oracle, dev, d, dtype):
+    note(f"qk_rmsnorm d={d} {dtype}")
     g = gen(dev, 5)
     T, hq, hkv = 37, 16, 8
-    qkv = randn_bf16((T, (hq + 2 * hkv) * d), dev, g, 2.0)
+    dt = TORCH_DT[dtype]
+    qkv = (torch.randn((T, (hq + 2 * hkv) * d), device=dev, generator=g) * 2.0).to(dt)
     q = qkv[:, :hq * d].view(T, hq, d)
     k = qkv[:, hq * d:(hq + hkv) * d].view(T, hkv, d)
-    qw = (torch.rand(d, device=dev, generator=g) + 0.5).to(torch.bfloat16)
-    kw = randn_bf16((d,), dev, g)
+    qw = (torch.rand(d, device=dev, generator=g) + 0.5).to(dt)
+    kw = torch.randn(d, device=dev, generator=g).to(dt)
     qh, kh = u16(q).copy(), u16(k).copy()
-    oracle.qk_rmsnorm(qh, kh, u16(qw), u16(kw), 1e-6)
+    oracle.qk_rmsnorm(qh, kh, u16(qw), u16(kw), 1e-6, dtype=dtype)
     capi.qk_rmsnorm(q, k, qw, kw, 1e-6)
     torch.cuda.synchronize()
     assert bf16_ulp_dist(u16(q), qh).max() <= 1
     assert bf16_ulp_dist(u16(k), kh).max() <= 1
 
 
-def test_qk_rmsnorm_fused_equals_separate(dev):
-    # tests/layers/test_normalization.cpp:21-53, here bitwise.
-    note("qk_rmsnorm fused vs separate")
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+def test_qk_rmsnorm_fused_equals_separate(dev, dtype):
+    # tests/layers/test_normalization.cpp:21-53 (fp16, T 7, 16q/8kv, d 128,
+    # eps 1e-6, randn weights, allclose 1e-3), here bitwise and in both dtypes.
+    note(f"qk_rmsnorm fused vs separate {dtype}")
     g = gen(dev, 6)
-    q = randn_bf16((7, 16, 128), dev, g)
-    k = randn_bf16((7, 8, 128), dev, g)
-    qw, kw = randn_bf16((128,), dev, g), randn_bf16((128,), dev, g)
+    dt = TORCH_DT[dtype]
+    q = torch.randn((7, 16, 128), device=dev, generator=g).to(dt)
+    k = torch.randn((7, 8, 128), device=dev, generator=g).to(dt)
+    qw = torch.randn(128, device=dev, generator=g).to(dt)
+    kw = torch.randn(128, device=dev, generator=g).to(dt)
     qa, ka, qb, kb = q.clone(), k.clone(), q.clone(), k.clone()
     capi.qk_rmsnorm(qa, ka, qw, kw, 1e-6)
     capi.qk_rmsnorm(qb, None, qw, None, 1e-6)
@@ -209,13 +218,14 @@ def test_qk_rmsnorm_fused_equals_separate(dev):
     assert torch.equal(ka.view(torch.int16), kb.view(torch.int16))
 
 
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
 @pytest.mark.parametrize("d,rd,full", [(128, 128, False), (64, 64, False), (128, 64, False),
                                        (80, 80, True), (128, 128, True)])
-def test_rope(oracle, dev, d, rd, full):
-    note(f"rope d={d} rotary={rd} full_width_cache={full}")
+def test_rope(oracle, dev, d, rd, full, dtype):
+    note(f"rope d={d} rotary={rd} full_width_cache={full} {dtype}")
     g = gen(dev, 7)
     T, hq, hkv = 45, 8, 2
-    qkv = randn_bf16((T, (hq + 2 * hkv) * d), dev, g)
+    qkv = torch.randn((T, (hq + 2 * hkv) * d), device=dev, generator=g).to(TORCH_DT[dtype])
     q = qkv[:, :hq * d].view(T, hq, d)
     k = qkv[:, hq * d:(hq + hkv) * d].view(T, hkv, d)
     pos = torch.randint(0, 4096, (T,), device=dev, generator=g, dtype=torch.int32)
@@ -223,11 +233,11 @@ def test_rope(oracle, dev, d, rd, full):
     if full:
         cos, sin = torch.cat([cos, cos], 1).contiguous(), torch.cat([sin, sin], 1).contiguous()
     qh, kh = u16(q).copy(), u16(k).copy()
-    oracle.rope(qh, kh, cos.cpu().numpy(), sin.cpu().numpy(), pos.cpu().numpy(), rd)
+    oracle.rope(qh, kh, cos.cpu().numpy(), sin.cpu().numpy(), pos.cpu().numpy(), rd, dtype=dtype)
     capi.rope(pos, q, k, cos, sin, rd)
     torch.cuda.synchronize()
-    assert_bf16_close(u16(q), qh, what="rope q")
-    assert_bf16_close(u16(k), kh, what="rope k")
+    assert_bf16_close(u16(q), qh, what="rope q", dtype=dtype)
+    assert_bf16_close(u16(k), kh, what="rope k", dtype=dtype)
 
 
 def _fused_inputs(dev, T, hq, hkv, d, seed, slots=None):

@@ -211,7 +211,86 @@ def test_rmsnorm_constant_row(oracle):
     assert bf16_ulp_dist(q[0, 0], w).max() <= 1
 
 
+def test_f16_encoding_matches_numpy(oracle):
+    """The oracle's binary16 encode/decode against numpy's float16 casts:
+    normals, subnormals, ties, overflow to infinity, signed zeros."""
+    rng = np.random.default_rng(40)
+    x = np.concatenate([
+        rng.standard_normal(20000).astype(np.float32) * 10.0 ** rng.integers(-8, 5, 20000),
+        np.array([0.0, -0.0, 65504.0, 65519.0, 65520.0, 1e6, -1e6, 6.1e-5, 5.96e-8, 2.98e-8,
+                  1.0 + 2.0 ** -11, 1.0 + 3 * 2.0 ** -11, np.inf, -np.inf], np.float32)])
+    with np.errstate(over="ignore"):
+        want = x.astype(np.float16).view(np.uint16)
+    np.testing.assert_array_equal(oracle.f32_to_f16_bits(x), want)
+    back = oracle.f16_bits_to_f32(want)
+    np.testing.assert_array_equal(back, want.view(np.float16).astype(np.float32))
+
+
+def rand_f16(rng, shape, scale=1.0):
+    return (rng.standard_normal(shape).astype(np.float32) * scale).astype(np.float16).view(np.uint16)
+
+
+def f16_f32(b):
+    return b.view(np.float16).astype(np.float32)
+
+
+def test_rmsnorm_fp16_matches_torch_rms_norm(oracle):
+    """fp16 rows (the reference's fp16 dispatch, normalization.cu:346-365)
+    against torch's rms_norm in fp32 rounded once to fp16."""
+    rng = np.random.default_rng(41)
+    T, qh, kh, d, eps = 7, 16, 8, 128, 1e-6
+    q = rand_f16(rng, (T, qh, d), 3.0)
+    k = rand_f16(rng, (T, kh, d), 0.5)
+    qw = rng.uniform(0.5, 1.5, d).astype(np.float16).view(np.uint16)
+    kw = rng.standard_normal(d).astype(np.float16).view(np.uint16)
+    q2, k2 = q.copy(), k.copy()
+    oracle.qk_rmsnorm(q2, k2, qw, kw, eps, dtype="fp16")
+    for x, y, w in ((q, q2, qw), (k, k2, kw)):
+        xt = torch.from_numpy(f16_f32(x))
+        ref = torch.nn.functional.rms_norm(xt, (d,), eps=eps) * torch.from_numpy(f16_f32(w))
+        assert bf16_ulp_dist(y, to_u16(ref.to(torch.float16))).max() <= 1
+
+
+def test_rmsnorm_fp16_fused_equals_separate(oracle):
+    # tests/layers/test_normalization.cpp:21-53 at its own dtype (fp16) and
+    # shape: q+k in one call == one call each, bit for bit.
+    rng = np.random.default_rng(42)
+    q = rand_f16(rng, (7, 16, 128))
+    k = rand_f16(rng, (7, 8, 128))
+    qw, kw = rand_f16(rng, (128,)), rand_f16(rng, (128,))
+    qa, ka, qb, kb = q.copy(), k.copy(), q.copy(), k.copy()
+    oracle.qk_rmsnorm(qa, ka, qw, kw, 1e-6, dtype="fp16")
+    oracle.qk_rmsnorm(qb, None, qw, None, 1e-6, dtype="fp16")
+    oracle.qk_rmsnorm(kb, None, kw, None, 1e-6, dtype="fp16")
+    np.testing.assert_array_equal(qa, qb)
+    np.testing.assert_array_equal(ka, kb)
+
+
 # ------------------------------------------------------------------ RoPE
+
+def test_rope_fp16_matches_transformers_neox(oracle):
+    """fp16 rows (rotary_embedding.cu:124-146 dispatches fp16 too) against HF
+    transformers' apply_rotary_pos_emb in fp32, rounded once to fp16."""
+    from transformers.models.qwen3.modeling_qwen3 import apply_rotary_pos_emb
+    rng = np.random.default_rng(43)
+    T, qh, kh, d = 33, 4, 2, 128
+    q = rand_f16(rng, (T, qh, d))
+    k = rand_f16(rng, (T, kh, d))
+    pos = rng.integers(0, 40960, T).astype(np.int32)
+    cos, sin = oracle.cos_sin_cache(40960, d, 1e6)
+    q2, k2 = q.copy(), k.copy()
+    oracle.rope(q2, k2, cos, sin, pos, dtype="fp16")
+    cf = torch.from_numpy(np.concatenate([cos[pos], cos[pos]], -1))
+    sf = torch.from_numpy(np.concatenate([sin[pos], sin[pos]], -1))
+    qt, kt = torch.from_numpy(f16_f32(q)), torch.from_numpy(f16_f32(k))
+    qr, kr = apply_rotary_pos_emb(qt, kt, cf, sf, unsqueeze_dim=1)
+    assert bf16_ulp_dist(q2, to_u16(qr.to(torch.float16))).max() <= 1
+    assert bf16_ulp_dist(k2, to_u16(kr.to(torch.float16))).max() <= 1
+    # position 0 is the identity
+    z = q[:1].copy()
+    oracle.rope(z, z.copy(), cos, sin, np.zeros(1, np.int32), dtype="fp16")
+    np.testing.assert_array_equal(z, q[:1])
+
 
 def test_rope_matches_transformers_neox(oracle):
     """HF transformers' Qwen3 apply_rotary_pos_emb (rotate_half, full-width
