@@ -3,7 +3,9 @@
 // Reference semantics:
 //   RMSNorm per (token, head) row: fused_qk_rmsnorm_3d_strided_vec_kernel
 //     (src/layers/normalization.cu:99-170): s = sum(x^2) in fp32,
-//     scale = rsqrt(s / d + eps), x <- bf16((x * scale) * w).
+//     scale = rsqrt(s / d + eps), x <- T((x * scale) * w), T = bf16 or fp16
+//     for the standalone norm and RoPE (the reference dispatches both); the
+//     fused pass below writes the bf16 pool and is bf16.
 //   RoPE: rotate-half with a half-width fp32 cos/sin cache
 //     (src/layers/rotary_embedding.cu:50-66): for i < h = rotary_dim / 2,
 //     x'[i] = x[i] c_i - x[i+h] s_i, x'[i+h] = x[i+h] c_i + x[i] s_i.
