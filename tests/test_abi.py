@@ -116,6 +116,39 @@ def test_decode_plan_host_logic():
         capi.decode_plan([3, 10], 16, 8, 128)  # kv_indptr[0] != 0
 
 
+def test_decode_plan_covers_any_batch_property():
+    """Property over random batches (0-600 requests, lengths 0-40,000, GQA
+    layouts): the plan's units of W tokens cover the batch, the unit size the
+    device derives from kv_indptr (clamp(round16(ceil(total / units)),
+    W_min, W)) also covers it, W is a 16-token multiple in [64, 8192], the
+    plan accepts its own batch, and the workspace is two partial slots per
+    unit. A uniform-by-construction check of the coupling between the host
+    plan and the device's unit sizing."""
+    import numpy as np
+    from hypothesis import given, settings, strategies as st
+
+    @settings(max_examples=300, deadline=None)
+    @given(st.integers(0, 600), st.integers(0, 40000), st.sampled_from([(16, 8), (32, 8), (32, 4),
+                                                                       (64, 4), (8, 8), (40, 8)]),
+           st.integers(0, 2 ** 31 - 1))
+    def check(n, max_len, heads, seed):
+        hq, hkv = heads
+        rng = np.random.default_rng(seed)
+        lens = rng.integers(0, max_len + 1, n)
+        ip = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+        plan = capi.decode_plan(ip, hq, hkv, 128)
+        total = int(ip[-1])
+        W = plan.kv_chunk_size
+        assert W % 16 == 0 and 64 <= W <= 8192 and plan.min_chunk_size == 64
+        assert plan.max_total_tokens == plan.num_units * W >= total
+        w_dev = min(W, max(64, -(-(-(-total // plan.num_units)) // 16) * 16))
+        assert plan.num_units * w_dev >= total
+        assert capi.decode_plan_check(plan, ip) == 0
+        assert plan.workspace_bytes == ws_bytes(plan.num_units, hq)
+
+    check()
+
+
 def test_decode_plan_check_host():
     """A plan serves any batch with at most batch_size requests and
     max_total_tokens tokens, whatever the per-request lengths; beyond it the
