@@ -212,6 +212,9 @@ def setup_mixed(torch, wl, w, dev, layers, seed=0):
         pool[0, l].normal_(generator=g)
         pool[1, l].normal_(generator=g)
     backend = sb.HipAttnBackend(cache, hq, hkv, D)
+    # A/B switches: the one-launch mixed step (default) and, without it, the
+    # side-stream overlap of separate launches (default).
+    backend.set_fused_mixed(os.environ.get("SGL_FUSED_MIXED", "1") != "0")
     backend.set_overlap_mixed(os.environ.get("SGL_OVERLAP_MIXED", "1") != "0")
     page_table = torch.from_numpy(b.page_table).to(dev)
     backend.set_page_table(page_table)

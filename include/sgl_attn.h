@@ -39,7 +39,7 @@ const char* sgl_status_string(int status);
 
 /* Library version, to check that the loaded .so matches this header. */
 int sgl_abi_version(void);
-#define SGL_ABI_VERSION 10
+#define SGL_ABI_VERSION 11
 
 /* ------------------------------------------------------------------ */
 /* KV-cache store                                                      */
@@ -327,6 +327,44 @@ int sgl_paged_prefill(const void* q, int64_t q_stride_token,
                       int num_kv_heads, int head_dim, float sm_scale, void* o,
                       int64_t o_stride_token, int64_t o_stride_head,
                       void* stream);
+
+/*
+ * A mixed batch (decode rows beside prefill rows, the chunked-prefill step
+ * of FlashInferBackend::forward's prefill phase with one-token requests) in
+ * one launch plus the split merge: the first workgroups run the decode rows
+ * on decode_cus CUs while the causal-prefill items run on the others, then
+ * on every CU as the decode finishes (the HBM-bound decode and the
+ * MFMA-bound prefill side by side). num_kv_heads must divide 8.
+ *   sgl_mixed_decode_cus: the CU share for the decode rows (a multiple of
+ *     8), from their K/V token count and the prefill's flops
+ *     (4 D Hq sum_r sum_i (kv_r - qo_r + i + 1)).
+ *   sgl_decode_plan_cus: a decode plan (as sgl_decode_plan) whose units fill
+ *     decode_cus CUs; like any plan it serves smaller batches on replay.
+ *   sgl_paged_mixed: decode rows as sgl_paged_decode (dec_q_rows: query row
+ *     of each decode request, or NULL for rows 0..dec_batch-1) and prefill
+ *     rows as sgl_paged_prefill, sharing q, the caches and o. With no rows
+ *     of one kind it runs the other entry point alone.
+ * Replaces: the decode and prefill calls of one mixed step
+ *           (src/attention/flashinfer_backend.cu:553-679); the reference
+ *           runs them as separate kernels.
+ */
+int sgl_mixed_decode_cus(int64_t decode_kv_tokens, int num_kv_heads, int head_dim,
+                         double prefill_flops);
+int sgl_decode_plan_cus(const int32_t* kv_indptr_host, int batch_size,
+                        int num_qo_heads, int num_kv_heads, int head_dim,
+                        int decode_cus, sgl_decode_plan_t* plan);
+int sgl_paged_mixed(const sgl_decode_plan_t* plan, const void* q,
+                    int64_t q_stride_token, int64_t q_stride_head,
+                    const void* k_cache, const void* v_cache,
+                    int64_t kv_stride_slot, int64_t kv_stride_head,
+                    const int32_t* dec_indices, const int32_t* dec_kv_indptr,
+                    const int32_t* dec_q_rows, int dec_batch,
+                    const int32_t* pre_indices, const int32_t* pre_qo_indptr,
+                    const int32_t* pre_kv_indptr, const int32_t* pre_q_start,
+                    int pre_batch, int pre_max_qo_len, int num_qo_heads,
+                    int num_kv_heads, int head_dim, float sm_scale, void* o,
+                    int64_t o_stride_token, int64_t o_stride_head,
+                    void* workspace, int64_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------ */
 /* Residual path: RMSNorm, fused add + RMSNorm, gated activations      */

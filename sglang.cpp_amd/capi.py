@@ -25,7 +25,7 @@ SGL_INDEX_I32 = 0
 SGL_INDEX_I64 = 1
 SGL_DTYPE_BF16 = 0
 SGL_DTYPE_F16 = 1
-ABI_VERSION = 10
+ABI_VERSION = 11
 FUSED_NO_K_WRITEBACK = 1  # SGL_FUSED_NO_K_WRITEBACK
 
 
@@ -95,6 +95,11 @@ _SIGNATURES = {
                                              _i32, _i32, _vp], _i32),
     "sgl_paged_prefill": ([_vp, _i64, _i64, _vp, _vp, _i64, _i64, _vp, _vp, _vp, _vp, _i32,
                            _i32, _i32, _i32, _i32, _f32, _vp, _i64, _i64, _vp], _i32),
+    "sgl_mixed_decode_cus": ([_i64, _i32, _i32, ctypes.c_double], _i32),
+    "sgl_decode_plan_cus": ([_vp, _i32, _i32, _i32, _i32, _i32, ctypes.POINTER(DecodePlan)], _i32),
+    "sgl_paged_mixed": ([ctypes.POINTER(DecodePlan), _vp, _i64, _i64, _vp, _vp, _i64, _i64,
+                         _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32,
+                         _f32, _vp, _i64, _i64, _vp, _i64, _vp], _i32),
 }
 
 
@@ -407,6 +412,51 @@ def decode_plan(kv_indptr_host: Sequence[int], num_qo_heads: int, num_kv_heads: 
                                  num_qo_heads, num_kv_heads, head_dim, ctypes.byref(plan)),
            "sgl_decode_plan")
     return plan
+
+
+def mixed_decode_cus(decode_kv_tokens: int, num_kv_heads: int, head_dim: int,
+                     prefill_flops: float) -> int:
+    """CU share for the decode rows of a mixed step (sgl_mixed_decode_cus)."""
+    return lib().sgl_mixed_decode_cus(int(decode_kv_tokens), num_kv_heads, head_dim,
+                                      float(prefill_flops))
+
+
+def decode_plan_cus(kv_indptr_host: Sequence[int], num_qo_heads: int, num_kv_heads: int,
+                    head_dim: int, decode_cus: int) -> DecodePlan:
+    """A decode plan whose units fill decode_cus CUs (sgl_decode_plan_cus)."""
+    arr = (ctypes.c_int32 * len(kv_indptr_host))(*[int(x) for x in kv_indptr_host])
+    plan = DecodePlan()
+    _check(lib().sgl_decode_plan_cus(ctypes.cast(arr, ctypes.c_void_p), len(kv_indptr_host) - 1,
+                                     num_qo_heads, num_kv_heads, head_dim, decode_cus,
+                                     ctypes.byref(plan)), "sgl_decode_plan_cus")
+    return plan
+
+
+def paged_mixed(plan: DecodePlan, q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                dec_indices: torch.Tensor, dec_kv_indptr: torch.Tensor,
+                dec_q_rows: Optional[torch.Tensor], pre_indices: torch.Tensor,
+                pre_qo_indptr: torch.Tensor, pre_kv_indptr: torch.Tensor,
+                pre_q_start: Optional[torch.Tensor], pre_max_qo_len: int, o: torch.Tensor,
+                workspace: torch.Tensor, sm_scale: Optional[float] = None) -> None:
+    """Decode rows and prefill rows of one mixed batch in one launch (sgl_paged_mixed)."""
+    dev = _need_gpu(q, k_cache, v_cache, dec_indices, dec_kv_indptr, dec_q_rows, pre_indices,
+                    pre_qo_indptr, pre_kv_indptr, pre_q_start, o, workspace)
+    if q.dtype != torch.bfloat16 or k_cache.dtype != torch.bfloat16 or o.dtype != torch.bfloat16:
+        raise ValueError("attention supports bf16 q / KV / o only")
+    hq, D = q.shape[1], q.shape[2]
+    hkv = k_cache.shape[1]
+    ss, sh = _kv_strides(k_cache)
+    if v_cache.stride() != k_cache.stride():
+        raise ValueError("K and V caches must share strides")
+    scale = 1.0 / math.sqrt(D) if sm_scale is None else sm_scale
+    ws_bytes = workspace.numel() * workspace.element_size()
+    _check(lib().sgl_paged_mixed(ctypes.byref(plan), _p(q), q.stride(0), q.stride(1),
+                                 _p(k_cache), _p(v_cache), ss, sh, _p(dec_indices),
+                                 _p(dec_kv_indptr), _p(dec_q_rows), dec_kv_indptr.shape[0] - 1,
+                                 _p(pre_indices), _p(pre_qo_indptr), _p(pre_kv_indptr),
+                                 _p(pre_q_start), pre_qo_indptr.shape[0] - 1, pre_max_qo_len,
+                                 hq, hkv, D, scale, _p(o), o.stride(0), o.stride(1),
+                                 _p(workspace), ws_bytes, _stream(dev)), "sgl_paged_mixed")
 
 
 def decode_plan_check(plan: DecodePlan, kv_indptr_host: Sequence[int]) -> int:

@@ -80,6 +80,8 @@ PYBIND11_MODULE(sgl_backend, m) {
            [](const Batch& b, int bs) { return hip_meta(b)->get_last_indices(bs); })
       .def("num_decode_rows", [](const Batch& b) { return hip_meta(b)->num_decode; })
       .def("num_prefill_rows", [](const Batch& b) { return hip_meta(b)->num_prefill; })
+      .def("fused_mixed_cus",  // CUs of the decode rows in a one-launch mixed step, else 0
+           [](const Batch& b) { return hip_meta(b)->fused ? hip_meta(b)->dec_cus : 0; })
       .def("decode_plan", [](const Batch& b) { return plan_dict(hip_meta(b)->dec_plan); })
       .def("uses_capture_buffers",
            [](const Batch& b) { return hip_meta(b)->use_capture_buffers; })
@@ -106,6 +108,8 @@ PYBIND11_MODULE(sgl_backend, m) {
       .def(py::init<std::shared_ptr<BaseKVCachePool>, int, int, int>(), py::arg("kv_cache"),
            py::arg("num_qo_heads"), py::arg("num_kv_heads"), py::arg("head_dim"))
       .def("set_page_table", &HipAttnBackend::set_page_table)
+      .def("set_fused_mixed", &HipAttnBackend::set_fused_mixed)
+      .def("fused_mixed", &HipAttnBackend::fused_mixed)
       .def("set_overlap_mixed", &HipAttnBackend::set_overlap_mixed)
       .def("overlap_mixed", &HipAttnBackend::overlap_mixed)
       .def("prepare_metadata", &HipAttnBackend::prepare_metadata)

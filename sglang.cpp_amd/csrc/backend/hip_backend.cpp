@@ -136,6 +136,12 @@ HipAttnBackend::HipAttnBackend(std::shared_ptr<BaseKVCachePool> kv_cache, int nu
               "num_qo_heads must be a positive multiple of num_kv_heads");
   TORCH_CHECK(head_dim == 128, "HipAttnBackend is built for head_dim 128");
   TORCH_CHECK(kv_cache_->dtype() == torch::kBFloat16, "HipAttnBackend needs a bf16 KV pool");
+  int cus = 0;
+  if (kv_cache_->device().is_cuda() &&
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount,
+                            kv_cache_->device().index()) == hipSuccess &&
+      cus > 0)
+    device_cus_ = cus;
 }
 
 void HipAttnBackend::set_page_table(const torch::Tensor& page_table) {
@@ -176,7 +182,8 @@ std::shared_ptr<HipAttnMetadata> HipAttnBackend::metadata_of(Batch& batch) const
 // Decode rows for the requests `reqs` of the batch (indices into padded_reqs),
 // their queries at rows q_rows.
 void HipAttnBackend::build_decode_rows(HipAttnMetadata& meta, const std::vector<int>& reqs,
-                                       const std::vector<int32_t>& q_rows, const Batch& batch) {
+                                       const std::vector<int32_t>& q_rows, const Batch& batch,
+                                       int decode_cus) {
   const int n = static_cast<int>(reqs.size());
   std::vector<int32_t> kv_indptr(n + 1, 0), table_idx(n);
   for (int i = 0; i < n; ++i) {
@@ -196,9 +203,14 @@ void HipAttnBackend::build_decode_rows(HipAttnMetadata& meta, const std::vector<
                                      meta.dec_indices.data_ptr<int32_t>(), n,
                                      current_stream(kv_cache_->device())),
             "sgl_build_decode_indices");
-  check_sgl(sgl_decode_plan(kv_indptr.data(), n, num_qo_heads_, num_kv_heads_, head_dim_,
-                            &meta.dec_plan),
-            "sgl_decode_plan");
+  if (decode_cus > 0)
+    check_sgl(sgl_decode_plan_cus(kv_indptr.data(), n, num_qo_heads_, num_kv_heads_, head_dim_,
+                                  decode_cus, &meta.dec_plan),
+              "sgl_decode_plan_cus");
+  else
+    check_sgl(sgl_decode_plan(kv_indptr.data(), n, num_qo_heads_, num_kv_heads_, head_dim_,
+                              &meta.dec_plan),
+              "sgl_decode_plan");
   workspace(meta.dec_plan.workspace_bytes);
 }
 
@@ -253,9 +265,27 @@ void HipAttnBackend::prepare_metadata(Batch& batch) {
     (q_len == 1 ? dec : pre).push_back(i);
   }
   if (!dec.empty()) {
+    // Both kinds of rows: one launch with the decode rows on the CU share
+    // their K/V bytes need next to the prefill's flops.
+    if (!pre.empty() && fused_mixed_ && num_kv_heads_ <= 8 && 8 % num_kv_heads_ == 0) {
+      int64_t dec_tokens = 0;
+      for (int i : dec) dec_tokens += batch.padded_reqs[i]->device_len();
+      double flops = 0.0;
+      for (int i : pre) {
+        const double qo = meta->qo_indptr_host[i + 1] - meta->qo_indptr_host[i];
+        const double kv = batch.padded_reqs[i]->device_len();
+        flops += qo * (kv - qo) + qo * (qo + 1) / 2;
+      }
+      flops *= 4.0 * head_dim_ * num_qo_heads_;
+      const int h = sgl_mixed_decode_cus(dec_tokens, num_kv_heads_, head_dim_, flops);
+      if (h < device_cus_) {
+        meta->fused = true;
+        meta->dec_cus = h;
+      }
+    }
     std::vector<int32_t> rows;
     for (int i : dec) rows.push_back(meta->qo_indptr_host[i]);
-    build_decode_rows(*meta, dec, rows, batch);
+    build_decode_rows(*meta, dec, rows, batch, meta->dec_cus);
   }
   if (!pre.empty()) {
     const int n = static_cast<int>(pre.size());
@@ -319,6 +349,32 @@ torch::Tensor HipAttnBackend::attend(const torch::Tensor& q_in, int layer_id, Ba
   // this also holds inside a captured graph. The persistent decode launch
   // goes first so its workgroups are resident before the prefill tiles take
   // the remaining slots (the other order measured no gain).
+  if (meta->fused) {
+    // Decode units and prefill items in one launch (decode on dec_cus CUs).
+    torch::Tensor& ws = !meta->use_capture_buffers ? workspace(meta->dec_plan.workspace_bytes)
+                                                   : mixed_->workspace;
+    if (!meta->use_capture_buffers) {
+      hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+      check_hip(hipStreamIsCapturing(static_cast<hipStream_t>(stream), &cs),
+                "hipStreamIsCapturing");
+      if (cs != hipStreamCaptureStatusNone) workspace_captured_ = true;
+    }
+    TORCH_CHECK(ws.numel() >= meta->dec_plan.workspace_bytes, "decode workspace too small");
+    check_sgl(sgl_paged_mixed(&meta->dec_plan, q.data_ptr(), q.stride(0), q.stride(1),
+                              kc.data_ptr(), vc.data_ptr(), kc.stride(0), kc.stride(1),
+                              meta->dec_indices.data_ptr<int32_t>(),
+                              meta->dec_kv_indptr.data_ptr<int32_t>(),
+                              meta->dec_q_rows.data_ptr<int32_t>(), meta->num_decode,
+                              meta->pre_indices.data_ptr<int32_t>(),
+                              meta->pre_qo_indptr.data_ptr<int32_t>(),
+                              meta->pre_kv_indptr.data_ptr<int32_t>(),
+                              meta->pre_q_start.data_ptr<int32_t>(), meta->num_prefill,
+                              meta->max_qo_len, num_qo_heads_, num_kv_heads_, head_dim_, sm_scale,
+                              o.data_ptr(), o.stride(0), o.stride(1), ws.data_ptr(), ws.numel(),
+                              stream),
+              "sgl_paged_mixed");
+    return o.view({-1, num_qo_heads_ * head_dim_});
+  }
   const bool fork = overlap_mixed_ && meta->num_decode > 0 && meta->num_prefill > 0;
   void* pre_stream = stream;
   if (fork) {
@@ -567,12 +623,20 @@ void HipAttnBackend::prepare_mixed_for_capture(Batch& batch) {
   meta->use_capture_buffers = true;
   meta->indptr = mixed_->qo_indptr.slice(0, 0, bs + 1);
   meta->num_decode = n_dec;
+  // The one-launch split is fixed at capture, from the captured batch's sizes.
+  meta->fused = src->fused;
+  meta->dec_cus = src->dec_cus;
   if (n_dec > 0) {
     std::vector<int32_t> worst(n_dec + 1);
     for (int i = 0; i <= n_dec; ++i) worst[i] = static_cast<int32_t>(i * L);
-    check_sgl(sgl_decode_plan(worst.data(), n_dec, num_qo_heads_, num_kv_heads_, head_dim_,
-                              &meta->dec_plan),
-              "sgl_decode_plan");
+    if (meta->fused)
+      check_sgl(sgl_decode_plan_cus(worst.data(), n_dec, num_qo_heads_, num_kv_heads_, head_dim_,
+                                    meta->dec_cus, &meta->dec_plan),
+                "sgl_decode_plan_cus");
+    else
+      check_sgl(sgl_decode_plan(worst.data(), n_dec, num_qo_heads_, num_kv_heads_, head_dim_,
+                                &meta->dec_plan),
+                "sgl_decode_plan");
     TORCH_CHECK(meta->dec_plan.workspace_bytes <= mixed_->workspace.numel(),
                 "mixed capture workspace too small");
     meta->dec_kv_indptr = mixed_->dec_kv_indptr.slice(0, 0, n_dec + 1);

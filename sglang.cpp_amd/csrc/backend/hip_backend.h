@@ -62,6 +62,10 @@ struct HipAttnMetadata : public BaseAttnMetadata {
   int num_decode = 0;
   torch::Tensor dec_kv_indptr, dec_indices, dec_q_rows, dec_table_idx;
   sgl_decode_plan_t dec_plan{};
+  // Mixed batches run as one launch (sgl_paged_mixed) with the decode rows
+  // on dec_cus CUs; otherwise decode and prefill are separate launches.
+  bool fused = false;
+  int dec_cus = 0;
 
   // Prefill rows: requests of a prefill-phase batch with qo_len > 1.
   int num_prefill = 0;
@@ -111,8 +115,12 @@ class HipAttnBackend : public BaseAttnBackend {
   // [T, Hq * D].
   torch::Tensor attend(const torch::Tensor& q, int layer_id, Batch& batch);
 
-  // Mixed batches: run the prefill rows on a side stream beside the decode
-  // rows (default on).
+  // Mixed batches: one launch with the decode rows on a share of the CUs and
+  // the prefill rows on the others (default on, for kv-head counts dividing
+  // 8); otherwise, with overlap_mixed, the prefill rows on a side stream
+  // beside the decode launch (default on).
+  void set_fused_mixed(bool on) { fused_mixed_ = on; }
+  bool fused_mixed() const { return fused_mixed_; }
   void set_overlap_mixed(bool on) { overlap_mixed_ = on; }
   bool overlap_mixed() const { return overlap_mixed_; }
 
@@ -126,7 +134,8 @@ class HipAttnBackend : public BaseAttnBackend {
   torch::Tensor& workspace(int64_t bytes);
   torch::Tensor to_device(const std::vector<int32_t>& host, HipAttnMetadata& meta);
   void build_decode_rows(HipAttnMetadata& meta, const std::vector<int>& reqs,
-                         const std::vector<int32_t>& q_rows, const Batch& batch);
+                         const std::vector<int32_t>& q_rows, const Batch& batch,
+                         int decode_cus = 0);
 
   void prepare_mixed_for_capture(Batch& batch);
   void prepare_mixed_for_replay(Batch& batch);
@@ -167,6 +176,8 @@ class HipAttnBackend : public BaseAttnBackend {
   void* side_stream();
   void* side_stream_ = nullptr;
   bool overlap_mixed_ = true;
+  bool fused_mixed_ = true;
+  int device_cus_ = 256;
   hipEvent_t fork_event_ = nullptr;
   hipEvent_t join_event_ = nullptr;
 };

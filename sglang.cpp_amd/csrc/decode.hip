@@ -38,6 +38,7 @@
 #include <mutex>
 
 #include "common.h"
+#include "prefill_impl.h"
 
 namespace sgl {
 namespace {
@@ -175,8 +176,10 @@ struct HeadState {
 // One wave: kv head h over the `len` tokens whose slots are sidx[0, len)
 // (one piece of a request). whole: the piece is the whole request (output
 // written directly); otherwise it goes to partial slot pslot. kState: leave
-// the state in *st instead (no output), with no per-step workgroup barrier
-// (the waves of the small-batch kernel take pieces of different lengths).
+// the state in *st instead (no output). kBarrier: a workgroup barrier per
+// step, for workgroups whose waves are exactly one unit's kv heads (the
+// waves of the small-batch kernel, and units sharing a workgroup, take
+// pieces of different lengths).
 //
 // Per 16-token step (v_mfma, lane l, n = l % 16, j = l / 16):
 //   S^T[tok, head] = K . Q^T          4 x 16x16x32: rows tok, columns head
@@ -188,7 +191,7 @@ struct HeadState {
 //
 // K and V of step t + 1 are in flight during step t; the Q rows are loaded
 // first and the first step's K/V rows issued before Q is waited for.
-template <bool kState>
+template <bool kState, bool kBarrier = !kState>
 __device__ __forceinline__ void decode_head(const DecodeArgs& a, WaveLds& L, const int32_t* sidx,
                                             int pslot, bool whole, int h, int len, int qrow,
                                             int lane, HeadState* st = nullptr) {
@@ -280,7 +283,7 @@ __device__ __forceinline__ void decode_head(const DecodeArgs& a, WaveLds& L, con
     // Keep the workgroup's waves (one per kv head) in step: together they
     // read each token's whole [Hkv, D] row, which DRAM serves better as one
     // burst than as per-head pieces spread over time.
-    if constexpr (!kState) __builtin_amdgcn_s_barrier();
+    if constexpr (kBarrier) __builtin_amdgcn_s_barrier();
     const int tn = t + kStep;
     const int kslot_next = sidx[min(tn + n, len - 1)];
     const f32x4_t sacc = qk(kr);
@@ -331,9 +334,9 @@ __device__ __forceinline__ void decode_head(const DecodeArgs& a, WaveLds& L, con
   }
 }
 
-// Zero output row of an empty request (kv_len 0).
-__device__ __forceinline__ void zero_row(const DecodeArgs& a, int qrow) {
-  for (int e = threadIdx.x; e < a.hq * (kD / 8); e += blockDim.x) {
+// Zero output row of an empty request (kv_len 0), by threads t, t + n, ...
+__device__ __forceinline__ void zero_row(const DecodeArgs& a, int qrow, int t, int n) {
+  for (int e = t; e < a.hq * (kD / 8); e += n) {
     const int hh = e / (kD / 8);
     stg128(a.o + static_cast<int64_t>(qrow) * a.o_st + static_cast<int64_t>(hh) * a.o_sh +
                (e - hh * (kD / 8)) * 8,
@@ -341,47 +344,59 @@ __device__ __forceinline__ void zero_row(const DecodeArgs& a, int qrow) {
   }
 }
 
-// Persistent, token-balanced schedule: workgroup u takes the tokens
+// LDS bytes of one unit: the per-wave Q copies, then the unit's slot indices.
+__device__ __host__ inline size_t unit_lds_bytes(int hkv, int chunk) {
+  return static_cast<size_t>(hkv) * sizeof(WaveLds) + static_cast<size_t>(chunk) * sizeof(int32_t);
+}
+
+// Persistent, token-balanced schedule: unit u takes the tokens
 // [u W, (u+1) W) of the flattened stream, which may cover the tail of one
-// request, whole requests and the head of another. Waves take the kv heads.
-// Budget 128 VGPRs (up to 4 waves per SIMD, above the ~2 the schedule keeps
-// resident): a tighter budget spills, and scratch traffic in the step loop
-// costs ~9%.
-__global__ void __launch_bounds__(kMaxKvHeads * kWave)
-    __attribute__((amdgpu_waves_per_eu(4))) paged_decode_kernel(DecodeArgs a) {
-  extern __shared__ __attribute__((aligned(16))) char smem[];
-  const int u = blockIdx.x;
+// request, whole requests and the head of another; one wave per kv head.
+// The workgroup (index blk) holds UPW units, unit blk UPW + g on waves
+// [g hkv, (g + 1) hkv) with LDS region g (unit_lds_bytes each); units past
+// num_units idle. kBarrier: the units' waves keep in step (UPW = 1 only).
+template <int UPW, bool kBarrier>
+__device__ __forceinline__ void decode_units(const DecodeArgs& a, char* smem, int blk) {
+  static_assert(UPW == 1 || !kBarrier, "a per-step barrier needs one unit per workgroup");
+  const int lane = threadIdx.x & 63;
+  const int wave_all = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform per wave
+  const int g = UPW == 1 ? 0 : wave_all / a.hkv;
+  const int wave = wave_all - g * a.hkv;  // the kv head
+  const int gt = static_cast<int>(threadIdx.x) - g * a.hkv * kWave;  // thread index in the unit
+  const int gn = a.hkv * kWave;
+  const int u = blk * UPW + g;
   const int total = a.kv_indptr[a.batch];
   const int W = unit_tokens(a, total);
   const int tok0 = u * W;
   const int tok1 = min(total, tok0 + W);
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform per wave
   const bool last_unit = tok1 == total;
   // The merge kernel, stream-ordered after this launch, reports capacity
   // overflows; every launch starts from a clear status.
-  if (u == 0 && threadIdx.x == 0) *a.status = SGL_OK;
-
-  if (tok0 >= tok1) {
+  if (u == 0 && gt == 0) *a.status = SGL_OK;
+  const bool active = u < a.num_units && tok0 < tok1;
+  char* base = smem + g * unit_lds_bytes(a.hkv, a.chunk);
+  int32_t* sidx = reinterpret_cast<int32_t*>(base + a.hkv * sizeof(WaveLds));
+  int r = 0;
+  if (active) {
+    // First i in [0, batch] with kv_indptr[i] >= tok0 (uniform binary search).
+    int lo = 0, hi = a.batch;
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (a.kv_indptr[mid] < tok0) lo = mid + 1; else hi = mid;
+    }
+    // Request lo - 1 runs across tok0 when its end kv_indptr[lo] lies past tok0.
+    r = (lo > 0 && a.kv_indptr[lo] > tok0) ? lo - 1 : lo;
+    // Stage the unit's slot indices (shared by every kv head) in LDS.
+    for (int e = gt; e < tok1 - tok0; e += gn) sidx[e] = a.indices[tok0 + e];
+  }
+  __syncthreads();
+  if (!active) {
     // Past the end of the token stream: only an all-empty batch needs work.
     if (total == 0 && u == 0)
-      for (int r = 0; r < a.batch; ++r) zero_row(a, a.q_indptr ? a.q_indptr[r] : r);
+      for (int rr = 0; rr < a.batch; ++rr) zero_row(a, a.q_indptr ? a.q_indptr[rr] : rr, gt, gn);
     return;
   }
-  // First i in [0, batch] with kv_indptr[i] >= tok0 (uniform binary search).
-  int lo = 0, hi = a.batch;
-  while (lo < hi) {
-    const int mid = (lo + hi) >> 1;
-    if (a.kv_indptr[mid] < tok0) lo = mid + 1; else hi = mid;
-  }
-  // Request lo - 1 runs across tok0 when its end kv_indptr[lo] lies past tok0.
-  int r = (lo > 0 && a.kv_indptr[lo] > tok0) ? lo - 1 : lo;
-
-  // Stage the unit's slot indices (shared by every kv head) in LDS.
-  int32_t* sidx = reinterpret_cast<int32_t*>(smem + a.hkv * sizeof(WaveLds));
-  for (int e = threadIdx.x; e < tok1 - tok0; e += blockDim.x) sidx[e] = a.indices[tok0 + e];
-  __syncthreads();
-  WaveLds& L = reinterpret_cast<WaveLds*>(smem)[wave];
+  WaveLds& L = reinterpret_cast<WaveLds*>(base)[wave];
 
   for (; r < a.batch; ++r) {
     const int rb = a.kv_indptr[r];
@@ -391,7 +406,7 @@ __global__ void __launch_bounds__(kMaxKvHeads * kWave)
     if (rb >= tok1 && !(last_unit && rb == total)) break;
     const int qrow = a.q_indptr ? a.q_indptr[r] : r;
     if (re == rb) {  // empty request: zero output row
-      zero_row(a, qrow);
+      zero_row(a, qrow, gt, gn);
       continue;
     }
     const int s0 = max(rb, tok0);
@@ -399,10 +414,40 @@ __global__ void __launch_bounds__(kMaxKvHeads * kWave)
     if (s1 <= s0) continue;
     const bool whole = rb >= tok0 && re <= tok1;
     const int pslot = 2 * u + (rb > tok0 ? 1 : 0);
-    decode_head<false>(a, L, sidx + (s0 - tok0), pslot, whole, wave, s1 - s0, qrow, lane);
+    decode_head<false, kBarrier>(a, L, sidx + (s0 - tok0), pslot, whole, wave, s1 - s0, qrow,
+                                 lane);
   }
 }
 
+// One unit per workgroup (one wave per kv head), about 8 waves per CU.
+// Budget 128 VGPRs (up to 4 waves per SIMD, above the ~2 the schedule keeps
+// resident): a tighter budget spills, and scratch traffic in the step loop
+// costs ~9%.
+__global__ void __launch_bounds__(kMaxKvHeads * kWave)
+    __attribute__((amdgpu_waves_per_eu(4))) paged_decode_kernel(DecodeArgs a) {
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  decode_units<1, true>(a, smem, blockIdx.x);
+}
+
+
+// Decode units and causal-prefill items in one launch: workgroups
+// [0, dec_blocks) take UPW decode units each (8 waves = UPW x hkv), the rest
+// take the prefill's 8-wave items in heavy-first order. Blocks are
+// dispatched in index order, so the decode workgroups occupy dec_blocks CUs
+// (one per CU: a workgroup holds every register of its CU) while the
+// prefill items fill the others and, as the decode finishes, every CU; the
+// HBM-bound decode and the MFMA-bound prefill then run side by side instead
+// of one after the other.
+template <int UPW>
+__global__ void __launch_bounds__(512, 1) mixed_attention_kernel(DecodeArgs d, pf::PrefillArgs p,
+                                                                  int dec_blocks) {
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  if (static_cast<int>(blockIdx.x) < dec_blocks)
+    decode_units<UPW, false>(d, smem, blockIdx.x);
+  else
+    pf::prefill_item<8, false, 1>(p, smem, static_cast<int>(blockIdx.x) - dec_blocks,
+                                  static_cast<int>(gridDim.x) - dec_blocks);
+}
 
 // Small batches (every unit at the 64-token minimum and at most one
 // workgroup per CU for each (request, kv head)): one 8-wave workgroup per
@@ -585,8 +630,11 @@ static int device_cu_count() {
   return cached;
 }
 
-extern "C" int sgl_decode_plan(const int32_t* kv_indptr_host, int batch_size, int num_qo_heads,
-                               int num_kv_heads, int head_dim, sgl_decode_plan_t* plan) {
+// A plan whose units number about units_target (0: one unit per resident
+// workgroup of the whole device).
+static int decode_plan_for(const int32_t* kv_indptr_host, int batch_size, int num_qo_heads,
+                           int num_kv_heads, int head_dim, int64_t units_target,
+                           sgl_decode_plan_t* plan) {
   if (!plan || !kv_indptr_host || batch_size < 0 || num_qo_heads <= 0 || num_kv_heads <= 0)
     return SGL_ERR_INVALID_ARG;
   if (num_qo_heads % num_kv_heads != 0) return SGL_ERR_INVALID_ARG;
@@ -607,7 +655,7 @@ extern "C" int sgl_decode_plan(const int32_t* kv_indptr_host, int batch_size, in
   // by 3-4% (more streams lose DRAM locality faster than they add latency
   // hiding), and 4 starve long contexts.
   int units_per_cu = 8 / num_kv_heads > 1 ? 8 / num_kv_heads : 1;
-  const int64_t units_target = static_cast<int64_t>(device_cu_count()) * units_per_cu;
+  if (units_target <= 0) units_target = static_cast<int64_t>(device_cu_count()) * units_per_cu;
   auto round16 = [](int64_t x) { return (x + kStep - 1) / kStep * kStep; };
   int64_t W = round16((total + units_target - 1) / units_target);
   if (W < kMinUnit) W = kMinUnit;
@@ -634,6 +682,43 @@ extern "C" int sgl_decode_plan(const int32_t* kv_indptr_host, int batch_size, in
   plan->max_total_tokens = units * W;
   plan->workspace_bytes = workspace_layout(static_cast<int>(units), num_qo_heads).total;
   return SGL_OK;
+}
+
+extern "C" int sgl_decode_plan(const int32_t* kv_indptr_host, int batch_size, int num_qo_heads,
+                               int num_kv_heads, int head_dim, sgl_decode_plan_t* plan) {
+  return decode_plan_for(kv_indptr_host, batch_size, num_qo_heads, num_kv_heads, head_dim, 0, plan);
+}
+
+extern "C" int sgl_decode_plan_cus(const int32_t* kv_indptr_host, int batch_size,
+                                   int num_qo_heads, int num_kv_heads, int head_dim,
+                                   int decode_cus, sgl_decode_plan_t* plan) {
+  if (num_kv_heads <= 0 || num_kv_heads > 8 || 8 % num_kv_heads != 0) return SGL_ERR_UNSUPPORTED;
+  if (decode_cus <= 0) return SGL_ERR_INVALID_ARG;
+  return decode_plan_for(kv_indptr_host, batch_size, num_qo_heads, num_kv_heads, head_dim,
+                         static_cast<int64_t>(decode_cus) * (8 / num_kv_heads), plan);
+}
+
+// Per-CU rates behind the split, measured on MI355X at config 5's shapes
+// (32q/4kv, d128): the decode streams about 37.5 GB/s of K/V per CU when it
+// has only part of the device (it needs ~170 CUs to reach HBM bandwidth),
+// and the causal prefill computes about 3.9 TFLOP/s per CU.
+constexpr double kDecodeBytesPerCu = 37.5e9;
+constexpr double kPrefillFlopsPerCu = 3.9e12;
+
+extern "C" int sgl_mixed_decode_cus(int64_t decode_kv_tokens, int num_kv_heads, int head_dim,
+                                    double prefill_flops) {
+  const int cus = device_cu_count();
+  if (decode_kv_tokens <= 0 || num_kv_heads <= 0 || head_dim <= 0) return 8;
+  if (!(prefill_flops > 0.0)) return cus;
+  const double dec = static_cast<double>(decode_kv_tokens) * num_kv_heads * head_dim * 4.0 /
+                     kDecodeBytesPerCu;
+  const double pre = prefill_flops / kPrefillFlopsPerCu;
+  // The decode's share of the CU-time, leaning 5% towards the decode: the
+  // prefill absorbs imbalance better (its items fill freed CUs heavy-first).
+  int h = static_cast<int>(cus * dec / (dec + pre) * 1.05 / 8.0 + 0.5) * 8;
+  if (h < 8) h = 8;
+  if (h > cus) h = cus;
+  return h;
 }
 
 extern "C" int sgl_decode_plan_check(const sgl_decode_plan_t* plan,
@@ -765,6 +850,77 @@ extern "C" int sgl_paged_decode(const sgl_decode_plan_t* plan, const void* q,
   if (!aligned16(workspace)) return SGL_ERR_ALIGNMENT;
   bind_workspace(a, plan, workspace);
   return launch_decode(a, plan, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int sgl_paged_mixed(const sgl_decode_plan_t* plan, const void* q,
+                               int64_t q_stride_token, int64_t q_stride_head,
+                               const void* k_cache, const void* v_cache, int64_t kv_stride_slot,
+                               int64_t kv_stride_head, const int32_t* dec_indices,
+                               const int32_t* dec_kv_indptr, const int32_t* dec_q_rows,
+                               int dec_batch, const int32_t* pre_indices,
+                               const int32_t* pre_qo_indptr, const int32_t* pre_kv_indptr,
+                               const int32_t* pre_q_start, int pre_batch, int pre_max_qo_len,
+                               int num_qo_heads, int num_kv_heads, int head_dim, float sm_scale,
+                               void* o, int64_t o_stride_token, int64_t o_stride_head,
+                               void* workspace, int64_t workspace_bytes, void* stream) {
+  if (!plan || dec_batch < 0 || pre_batch < 0 || pre_max_qo_len < 0) return SGL_ERR_INVALID_ARG;
+  if (num_kv_heads <= 0 || num_kv_heads > 8 || 8 % num_kv_heads != 0) return SGL_ERR_UNSUPPORTED;
+  const bool has_pre = pre_batch > 0 && pre_max_qo_len > 0;
+  if (dec_batch == 0 || !has_pre) {
+    int st = SGL_OK;
+    if (dec_batch > 0)
+      st = sgl_paged_decode(plan, q, q_stride_token, q_stride_head, k_cache, v_cache,
+                            kv_stride_slot, kv_stride_head, dec_indices, dec_kv_indptr,
+                            dec_q_rows, dec_batch, num_qo_heads, num_kv_heads, head_dim, sm_scale,
+                            o, o_stride_token, o_stride_head, workspace, workspace_bytes, stream);
+    if (st == SGL_OK && has_pre)
+      st = sgl_paged_prefill(q, q_stride_token, q_stride_head, k_cache, v_cache, kv_stride_slot,
+                             kv_stride_head, pre_indices, pre_qo_indptr, pre_kv_indptr,
+                             pre_q_start, pre_batch, pre_max_qo_len, num_qo_heads, num_kv_heads,
+                             head_dim, sm_scale, o, o_stride_token, o_stride_head, stream);
+    return st;
+  }
+  DecodeArgs d;
+  int st = decode_args(plan, q, q_stride_token, q_stride_head, k_cache, v_cache, kv_stride_slot,
+                       kv_stride_head, dec_indices, dec_kv_indptr, dec_q_rows, dec_batch,
+                       num_qo_heads, num_kv_heads, head_dim, sm_scale, o, o_stride_token,
+                       o_stride_head, d);
+  if (st != SGL_OK) return st;
+  if (workspace == nullptr || workspace_bytes < plan->workspace_bytes) return SGL_ERR_CAPACITY;
+  if (!aligned16(workspace)) return SGL_ERR_ALIGNMENT;
+  bind_workspace(d, plan, workspace);
+  pf::PrefillArgs p;
+  st = pf::prefill_args(q, q_stride_token, q_stride_head, k_cache, v_cache, kv_stride_slot,
+                        kv_stride_head, pre_indices, pre_qo_indptr, pre_kv_indptr, pre_q_start,
+                        num_qo_heads, num_kv_heads, head_dim, sm_scale, o, o_stride_token,
+                        o_stride_head, p);
+  if (st != SGL_OK) return st;
+  // The prefill role: 8-wave items of 256 packed rows (unpaired, heavy first).
+  const int64_t rows_max = static_cast<int64_t>(pre_max_qo_len) * p.group;
+  const int64_t tiles = (rows_max + 255) / 256;
+  const int64_t items = tiles * num_kv_heads * pre_batch;
+  const int upw = 8 / num_kv_heads;
+  // Decode workgroups rounded to a multiple of the 8 XCDs, so the prefill
+  // items keep their XCD-aware placement.
+  const int64_t dec_blocks = ((plan->num_units + upw - 1) / upw + 7) / 8 * 8;
+  if (items + dec_blocks > 0x7fffffff) return SGL_ERR_INVALID_ARG;
+  p.tiles_per_req = static_cast<int>(tiles);
+  size_t lds = static_cast<size_t>(upw) * unit_lds_bytes(num_kv_heads, plan->kv_chunk_size);
+  if (lds < static_cast<size_t>(pf::prefill_lds_bytes<8, 1>()))
+    lds = pf::prefill_lds_bytes<8, 1>();
+  const dim3 grid(static_cast<uint32_t>(dec_blocks + items));
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const int db = static_cast<int>(dec_blocks);
+  switch (upw) {
+    case 1: hipLaunchKernelGGL(mixed_attention_kernel<1>, grid, dim3(512), lds, s, d, p, db); break;
+    case 2: hipLaunchKernelGGL(mixed_attention_kernel<2>, grid, dim3(512), lds, s, d, p, db); break;
+    case 4: hipLaunchKernelGGL(mixed_attention_kernel<4>, grid, dim3(512), lds, s, d, p, db); break;
+    default: hipLaunchKernelGGL(mixed_attention_kernel<8>, grid, dim3(512), lds, s, d, p, db); break;
+  }
+  st = launch_status();
+  if (st != SGL_OK) return st;
+  hipLaunchKernelGGL(decode_merge_kernel, dim3(d.hkv, d.batch), dim3(256), 0, s, d);
+  return launch_status();
 }
 
 // ------------------------------------------------------------------ no-alloc variant

@@ -149,6 +149,39 @@ def test_decode_plan_covers_any_batch_property():
     check()
 
 
+def test_mixed_split_heuristic():
+    """Host logic, no GPU: the decode's CU share grows with its K/V bytes and shrinks with the
+    prefill's flops, in multiples of 8 within [8, CUs]."""
+    cus = capi.mixed_decode_cus(10 ** 6, 4, 128, 0.0)
+    assert cus >= 8 and cus % 8 == 0
+    a = capi.mixed_decode_cus(1_081_344, 4, 128, 171.8e9)  # config 5's layer
+    assert 8 <= a < cus and a % 8 == 0
+    assert capi.mixed_decode_cus(2_000_000, 4, 128, 171.8e9) >= a
+    assert capi.mixed_decode_cus(1_081_344, 4, 128, 400e9) <= a
+    assert capi.mixed_decode_cus(1, 4, 128, 1e15) == 8
+
+
+def test_decode_plan_cus_host():
+    """A plan for a decode sharing the device: about decode_cus x (8 / hkv)
+    units, the usual capacity contract; kv-head counts that do not divide 8
+    are refused."""
+    import numpy as np
+    rng = np.random.default_rng(3)
+    kv = rng.integers(1024, 32769, 64)
+    ip = np.concatenate([[0], np.cumsum(kv)])
+    for cus, hq, hkv in ((160, 32, 4), (64, 32, 8), (8, 16, 1)):
+        plan = capi.decode_plan_cus(ip, hq, hkv, 128, cus)
+        # units of at most 8192 tokens (the LDS-staged slot indices) bound the count from below
+        target = max(cus * (8 // hkv), -(-int(kv.sum()) // 8192))
+        assert target * 0.9 <= plan.num_units <= target
+        assert plan.max_total_tokens == plan.num_units * plan.kv_chunk_size >= int(kv.sum())
+        assert capi.decode_plan_check(plan, ip) == 0
+    with pytest.raises(capi.SglError):
+        capi.decode_plan_cus(ip, 48, 3, 128, 64)
+    with pytest.raises(capi.SglError):
+        capi.decode_plan_cus(ip, 32, 4, 128, 0)
+
+
 def test_decode_plan_check_host():
     """A plan serves any batch with at most batch_size requests and
     max_total_tokens tokens, whatever the per-request lengths; beyond it the

@@ -360,18 +360,21 @@ def test_backend_decode_graph_capture_replay(oracle, dev, sb):
 
 @pytest.mark.gpu
 def test_backend_mixed_batch_overlap_and_graph_replay(oracle, dev, sb):
-    """A mixed batch (qo=1 rows beside a prefill chunk): the side-stream
-    overlap gives the same bits as the serial order, and a captured graph of
-    the step replays to the eager result every time."""
-    note("backend mixed batch: overlap and graph replay")
+    """A mixed batch (qo=1 rows beside a prefill chunk): with separate
+    launches the side-stream overlap gives the same bits as the serial order;
+    the one-launch path (decode rows on a CU share) matches the oracle; and a
+    captured graph of the step replays to the eager result every time."""
+    note("backend mixed batch: overlap, one launch and graph replay")
     rng = np.random.default_rng(53)
     kv = [900, 3000, 17, 4096 + 512]
     cached = [899, 2999, 16, 4096]
     b = wl.make_paged_batch(rng, cached, kv, page_size=16)
     s = Setup(sb, dev, b, 32, 4, 54, layers=1)
     s.snapshot()
+    s.backend.set_fused_mixed(False)
     s.backend.prepare_metadata(s.batch)
     assert s.batch.num_decode_rows() == 3 and s.batch.num_prefill_rows() == 1
+    assert s.batch.fused_mixed_cus() == 0
     s.backend.set_overlap_mixed(False)
     o_serial = s.backend.forward(s.q, s.k, s.v, 0, s.batch).clone()
     s.backend.set_overlap_mixed(True)
@@ -380,6 +383,12 @@ def test_backend_mixed_batch_overlap_and_graph_replay(oracle, dev, sb):
     assert torch.equal(o_serial.view(torch.int16), o_overlap.view(torch.int16))
     ref, _, _ = s.expected(oracle, 0, 1 / math.sqrt(D))
     assert_attn_close(o_overlap.float().cpu().numpy(), ref, what="mixed overlap")
+    s.backend.set_fused_mixed(True)
+    s.backend.prepare_metadata(s.batch)
+    assert s.batch.fused_mixed_cus() >= 8
+    o_fused = s.backend.forward(s.q, s.k, s.v, 0, s.batch).clone()
+    torch.cuda.synchronize()
+    assert_attn_close(o_fused.float().cpu().numpy(), ref, what="mixed one launch")
 
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())

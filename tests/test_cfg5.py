@@ -124,6 +124,8 @@ def test_cfg5_mixed_eager_and_graph_replay(oracle, dev):
     b = st["batch"]
     c.backend.prepare_metadata(b)
     assert b.num_decode_rows() == N_DEC and b.num_prefill_rows() == 1
+    # the one-launch mixed path: decode rows on a share of the CUs
+    assert 8 <= b.fused_mixed_cus() < 256
     o = c.backend.forward(st["q"], st["k"], st["v"], 0, b)
     torch.cuda.synchronize()
     c.apply_store(st)
@@ -145,7 +147,7 @@ def test_cfg5_mixed_eager_and_graph_replay(oracle, dev):
     cap = sb.Batch(True, [sb.Req(r.table_idx, r.cached_len, r.device_len())
                           for r in b.padded_reqs], b.positions, static_loc)
     be.prepare_for_capture(cap)
-    assert cap.uses_capture_buffers()
+    assert cap.uses_capture_buffers() and cap.fused_mixed_cus() == b.fused_mixed_cus()
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):

@@ -575,6 +575,51 @@ def test_prefill_long_no_prefix_matches_textbook(oracle, dev):
     check_prefill(oracle, dev, b, 16, 8, 26, "textbook causal")
 
 
+def _run_mixed(dev, batch, hq, hkv, seed, decode_cus):
+    """One sgl_paged_mixed call over a batch: requests with qo == 1 as decode
+    rows, the others as prefill rows, sharing q, the pool and o."""
+    kc, vc = _pool(dev, batch.num_slots, hkv, 128, seed)
+    g = gen(dev, seed + 100)
+    rows = int(batch.qo_indptr[-1])
+    q = randn_bf16((rows, hq, 128), dev, g)
+    o = torch.full((rows, hq, 128), float("nan"), device=dev, dtype=torch.bfloat16)
+    qo, kv = batch.qo_lens, batch.kv_lens
+    dec = [r for r in range(batch.batch_size) if qo[r] == 1]
+    pre = [r for r in range(batch.batch_size) if qo[r] > 1]
+    seg = lambda r: batch.indices[batch.kv_indptr[r]:batch.kv_indptr[r + 1]]  # noqa: E731
+    dec_ip = np.concatenate([[0], np.cumsum(kv[dec])]).astype(np.int32)
+    pre_qo = np.concatenate([[0], np.cumsum(qo[pre])]).astype(np.int32)
+    pre_kv = np.concatenate([[0], np.cumsum(kv[pre])]).astype(np.int32)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.int32)).to(dev)  # noqa: E731
+    plan = capi.decode_plan_cus(dec_ip, hq, hkv, 128, decode_cus)
+    ws = capi.decode_workspace(plan, dev)
+    capi.paged_mixed(plan, q, kc, vc, t(np.concatenate([seg(r) for r in dec])), t(dec_ip),
+                     t(batch.qo_indptr[dec]), t(np.concatenate([seg(r) for r in pre])), t(pre_qo),
+                     t(pre_kv), t(batch.qo_indptr[pre]), int(qo[pre].max()), o, ws)
+    torch.cuda.synchronize()
+    return q, kc, vc, o, ws
+
+
+@pytest.mark.parametrize("hq,hkv,decode_cus", [(32, 4, 160), (32, 4, 8), (32, 8, 64), (16, 2, 96),
+                                               (8, 1, 200), (32, 4, 256)])
+def test_paged_mixed_one_launch(oracle, dev, hq, hkv, decode_cus):
+    """sgl_paged_mixed (decode units and prefill items in one launch, decode
+    on decode_cus CUs): decode rows with kv 1..6000 beside two prefill chunks
+    (one on a cached prefix), rows interleaved by request, all against the
+    oracle; the status word stays OK."""
+    note(f"paged mixed hq={hq} hkv={hkv} decode_cus={decode_cus}")
+    rng = np.random.default_rng(33 + hkv + decode_cus)
+    kv_dec = [int(x) for x in rng.integers(1, 6000, 13)]
+    cached = [x - 1 for x in kv_dec[:5]] + [300] + [x - 1 for x in kv_dec[5:]] + [0]
+    dev_lens = kv_dec[:5] + [300 + 700] + kv_dec[5:] + [200]
+    b = wl.make_paged_batch(rng, cached, dev_lens, page_size=16)
+    q, kc, vc, o, ws = _run_mixed(dev, b, hq, hkv, 34, decode_cus)
+    ref = oracle.prefill(u16(q).copy(), u16(kc), u16(vc), b.indices, b.qo_indptr, b.kv_indptr,
+                         1 / math.sqrt(128))
+    assert_attn_close(o.float().cpu().numpy(), ref, what=f"mixed {hq}/{hkv} cus {decode_cus}")
+    assert capi.decode_status(ws) == 0
+
+
 def test_prefill_mixed_decode_rows(oracle, dev):
     """Config-5 shape of batch (qo 1 rows next to a 2048 chunk), scaled down."""
     note("prefill with qo=1 rows beside a long chunk")
