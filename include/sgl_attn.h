@@ -339,11 +339,15 @@ int sgl_paged_prefill(const void* q, int64_t q_stride_token,
  *     8), from their K/V token count and the prefill's flops
  *     (4 D Hq sum_r sum_i (kv_r - qo_r + i + 1)).
  *   sgl_decode_plan_cus: a decode plan (as sgl_decode_plan) whose units fill
- *     decode_cus CUs; like any plan it serves smaller batches on replay.
+ *     decode_cus CUs, each unit short enough for the fused launch's LDS
+ *     (at 1 or 2 kv heads long batches then get more units than that); like
+ *     any plan it serves smaller batches on replay.
  *   sgl_paged_mixed: decode rows as sgl_paged_decode (dec_q_rows: query row
  *     of each decode request, or NULL for rows 0..dec_batch-1) and prefill
  *     rows as sgl_paged_prefill, sharing q, the caches and o. With no rows
- *     of one kind it runs the other entry point alone.
+ *     of one kind it runs the other entry point alone; with a plan whose
+ *     units are too long for the fused launch (sgl_decode_plan at 1 or 2
+ *     kv heads) it runs the two entry points one after the other.
  * Replaces: the decode and prefill calls of one mixed step
  *           (src/attention/flashinfer_backend.cu:553-679); the reference
  *           runs them as separate kernels.

@@ -630,10 +630,23 @@ static int device_cu_count() {
   return cached;
 }
 
+// LDS of one fused decode + prefill workgroup (the CU's whole LDS).
+constexpr size_t kMixedLds = 160 * 1024;
+
+// Longest unit whose slot indices fit the fused launch's LDS next to the
+// other units of its workgroup (8 / hkv units per 8-wave workgroup).
+static int mixed_max_unit(int num_kv_heads) {
+  const size_t per_unit = kMixedLds / (8 / num_kv_heads);
+  const int64_t w = (static_cast<int64_t>(per_unit) -
+                     static_cast<int64_t>(num_kv_heads) * static_cast<int64_t>(sizeof(WaveLds))) /
+                    static_cast<int64_t>(sizeof(int32_t)) / kStep * kStep;
+  return static_cast<int>(w < kMaxChunkTokens ? w : kMaxChunkTokens);
+}
+
 // A plan whose units number about units_target (0: one unit per resident
-// workgroup of the whole device).
+// workgroup of the whole device) and hold at most max_unit tokens.
 static int decode_plan_for(const int32_t* kv_indptr_host, int batch_size, int num_qo_heads,
-                           int num_kv_heads, int head_dim, int64_t units_target,
+                           int num_kv_heads, int head_dim, int64_t units_target, int max_unit,
                            sgl_decode_plan_t* plan) {
   if (!plan || !kv_indptr_host || batch_size < 0 || num_qo_heads <= 0 || num_kv_heads <= 0)
     return SGL_ERR_INVALID_ARG;
@@ -659,7 +672,7 @@ static int decode_plan_for(const int32_t* kv_indptr_host, int batch_size, int nu
   auto round16 = [](int64_t x) { return (x + kStep - 1) / kStep * kStep; };
   int64_t W = round16((total + units_target - 1) / units_target);
   if (W < kMinUnit) W = kMinUnit;
-  if (W > kMaxChunkTokens) W = kMaxChunkTokens;
+  if (W > max_unit) W = max_unit;
   const int64_t units = total > 0 ? (total + W - 1) / W : 1;
   if (units > 0x7fffffff / 2) return SGL_ERR_UNSUPPORTED;
   // The device picks w = clamp(round16(ceil(total / units)), W_min, W) <= W.
@@ -686,7 +699,8 @@ static int decode_plan_for(const int32_t* kv_indptr_host, int batch_size, int nu
 
 extern "C" int sgl_decode_plan(const int32_t* kv_indptr_host, int batch_size, int num_qo_heads,
                                int num_kv_heads, int head_dim, sgl_decode_plan_t* plan) {
-  return decode_plan_for(kv_indptr_host, batch_size, num_qo_heads, num_kv_heads, head_dim, 0, plan);
+  return decode_plan_for(kv_indptr_host, batch_size, num_qo_heads, num_kv_heads, head_dim, 0,
+                         kMaxChunkTokens, plan);
 }
 
 extern "C" int sgl_decode_plan_cus(const int32_t* kv_indptr_host, int batch_size,
@@ -695,7 +709,8 @@ extern "C" int sgl_decode_plan_cus(const int32_t* kv_indptr_host, int batch_size
   if (num_kv_heads <= 0 || num_kv_heads > 8 || 8 % num_kv_heads != 0) return SGL_ERR_UNSUPPORTED;
   if (decode_cus <= 0) return SGL_ERR_INVALID_ARG;
   return decode_plan_for(kv_indptr_host, batch_size, num_qo_heads, num_kv_heads, head_dim,
-                         static_cast<int64_t>(decode_cus) * (8 / num_kv_heads), plan);
+                         static_cast<int64_t>(decode_cus) * (8 / num_kv_heads),
+                         mixed_max_unit(num_kv_heads), plan);
 }
 
 // Per-CU rates behind the split, measured on MI355X at config 5's shapes
@@ -866,7 +881,10 @@ extern "C" int sgl_paged_mixed(const sgl_decode_plan_t* plan, const void* q,
   if (!plan || dec_batch < 0 || pre_batch < 0 || pre_max_qo_len < 0) return SGL_ERR_INVALID_ARG;
   if (num_kv_heads <= 0 || num_kv_heads > 8 || 8 % num_kv_heads != 0) return SGL_ERR_UNSUPPORTED;
   const bool has_pre = pre_batch > 0 && pre_max_qo_len > 0;
-  if (dec_batch == 0 || !has_pre) {
+  // A plan with longer units than the fused launch's LDS holds (one from
+  // sgl_decode_plan at 1 or 2 kv heads) runs as the two entry points.
+  const bool fits = plan->kv_chunk_size > 0 && plan->kv_chunk_size <= mixed_max_unit(num_kv_heads);
+  if (dec_batch == 0 || !has_pre || !fits) {
     int st = SGL_OK;
     if (dec_batch > 0)
       st = sgl_paged_decode(plan, q, q_stride_token, q_stride_head, k_cache, v_cache,
@@ -908,6 +926,7 @@ extern "C" int sgl_paged_mixed(const sgl_decode_plan_t* plan, const void* q,
   size_t lds = static_cast<size_t>(upw) * unit_lds_bytes(num_kv_heads, plan->kv_chunk_size);
   if (lds < static_cast<size_t>(pf::prefill_lds_bytes<8, 1>()))
     lds = pf::prefill_lds_bytes<8, 1>();
+  if (lds > kMixedLds) return SGL_ERR_INVALID_ARG;  // excluded by `fits`
   const dim3 grid(static_cast<uint32_t>(dec_blocks + items));
   const hipStream_t s = static_cast<hipStream_t>(stream);
   const int db = static_cast<int>(dec_blocks);

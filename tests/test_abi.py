@@ -169,10 +169,15 @@ def test_decode_plan_cus_host():
     rng = np.random.default_rng(3)
     kv = rng.integers(1024, 32769, 64)
     ip = np.concatenate([[0], np.cumsum(kv)])
-    for cus, hq, hkv in ((160, 32, 4), (64, 32, 8), (8, 16, 1)):
+    for cus, hq, hkv in ((160, 32, 4), (64, 32, 8), (8, 16, 1), (8, 16, 2), (32, 8, 1)):
         plan = capi.decode_plan_cus(ip, hq, hkv, 128, cus)
-        # units of at most 8192 tokens (the LDS-staged slot indices) bound the count from below
-        target = max(cus * (8 // hkv), -(-int(kv.sum()) // 8192))
+        # The fused launch stages each unit's slot indices (4 bytes a token)
+        # and each kv head's Q rows (16 x 136 bf16) in LDS for 8 / hkv units
+        # per workgroup: all of it within the CU's 160 KiB.
+        assert (8 // hkv) * (hkv * 16 * 136 * 2 + 4 * plan.kv_chunk_size) <= 160 * 1024
+        # The longest unit that fits bounds the count from below.
+        w_max = min(8192, ((160 * 1024 // (8 // hkv) - hkv * 4352) // 4) // 16 * 16)
+        target = max(cus * (8 // hkv), -(-int(kv.sum()) // w_max))
         assert target * 0.9 <= plan.num_units <= target
         assert plan.max_total_tokens == plan.num_units * plan.kv_chunk_size >= int(kv.sum())
         assert capi.decode_plan_check(plan, ip) == 0

@@ -620,6 +620,26 @@ def test_paged_mixed_one_launch(oracle, dev, hq, hkv, decode_cus):
     assert capi.decode_status(ws) == 0
 
 
+@pytest.mark.parametrize("hq,hkv", [(8, 1), (16, 2)])
+def test_paged_mixed_long_units(oracle, dev, hq, hkv):
+    """Long decode rows on few CUs at 1 and 2 kv heads: 8 or 4 units share a
+    fused workgroup's LDS, so the plan caps the unit length (4032 and 8064
+    tokens) rather than exceed it; results against the oracle."""
+    note(f"paged mixed long units hq={hq} hkv={hkv}")
+    rng = np.random.default_rng(35 + hkv)
+    kv_dec = [int(x) for x in rng.integers(30000, 45000, 7)]
+    cached = [x - 1 for x in kv_dec] + [200]
+    b = wl.make_paged_batch(rng, cached, kv_dec + [500], page_size=16)
+    plan = capi.decode_plan_cus(np.concatenate([[0], np.cumsum(kv_dec)]).astype(np.int32),
+                                hq, hkv, 128, 8)
+    assert plan.kv_chunk_size <= (4032 if hkv == 1 else 8064)
+    q, kc, vc, o, ws = _run_mixed(dev, b, hq, hkv, 36, 8)
+    ref = oracle.prefill(u16(q).copy(), u16(kc), u16(vc), b.indices, b.qo_indptr, b.kv_indptr,
+                         1 / math.sqrt(128))
+    assert_attn_close(o.float().cpu().numpy(), ref, what=f"mixed long units {hq}/{hkv}")
+    assert capi.decode_status(ws) == 0
+
+
 def test_prefill_mixed_decode_rows(oracle, dev):
     """Config-5 shape of batch (qo 1 rows next to a 2048 chunk), scaled down."""
     note("prefill with qo=1 rows beside a long chunk")
