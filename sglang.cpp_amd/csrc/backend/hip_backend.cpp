@@ -343,12 +343,6 @@ torch::Tensor HipAttnBackend::attend(const torch::Tensor& q_in, int layer_id, Ba
   auto vc = kv_cache_->v_cache(layer_id).view({-1, num_kv_heads_, head_dim_});
   void* stream = current_stream(kv_cache_->device());
   const float sm_scale = 1.0f / std::sqrt(static_cast<float>(head_dim_));
-  // A mixed batch runs the prefill rows on a side stream next to the decode
-  // rows (they write disjoint rows of o): the MFMA-bound prefill and the
-  // HBM-bound decode then share the GPU. Fork and join are event edges, so
-  // this also holds inside a captured graph. The persistent decode launch
-  // goes first so its workgroups are resident before the prefill tiles take
-  // the remaining slots (the other order measured no gain).
   if (meta->fused) {
     // Decode units and prefill items in one launch (decode on dec_cus CUs).
     torch::Tensor& ws = !meta->use_capture_buffers ? workspace(meta->dec_plan.workspace_bytes)
@@ -375,6 +369,12 @@ torch::Tensor HipAttnBackend::attend(const torch::Tensor& q_in, int layer_id, Ba
               "sgl_paged_mixed");
     return o.view({-1, num_qo_heads_ * head_dim_});
   }
+  // Otherwise a mixed batch runs the prefill rows on a side stream next to
+  // the decode rows (they write disjoint rows of o): the MFMA-bound prefill
+  // and the HBM-bound decode then share the GPU. Fork and join are event
+  // edges, so this also holds inside a captured graph. The persistent decode
+  // launch goes first so its workgroups are resident before the prefill
+  // tiles take the remaining slots (the other order measured no gain).
   const bool fork = overlap_mixed_ && meta->num_decode > 0 && meta->num_prefill > 0;
   void* pre_stream = stream;
   if (fork) {
@@ -441,6 +441,10 @@ void HipAttnBackend::init_capture_graph(int max_seq_len, const std::vector<int>&
   auto cap = std::make_unique<CaptureState>();
   cap->max_seq_len = max_seq_len;
   cap->max_bs = *std::max_element(bs_list.begin(), bs_list.end());
+  TORCH_CHECK(*std::min_element(bs_list.begin(), bs_list.end()) > 0,
+              "batch sizes must be positive");
+  TORCH_CHECK(static_cast<int64_t>(cap->max_bs) * max_seq_len <= 0x7fffffff,
+              "max batch size x max_seq_len must fit int32 token offsets");
   const auto dev = kI32.device(kv_cache_->device());
   cap->kv_indptr = torch::zeros({cap->max_bs + 1}, dev);
   cap->indices = torch::zeros({static_cast<int64_t>(cap->max_bs) * max_seq_len}, dev);
@@ -543,6 +547,9 @@ void HipAttnBackend::init_mixed_capture_graph(int max_seq_len, int max_decode_ro
                   max_prefill_qo > 1 && max_prefill_qo <= max_seq_len,
               "init_mixed_capture_graph: need max_seq_len > 0, max_decode_rows >= 0, "
               "max_prefill_reqs > 0 and 1 < max_prefill_qo <= max_seq_len");
+  TORCH_CHECK(static_cast<int64_t>(max_decode_rows) * max_seq_len <= 0x7fffffff &&
+                  static_cast<int64_t>(max_prefill_reqs) * max_seq_len <= 0x7fffffff,
+              "init_mixed_capture_graph: rows x max_seq_len must fit int32 token offsets");
   auto m = std::make_unique<MixedCapture>();
   m->max_seq_len = max_seq_len;
   m->max_dec = max_decode_rows;
@@ -558,7 +565,11 @@ void HipAttnBackend::init_mixed_capture_graph(int max_seq_len, int max_decode_ro
   m->pre_kv_indptr = torch::zeros({max_prefill_reqs + 1}, dev);
   m->pre_q_start = torch::zeros({max_prefill_reqs}, dev);
   m->pre_indices = torch::zeros({max_prefill_reqs * L}, dev);
-  // Workspace for the largest worst-case decode plan of any row count.
+  // Workspace for the largest worst-case decode plan of any row count: the
+  // plan of a two-launch step, or of a one-launch step, whose units are at
+  // most max(decode CUs x 8 / hkv, tokens / the fused launch's unit cap) --
+  // largest at the whole device's CUs.
+  const bool fusable = num_kv_heads_ <= 8 && 8 % num_kv_heads_ == 0;
   int64_t ws_bytes = 256;
   std::vector<int32_t> worst(1, 0);
   for (int n = 1; n <= max_decode_rows; ++n) {
@@ -567,6 +578,12 @@ void HipAttnBackend::init_mixed_capture_graph(int max_seq_len, int max_decode_ro
     check_sgl(sgl_decode_plan(worst.data(), n, num_qo_heads_, num_kv_heads_, head_dim_, &plan),
               "sgl_decode_plan");
     ws_bytes = std::max<int64_t>(ws_bytes, plan.workspace_bytes);
+    if (fusable) {
+      check_sgl(sgl_decode_plan_cus(worst.data(), n, num_qo_heads_, num_kv_heads_, head_dim_,
+                                    device_cus_, &plan),
+                "sgl_decode_plan_cus");
+      ws_bytes = std::max<int64_t>(ws_bytes, plan.workspace_bytes);
+    }
   }
   m->workspace = torch::empty({ws_bytes}, torch::TensorOptions().dtype(torch::kUInt8).device(
                                               kv_cache_->device()));
