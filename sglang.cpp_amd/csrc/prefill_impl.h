@@ -57,6 +57,11 @@ __device__ __forceinline__ u32x4_t lds_read_b128(uint32_t addr) {
   return v;
 }
 
+template <int OFF>
+__device__ __forceinline__ void lds_write_b128(uint32_t addr, const u32x4_t& v) {
+  asm volatile("ds_write_b128 %0, %1 offset:%2" : : "v"(addr), "v"(v), "i"(OFF));
+}
+
 // ds_read_b64_tr_b16: within each group of 16 lanes, lane i receives element
 // i % 4 of the 4-element (8-byte) pieces addressed by lanes 4 e + i / 4,
 // e < 4 -- a 4 x 16 -> 16 x 4 transpose of 16-bit data.
@@ -135,6 +140,14 @@ __device__ __forceinline__ void issue_half(const char* const (&lane_base)[2], ui
 // Waits until this wave's LDS gathers have landed (vmcnt(0); expcnt and
 // lgkmcnt left at their maxima).
 __device__ __forceinline__ void wait_gathers() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// Waits until at most N of this wave's vector memory operations are
+// outstanding (they complete in issue order, so every older one is done).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt(((N >> 4) << 14) | 0x0F70 | (N & 15));
+}
 
 struct RowState {
   f32x16_t acc[4];  // O^T: acc[db][4 g + i] holds d = 32 db + 8 g + 4 hl + i
@@ -316,9 +329,16 @@ __device__ __forceinline__ void pv_steps(const LaneAddr& la, const bf16x8_t (&po
 // The work of item `lin` of `n_items` (the kernel's block index and grid
 // size, or an offset range of a fused launch), with the workgroup's LDS at
 // lds_raw (prefill_lds_bytes<W, KS>() bytes, 16-byte aligned).
+// LDS of one group's tiles: two K/V buffers, or with KS = 2 a third K
+// buffer after them (the short-share schedule below).
+template <int KS>
+constexpr int group_lds_bytes() {
+  return KS == 2 ? 2 * kTileBytes + kTileBytes / 2 : 2 * kTileBytes;
+}
+
 template <int W, int KS>
 constexpr int prefill_lds_bytes() {
-  constexpr int ring = KS * 2 * kTileBytes;
+  constexpr int ring = KS * group_lds_bytes<KS>();
   constexpr int xch = (KS - 1) * 66 * 64 * (W / KS) * 4;
   return ring > xch ? ring : xch;
 }
@@ -414,7 +434,7 @@ __device__ __forceinline__ void prefill_item(PrefillArgs a, char* lds_raw, int l
   // Two K/V buffers per group; the loop is unrolled by two so each read
   // names its buffer by a compile-time offset. With KS > 1 the same memory
   // then carries the other groups' softmax states to group 0.
-  Tile* tiles = reinterpret_cast<Tile*>(lds_raw) + 2 * split;
+  Tile* tiles = reinterpret_cast<Tile*>(lds_raw + split * group_lds_bytes<KS>());
   // This group's kv tiles [tb, te) and the steps every group runs (equal,
   // so the workgroup-wide barriers match).
   const int share = (ntiles + KS - 1) / KS;
@@ -465,83 +485,197 @@ __device__ __forceinline__ void prefill_item(PrefillArgs a, char* lds_raw, int l
   rs.m = -INFINITY;
   rs.l = 0.f;
 
-  // Software pipeline over 64-token tiles. Iteration t computes S(t + 1)
-  // on the matrix cores while the vector ALUs turn S(t) into P(t), then
-  // O += P(t) V(t). K tiles are therefore gathered one tile ahead of V
-  // tiles: during iteration t the gathers of K(t + 2) and V(t + 1) are in
-  // flight. Tile j's K and V use buffer j % 2. Slot indices of tile t + 2
-  // serve K(t + 2) now and V(t + 2) in the next iteration.
-  // The slots of tiles 0 and 1 are waited for together before any gather
-  // is issued (a gather between them would make the wait for the later
-  // slots wait for the gather too: loads complete in order).
-  int32_t sl_k[16 / GW], sl_v[16 / GW];
-  load_slots<GW>(idx, tb * kBN, kv_len, tid, sl_k);
-  load_slots<GW>(idx, (tb + 1) * kBN, kv_len, tid, sl_v);
-  wait_gathers();
-  if (tb < te) {
-    issue_half<GW>(klane, ss_bytes, sl_k, tiles[0].k, wave);
-    issue_half<GW>(vlane, ss_bytes, sl_k, tiles[0].v, wave);
-  }
-  if (tb + 1 < te) issue_half<GW>(klane, ss_bytes, sl_v, tiles[1].k, wave);
-  load_slots<GW>(idx, (tb + 2) * kBN, kv_len, tid, sl_k);
-  // Q^T operand: q[qtok][qhead][16 s + 8 hl .. +8], s < 8. Loaded after
-  // the first gathers are issued: loads complete in order, so Q issued
-  // earlier would delay the slot indices the gathers wait for.
-  bf16x8_t qop[8];
-  {
-    const uint16_t* qp =
-        a.q + static_cast<int64_t>(qo_beg + qtok) * a.q_st + static_cast<int64_t>(qhead) * a.q_sh;
+  // Short shares (KS = 2, at most three kv tiles per group; launches that
+  // are latency-bound, not bandwidth-bound): every tile's gathers are issued
+  // at once -- K(0), V(0), K(1), V(1), K(2) into LDS (the group's 80 KiB) and
+  // V(2) into registers, written to V(0)'s buffer once P(0) V(0) is done --
+  // so the group waits for one memory round trip instead of one per tile.
+  // Every wave issues the same operations whatever its group's tile count
+  // (tiles past the share gather the clamped last token), so the vmcnt
+  // counts below are exact: 8 gathers per tile half (16 / GW), 8 Q loads.
+  auto short_share = [&](auto NSc) {
+    constexpr int NS = decltype(NSc)::value;
+    static_assert(GW == 2 && NS >= 1 && NS <= 3, "short shares: 2-wave groups, <= 3 tiles");
+    constexpr int kOps = 16 / GW;
+    int32_t sl[NS][kOps];
+    static_for<0, NS>([&](auto I) {
+      constexpr int i = decltype(I)::value;
+      load_slots<GW>(idx, (tb + i) * kBN, kv_len, tid, sl[i]);
+    });
+    wait_gathers();
+    issue_half<GW>(klane, ss_bytes, sl[0], tiles[0].k, wave);
+    issue_half<GW>(vlane, ss_bytes, sl[0], tiles[0].v, wave);
+    if constexpr (NS > 1) issue_half<GW>(klane, ss_bytes, sl[1], tiles[1].k, wave);
+    // Q^T operand (rows past the item read row 0 and are zeroed: the loads
+    // are unconditional so every wave issues the same count).
+    bf16x8_t qop[8];
+    {
+      const uint16_t* qp = a.q + static_cast<int64_t>(qo_beg + qtok) * a.q_st +
+                           static_cast<int64_t>(qhead) * a.q_sh;
+      u32x4_t qv[8];
 #pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      u32x4_t v = row_ok ? ldg128(qp + 16 * s + 8 * hl) : u32x4_t{0, 0, 0, 0};
-      qop[s] = as_bf16x8(v);
+      for (int s = 0; s < 8; ++s) qv[s] = ldg128(qp + 16 * s + 8 * hl);
+#pragma unroll
+      for (int s = 0; s < 8; ++s) qop[s] = as_bf16x8(row_ok ? qv[s] : u32x4_t{0, 0, 0, 0});
+    }
+    if constexpr (NS > 1) issue_half<GW>(vlane, ss_bytes, sl[1], tiles[1].v, wave);
+    if constexpr (NS > 2) issue_half<GW>(klane, ss_bytes, sl[2], tiles[2].k, wave);
+    // V(2) into registers, lane for lane what issue_half would gather.
+    u32x4_t v2[NS > 2 ? kOps : 1];
+    if constexpr (NS > 2) {
+#pragma unroll
+      for (int u = 0; u < kOps; ++u)
+        v2[u] = ldg128(vlane[u & 1] + static_cast<uint64_t>(static_cast<uint32_t>(sl[2][u])) *
+                                          ss_bytes);
+    }
+    // K(0), V(0), K(1) and Q landed (younger: V(1), K(2), V(2)).
+    wait_vm<(NS > 1 ? kOps : 0) + (NS > 2 ? 2 * kOps : 0)>();
+    __builtin_amdgcn_s_barrier();
+    LaneAddr la2 = la;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) la2.k[k] += 2 * kTileBytes;
+    f32x16_t s_a[2], s_b[2];
+    bf16x8_t pop[4];
+    qk_tile<0>(la, qop, s_a);
+    // One step: P(t) from s_cur, S(t + 1) into s_next from K buffer KB
+    // (none on the last tile), O += P(t) V(t) from V buffer VB.
+    auto run = [&](auto Ic, auto KBc, auto VBc, f32x16_t(&s_cur)[2], f32x16_t(&s_next)[2]) {
+      constexpr int i = decltype(Ic)::value;
+      constexpr int kb = decltype(KBc)::value;
+      constexpr int vb = decltype(VBc)::value;
+      if (tb + i >= te) return;
+      u32x2_t vr[4][8];
+      if constexpr (i + 1 < NS) {
+        // K buffer 2 lies past the 16-bit LDS offset range from buffer 0's
+        // addresses: its reads use addresses rebased to it.
+        constexpr int kbo = kb == 2 ? 0 : kb;
+        const LaneAddr& lk = kb == 2 ? la2 : la;
+        u32x4_t kbuf[16];
+        qk_tile_prefetch<kbo>(lk, kbuf);
+        softmax_head(a, s_cur, rs, (tb + i) * kBN, first_masked, allow, kv_len, hl);
+        lgkm_wait<0>(kbuf[kKAhead - 1]);
+        qk_tile_run<kbo>(lk, qop, s_next, kbuf);
+      } else {
+        softmax_head(a, s_cur, rs, (tb + i) * kBN, first_masked, allow, kv_len, hl);
+      }
+      softmax_exp_half<0>(a, s_cur, rs, pop);
+      pv_reads<vb, 0>(la, vr[0]);
+      pv_steps<vb, 0, 2>(la, pop, vr, rs);
+      softmax_exp_half<1>(a, s_cur, rs, pop);
+      pv_steps<vb, 2, 4>(la, pop, vr, rs);
+    };
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    run(I0{}, I1{}, I0{}, s_a, s_b);
+    if constexpr (NS > 1) {
+      // K(2) and V(1) landed (younger: V(2)); every wave is done with V(0).
+      wait_vm<(NS > 2 ? kOps : 0)>();
+      __builtin_amdgcn_s_barrier();
+      if constexpr (NS > 2) {
+        const uint32_t vdst = lds_addr(tiles[0].v) + (4 * wave) * kD * 2 + lane * 16;
+        static_for<0, kOps>([&](auto U) {
+          constexpr int u = decltype(U)::value;
+          lds_write_b128<4 * GW * u * kD * 2>(vdst, v2[u]);
+        });
+      }
+      run(I1{}, I2{}, I1{}, s_b, s_a);
+    }
+    if constexpr (NS > 2) {
+      asm volatile("s_waitcnt lgkmcnt(0)");  // V(2) written by this wave
+      __builtin_amdgcn_s_barrier();
+      run(I2{}, I0{}, I0{}, s_a, s_b);
+    }
+  };
+  bool short_done = false;
+  if constexpr (KS == 2) {
+    if (share <= 3) {
+      short_done = true;
+      if (share == 1) short_share(std::integral_constant<int, 1>{});
+      else if (share == 2) short_share(std::integral_constant<int, 2>{});
+      else short_share(std::integral_constant<int, 3>{});
     }
   }
-  wait_gathers();
-  __syncthreads();
-
-  // Scores of the current and next tile; the two arrays swap roles every
-  // step (the loop is unrolled by two), so no register copies move them.
-  f32x16_t s_a[2], s_b[2];
-  bf16x8_t pop[4];
-  qk_tile<0>(la, qop, s_a);
-  __syncthreads();  // every wave has read K(0) before K(2) overwrites it
-
-  auto step = [&](auto B, int t, f32x16_t(&s_cur)[2], f32x16_t(&s_next)[2]) {
-    constexpr int buf = decltype(B)::value;  // (t - tb) % 2
-    if (t + 2 < te) issue_half<GW>(klane, ss_bytes, sl_k, tiles[buf].k, wave);
-    if (t + 1 < te) issue_half<GW>(vlane, ss_bytes, sl_v, tiles[buf ^ 1].v, wave);
-#pragma unroll
-    for (int u = 0; u < 16 / GW; ++u) sl_v[u] = sl_k[u];
-    load_slots<GW>(idx, (t + 3) * kBN, kv_len, tid, sl_k);
-    if (t < te && (!kPair || t < my_tiles)) {
-      // S(t + 1)'s first K operand reads go out before the mask / max of
-      // S(t), which hides their LDS latency (K(t + 1) landed and became
-      // visible at the previous step's barrier). The full wait after the
-      // VALU work keeps the counted waits exact whatever the compiler
-      // placed in between.
-      u32x4_t kb[16];
-      qk_tile_prefetch<buf ^ 1>(la, kb);
-      softmax_head(a, s_cur, rs, t * kBN, first_masked, allow, kv_len, hl);
-      lgkm_wait<0>(kb[kKAhead - 1]);
-      // The VALU work of P(t) is split so each half runs beside MFMAs: the
-      // first half beside S(t + 1), the second beside the first half of
-      // O += P(t) V(t).
-      u32x2_t vr[4][8];
-      qk_tile_run<buf ^ 1>(la, qop, s_next, kb);  // S(t + 1); unused after the last tile
-      softmax_exp_half<0>(a, s_cur, rs, pop);
-      pv_reads<buf, 0>(la, vr[0]);
-      pv_steps<buf, 0, 2>(la, pop, vr, rs);
-      softmax_exp_half<1>(a, s_cur, rs, pop);
-      pv_steps<buf, 2, 4>(la, pop, vr, rs);
+  if (!short_done) {
+    // Software pipeline over 64-token tiles. Iteration t computes S(t + 1)
+    // on the matrix cores while the vector ALUs turn S(t) into P(t), then
+    // O += P(t) V(t). K tiles are therefore gathered one tile ahead of V
+    // tiles: during iteration t the gathers of K(t + 2) and V(t + 1) are in
+    // flight. Tile j's K and V use buffer j % 2. Slot indices of tile t + 2
+    // serve K(t + 2) now and V(t + 2) in the next iteration.
+    // The slots of tiles 0 and 1 are waited for together before any gather
+    // is issued (a gather between them would make the wait for the later
+    // slots wait for the gather too: loads complete in order).
+    int32_t sl_k[16 / GW], sl_v[16 / GW];
+    load_slots<GW>(idx, tb * kBN, kv_len, tid, sl_k);
+    load_slots<GW>(idx, (tb + 1) * kBN, kv_len, tid, sl_v);
+    wait_gathers();
+    if (tb < te) {
+      issue_half<GW>(klane, ss_bytes, sl_k, tiles[0].k, wave);
+      issue_half<GW>(vlane, ss_bytes, sl_k, tiles[0].v, wave);
+    }
+    if (tb + 1 < te) issue_half<GW>(klane, ss_bytes, sl_v, tiles[1].k, wave);
+    load_slots<GW>(idx, (tb + 2) * kBN, kv_len, tid, sl_k);
+    // Q^T operand: q[qtok][qhead][16 s + 8 hl .. +8], s < 8. Loaded after
+    // the first gathers are issued: loads complete in order, so Q issued
+    // earlier would delay the slot indices the gathers wait for.
+    bf16x8_t qop[8];
+    {
+      const uint16_t* qp =
+          a.q + static_cast<int64_t>(qo_beg + qtok) * a.q_st + static_cast<int64_t>(qhead) * a.q_sh;
+  #pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        u32x4_t v = row_ok ? ldg128(qp + 16 * s + 8 * hl) : u32x4_t{0, 0, 0, 0};
+        qop[s] = as_bf16x8(v);
+      }
     }
     wait_gathers();
     __syncthreads();
-  };
-  for (int i = 0; i < nsteps; i += 2) {
-    step(std::integral_constant<int, 0>{}, tb + i, s_a, s_b);
-    if (i + 1 >= nsteps) break;
-    step(std::integral_constant<int, 1>{}, tb + i + 1, s_b, s_a);
+
+    // Scores of the current and next tile; the two arrays swap roles every
+    // step (the loop is unrolled by two), so no register copies move them.
+    f32x16_t s_a[2], s_b[2];
+    bf16x8_t pop[4];
+    qk_tile<0>(la, qop, s_a);
+    __syncthreads();  // every wave has read K(0) before K(2) overwrites it
+
+    auto step = [&](auto B, int t, f32x16_t(&s_cur)[2], f32x16_t(&s_next)[2]) {
+      constexpr int buf = decltype(B)::value;  // (t - tb) % 2
+      if (t + 2 < te) issue_half<GW>(klane, ss_bytes, sl_k, tiles[buf].k, wave);
+      if (t + 1 < te) issue_half<GW>(vlane, ss_bytes, sl_v, tiles[buf ^ 1].v, wave);
+  #pragma unroll
+      for (int u = 0; u < 16 / GW; ++u) sl_v[u] = sl_k[u];
+      load_slots<GW>(idx, (t + 3) * kBN, kv_len, tid, sl_k);
+      if (t < te && (!kPair || t < my_tiles)) {
+        // S(t + 1)'s first K operand reads go out before the mask / max of
+        // S(t), which hides their LDS latency (K(t + 1) landed and became
+        // visible at the previous step's barrier). The full wait after the
+        // VALU work keeps the counted waits exact whatever the compiler
+        // placed in between.
+        u32x4_t kb[16];
+        qk_tile_prefetch<buf ^ 1>(la, kb);
+        softmax_head(a, s_cur, rs, t * kBN, first_masked, allow, kv_len, hl);
+        lgkm_wait<0>(kb[kKAhead - 1]);
+        // The VALU work of P(t) is split so each half runs beside MFMAs: the
+        // first half beside S(t + 1), the second beside the first half of
+        // O += P(t) V(t).
+        u32x2_t vr[4][8];
+        qk_tile_run<buf ^ 1>(la, qop, s_next, kb);  // S(t + 1); unused after the last tile
+        softmax_exp_half<0>(a, s_cur, rs, pop);
+        pv_reads<buf, 0>(la, vr[0]);
+        pv_steps<buf, 0, 2>(la, pop, vr, rs);
+        softmax_exp_half<1>(a, s_cur, rs, pop);
+        pv_steps<buf, 2, 4>(la, pop, vr, rs);
+      }
+      wait_gathers();
+      __syncthreads();
+    };
+    for (int i = 0; i < nsteps; i += 2) {
+      step(std::integral_constant<int, 0>{}, tb + i, s_a, s_b);
+      if (i + 1 >= nsteps) break;
+      step(std::integral_constant<int, 1>{}, tb + i + 1, s_b, s_a);
+    }
+
   }
 
   if constexpr (KS > 1) {

@@ -559,6 +559,21 @@ def test_prefill_ragged(oracle, dev, hq, hkv):
     check_prefill(oracle, dev, b, hq, hkv, 22, f"prefill ragged {hq}/{hkv}")
 
 
+@pytest.mark.parametrize("hq,hkv,qo_last", [(16, 8, 100), (32, 4, 32)])
+def test_prefill_split_kv_short_shares(oracle, dev, hq, hkv, qo_last):
+    """Launches that leave CUs idle (at most one 64-row item per CU) split
+    each item's kv tiles between two 2-wave groups. Requests of 1, 3, 5, 6
+    and 10 kv tiles give the groups 1/0, 2/1, 3/2, 3/3 tiles (every tile's
+    gathers in flight at once, the third V tile staged in registers) and 5/5
+    (the double-buffered ring); the last request spans several items."""
+    note(f"prefill split-kv short shares hq={hq} hkv={hkv}")
+    rng = np.random.default_rng(37)
+    cached = [0, 100, 250, 352, 600, 40]
+    dev_lens = [32, 132, 282, 384, 632, 40 + qo_last]
+    b = wl.make_paged_batch(rng, cached, dev_lens, page_size=16)
+    check_prefill(oracle, dev, b, hq, hkv, 38, f"split-kv short shares {hq}/{hkv}")
+
+
 def test_prefill_chunked_extend_and_empty_extend(oracle, dev):
     """Chunked prefill: a second chunk on its first chunk's cache; extend 0 -> qo 1."""
     note("prefill chunked extend / zero extend")
