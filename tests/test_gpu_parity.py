@@ -635,6 +635,34 @@ def test_paged_mixed_one_launch(oracle, dev, hq, hkv, decode_cus):
     assert capi.decode_status(ws) == 0
 
 
+@pytest.mark.parametrize("seed", range(4))
+def test_paged_mixed_random(oracle, dev, seed):
+    """Seeded random mixed batches through sgl_paged_mixed: head layout,
+    decode rows (some empty), one to three prefill requests with or without
+    a cached prefix, interleaved in random order, and the decode CU share;
+    every row against the oracle."""
+    rng = np.random.default_rng(500 + seed)
+    hkv = int(rng.choice([1, 2, 4, 8]))
+    hq = hkv * int(rng.choice([1, 2, 4, 8]))
+    n_dec, n_pre = int(rng.integers(1, 24)), int(rng.integers(1, 4))
+    kv_dec = [int(x) for x in rng.integers(0, 5000, n_dec)]
+    kv_dec[0] = max(kv_dec[0], 1)
+    pre_prefix = [int(x) for x in rng.integers(0, 600, n_pre)]
+    pre_qo = [int(x) for x in rng.integers(2, 400, n_pre)]
+    reqs = [(max(k - 1, 0), k) for k in kv_dec] + [(p, p + q) for p, q in zip(pre_prefix, pre_qo)]
+    order = rng.permutation(len(reqs))
+    cached = [reqs[i][0] for i in order]
+    dev_lens = [reqs[i][1] for i in order]
+    cus = int(rng.integers(1, 32)) * 8
+    note(f"paged mixed random seed={seed} hq={hq} hkv={hkv} dec={n_dec} pre={n_pre} cus={cus}")
+    b = wl.make_paged_batch(rng, cached, dev_lens, page_size=16)
+    q, kc, vc, o, ws = _run_mixed(dev, b, hq, hkv, 40 + seed, cus)
+    ref = oracle.prefill(u16(q).copy(), u16(kc), u16(vc), b.indices, b.qo_indptr, b.kv_indptr,
+                         1 / math.sqrt(128))
+    assert_attn_close(o.float().cpu().numpy(), ref, what=f"mixed random seed {seed}")
+    assert capi.decode_status(ws) == 0
+
+
 @pytest.mark.parametrize("hq,hkv", [(8, 1), (16, 2)])
 def test_paged_mixed_long_units(oracle, dev, hq, hkv):
     """Long decode rows on few CUs at 1 and 2 kv heads: 8 or 4 units share a
