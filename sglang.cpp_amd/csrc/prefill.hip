@@ -29,8 +29,10 @@ namespace sgl {
 namespace pf {
 namespace {
 
+// Two workgroups per CU at 4 waves, one at 8; the split-kv variant (KS = 2)
+// holds the whole LDS, so one.
 template <int W, bool kPair, int KS>
-__global__ void __launch_bounds__(64 * W, 8 / W) paged_prefill_kernel(PrefillArgs a) {
+__global__ void __launch_bounds__(64 * W, KS == 2 ? 1 : 8 / W) paged_prefill_kernel(PrefillArgs a) {
   __shared__ __attribute__((aligned(16))) char lds_raw[prefill_lds_bytes<W, KS>()];
   prefill_item<W, kPair, KS>(a, lds_raw, blockIdx.x, gridDim.x);
 }
