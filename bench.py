@@ -103,6 +103,45 @@ class Timer:
         return wall_ms, ev_ms
 
 
+    def run_graph(self, fn, steps, warmup):
+        """The same K steps captured as one hipGraph of K back-to-back calls
+        and replayed once (after warm-up replays), so that for calls shorter
+        than the host's per-call launch cost (a Python ctypes call and a
+        kernel launch) the events time the kernels and not the gaps between
+        them. Returns (wall ms, event ms) per step."""
+        torch = self.torch
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            fn()
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(steps):
+                fn()
+        w0 = time.perf_counter()
+        graph.replay()
+        torch.cuda.synchronize()
+        while time.perf_counter() - w0 < self.min_warm_s:
+            graph.replay()
+            torch.cuda.synchronize()
+        stream = torch.cuda.current_stream()
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        start.record(stream)
+        graph.replay()
+        end.record(stream)
+        torch.cuda.synchronize()
+        wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+        ev_ms = start.elapsed_time(end) / steps
+        del graph
+        return wall_ms, ev_ms
+
+
 def load_traffic(key):
     try:
         return json.loads(PROFILE_TRAFFIC.read_text()).get(key)
@@ -505,11 +544,18 @@ def run_workload(name, torch, capi, wl, dev, steps, warmup, cfg5_layers, min_war
                "kernel_ms": ev, "bytes": nbytes, "GB/s": nbytes / (wall * 1e-3) / 1e9,
                "roofline": roofline_hbm(nbytes, ev, f"{kname}_qwen3_8b")}
         return None, rec
+    # Configurations 1 and 2 are single calls of about 10 us, less than the
+    # host's per-call launch cost from Python: they are timed as a captured
+    # graph of the K calls (the eager figures are kept beside them).
     if name in ("cfg1", "cfg4"):
         w = wl.cfg1_decode_small() if name == "cfg1" else wl.cfg4_decode_large()
         step, nbytes, flops, _ = setup_decode(torch, capi, wl, w, dev)
         wall, ev = timer.run(step, steps, warmup)
-        rec = {"workload": w.name, "ms_per_step": wall, "kernel_ms": ev, "bytes": nbytes,
+        eager = {}
+        if name == "cfg1":
+            eager = {"eager_ms_per_step": wall, "eager_kernel_ms": ev, "timing": "graph"}
+            wall, ev = timer.run_graph(step, steps, warmup)
+        rec = {"workload": w.name, "ms_per_step": wall, "kernel_ms": ev, **eager, "bytes": nbytes,
                "GB/s": nbytes / (wall * 1e-3) / 1e9,
                "roofline": roofline_hbm(nbytes, ev, "paged_decode_" + name)}
         return w, rec
@@ -518,7 +564,11 @@ def run_workload(name, torch, capi, wl, dev, steps, warmup, cfg5_layers, min_war
         key = "paged_prefill_cfg2" if name == "cfg2" else "paged_prefill_cfg5_chunk"
         step, nbytes, flops = setup_prefill(torch, capi, wl, w, dev)
         wall, ev = timer.run(step, steps, warmup)
-        rec = {"workload": w.name, "ms_per_step": wall, "kernel_ms": ev, "flops": flops,
+        eager = {}
+        if name == "cfg2":
+            eager = {"eager_ms_per_step": wall, "eager_kernel_ms": ev, "timing": "graph"}
+            wall, ev = timer.run_graph(step, steps, warmup)
+        rec = {"workload": w.name, "ms_per_step": wall, "kernel_ms": ev, **eager, "flops": flops,
                "bytes": nbytes, "TFLOP/s": flops / (wall * 1e-3) / 1e12,
                "GB/s": nbytes / (wall * 1e-3) / 1e9,
                "roofline": roofline_mfma(flops, ev, key),
@@ -630,6 +680,9 @@ def main():
                   "num_qo_heads": s.num_qo_heads, "num_kv_heads": s.num_kv_heads,
                   "head_dim": s.head_dim, "page_size": w.batch.page_size,
                   "sum_kv": int(w.batch.kv_lens.sum()), "parallelism": "single GPU"}
+    if head.get("timing") == "graph":
+        config["timing"] = "one hipGraph of the K calls (eager figures in extra)"
+        extra.setdefault(args.workload, {k: head[k] for k in ("eager_ms_per_step", "eager_kernel_ms")})
     line = {
         "metric": METRIC,
         "value": round(value, 2),
