@@ -45,6 +45,17 @@ __device__ __forceinline__ void rmsnorm8(float (&x)[8], const uint16_t* __restri
   for (int i = 0; i < 8; ++i) x[i] = round_t<DT>((x[i] * scale) * wf[i]);
 }
 
+// One rotated value: x c + p' s, p' the partner with its sign flipped on
+// the first half (x c - p s there: negation is exact), as one multiply and
+// one fused multiply-add wherever RoPE is applied, so every path rounds
+// alike.
+__device__ __forceinline__ float rope_one(float x, float p_signed, float c, float s) {
+  return fmaf(p_signed, s, x * c);
+}
+
+// Sign bits of both 16-bit halves of a packed word (bf16 and fp16 alike).
+constexpr uint32_t kSign2 = 0x80008000u;
+
 // Rotate-half RoPE of the 8 values this lane holds; x must hold DT values.
 template <int LPR, int DT>
 __device__ __forceinline__ void rope8(float (&x)[8], const float* __restrict__ cos_row,
@@ -63,6 +74,7 @@ __device__ __forceinline__ void rope8(float (&x)[8], const float* __restrict__ c
     } else {
       pw = static_cast<uint32_t>(__shfl_xor(static_cast<int>(w), HALF, kWave));
     }
+    pw ^= first ? kSign2 : 0u;
     p[2 * i] = to_f32<DT>(pw & 0xffffu);
     p[2 * i + 1] = to_f32<DT>(pw >> 16);
   }
@@ -73,9 +85,7 @@ __device__ __forceinline__ void rope8(float (&x)[8], const float* __restrict__ c
   const float c[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
   const float s[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    x[i] = first ? (x[i] * c[i] - p[i] * s[i]) : (x[i] * c[i] + p[i] * s[i]);
-  }
+  for (int i = 0; i < 8; ++i) x[i] = rope_one(x[i], p[i], c[i], s[i]);
 }
 
 // --- cos/sin cache ----------------------------------------------------------
@@ -235,7 +245,7 @@ __global__ void __launch_bounds__(128) rope_generic_kernel(
     const float o = to_f32<DT>(row[other]);
     const float c = cos_cache[pos * cos_width + ci];
     const float s = sin_cache[pos * cos_width + ci];
-    out[n] = first ? (v * c - o * s) : (v * c + o * s);
+    out[n] = rope_one(v, first ? -o : o, c, s);
   }
   __syncthreads();
   n = 0;
@@ -296,9 +306,10 @@ __global__ void __launch_bounds__(256) fused_qknorm_rope_store_kernel(
       if (tb * NT + k < num_tokens) stg128(v_cache + (slot[k] * hkv + h) * D + lane_in_row * 8, raw[k]);
     return;
   }
-  u32x4_t wv = {0, 0, 0, 0};
-  if (w != nullptr) wv = ldg128(w + lane_in_row * 8);
+  float wf[8];
+  if (w != nullptr) unpack8(ldg128(w + lane_in_row * 8), wf);
   const bool first = lane_in_row < HALF;
+  const uint32_t psign = first ? kSign2 : 0u;
   const int jj = first ? lane_in_row : lane_in_row - HALF;
   f32x4_t c0[NT], c1[NT], s0[NT], s1[NT];
 #pragma unroll
@@ -321,8 +332,6 @@ __global__ void __launch_bounds__(256) fused_qknorm_rope_store_kernel(
       for (int i = 0; i < 8; ++i) ss += x[i] * x[i];
       ss = group_sum<LPR>(ss);
       const float scale = rsqrtf(ss * (1.0f / D) + eps);
-      float wf[8];
-      unpack8(wv, wf);
 #pragma unroll
       for (int i = 0; i < 4; ++i)
         words[i] = pack_bf16x2((x[2 * i] * scale) * wf[2 * i], (x[2 * i + 1] * scale) * wf[2 * i + 1]);
@@ -335,13 +344,14 @@ __global__ void __launch_bounds__(256) fused_qknorm_rope_store_kernel(
       uint32_t pw;
       if constexpr (HALF == 8) pw = dpp_u32<0x128>(wd);
       else pw = static_cast<uint32_t>(__shfl_xor(static_cast<int>(wd), HALF, kWave));
+      pw ^= psign;
       p[2 * i] = bf16_lo(pw);
       p[2 * i + 1] = bf16_hi(pw);
     }
     const float c[8] = {c0[k][0], c0[k][1], c0[k][2], c0[k][3], c1[k][0], c1[k][1], c1[k][2], c1[k][3]};
     const float sn[8] = {s0[k][0], s0[k][1], s0[k][2], s0[k][3], s1[k][0], s1[k][1], s1[k][2], s1[k][3]};
 #pragma unroll
-    for (int i = 0; i < 8; ++i) x[i] = first ? (x[i] * c[i] - p[i] * sn[i]) : (x[i] * c[i] + p[i] * sn[i]);
+    for (int i = 0; i < 8; ++i) x[i] = rope_one(x[i], p[i], c[i], sn[i]);
     const u32x4_t packed = pack8(x);
     if (tb * NT + k < num_tokens) {
       if (is_q || k_back) stg128(src[k], packed);
