@@ -359,6 +359,7 @@ def test_decode_cfg1(oracle, dev):
     ref = oracle.decode(u16(q).copy(), u16(kc), u16(vc), w.batch.indices, w.batch.kv_indptr,
                         scale)
     assert_attn_close(o.float().cpu().numpy(), ref, what=w.name)
+    assert_attn_close(o.float().cpu().numpy(), ref, what=w.name)
 
 
 def test_decode_forced_split_and_q_indptr(oracle, dev):
