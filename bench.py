@@ -544,9 +544,9 @@ def run_workload(name, torch, capi, wl, dev, steps, warmup, cfg5_layers, min_war
                "kernel_ms": ev, "bytes": nbytes, "GB/s": nbytes / (wall * 1e-3) / 1e9,
                "roofline": roofline_hbm(nbytes, ev, f"{kname}_qwen3_8b")}
         return None, rec
-    # Configurations 1 and 2 are single calls of about 10 us, less than the
-    # host's per-call launch cost from Python: they are timed as a captured
-    # graph of the K calls (the eager figures are kept beside them).
+    # Configurations 1, 2 and 3 are single calls of 10-25 us, within a few us
+    # of the host's per-call launch cost from Python: they are timed as a
+    # captured graph of the K calls (the eager figures are kept beside them).
     if name in ("cfg1", "cfg4"):
         w = wl.cfg1_decode_small() if name == "cfg1" else wl.cfg4_decode_large()
         step, nbytes, flops, _ = setup_decode(torch, capi, wl, w, dev)
@@ -578,7 +578,9 @@ def run_workload(name, torch, capi, wl, dev, steps, warmup, cfg5_layers, min_war
         w = wl.cfg3_fused_store()
         step, nbytes = setup_fused(torch, capi, wl, w, dev)
         wall, ev = timer.run(step, steps, warmup)
-        rec = {"workload": w.name, "ms_per_step": wall, "kernel_ms": ev, "bytes": nbytes,
+        eager = {"eager_ms_per_step": wall, "eager_kernel_ms": ev, "timing": "graph"}
+        wall, ev = timer.run_graph(step, steps, warmup)
+        rec = {"workload": w.name, "ms_per_step": wall, "kernel_ms": ev, **eager, "bytes": nbytes,
                "GB/s": nbytes / (wall * 1e-3) / 1e9,
                "roofline": roofline_hbm(nbytes, ev, "fused_qknorm_rope_store_cfg3")}
         return w, rec
