@@ -57,6 +57,9 @@ def parse():
     ap.add_argument("--no-extra", action="store_true", help="headline workload only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--cfg5-layers", type=int, default=48)
+    ap.add_argument("--ceilings-only", action="store_true",
+                    help="only measure the practical ceilings of this GPU (stream read, MFMA "
+                         "issue on random and constant bf16 operands, empty launch) and print them")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB (steps times): "
                          "the known-size reference for rocprofv3 FETCH_SIZE / WRITE_SIZE")
@@ -526,6 +529,200 @@ def setup_sampling(torch, capi, dev, seed=0):
                                                   "top_p": 0.9}
 
 
+# ------------------------------------------------------------------ ceilings
+
+def load_probes():
+    """libsgl_probes.so (sglang.cpp_amd/csrc/probes/ceilings.hip): raises if
+    it is not built."""
+    import ctypes
+    path = REPO / "sglang.cpp_amd" / "libsgl_probes.so"
+    if not path.exists():
+        raise RuntimeError(f"{path} is not built (run __graft_entry__.build())")
+    lib = ctypes.CDLL(str(path))
+    vp, i64, i32, u32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_uint32
+    lib.sgl_probe_stream_read.argtypes = [vp, i64, i32, i32, vp, vp]
+    lib.sgl_probe_mfma_bf16.argtypes = [i32, i32, i32, u32, vp, vp, vp]
+    lib.sgl_probe_empty.argtypes = [i32, i32, vp]
+    lib.sgl_probe_page_read.argtypes = [vp, vp, i32, i64, i32, i32, vp, vp]
+    lib.sgl_probe_page_read.restype = i32
+    lib.sgl_probe_decode_read.argtypes = [vp, vp, vp, i32, i32, i32, i32, i32, vp, vp]
+    lib.sgl_probe_decode_read.restype = i32
+    for f in (lib.sgl_probe_stream_read, lib.sgl_probe_mfma_bf16, lib.sgl_probe_empty):
+        f.restype = i32
+    return lib
+
+
+def _probe_ok(st, what):
+    if st != 0:
+        raise RuntimeError(f"{what} failed: status {st}")
+
+
+MFMA_FLOPS = 32 * 32 * 16 * 2  # one v_mfma_f32_32x32x16_bf16
+
+
+def measure_ceilings(torch, dev, min_warm_s=0.5, sweep=None):
+    """Practical ceilings of this GPU, measured in this process:
+    stream_read: best GB/s of a plain 16-byte streaming read of 2 GiB over
+    grid sizes, loads in flight per lane (4, 8, 16), cached/non-temporal
+    loads and grid-stride/block-contiguous order; mfma_random / mfma_const: TFLOP/s of back-to-back 32x32x16
+    bf16 MFMAs (2 waves per SIMD on every CU) on random / constant operands,
+    with the shader clock (MHz) each ran at; empty_launch_us: per-launch time
+    of an empty 256-workgroup kernel, as a graph of 200 launches and eagerly."""
+    lib = load_probes()
+    s = torch.cuda.current_stream()
+    sp = s.cuda_stream
+    out = {}
+    # stream read
+    nbytes = 2 << 30
+    buf = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    buf.random_(0, 256)
+    sink = torch.zeros(4, dtype=torch.int32, device=dev)
+    best = (0.0, 0, 0)
+    for variant, grid in [(v | b, g) for b in (0, 8) for v in range(6)
+                          for g in (1024, 2048, 4096, 8192)]:
+        def go():
+            _probe_ok(lib.sgl_probe_stream_read(buf.data_ptr(), nbytes, grid, variant,
+                                                sink.data_ptr(), sp), "sgl_probe_stream_read")
+        for _ in range(3):
+            go()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        for _ in range(10):
+            go()
+        e1.record(s)
+        torch.cuda.synchronize()
+        gbs = nbytes / (e0.elapsed_time(e1) / 10 * 1e-3) / 1e9
+        if sweep is not None:
+            sweep.append({"probe": "stream_read", "variant": variant, "grid": grid,
+                          "GB/s": round(gbs, 1)})
+        if gbs > best[0]:
+            best = (gbs, grid, variant)
+    # paged read: 32 KiB pages in a seeded random order
+    page = 32 << 10
+    npages = nbytes // page
+    g = torch.Generator(device="cpu")
+    g.manual_seed(0)
+    order = torch.randperm(npages, generator=g).to(torch.int32).to(dev)
+    pbest = (0.0, 0, 0)
+    for pif, pgrid in [(f, gr) for f in (1, 2) for gr in (256, 512, 1024, 2048, 4096)]:
+        def gop():
+            _probe_ok(lib.sgl_probe_page_read(buf.data_ptr(), order.data_ptr(), npages, page, pgrid,
+                                              pif, sink.data_ptr(), sp), "sgl_probe_page_read")
+        for _ in range(3):
+            gop()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        for _ in range(10):
+            gop()
+        e1.record(s)
+        torch.cuda.synchronize()
+        gbs = nbytes / (e0.elapsed_time(e1) / 10 * 1e-3) / 1e9
+        if sweep is not None:
+            sweep.append({"probe": "page_read", "pages_in_flight": pif, "grid": pgrid,
+                          "GB/s": round(gbs, 1)})
+        if gbs > pbest[0]:
+            pbest = (gbs, pgrid, pif)
+    out["page_read_32k"] = {"GB/s": round(pbest[0], 1),
+                            "frac_of_published": round(pbest[0] / HBM_PEAK_GBS, 4),
+                            "grid": pbest[1], "pages_in_flight": pbest[2], "page_bytes": page,
+                            "bytes": nbytes}
+    # the paged decode's load pattern: K and V pools of 2^19 2-KiB slots
+    # (1 GiB each), 16-slot pages in a seeded random order
+    slots = nbytes // 2 // 2048
+    pages = torch.randperm(slots // 16, generator=g)
+    tok_order = (pages.view(-1, 1) * 16 + torch.arange(16).view(1, 16)).reshape(-1)
+    tok_order = tok_order.to(torch.int32).to(dev)
+    kpool, vpool = buf[: nbytes // 2], buf[nbytes // 2:]
+    dbest = {}
+    for kmode, dgrid, bar, depth in [(m, gr, br, dp) for m in range(4) for gr in (512, 1024)
+                                     for br in (1, 0) for dp in (2, 3)]:
+        def god():
+            _probe_ok(lib.sgl_probe_decode_read(kpool.data_ptr(), vpool.data_ptr(),
+                                                tok_order.data_ptr(), slots, dgrid, kmode, bar,
+                                                depth, sink.data_ptr(), sp),
+                      "sgl_probe_decode_read")
+        for _ in range(3):
+            god()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        for _ in range(10):
+            god()
+        e1.record(s)
+        torch.cuda.synchronize()
+        gbs = nbytes / (e0.elapsed_time(e1) / 10 * 1e-3) / 1e9
+        if sweep is not None:
+            sweep.append({"probe": "decode_read", "kmode": kmode, "grid": dgrid,
+                          "barrier": bar, "depth": depth, "GB/s": round(gbs, 1)})
+        key = ("k_operand_cached", "k_operand_nt", "k_rows_nt", "k_rows_cached")[kmode]
+        if gbs > dbest.get(key, 0.0):
+            dbest[key] = round(gbs, 1)
+    out["decode_read_pattern"] = {"GB/s": dbest, "bytes": nbytes, "page_slots": 16,
+                                  "slot_bytes": 2048}
+    del buf
+    out["stream_read"] = {"GB/s": round(best[0], 1), "frac_of_published": round(best[0] / HBM_PEAK_GBS, 4),
+                          "grid": best[1], "loads_in_flight": 4 << ((best[2] >> 1) & 3),
+                          "non_temporal": bool(best[2] & 1),
+                          "order": "block-contiguous" if best[2] & 8 else "grid-stride",
+                          "bytes": nbytes}
+    # MFMA issue
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    grid = 2 * cus
+    iters = 20000
+    fsink = torch.zeros(grid, dtype=torch.float32, device=dev)
+    clocks = torch.zeros(grid * 4, dtype=torch.int64, device=dev)
+    for kind, rnd in (("mfma_random", 1), ("mfma_const", 0)):
+        def go():
+            _probe_ok(lib.sgl_probe_mfma_bf16(grid, iters, rnd, 12345, fsink.data_ptr(),
+                                              clocks.data_ptr(), sp), "sgl_probe_mfma_bf16")
+        t0 = time.perf_counter()
+        go()
+        torch.cuda.synchronize()
+        while time.perf_counter() - t0 < min_warm_s:
+            go()
+            torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        for _ in range(5):
+            go()
+        e1.record(s)
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / 5
+        flops = grid * 4 * iters * 4 * MFMA_FLOPS
+        c = clocks.view(grid, 4).cpu().numpy().astype(np.float64)
+        mhz = np.median((c[:, 1] - c[:, 0]) / np.maximum(c[:, 3] - c[:, 2], 1) * 100.0)
+        tf = flops / (ms * 1e-3) / 1e12
+        out[kind] = {"TFLOP/s": round(tf, 1), "frac_of_published": round(tf / BF16_PEAK_TFLOPS, 4),
+                     "shader_clock_MHz": round(float(mhz), 0), "ms": round(ms, 4),
+                     "waves_per_simd": 2, "workgroups": grid}
+    # empty launch
+    def empty():
+        _probe_ok(lib.sgl_probe_empty(256, 256, torch.cuda.current_stream().cuda_stream),
+                  "sgl_probe_empty")
+    timer = Timer(torch, 0.1)
+    wall, ev = timer.run_graph(empty, 200, 10)
+    ewall, eev = timer.run(empty, 200, 10)
+    out["empty_launch_us"] = {"graph": round(ev * 1e3, 2), "eager": round(eev * 1e3, 2),
+                              "workgroups": 256}
+    return out
+
+
+def ceiling_fracs(extra, ceil):
+    """Each kernel's achieved rate over the practical ceiling of its bound."""
+    sr = ceil["stream_read"]["GB/s"]
+    mr = ceil["mfma_random"]["TFLOP/s"]
+    fr = {}
+    for name, rec in extra.items():
+        rl = rec.get("roofline") if isinstance(rec, dict) else None
+        if not rl:
+            continue
+        c = sr if rl["bound"] == "hbm" else mr
+        fr[name] = round(rl["achieved"] / c, 4)
+    return fr
+
+
 def run_workload(name, torch, capi, wl, dev, steps, warmup, cfg5_layers, min_warm_s=0.0):
     timer = Timer(torch, min_warm_s)
     if name == "sampling":
@@ -624,6 +821,12 @@ def main():
         print(json.dumps({"copy_bytes": n, "steps": args.steps}))
         return
 
+    if args.ceilings_only:
+        sweep = []
+        ceil = measure_ceilings(torch, dev, args.min_warm_seconds, sweep)
+        print(json.dumps({"ceilings": ceil, "sweep": sweep}), flush=True)
+        return
+
     w, head = run_workload(args.workload, torch, capi, wl, dev, args.steps, args.warmup,
                            args.cfg5_layers, args.min_warm_seconds)
     extra = {}
@@ -640,6 +843,15 @@ def main():
                 extra[name] = {"error": repr(e)}
             torch.cuda.empty_cache()
             print(f"[bench] {name}: {json.dumps(extra[name])}", file=sys.stderr, flush=True)
+
+    if not args.no_extra:
+        try:
+            ceil = measure_ceilings(torch, dev, args.min_warm_seconds)
+            extra["ceilings"] = ceil
+            extra["ceiling_frac"] = ceiling_fracs({args.workload: head, **extra}, ceil)
+        except Exception as e:  # report, keep the headline line
+            extra["ceilings"] = {"error": repr(e)}
+        print(f"[bench] ceilings: {json.dumps(extra['ceilings'])}", file=sys.stderr, flush=True)
 
     cpu = None
     if not args.no_cpu:

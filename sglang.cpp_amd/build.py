@@ -133,9 +133,31 @@ def build_backend(jobs: int = 8) -> Path:
     return out
 
 
+PROBES_NAME = "libsgl_probes.so"
+PROBES_SOURCE = "probes/ceilings.hip"
+
+
+def build_probes() -> Path:
+    """The hardware-ceiling probes the benchmark reports beside the
+    attention kernels (stream read, MFMA issue, empty launch); a library of
+    their own, outside the attention ABI."""
+    BUILD_DIR.mkdir(exist_ok=True)
+    obj = BUILD_DIR / "ceilings.hip.o"
+    _compile(CSRC / PROBES_SOURCE, obj)
+    out = PKG_DIR / PROBES_NAME
+    tmp = out.with_suffix(".so.tmp")
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", str(obj), "-o", str(tmp)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"probe link failed:\n{res.stdout}\n{res.stderr}")
+    os.replace(tmp, out)
+    return out
+
+
 def build(jobs: int = 8) -> None:
     build_lib(jobs)
     build_backend(jobs)
+    build_probes()
 
 
 if __name__ == "__main__":

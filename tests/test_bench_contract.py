@@ -81,3 +81,39 @@ def test_multi_gpu_request_is_refused():
                          capture_output=True, text=True, timeout=120)
     assert res.returncode != 0
     assert "one GPU" in res.stderr
+
+
+def _bench_module():
+    import importlib.util
+    spec = importlib.util.spec_from_file_location("_bench", REPO / "bench.py")
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def test_probe_library_exports_its_entry_points():
+    """The ceiling probes the bench reports are built beside the attention
+    library and export what bench.py binds (no GPU call)."""
+    import ctypes
+    path = REPO / "sglang.cpp_amd" / "libsgl_probes.so"
+    if not path.exists():
+        import pytest
+        pytest.skip("libsgl_probes.so not built")
+    lib = ctypes.CDLL(str(path))
+    for name in ("sgl_probe_stream_read", "sgl_probe_page_read", "sgl_probe_decode_read",
+                 "sgl_probe_mfma_bf16", "sgl_probe_empty"):
+        assert hasattr(lib, name), name
+    bench = _bench_module()
+    assert bench.load_probes() is not None
+
+
+def test_ceiling_fractions_use_the_bound_of_each_kernel():
+    bench = _bench_module()
+    ceil = {"stream_read": {"GB/s": 7000.0}, "mfma_random": {"TFLOP/s": 1800.0}}
+    extra = {"cfg4": {"roofline": {"bound": "hbm", "achieved": 6300.0}},
+             "prefill_chunk": {"roofline": {"bound": "mfma", "achieved": 900.0}},
+             "cfg5": {"graph_ms": 21.0}}
+    fr = bench.ceiling_fracs(extra, ceil)
+    assert fr == {"cfg4": 0.9, "prefill_chunk": 0.5}
+    # one MFMA of the probe: 32 x 32 x 16 multiply-adds
+    assert bench.MFMA_FLOPS == 32768
