@@ -110,14 +110,23 @@ def fused_qknorm_rope_store(qkv, k_cache, v_cache, q_weight, k_weight, cos, sin,
 def host_info() -> dict:
     """CPU model and the threads LibTorch uses."""
     model = platform.processor() or "unknown"
+    ident = {}
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
-                if line.startswith("model name"):
+                key = line.split(":", 1)[0].strip()
+                if key == "model name":
                     model = line.split(":", 1)[1].strip()
-                    break
+                elif key in ("cpu family", "model", "stepping", "cpu MHz") and key not in ident:
+                    ident[key] = line.split(":", 1)[1].strip()
+                elif not line.strip() and ident:
+                    break  # first processor's block only
     except OSError:
         pass
+    if ident:  # a virtualised host may report only the vendor in "model name"
+        model += " (family {}, model {}, stepping {}, {} MHz)".format(
+            ident.get("cpu family", "?"), ident.get("model", "?"), ident.get("stepping", "?"),
+            ident.get("cpu MHz", "?"))
     return {"cpu_model": model, "threads": torch.get_num_threads(),
             "host_cpus": len(os.sched_getaffinity(0))}
 
