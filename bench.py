@@ -636,7 +636,7 @@ def measure_ceilings(torch, dev, min_warm_s=0.5, sweep=None):
     tok_order = tok_order.to(torch.int32).to(dev)
     kpool, vpool = buf[: nbytes // 2], buf[nbytes // 2:]
     dbest = {}
-    for kmode, dgrid, bar, depth in [(m, gr, br, dp) for m in range(4) for gr in (512, 1024)
+    for kmode, dgrid, bar, depth in [(m, gr, br, dp) for m in range(4) for gr in (256, 512, 1024)
                                      for br in (1, 0) for dp in (2, 3)]:
         def god():
             _probe_ok(lib.sgl_probe_decode_read(kpool.data_ptr(), vpool.data_ptr(),
