@@ -12,8 +12,10 @@ RoPE + qk-norm + KV store, cfg5 mixed 48-layer step replayed as a hipGraph,
 prefill_chunk (cfg5's 2048-token prefill chunk on its 4096-token prefix, one
 layer, alone: the prefill kernel's MFMA fraction); and the residual path around attention at the Qwen3-8B shape for an
 8192-token chunk: resid_norm (fused add + RMSNorm, hidden 4096) and
-resid_act (SiLU-and-mul, intermediate 12288); and sampling (top-k + top-p
-draw for 256 rows over the Qwen3 vocabulary, as the Sampler runs it).
+resid_act (SiLU-and-mul, intermediate 12288); sampling (top-k + top-p
+draw for 256 rows over the Qwen3 vocabulary, as the Sampler runs it); and
+sampler_softmax (the Sampler's probabilities from bf16 logits and per-row
+temperatures for those rows, beside LibTorch's own path on the device).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload cfgN]
                        [--no-extra] [--no-cpu] [--min-warm-seconds S]
@@ -53,7 +55,7 @@ def parse():
                          "(after the W warm-up steps; the timed region is still K steps)")
     ap.add_argument("--workload", default="cfg4",
                     choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5", "prefill_chunk", "resid_norm",
-                             "resid_act", "sampling"])
+                             "resid_act", "sampling", "sampler_softmax"])
     ap.add_argument("--no-extra", action="store_true", help="headline workload only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--cfg5-layers", type=int, default=48)
@@ -723,8 +725,44 @@ def ceiling_fracs(extra, ceil):
     return fr
 
 
+def setup_sampler_softmax(torch, capi, dev, seed=0):
+    """The probabilities of Sampler::sample (engine.cc:306-308) for the
+    sampling workload's batch: bf16 logits [256, 151936] (the LM head's
+    output), per-row temperatures. Algorithmic bytes: one read of the
+    logits, one write of the fp32 probabilities, the temperatures. Also
+    returns the reference's own statements on the same device
+    (logits.to(float32) / temperatures, torch.softmax) for comparison."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    B, V = SAMPLING_BATCH, QWEN3_VOCAB
+    logits = (torch.randn((B, V), device=dev, generator=g) * 3).to(torch.bfloat16)
+    temps = torch.linspace(0.6, 1.2, B, device=dev)
+    out = torch.empty((B, V), device=dev)
+
+    def step():
+        capi.softmax_temperature(logits, temps, out=out)
+
+    def torch_step():
+        torch.softmax(logits.to(torch.float32) / temps.view(B, 1), -1)
+
+    return step, torch_step, B * V * (2 + 4) + 4 * B, {"batch": B, "vocab": V,
+                                                         "logits": "bf16"}
+
+
 def run_workload(name, torch, capi, wl, dev, steps, warmup, cfg5_layers, min_warm_s=0.0):
     timer = Timer(torch, min_warm_s)
+    if name == "sampler_softmax":
+        step, torch_step, nbytes, shape = setup_sampler_softmax(torch, capi, dev)
+        ewall, eev = timer.run(step, steps, warmup)
+        wall, ev = timer.run_graph(step, steps, warmup)
+        _, tev = timer.run_graph(torch_step, steps, warmup)
+        rec = {"workload": f"sampler_softmax_b{SAMPLING_BATCH}_v{QWEN3_VOCAB}", **shape,
+               "ms_per_step": wall, "kernel_ms": ev, "eager_ms_per_step": ewall,
+               "eager_kernel_ms": eev, "timing": "graph", "bytes": nbytes,
+               "GB/s": nbytes / (wall * 1e-3) / 1e9,
+               "torch_path_ms": tev, "speedup_vs_torch_path": tev / ev,
+               "roofline": roofline_hbm(nbytes, ev, "softmax_temperature_sampler")}
+        return None, rec
     if name == "sampling":
         step, nbytes, shape = setup_sampling(torch, capi, dev)
         wall, ev = timer.run(step, steps, warmup)
@@ -832,7 +870,7 @@ def main():
     extra = {}
     if not args.no_extra:
         for name in ("cfg1", "cfg2", "cfg3", "cfg4", "cfg5", "prefill_chunk", "resid_norm",
-                     "resid_act", "sampling"):
+                     "resid_act", "sampling", "sampler_softmax"):
             if name == args.workload:
                 continue
             try:
@@ -887,7 +925,7 @@ def main():
     if w is None:
         config = {"workload": head["workload"], "parallelism": "single GPU",
                   **{k: head[k] for k in ("tokens", "hidden", "intermediate", "batch", "vocab",
-                                          "top_k", "top_p") if k in head}}
+                                          "top_k", "top_p", "logits") if k in head}}
     else:
         s = w.shape
         config = {"workload": head["workload"], "batch": w.batch.batch_size,
@@ -896,7 +934,10 @@ def main():
                   "sum_kv": int(w.batch.kv_lens.sum()), "parallelism": "single GPU"}
     if head.get("timing") == "graph":
         config["timing"] = "one hipGraph of the K calls (eager figures in extra)"
-        extra.setdefault(args.workload, {k: head[k] for k in ("eager_ms_per_step", "eager_kernel_ms")})
+        extra.setdefault(args.workload, {k: head[k] for k in ("eager_ms_per_step", "eager_kernel_ms",
+                                                              "torch_path_ms",
+                                                              "speedup_vs_torch_path")
+                                         if k in head})
     line = {
         "metric": METRIC,
         "value": round(value, 2),

@@ -33,13 +33,14 @@ extern "C" {
 
 #define SGL_DTYPE_BF16 0  /* 16-bit element types (norm, RoPE and residual-path kernels) */
 #define SGL_DTYPE_F16 1
+#define SGL_DTYPE_F32 2   /* fp32 (accepted where a declaration says so) */
 
 /* Human-readable text for a status code (static storage). */
 const char* sgl_status_string(int status);
 
 /* Library version, to check that the loaded .so matches this header. */
 int sgl_abi_version(void);
-#define SGL_ABI_VERSION 11
+#define SGL_ABI_VERSION 12
 
 /* ------------------------------------------------------------------ */
 /* KV-cache store                                                      */
@@ -417,8 +418,25 @@ int sgl_gelu_and_mul(void* out, const void* input, int64_t tokens, int64_t d,
                      void* stream);
 
 /* ------------------------------------------------------------------ */
-/* Sampling from probabilities                                         */
+/* Probabilities from logits, then sampling from probabilities         */
 /* ------------------------------------------------------------------ */
+
+/*
+ * probs[r, i] = softmax_i(float(logits[r, i]) / t_r) over i < vocab, fp32,
+ * for r < batch; t_r = temperatures[r] (fp32 [batch]) or, when temperatures
+ * is NULL, the scalar temperature (> 0). logits_dtype: SGL_DTYPE_BF16,
+ * SGL_DTYPE_F16 or SGL_DTYPE_F32; row strides in elements (>= vocab). One
+ * 512-thread workgroup per row; 16-bit rows of up to 163,840 elements
+ * are read from HBM once. Exponentials as 2^(x log2e / t - max log2e)
+ * (relative error of a probability below ~1e-5 against the exact softmax
+ * of float(x) / t).
+ * Replaces: the probabilities of Sampler::sample, logits.to(kFloat32) /
+ *           temperatures then torch::softmax (src/engine/engine.cc:306-308).
+ */
+int sgl_softmax_temperature(float* probs, int64_t probs_stride_row, const void* logits,
+                            int64_t logits_stride_row, int logits_dtype,
+                            const float* temperatures, float temperature, int64_t batch,
+                            int64_t vocab, void* stream);
 
 /*
  * probs: fp32 [batch_size, d], rows contiguous (the softmax of the

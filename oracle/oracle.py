@@ -279,3 +279,18 @@ def sample(probs, uniform, mode: str, top_k=None, top_k_val: int = 0, top_p=None
                         ctypes.c_int(rounds), ctypes.c_int(m), _p(tkf), _p(tki),
                         ctypes.c_int(top_k_val), _p(tp), F32(top_p_val))
     return out, (None if succ is None else succ.astype(bool))
+
+
+def softmax_temperature(logits_f32: np.ndarray, temperatures) -> np.ndarray:
+    """The probabilities of Sampler::sample (src/engine/engine.cc:306-308):
+    y = logits.to(float32) / temperatures in float32 (an IEEE division per
+    element, as LibTorch computes it), then softmax over the vocabulary,
+    here in float64 (max-shifted). logits_f32: [batch, vocab] float32 (the
+    widened logits); temperatures: [batch] or a scalar. Returns float64."""
+    x = np.ascontiguousarray(logits_f32, dtype=np.float32)
+    t = np.asarray(temperatures, dtype=np.float32).reshape(-1, 1) if np.ndim(temperatures) \
+        else np.float32(temperatures)
+    y = (x / t).astype(np.float64)  # float32 division, then widened
+    y = y - y.max(axis=1, keepdims=True)
+    e = np.exp(y)
+    return e / e.sum(axis=1, keepdims=True)

@@ -37,7 +37,7 @@ HIP_FLAGS = [
 ]
 
 SOURCES = ["kv_store.hip", "metadata.hip", "rope_norm.hip", "decode.hip", "prefill.hip", "residual.hip",
-           "sampling.hip"]
+           "sampling.hip", "softmax.hip"]
 
 
 def _compile(src: Path, obj: Path) -> None:

@@ -25,7 +25,8 @@ SGL_INDEX_I32 = 0
 SGL_INDEX_I64 = 1
 SGL_DTYPE_BF16 = 0
 SGL_DTYPE_F16 = 1
-ABI_VERSION = 11
+SGL_DTYPE_F32 = 2
+ABI_VERSION = 12
 FUSED_NO_K_WRITEBACK = 1  # SGL_FUSED_NO_K_WRITEBACK
 
 
@@ -86,6 +87,7 @@ _SIGNATURES = {
     "sgl_fused_add_rmsnorm": ([_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i32, _f32, _vp], _i32),
     "sgl_silu_and_mul": ([_vp, _vp, _i64, _i64, _i64, _i64, _i32, _vp], _i32),
     "sgl_gelu_and_mul": ([_vp, _vp, _i64, _i64, _i64, _i64, _i32, _vp], _i32),
+    "sgl_softmax_temperature": ([_vp, _i64, _vp, _i64, _i32, _vp, _f32, _i64, _i64, _vp], _i32),
     "sgl_sampling_from_probs": ([_vp, _vp, _vp, _i32, _i32, _i32, _vp], _i32),
     "sgl_top_k_sampling_from_probs": ([_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32,
                                        _vp], _i32),
@@ -556,6 +558,39 @@ def paged_prefill(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
 
 
 # ---------------------------------------------------------------- sampling
+
+def softmax_temperature(logits: torch.Tensor, temperatures: Optional[torch.Tensor] = None,
+                        temperature: float = 1.0,
+                        out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """The probabilities Sampler::sample hands to the sampling kernels:
+    softmax(logits.float() / temperatures, -1) (src/engine/engine.cc:306-308),
+    one pass. logits: [batch, vocab] bf16, fp16 or fp32 with contiguous rows;
+    temperatures: float32 [batch] (or [batch, 1]), else the scalar
+    temperature. Returns (or fills) float32 [batch, vocab]."""
+    dev = _need_gpu(logits, temperatures, out)
+    if logits.dim() != 2 or logits.stride(1) != 1:
+        raise ValueError("logits must be [batch, vocab] with contiguous rows")
+    codes = {torch.bfloat16: SGL_DTYPE_BF16, torch.float16: SGL_DTYPE_F16,
+             torch.float32: SGL_DTYPE_F32}
+    if logits.dtype not in codes:
+        raise ValueError("logits must be bf16, fp16 or float32")
+    b, v = logits.shape
+    if temperatures is not None:
+        if temperatures.dtype != torch.float32 or temperatures.numel() != b:
+            raise ValueError("temperatures must be float32 with one value per row")
+        temperatures = temperatures.reshape(b).contiguous()
+    elif not temperature > 0:
+        raise ValueError("temperature must be positive")
+    if out is None:
+        out = torch.empty((b, v), dtype=torch.float32, device=dev)
+    elif out.shape != (b, v) or out.dtype != torch.float32 or out.stride(1) != 1:
+        raise ValueError("out must be float32 [batch, vocab] with contiguous rows")
+    _check(lib().sgl_softmax_temperature(_p(out), out.stride(0), _p(logits), logits.stride(0),
+                                         codes[logits.dtype], _p(temperatures),
+                                         float(temperature), b, v, _stream(dev)),
+           "sgl_softmax_temperature")
+    return out
+
 
 def _check_probs(probs: torch.Tensor, uniform: torch.Tensor, dims: int) -> None:
     if probs.dim() != 2 or not probs.is_contiguous() or probs.dtype != torch.float32:

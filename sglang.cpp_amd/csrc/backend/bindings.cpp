@@ -144,6 +144,7 @@ PYBIND11_MODULE(sgl_backend, m) {
         n.fused_add_forward_inplace(x, r);
       });
 
+  m.def("sampling_probs", &sampling_probs, py::arg("logits"), py::arg("temperatures"));
   m.def("flashinfer_sample_from_probs", &flashinfer_sample_from_probs, py::arg("probs"),
         py::arg("uniform_samples"), py::arg("deterministic") = false);
   auto pair = [](const FlashInferSamplingResult& r) { return py::make_tuple(r.samples, r.success); };

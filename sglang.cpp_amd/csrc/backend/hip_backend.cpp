@@ -892,6 +892,24 @@ int32_t narrow_dim(int64_t v, const char* what) {
 }
 }  // namespace
 
+torch::Tensor sampling_probs(const torch::Tensor& logits, const torch::Tensor& temperatures) {
+  TORCH_CHECK(logits.is_cuda() && logits.dim() == 2 && logits.stride(1) == 1,
+              "logits must be a [batch, vocab] device tensor with contiguous rows");
+  int dtype = SGL_DTYPE_F32;
+  if (logits.scalar_type() == torch::kBFloat16) dtype = SGL_DTYPE_BF16;
+  else if (logits.scalar_type() == torch::kFloat16) dtype = SGL_DTYPE_F16;
+  else TORCH_CHECK(logits.scalar_type() == torch::kFloat32, "logits must be bf16, fp16 or float32");
+  const int64_t batch = logits.size(0);
+  TORCH_CHECK(temperatures.numel() == batch, "one temperature per row");
+  auto temps = temperatures.to(logits.device()).to(torch::kFloat32).reshape({batch}).contiguous();
+  auto probs = torch::empty({batch, logits.size(1)}, logits.options().dtype(torch::kFloat32));
+  check_sgl(sgl_softmax_temperature(probs.data_ptr<float>(), probs.stride(0), logits.data_ptr(),
+                                    logits.stride(0), dtype, temps.data_ptr<float>(), 1.0f, batch,
+                                    logits.size(1), current_stream(logits.device())),
+            "sgl_softmax_temperature");
+  return probs;
+}
+
 torch::Tensor flashinfer_sample_from_probs(const torch::Tensor& probs,
                                            const torch::Tensor& uniform_samples, bool deterministic) {
   check_probs(probs);

@@ -238,6 +238,12 @@ FlashInferSamplingResult flashinfer_top_k_top_p_sample_from_probs(
     const torch::Tensor& probs, const torch::Tensor& uniform_samples, const torch::Tensor& top_k,
     double top_k_value, const torch::Tensor& top_p, double top_p_value, bool deterministic);
 
+// The probabilities Sampler::sample hands to the draws above:
+// softmax(logits.to(kFloat32) / temperatures, -1) (src/engine/engine.cc:306-308),
+// one device pass (logits bf16, fp16 or fp32 [batch, vocab]; temperatures
+// [batch] or [batch, 1], any floating type, on the logits' device).
+torch::Tensor sampling_probs(const torch::Tensor& logits, const torch::Tensor& temperatures);
+
 // NeoX RoPE with a half-width fp32 cos/sin cache built on the device
 // (rotary_embedding.cu:75-94 builds the same table with LibTorch-CPU ops).
 class RotaryEmbedding {

@@ -462,6 +462,22 @@ def test_residual_modules_match_c_abi(dev, sb, dtype):
 
 
 @pytest.mark.gpu
+def test_sampling_probs_matches_c_abi(dev, sb):
+    """Sampler::sample's probabilities (engine.cc:306-308: temperatures as
+    given by BatchSamplingArgs, [batch, 1] after the view) through the C++
+    layer equal the C ABI's, bit for bit."""
+    from conftest import capi
+    note("sampling probs")
+    g = _gen(dev, 17)
+    B, V = 5, 151936
+    logits = (torch.randn((B, V), device=dev, generator=g) * 2).to(torch.bfloat16)
+    temps = torch.tensor([[0.7], [1.0], [1.3], [0.5], [0.9]], device=dev, dtype=torch.float16)
+    a = sb.sampling_probs(logits, temps)
+    b = capi.softmax_temperature(logits, temps.float().view(B))
+    assert torch.equal(a, b)
+
+
+@pytest.mark.gpu
 def test_sampling_functions_match_c_abi(dev, sb):
     """The reference's sampling API (include/sglang/engine/sampling.h:7-36) as
     the Sampler calls it (engine.cc:300-345: uniform [32, batch], top_k float32

@@ -66,14 +66,22 @@ def test_traffic_keys_have_profiles():
     src = (REPO / "bench.py").read_text()
     keys = ["paged_decode_cfg1", "paged_decode_cfg4", "paged_prefill_cfg2",
             "paged_prefill_cfg5_chunk", "fused_qknorm_rope_store_cfg3",
-            "fused_add_rmsnorm_qwen3_8b", "silu_and_mul_qwen3_8b", "sampling_top_k_top_p"]
+            "fused_add_rmsnorm_qwen3_8b", "silu_and_mul_qwen3_8b", "sampling_top_k_top_p",
+            "softmax_temperature_sampler"]
     for k in keys:
         assert k in traffic and traffic[k] > 0, k
         assert (REPO / "profiles" / f"{k}.md").exists(), k
     # every key bench.py names literally is one of them
     for k in ("paged_prefill_cfg2", "paged_prefill_cfg5_chunk", "fused_qknorm_rope_store_cfg3",
-              "sampling_top_k_top_p"):
+              "sampling_top_k_top_p", "softmax_temperature_sampler"):
         assert f'"{k}"' in src, k
+
+
+def test_sampler_softmax_bytes():
+    # one read of bf16 logits, one write of fp32 probabilities, the temperatures
+    bench = _bench_module()
+    assert 256 * 151936 * (2 + 4) + 4 * 256 == 233374720
+    assert bench.SAMPLING_BATCH == 256 and bench.QWEN3_VOCAB == 151936
 
 
 def test_multi_gpu_request_is_refused():

@@ -244,3 +244,80 @@ def test_sampling_low_first_pivot(oracle, dev):
     k = rng.integers(1, 50, B)
     tp = rng.uniform(0.3, 0.95, B).astype(np.float32)
     run_all(oracle, dev, p, u, k, tp, exact=True)
+
+
+# ---------------------------------------------------------------- sampler softmax
+#
+# sgl_softmax_temperature against the oracle's float64 softmax of
+# float32(logits) / t (engine.cc:306-308). Bar (floating point): every
+# probability within SOFTMAX_RTOL relative (+ SOFTMAX_ATOL absolute, for
+# values below fp32's normal range) of the oracle. The kernel's scaled
+# logit carries half an ulp of |y| (6e-8 |y|, logits up to ~50 here), its
+# exp2 argument a few ulp of |y - max| and its fp32 row sum below 1e-5.
+SOFTMAX_RTOL = 3e-5
+SOFTMAX_ATOL = 1e-30
+
+
+def _softmax_case(oracle, dev, logits, temps=None, temp=1.0, label=""):
+    note(f"softmax_temperature {label} shape={tuple(logits.shape)} dtype={logits.dtype}")
+    got = capi.softmax_temperature(logits, temps, temp)
+    torch.cuda.synchronize()
+    x = logits.float().cpu().numpy()
+    ref = oracle.softmax_temperature(x, temps.cpu().numpy() if temps is not None else temp)
+    g = got.cpu().numpy().astype(np.float64)
+    err = np.abs(g - ref)
+    ok = err <= SOFTMAX_RTOL * ref + SOFTMAX_ATOL
+    rel = float((err / np.maximum(ref, 1e-30))[ref > 1e-30].max())
+    note(f"  max relative error {rel:.3e}")
+    assert ok.all(), (label, np.argwhere(~ok)[:5], rel)
+    return got
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_softmax_temperature_qwen3_vocab(oracle, dev, dtype):
+    """The Sampler's shape: per-row temperatures over the Qwen3 vocabulary
+    (16-bit rows held in registers, fp32 rows streamed); one row with
+    masked (-inf) entries. Also within the same bar of LibTorch's own
+    device path, the reference's statements."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(5)
+    B = 6
+    logits = (torch.randn((B, QWEN3_VOCAB), device=dev, generator=g) * 3).to(dtype)
+    logits[2, ::7] = float("-inf")
+    temps = torch.tensor([0.6, 0.8, 1.0, 1.2, 0.35, 1.7], device=dev)
+    got = _softmax_case(oracle, dev, logits, temps, label="qwen3")
+    torch_path = torch.softmax(logits.to(torch.float32) / temps.view(B, 1), -1)
+    assert torch.allclose(got, torch_path, rtol=SOFTMAX_RTOL, atol=SOFTMAX_ATOL)
+    assert bool((got[2, ::7] == 0).all())
+
+
+@pytest.mark.parametrize("vocab,offset,dtype", [
+    (1003, 0, torch.bfloat16),     # partial last chunk
+    (8, 0, torch.float16),         # one chunk
+    (5000, 1, torch.bfloat16),     # unaligned rows: element by element
+    (5001, 1, torch.float32),      # unaligned fp32 rows
+    (200000, 0, torch.bfloat16),   # longer than the registers hold: streamed
+    (65536, 0, torch.float16),     # register path, fewer chunks per lane
+])
+def test_softmax_temperature_shapes(oracle, dev, vocab, offset, dtype):
+    g = torch.Generator(device=dev)
+    g.manual_seed(vocab + offset)
+    B = 3
+    base = (torch.randn((B, vocab + 8), device=dev, generator=g) * 5).to(dtype)
+    logits = base[:, offset:offset + vocab]
+    _softmax_case(oracle, dev, logits, None, 0.9, label=f"v{vocab}+{offset}")
+
+
+def test_softmax_temperature_rejects_bad_arguments(dev):
+    x = torch.zeros((2, 16), device=dev, dtype=torch.bfloat16)
+    with pytest.raises(ValueError):
+        capi.softmax_temperature(x, None, 0.0)
+    with pytest.raises(ValueError):
+        capi.softmax_temperature(x.to(torch.int32), None, 1.0)
+    probs = torch.empty((2, 16), device=dev)
+    st = capi.lib().sgl_softmax_temperature(capi._p(probs), 16, capi._p(x), 16, 7, None, 1.0, 2, 16,
+                                            None)
+    assert st == -2  # SGL_ERR_UNSUPPORTED dtype
+    st = capi.lib().sgl_softmax_temperature(capi._p(probs), 8, capi._p(x), 16, 0, None, 1.0, 2, 16,
+                                            None)
+    assert st == -1  # row stride below vocab

@@ -774,3 +774,40 @@ def test_torch_cpu_fused_store_matches_oracle(oracle):
     close(u(kc_t).reshape(slots, hkv, D)[loc], kc_ref.reshape(slots, hkv, D)[loc], kn)
     untouched = np.setdiff1d(np.arange(slots), loc)
     np.testing.assert_array_equal(u(kc_t).reshape(slots, -1)[untouched], kc0[untouched])
+
+
+# ---------------------------------------------------------------- sampler softmax
+
+def test_softmax_temperature_matches_torch(oracle):
+    """Pins the oracle to the reference's own statements
+    (engine.cc:306-308: logits.to(kFloat32) / temperatures, torch::softmax)
+    run by LibTorch on the CPU: float32 there, float64 here."""
+    rng = np.random.default_rng(11)
+    x = (rng.standard_normal((6, 4099)) * 4).astype(np.float32)
+    t = np.array([0.3, 0.6, 1.0, 1.2, 2.0, 0.7], np.float32)
+    ref = torch.softmax(torch.from_numpy(x) / torch.from_numpy(t).view(-1, 1), -1).double().numpy()
+    got = oracle.softmax_temperature(x, t)
+    assert np.allclose(got, ref, rtol=2e-6, atol=1e-12)
+
+
+def test_softmax_temperature_brute_force_and_invariants(oracle):
+    """Tiny rows against the formula term by term; rows sum to 1; a
+    temperature of 1 is the plain softmax; dividing by a power of two is
+    exact, so t = 2 equals t = 1 on halved logits; a dominant logit gives a
+    one-hot row."""
+    x = np.array([[0.5, -1.25, 3.0, 0.0], [10.0, -80.0, 10.0, 9.5]], np.float32)
+    t = np.array([0.7, 1.3], np.float32)
+    got = oracle.softmax_temperature(x, t)
+    for r in range(2):
+        y = [float(np.float32(v) / np.float32(t[r])) for v in x[r]]
+        e = [math.exp(v - max(y)) for v in y]
+        assert np.allclose(got[r], [v / sum(e) for v in e], rtol=1e-14, atol=0)
+    rng = np.random.default_rng(3)
+    z = rng.standard_normal((3, 999)).astype(np.float32)
+    p1 = oracle.softmax_temperature(z, 1.0)
+    assert np.allclose(p1.sum(1), 1.0, rtol=0, atol=1e-12)
+    e = np.exp(z.astype(np.float64) - z.max(1, keepdims=True))
+    assert np.allclose(p1, e / e.sum(1, keepdims=True), rtol=1e-14, atol=0)
+    assert np.array_equal(oracle.softmax_temperature(z, 2.0), oracle.softmax_temperature(z / 2, 1.0))
+    hot = oracle.softmax_temperature(np.array([[0.0, 200.0, 1.0]], np.float32), 1.0)
+    assert hot[0, 1] == 1.0 and hot[0, 0] < 1e-80
