@@ -15,7 +15,9 @@ layer, alone: the prefill kernel's MFMA fraction); and the residual path around 
 resid_act (SiLU-and-mul, intermediate 12288); sampling (top-k + top-p
 draw for 256 rows over the Qwen3 vocabulary, as the Sampler runs it); and
 sampler_softmax (the Sampler's probabilities from bf16 logits and per-row
-temperatures for those rows, beside LibTorch's own path on the device).
+temperatures for those rows, beside LibTorch's own path on the device);
+and sampler_step (that softmax and the top-k + top-p draw in one launch,
+beside our two launches and LibTorch's probabilities followed by our draw).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload cfgN]
                        [--no-extra] [--no-cpu] [--min-warm-seconds S]
@@ -55,7 +57,7 @@ def parse():
                          "(after the W warm-up steps; the timed region is still K steps)")
     ap.add_argument("--workload", default="cfg4",
                     choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5", "prefill_chunk", "resid_norm",
-                             "resid_act", "sampling", "sampler_softmax"])
+                             "resid_act", "sampling", "sampler_softmax", "sampler_step"])
     ap.add_argument("--no-extra", action="store_true", help="headline workload only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--cfg5-layers", type=int, default=48)
@@ -749,8 +751,55 @@ def setup_sampler_softmax(torch, capi, dev, seed=0):
                                                          "logits": "bf16"}
 
 
+def setup_sampler_step(torch, capi, dev, seed=0):
+    """The whole Sampler step as engine.cc:306-333 runs it for the sampling
+    workload's rows: bf16 logits [256, 151936], per-row temperatures,
+    top-k 50 + top-p 0.9, uniform [32, 256]. Returns the fused launch
+    (probabilities computed inside the draw, never stored), our two launches
+    (softmax_temperature, then the draw) and the reference's statements for
+    the probabilities (LibTorch) followed by our draw. Algorithmic bytes of
+    the step: one read of the logits."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    B, V = SAMPLING_BATCH, QWEN3_VOCAB
+    logits = (torch.randn((B, V), device=dev, generator=g) * 3).to(torch.bfloat16)
+    temps = torch.linspace(0.6, 1.2, B, device=dev)
+    u = torch.rand((32, B), device=dev, generator=g)
+    k = torch.full((B,), 50, dtype=torch.int32, device=dev)
+    tp = torch.full((B,), 0.9, dtype=torch.float32, device=dev)
+    probs = torch.empty((B, V), device=dev)
+
+    def fused():
+        capi.sampling_from_logits(logits, u, "top_k_top_p", temps, top_k=k, top_p=tp)
+
+    def two():
+        capi.softmax_temperature(logits, temps, out=probs)
+        capi.top_k_top_p_sampling_from_probs(probs, u, k, 0, tp, 0.0)
+
+    def torch_probs():
+        p = torch.softmax(logits.to(torch.float32) / temps.view(B, 1), -1).contiguous()
+        capi.top_k_top_p_sampling_from_probs(p, u, k, 0, tp, 0.0)
+
+    return fused, two, torch_probs, B * V * 2 + 4 * B + 32 * B * 4, {
+        "batch": B, "vocab": V, "logits": "bf16", "top_k": 50, "top_p": 0.9}
+
+
 def run_workload(name, torch, capi, wl, dev, steps, warmup, cfg5_layers, min_warm_s=0.0):
     timer = Timer(torch, min_warm_s)
+    if name == "sampler_step":
+        fused, two, torch_probs, nbytes, shape = setup_sampler_step(torch, capi, dev)
+        ewall, eev = timer.run(fused, steps, warmup)
+        wall, ev = timer.run_graph(fused, steps, warmup)
+        _, two_ev = timer.run_graph(two, steps, warmup)
+        _, tp_ev = timer.run_graph(torch_probs, steps, warmup)
+        rec = {"workload": f"sampler_step_top_k_top_p_b{SAMPLING_BATCH}_v{QWEN3_VOCAB}", **shape,
+               "ms_per_step": wall, "kernel_ms": ev, "eager_ms_per_step": ewall,
+               "eager_kernel_ms": eev, "timing": "graph", "bytes": nbytes,
+               "GB/s": nbytes / (wall * 1e-3) / 1e9,
+               "two_launch_ms": two_ev, "torch_probs_then_draw_ms": tp_ev,
+               "speedup_vs_torch_probs_then_draw": tp_ev / ev,
+               "roofline": roofline_hbm(nbytes, ev, None)}
+        return None, rec
     if name == "sampler_softmax":
         step, torch_step, nbytes, shape = setup_sampler_softmax(torch, capi, dev)
         ewall, eev = timer.run(step, steps, warmup)
@@ -870,7 +919,7 @@ def main():
     extra = {}
     if not args.no_extra:
         for name in ("cfg1", "cfg2", "cfg3", "cfg4", "cfg5", "prefill_chunk", "resid_norm",
-                     "resid_act", "sampling", "sampler_softmax"):
+                     "resid_act", "sampling", "sampler_softmax", "sampler_step"):
             if name == args.workload:
                 continue
             try:
@@ -936,7 +985,9 @@ def main():
         config["timing"] = "one hipGraph of the K calls (eager figures in extra)"
         extra.setdefault(args.workload, {k: head[k] for k in ("eager_ms_per_step", "eager_kernel_ms",
                                                               "torch_path_ms",
-                                                              "speedup_vs_torch_path")
+                                                              "speedup_vs_torch_path",
+                                                              "two_launch_ms",
+                                                              "torch_probs_then_draw_ms")
                                          if k in head})
     line = {
         "metric": METRIC,

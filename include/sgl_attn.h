@@ -490,6 +490,28 @@ int sgl_top_k_top_p_sampling_from_probs(const float* probs, const float* uniform
                                         int top_k_val, float top_p_val, int d,
                                         int max_rounds, int deterministic, void* stream);
 
+/*
+ * The draws above from logits instead of probabilities: row r's
+ * probabilities are those sgl_softmax_temperature would write for the same
+ * logits and temperature (computed on the fly, the same bits when its probs
+ * buffer is 16-byte aligned), so the samples and success flags equal those
+ * of sgl_softmax_temperature followed by the mode's draw; the probabilities
+ * are never stored. mode: 0 plain (uniform fp32 [batch_size]), 1 top-k
+ * (top_k_f fp32 [batch] or top_k_val), 2 top-p (top_p_arr or top_p_val),
+ * 3 top-k + top-p (top_k_i int32 [batch] or top_k_val, and top p); modes
+ * 1-3 take uniform fp32 [max_rounds, batch_size] and write success when
+ * given. logits_dtype and temperatures as for sgl_softmax_temperature.
+ * Replaces: Sampler::sample's probabilities and draw together
+ *           (src/engine/engine.cc:306-333: torch::softmax of the scaled
+ *           logits, then flashinfer_*_sample_from_probs).
+ */
+int sgl_sampling_from_logits(const void* logits, int64_t logits_stride_row, int logits_dtype,
+                             const float* temperatures, float temperature, const float* uniform,
+                             int mode, const float* top_k_f, const int32_t* top_k_i,
+                             int top_k_val, const float* top_p_arr, float top_p_val,
+                             int32_t* out, uint8_t* success, int batch_size, int d,
+                             int max_rounds, void* stream);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 #endif

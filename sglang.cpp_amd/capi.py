@@ -88,6 +88,8 @@ _SIGNATURES = {
     "sgl_silu_and_mul": ([_vp, _vp, _i64, _i64, _i64, _i64, _i32, _vp], _i32),
     "sgl_gelu_and_mul": ([_vp, _vp, _i64, _i64, _i64, _i64, _i32, _vp], _i32),
     "sgl_softmax_temperature": ([_vp, _i64, _vp, _i64, _i32, _vp, _f32, _i64, _i64, _vp], _i32),
+    "sgl_sampling_from_logits": ([_vp, _i64, _i32, _vp, _f32, _vp, _i32, _vp, _vp, _i32, _vp, _f32,
+                                  _vp, _vp, _i32, _i32, _i32, _vp], _i32),
     "sgl_sampling_from_probs": ([_vp, _vp, _vp, _i32, _i32, _i32, _vp], _i32),
     "sgl_top_k_sampling_from_probs": ([_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32,
                                        _vp], _i32),
@@ -590,6 +592,49 @@ def softmax_temperature(logits: torch.Tensor, temperatures: Optional[torch.Tenso
                                          float(temperature), b, v, _stream(dev)),
            "sgl_softmax_temperature")
     return out
+
+
+def sampling_from_logits(logits: torch.Tensor, uniform_samples: torch.Tensor, mode: str,
+                         temperatures: Optional[torch.Tensor] = None, temperature: float = 1.0,
+                         top_k: Optional[torch.Tensor] = None, top_k_val: int = 0,
+                         top_p: Optional[torch.Tensor] = None, top_p_val: float = 0.0):
+    """Sampler::sample's probabilities and draw in one launch (engine.cc:306-333):
+    mode "plain" (uniform [batch]), "top_k" (top_k float32 [batch]), "top_p",
+    "top_k_top_p" (top_k int32 [batch]); the filtered modes take uniform
+    [max_rounds, batch]. Returns (samples int32 [batch], success bool [batch]
+    or None for the plain draw); equal to softmax_temperature followed by
+    the mode's draw from probabilities."""
+    m = {"plain": 0, "top_k": 1, "top_p": 2, "top_k_top_p": 3}[mode]
+    dev = _need_gpu(logits, uniform_samples, temperatures, top_k, top_p)
+    if logits.dim() != 2 or logits.stride(1) != 1:
+        raise ValueError("logits must be [batch, vocab] with contiguous rows")
+    codes = {torch.bfloat16: SGL_DTYPE_BF16, torch.float16: SGL_DTYPE_F16,
+             torch.float32: SGL_DTYPE_F32}
+    if logits.dtype not in codes:
+        raise ValueError("logits must be bf16, fp16 or float32")
+    b, v = logits.shape
+    dims = 1 if m == 0 else 2
+    if (uniform_samples.dtype != torch.float32 or not uniform_samples.is_contiguous()
+            or uniform_samples.dim() != dims or uniform_samples.shape[-1] != b):
+        raise ValueError("uniform_samples must be contiguous float32 "
+                         + ("[batch]" if dims == 1 else "[max_rounds, batch]"))
+    if temperatures is not None:
+        temperatures = temperatures.to(torch.float32).reshape(b).contiguous()
+    elif not temperature > 0:
+        raise ValueError("temperature must be positive")
+    tkf = _opt(top_k, torch.float32, b, "top_k") if m == 1 else None
+    tki = _opt(top_k, torch.int32, b, "top_k") if m == 3 else None
+    tp = _opt(top_p, torch.float32, b, "top_p") if m >= 2 else None
+    out = torch.empty(b, dtype=torch.int32, device=dev)
+    succ = None if m == 0 else torch.empty(b, dtype=torch.bool, device=dev)
+    rounds = 1 if m == 0 else uniform_samples.shape[0]
+    _check(lib().sgl_sampling_from_logits(_p(logits), logits.stride(0), codes[logits.dtype],
+                                          _p(temperatures), float(temperature),
+                                          _p(uniform_samples), m, _p(tkf), _p(tki),
+                                          int(top_k_val), _p(tp), float(top_p_val), _p(out),
+                                          _p(succ), b, v, rounds, _stream(dev)),
+           "sgl_sampling_from_logits")
+    return out, succ
 
 
 def _check_probs(probs: torch.Tensor, uniform: torch.Tensor, dims: int) -> None:

@@ -145,6 +145,15 @@ PYBIND11_MODULE(sgl_backend, m) {
       });
 
   m.def("sampling_probs", &sampling_probs, py::arg("logits"), py::arg("temperatures"));
+  m.def("sample_from_logits",
+        [](torch::Tensor logits, torch::Tensor temps, torch::Tensor u,
+           c10::optional<torch::Tensor> k, c10::optional<torch::Tensor> p) {
+          auto r = sample_from_logits(logits, temps, u, k.value_or(torch::Tensor()),
+                                      p.value_or(torch::Tensor()));
+          return py::make_tuple(r.samples, r.success);
+        },
+        py::arg("logits"), py::arg("temperatures"), py::arg("uniform_samples"),
+        py::arg("top_k") = py::none(), py::arg("top_p") = py::none());
   m.def("flashinfer_sample_from_probs", &flashinfer_sample_from_probs, py::arg("probs"),
         py::arg("uniform_samples"), py::arg("deterministic") = false);
   auto pair = [](const FlashInferSamplingResult& r) { return py::make_tuple(r.samples, r.success); };

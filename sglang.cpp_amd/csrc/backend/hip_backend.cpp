@@ -910,6 +910,46 @@ torch::Tensor sampling_probs(const torch::Tensor& logits, const torch::Tensor& t
   return probs;
 }
 
+FlashInferSamplingResult sample_from_logits(const torch::Tensor& logits,
+                                            const torch::Tensor& temperatures,
+                                            const torch::Tensor& uniform_samples,
+                                            const torch::Tensor& top_k, const torch::Tensor& top_p) {
+  TORCH_CHECK(logits.is_cuda() && logits.dim() == 2 && logits.stride(1) == 1,
+              "logits must be a [batch, vocab] device tensor with contiguous rows");
+  int dtype = SGL_DTYPE_F32;
+  if (logits.scalar_type() == torch::kBFloat16) dtype = SGL_DTYPE_BF16;
+  else if (logits.scalar_type() == torch::kFloat16) dtype = SGL_DTYPE_F16;
+  else TORCH_CHECK(logits.scalar_type() == torch::kFloat32, "logits must be bf16, fp16 or float32");
+  const int64_t batch = logits.size(0);
+  TORCH_CHECK(temperatures.numel() == batch, "one temperature per row");
+  auto temps = temperatures.to(logits.device()).to(torch::kFloat32).reshape({batch}).contiguous();
+  const bool has_k = top_k.defined(), has_p = top_p.defined();
+  const int mode = has_k && has_p ? 3 : has_k ? 1 : has_p ? 2 : 0;
+  TORCH_CHECK(uniform_samples.is_cuda() && uniform_samples.scalar_type() == torch::kFloat32 &&
+                  uniform_samples.is_contiguous() && uniform_samples.dim() == (mode == 0 ? 1 : 2) &&
+                  uniform_samples.size(-1) == batch,
+              "uniform_samples must be contiguous float32 [batch] (plain draw) or [rounds, batch]");
+  torch::Tensor k_f, k_i, p_f;
+  if (mode == 1) k_f = top_k.to(logits.device()).to(torch::kFloat32).reshape({batch}).contiguous();
+  if (mode == 3) k_i = top_k.to(logits.device()).to(torch::kInt32).reshape({batch}).contiguous();
+  if (mode >= 2) p_f = top_p.to(logits.device()).to(torch::kFloat32).reshape({batch}).contiguous();
+  FlashInferSamplingResult r;
+  r.samples = torch::empty({batch}, logits.options().dtype(torch::kInt32));
+  if (mode != 0) r.success = torch::empty({batch}, logits.options().dtype(torch::kBool));
+  check_sgl(sgl_sampling_from_logits(
+                logits.data_ptr(), logits.stride(0), dtype, temps.data_ptr<float>(), 1.0f,
+                uniform_samples.data_ptr<float>(), mode,
+                k_f.defined() ? k_f.data_ptr<float>() : nullptr,
+                k_i.defined() ? k_i.data_ptr<int32_t>() : nullptr, 0,
+                p_f.defined() ? p_f.data_ptr<float>() : nullptr, 0.0f, r.samples.data_ptr<int32_t>(),
+                mode != 0 ? reinterpret_cast<uint8_t*>(r.success.data_ptr<bool>()) : nullptr,
+                narrow_dim(batch, "batch"), narrow_dim(logits.size(1), "vocab"),
+                mode == 0 ? 1 : narrow_dim(uniform_samples.size(0), "rounds"),
+                current_stream(logits.device())),
+            "sgl_sampling_from_logits");
+  return r;
+}
+
 torch::Tensor flashinfer_sample_from_probs(const torch::Tensor& probs,
                                            const torch::Tensor& uniform_samples, bool deterministic) {
   check_probs(probs);

@@ -244,6 +244,17 @@ FlashInferSamplingResult flashinfer_top_k_top_p_sample_from_probs(
 // [batch] or [batch, 1], any floating type, on the logits' device).
 torch::Tensor sampling_probs(const torch::Tensor& logits, const torch::Tensor& temperatures);
 
+// Sampler::sample's probabilities and draw in one launch (engine.cc:306-333):
+// the draw the reference picks from which of top_k / top_p are defined
+// (both: top_k as int32; top_k only: as float32), uniform_samples [batch]
+// for the plain draw or [rounds, batch] otherwise; the probabilities are
+// sampling_probs' bits and are not stored. success is undefined for the
+// plain draw.
+FlashInferSamplingResult sample_from_logits(const torch::Tensor& logits,
+                                            const torch::Tensor& temperatures,
+                                            const torch::Tensor& uniform_samples,
+                                            const torch::Tensor& top_k, const torch::Tensor& top_p);
+
 // NeoX RoPE with a half-width fp32 cos/sin cache built on the device
 // (rotary_embedding.cu:75-94 builds the same table with LibTorch-CPU ops).
 class RotaryEmbedding {

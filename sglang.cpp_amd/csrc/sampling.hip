@@ -38,6 +38,7 @@
 #include <math.h>
 
 #include "common.h"
+#include "sampler_prob.h"
 
 namespace sgl {
 namespace {
@@ -73,6 +74,46 @@ struct SampleArgs {
   float top_p_val;
   int mode;  // 0 plain, 1 top-k, 2 top-p, 3 top-k + top-p
   bool vec;  // rows 16-byte aligned (d % 4 == 0 and an aligned base)
+  // Draws from logits (probs == nullptr): the probabilities are computed on
+  // the fly by sampler_prob.h, bit for bit those sgl_softmax_temperature
+  // writes.
+  const void* logits;
+  int64_t x_st;        // logits row stride (elements)
+  const float* temps;  // [batch] or null
+  float temp;
+  bool stats_vec;      // logits rows 16-byte aligned (the softmax kernel's vector path)
+  int logit_dtype;
+};
+
+// Where a draw reads the probability of element e of its row: the fp32
+// probabilities, or the logits through the Sampler's softmax.
+struct ProbRow {
+  const float* p;
+  __device__ f32x4_t load4(int64_t e) const { return *reinterpret_cast<const f32x4_t*>(p + e); }
+  __device__ float load1(int64_t e) const { return p[e]; }
+};
+
+template <int DT>
+struct LogitRow {
+  const char* x;
+  float inv_t, m, inv_s;
+  // Four consecutive elements from e (e % 4 == 0 on a 16-byte aligned row).
+  __device__ f32x4_t load4(int64_t e) const {
+    u32x4_t v;
+    if constexpr (DT == SGL_DTYPE_F32) {
+      v = *reinterpret_cast<const u32x4_t*>(x + e * 4);
+    } else {
+      const u32x2_t h = *reinterpret_cast<const u32x2_t*>(x + e * 2);
+      v = u32x4_t{h[0], h[1], 0u, 0u};
+    }
+    f32x4_t r;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) r[j] = sp::prob(sp::Elem<DT>::at(v, j), inv_t, m, inv_s);
+    return r;
+  }
+  __device__ float load1(int64_t e) const {
+    return sp::prob(sp::Elem<DT>::load1(x, e), inv_t, m, inv_s);
+  }
 };
 
 struct Shared {
@@ -134,20 +175,20 @@ struct BlockVals {
   f32x4_t v[kSub];
 };
 
-__device__ __forceinline__ void load_block(const float* __restrict__ row, int b, int d, bool full,
-                                           BlockVals& bv) {
+template <class Src>
+__device__ __forceinline__ void load_block(const Src& row, int b, int d, bool full, BlockVals& bv) {
   const int lane = threadIdx.x & 63;
   const int e0 = b * kBlock + kVec * lane;
   if (full) {
 #pragma unroll
-    for (int s = 0; s < kSub; ++s) bv.v[s] = *reinterpret_cast<const f32x4_t*>(row + e0 + kSpan * s);
+    for (int s = 0; s < kSub; ++s) bv.v[s] = row.load4(e0 + kSpan * s);
   } else {
 #pragma unroll
     for (int s = 0; s < kSub; ++s)
 #pragma unroll
       for (int j = 0; j < kVec; ++j) {
         const int e = e0 + kSpan * s + j;
-        bv.v[s][j] = e < d ? row[e] : 0.f;
+        bv.v[s][j] = e < d ? row.load1(e) : 0.f;
       }
   }
 }
@@ -222,9 +263,9 @@ __device__ __forceinline__ void sweep_block(const BlockVals& bv, int b, float th
 // kCompact: also copy the probabilities above cthr (the caller has zeroed
 // sh.ncand; an overflow shows as sh.ncand > kCandCap). Waves take blocks
 // round-robin, two blocks (8 loads per lane) in flight.
-template <bool kCompact>
-__device__ __forceinline__ void sweep(const float* __restrict__ row, int d, bool vec, float thr,
-                                      float cthr, Shared& sh) {
+template <bool kCompact, class Src>
+__device__ __forceinline__ void sweep(const Src& row, int d, bool vec, float thr, float cthr,
+                                      Shared& sh) {
   const int wave = threadIdx.x >> 6;
   const int nblk = (d + kBlock - 1) / kBlock;
   const int nfull = vec ? d / kBlock : 0;  // blocks loaded without bounds checks
@@ -280,8 +321,9 @@ __device__ __forceinline__ void sweep_cand(int d, float thr, Shared& sh) {
 // finds the first lane whose run crosses u, that lane walks its run to the
 // crossing block, and the wave scans that block. Leaves the index in
 // sh.sampled and its probability in sh.sampled_p.
-__device__ __forceinline__ void draw(const float* __restrict__ row, int d, bool vec, float thr,
-                                     float u, Shared& sh) {
+template <class Src>
+__device__ __forceinline__ void draw(const Src& row, int d, bool vec, float thr, float u,
+                                     Shared& sh) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int nblk = (d + kBlock - 1) / kBlock;
   if (wave == 0) {
@@ -319,13 +361,13 @@ __device__ __forceinline__ void draw(const float* __restrict__ row, int d, bool 
       if (vec && e0 + kPer <= d) {
 #pragma unroll
         for (int s = 0; s < kPer / 4; ++s) {
-          const f32x4_t v = *reinterpret_cast<const f32x4_t*>(row + e0 + 4 * s);
+          const f32x4_t v = row.load4(e0 + 4 * s);
 #pragma unroll
           for (int j = 0; j < 4; ++j) p[4 * s + j] = v[j];
         }
       } else {
 #pragma unroll
-        for (int i = 0; i < kPer; ++i) p[i] = e0 + i < d ? row[e0 + i] : 0.f;
+        for (int i = 0; i < kPer; ++i) p[i] = e0 + i < d ? row.load1(e0 + i) : 0.f;
       }
       float local = 0.f;
 #pragma unroll
@@ -363,16 +405,15 @@ __device__ __forceinline__ void draw(const float* __restrict__ row, int d, bool 
       }
     } else if (lane == 0) {
       sh.sampled = d - 1;
-      sh.sampled_p = row[d - 1];
+      sh.sampled_p = row.load1(d - 1);
     }
   }
   __syncthreads();
 }
 
-__global__ void __launch_bounds__(kThreads) sampling_kernel(SampleArgs a) {
-  __shared__ Shared sh;
+template <class Src>
+__device__ __forceinline__ void sample_row(const SampleArgs& a, const Src& row, Shared& sh) {
   const int row_id = blockIdx.x;
-  const float* __restrict__ row = a.probs + static_cast<int64_t>(row_id) * a.d;
   const bool cand_ok = a.mode != 0 && (a.d + kBlock - 1) / kBlock <= kCandBlocks;
   // The first sweep already copies the probabilities above cand_thr: at
   // most 1 / cand_thr of them in a normalised row, so any pivot at or above
@@ -436,13 +477,48 @@ __global__ void __launch_bounds__(kThreads) sampling_kernel(SampleArgs a) {
   }
 }
 
+// SRC < 0: rows of fp32 probabilities; else logits of element type SRC,
+// whose row max and sum are computed first exactly as the softmax kernel
+// computes them (its 512 statistics lanes; the other waves add nothing).
+template <int SRC>
+__global__ void __launch_bounds__(kThreads) sampling_kernel(SampleArgs a) {
+  __shared__ Shared sh;
+  const int row_id = blockIdx.x;
+  if constexpr (SRC < 0) {
+    sample_row(a, ProbRow{a.probs + static_cast<int64_t>(row_id) * a.d}, sh);
+  } else {
+    static_assert(kThreads >= sp::kStatLanes, "the statistics lanes are threads of the workgroup");
+    constexpr int B = 16 / sp::Elem<SRC>::kPer;
+    const char* x = static_cast<const char*>(a.logits) + static_cast<int64_t>(row_id) * a.x_st * B;
+    const float t = a.temps ? a.temps[row_id] : a.temp;
+    const float inv_t = 1.0f / t;
+    float mx, s;
+    sp::lane_stats<SRC>(x, a.d, a.stats_vec, threadIdx.x, inv_t, mx, s);
+    const float m = sp::block_max<kWaves>(mx, sh.wave_f);
+    const float inv_s = 1.0f / sp::block_sum<kWaves>(sp::lane_sum_at(mx, s, m), sh.wave_f);
+    sample_row(a, LogitRow<SRC>{x, inv_t, m, inv_s}, sh);
+  }
+}
+
 int launch_sampling(const SampleArgs& a, void* stream) {
   if (a.batch < 0 || a.d <= 0 || (a.mode != 0 && a.rounds <= 0)) return SGL_ERR_INVALID_ARG;
   if ((static_cast<int64_t>(a.d) + kBlock - 1) / kBlock > kMaxBlocks) return SGL_ERR_UNSUPPORTED;
   if (a.batch == 0) return SGL_OK;
-  if (!a.probs || !a.uniform || !a.out) return SGL_ERR_INVALID_ARG;
-  hipLaunchKernelGGL(sampling_kernel, dim3(a.batch), dim3(kThreads), 0,
-                     static_cast<hipStream_t>(stream), a);
+  if (!a.uniform || !a.out) return SGL_ERR_INVALID_ARG;
+  const dim3 grid(a.batch), block(kThreads);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (a.probs) {
+    hipLaunchKernelGGL(sampling_kernel<-1>, grid, block, 0, s, a);
+  } else if (a.logits) {
+    if (a.logit_dtype == SGL_DTYPE_BF16)
+      hipLaunchKernelGGL(sampling_kernel<SGL_DTYPE_BF16>, grid, block, 0, s, a);
+    else if (a.logit_dtype == SGL_DTYPE_F16)
+      hipLaunchKernelGGL(sampling_kernel<SGL_DTYPE_F16>, grid, block, 0, s, a);
+    else
+      hipLaunchKernelGGL(sampling_kernel<SGL_DTYPE_F32>, grid, block, 0, s, a);
+  } else {
+    return SGL_ERR_INVALID_ARG;
+  }
   return launch_status();
 }
 
@@ -506,5 +582,38 @@ extern "C" int sgl_top_k_top_p_sampling_from_probs(const float* probs, const flo
   a.top_k_val = top_k_val;
   a.top_p_arr = top_p_arr;
   a.top_p_val = top_p_val;
+  return launch_sampling(a, stream);
+}
+
+extern "C" int sgl_sampling_from_logits(const void* logits, int64_t logits_stride_row,
+                                        int logits_dtype, const float* temperatures,
+                                        float temperature, const float* uniform, int mode,
+                                        const float* top_k_f, const int32_t* top_k_i,
+                                        int top_k_val, const float* top_p_arr, float top_p_val,
+                                        int32_t* out, uint8_t* success, int batch_size, int d,
+                                        int max_rounds, void* stream) {
+  if (mode < 0 || mode > 3 || d <= 0 || logits_stride_row < d) return SGL_ERR_INVALID_ARG;
+  if (batch_size == 0) return SGL_OK;
+  if (!logits || (!temperatures && !(temperature > 0.f))) return SGL_ERR_INVALID_ARG;
+  int esize;
+  if (logits_dtype == SGL_DTYPE_BF16 || logits_dtype == SGL_DTYPE_F16) esize = 2;
+  else if (logits_dtype == SGL_DTYPE_F32) esize = 4;
+  else return SGL_ERR_UNSUPPORTED;
+  SampleArgs a = base_args(nullptr, uniform, out, mode == 0 ? nullptr : success, batch_size, d,
+                           mode == 0 ? 1 : max_rounds, mode);
+  a.logits = logits;
+  a.x_st = logits_stride_row;
+  a.logit_dtype = logits_dtype;
+  a.temps = temperatures;
+  a.temp = temperature;
+  a.stats_vec = aligned16(logits) && (logits_stride_row * esize) % 16 == 0;
+  a.vec = d % 4 == 0 && a.stats_vec;
+  if (mode == 1) a.top_k_f = top_k_f;
+  if (mode == 3) a.top_k_i = top_k_i;
+  a.top_k_val = top_k_val;
+  if (mode >= 2) {
+    a.top_p_arr = top_p_arr;
+    a.top_p_val = top_p_val;
+  }
   return launch_sampling(a, stream);
 }

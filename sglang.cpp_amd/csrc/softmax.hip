@@ -22,13 +22,17 @@
 #include <math.h>
 
 #include "common.h"
+#include "sampler_prob.h"
 
 namespace sgl {
 namespace {
 
+using sp::Elem;
+
 // 512 threads (two waves per SIMD, up to 256 VGPRs each): a 16-bit row of
-// 151,936 logits is 38 16-byte chunks (152 VGPRs) per lane.
-constexpr int kSmThreads = 512;
+// 151,936 logits is 38 16-byte chunks (152 VGPRs) per lane. The lanes are
+// the statistics lanes of sampler_prob.h.
+constexpr int kSmThreads = sp::kStatLanes;
 constexpr int kSmWaves = kSmThreads / kWave;
 constexpr int kMaxRegChunks = 40;  // 16-byte chunks a lane holds (160 VGPRs)
 // Word 3 of a raw buffer resource on gfx950 (32-bit data format, no
@@ -44,101 +48,12 @@ struct SoftmaxArgs {
   bool vec;            // 16-byte aligned rows (base and stride of both)
 };
 
-template <int DT>
-struct Elem;
-template <>
-struct Elem<SGL_DTYPE_BF16> {
-  static constexpr int kPer = 8;  // elements per 16-byte chunk
-  __device__ static float at(const u32x4_t& v, int j) {
-    const uint32_t w = v[j >> 1];
-    return (j & 1) ? bf16_hi(w) : bf16_lo(w);
-  }
-  __device__ static float load1(const void* p, int64_t i) {
-    return bf16_bits_to_f32(static_cast<const uint16_t*>(p)[i]);
-  }
-};
-template <>
-struct Elem<SGL_DTYPE_F16> {
-  static constexpr int kPer = 8;
-  __device__ static float at(const u32x4_t& v, int j) {
-    const uint32_t w = v[j >> 1];
-    return static_cast<float>(__builtin_bit_cast(f16_t, static_cast<uint16_t>((j & 1) ? w >> 16 : w)));
-  }
-  __device__ static float load1(const void* p, int64_t i) {
-    return static_cast<float>(__builtin_bit_cast(f16_t, static_cast<const uint16_t*>(p)[i]));
-  }
-};
-template <>
-struct Elem<SGL_DTYPE_F32> {
-  static constexpr int kPer = 4;
-  __device__ static float at(const u32x4_t& v, int j) { return __uint_as_float(v[j]); }
-  __device__ static float load1(const void* p, int64_t i) { return static_cast<const float*>(p)[i]; }
-};
-
-// Fixed-order workgroup reductions: wave reduction, then every wave folds
-// the 8 wave values in order.
-__device__ __forceinline__ float block_max(float x, float* sh) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) x = fmaxf(x, __shfl_xor(x, o, kWave));
-  __syncthreads();  // earlier readers of sh are done
-  if (lane == 0) sh[wave] = x;
-  __syncthreads();
-  float m = sh[0];
-#pragma unroll
-  for (int w = 1; w < kSmWaves; ++w) m = fmaxf(m, sh[w]);
-  return m;
-}
-
-__device__ __forceinline__ float block_sum(float x, float* sh) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o, kWave);
-  __syncthreads();
-  if (lane == 0) sh[wave] = x;
-  __syncthreads();
-  float s = 0.f;
-#pragma unroll
-  for (int w = 0; w < kSmWaves; ++w) s += sh[w];
-  return s;
-}
-
-constexpr float kLog2e = 1.4426950408889634f;
-
-// Running (max, sum of 2^((y - max) log2e)) of a lane, updated by n values.
-template <int N>
-__device__ __forceinline__ void online_update(const float (&y)[N], float& mx, float& s) {
-  float cm = y[0];
-#pragma unroll
-  for (int j = 1; j < N; ++j) cm = fmaxf(cm, y[j]);
-  if (cm > mx) {
-    s *= __builtin_amdgcn_exp2f((mx - cm) * kLog2e);  // 0 while mx = -inf
-    mx = cm;
-  }
-#pragma unroll
-  for (int j = 0; j < N; ++j) s += __builtin_amdgcn_exp2f((y[j] - mx) * kLog2e);
-}
-
-// Chunk c (elements [P c, P c + P), whole and inside the row) through
-// 16-byte global loads: the streaming path.
-template <int DT>
-__device__ __forceinline__ u32x4_t load_chunk(const char* row, int c) {
-  return *reinterpret_cast<const u32x4_t*>(row + static_cast<int64_t>(c) * 16);
-}
-
-// The elements of a chunk as fp32 scaled by 1 / t.
-template <int DT>
-__device__ __forceinline__ void scaled(const u32x4_t& v, float inv_t, float (&y)[Elem<DT>::kPer]) {
-#pragma unroll
-  for (int j = 0; j < Elem<DT>::kPer; ++j) y[j] = Elem<DT>::at(v, j) * inv_t;
-}
-
 // NC > 0 (16-byte aligned rows): the lane's whole chunks c = tid + T k,
 // k < NC, stay in registers (buffer loads: one lane offset, the chunk step
-// as the scalar offset, reads past the row return 0); NC == 0: every phase
-// streams the row (aligned rows by 16-byte loads, others element by
-// element). The partial last chunk of a row (d % P elements) belongs to one
-// lane, which takes it element by element.
+// as the scalar offset, reads past the row return 0); NC == 0: the row is
+// read again for the output. Either way the statistics follow
+// sp::lane_stats' order (whole chunks in k order, then the elements past
+// them one by one), so they are the same bits on both paths.
 template <int DT, int NC>
 __global__ void __launch_bounds__(kSmThreads) softmax_temperature_kernel(SoftmaxArgs a) {
   __shared__ float red[kSmWaves];
@@ -148,12 +63,13 @@ __global__ void __launch_bounds__(kSmThreads) softmax_temperature_kernel(Softmax
   const char* row = static_cast<const char*>(a.logits) + static_cast<int64_t>(r) * a.x_st * B;
   float* prow = a.probs + static_cast<int64_t>(r) * a.p_st;
   const int d = static_cast<int>(a.d);
-  const int nfull = a.vec ? d / P : 0;      // chunks taken 16 bytes at a time
-  const int e_tail = nfull * P;             // first element taken one by one
+  const int nfull = a.vec ? d / P : 0;  // chunks taken 16 bytes at a time
+  const int e_tail = nfull * P;         // first element taken one by one
   const int tid = threadIdx.x;
   const float t = a.temps ? a.temps[r] : a.temp;
   const float inv_t = 1.0f / t;
 
+  float mx, s;
   u32x4_t held[NC > 0 ? NC : 1];
   __amdgpu_buffer_rsrc_t prs;
   if constexpr (NC > 0) {
@@ -164,41 +80,30 @@ __global__ void __launch_bounds__(kSmThreads) softmax_temperature_kernel(Softmax
       held[k] = __builtin_bit_cast(
           u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rs, tid * 16, k * kSmThreads * 16, 0));
     prs = __builtin_amdgcn_make_buffer_rsrc(prow, 0, d * 4, kRawBufferWord3);
-  }
-
-  // Phase 1: running max and sum as the row arrives.
-  float mx = -INFINITY, s = 0.f;
-  if constexpr (NC > 0) {
+    mx = -INFINITY;
+    s = 0.f;
 #pragma unroll
     for (int k = 0; k < NC; ++k)
       if (tid + k * kSmThreads < nfull) {
         float y[P];
-        scaled<DT>(held[k], inv_t, y);
-        online_update(y, mx, s);
+        sp::scaled<DT>(held[k], inv_t, y);
+        sp::online_update(y, mx, s);
       }
-  } else {
-    for (int c = tid; c < nfull; c += kSmThreads) {
-      float y[P];
-      scaled<DT>(load_chunk<DT>(row, c), inv_t, y);
-      online_update(y, mx, s);
+    for (int e = e_tail + tid; e < d; e += kSmThreads) {
+      const float y[1] = {sp::scaled1(Elem<DT>::load1(row, e), inv_t)};
+      sp::online_update(y, mx, s);
     }
+  } else {
+    sp::lane_stats<DT>(row, d, a.vec, tid, inv_t, mx, s);
   }
-  // Elements past the whole chunks (the partial chunk, or every element of
-  // an unaligned row), one by one.
-  for (int e = e_tail + tid; e < d; e += kSmThreads) {
-    const float y[1] = {Elem<DT>::load1(row, e) * inv_t};
-    online_update(y, mx, s);
-  }
-  const float m = block_max(mx, red);
-  // The lane's sum relative to the row max (a lane with no element adds 0).
-  const float sl = mx == -INFINITY ? 0.f : s * __builtin_amdgcn_exp2f((mx - m) * kLog2e);
-  const float inv_s = 1.0f / block_sum(sl, red);
+  const float m = sp::block_max<kSmWaves>(mx, red);
+  const float inv_s = 1.0f / sp::block_sum<kSmWaves>(sp::lane_sum_at(mx, s, m), red);
 
-  // Phase 2: the probabilities.
-  auto prob = [&](float x) { return __builtin_amdgcn_exp2f((x * inv_t - m) * kLog2e) * inv_s; };
+  // The probabilities.
   if constexpr (NC > 0) {
     // Recompute y from the packed row: without this barrier the compiler
-    // keeps phase 1's fp32 values alive instead (twice the registers).
+    // keeps the fp32 values of the statistics pass alive instead (twice the
+    // registers).
 #pragma unroll
     for (int k = 0; k < NC; ++k) asm volatile("" : "+v"(held[k]));
 #pragma unroll
@@ -206,7 +111,7 @@ __global__ void __launch_bounds__(kSmThreads) softmax_temperature_kernel(Softmax
       if (tid + k * kSmThreads < nfull) {
         float p[P];
 #pragma unroll
-        for (int j = 0; j < P; ++j) p[j] = prob(Elem<DT>::at(held[k], j));
+        for (int j = 0; j < P; ++j) p[j] = sp::prob(Elem<DT>::at(held[k], j), inv_t, m, inv_s);
 #pragma unroll
         for (int q = 0; q < P / 4; ++q)
           __builtin_amdgcn_raw_buffer_store_b128(
@@ -215,17 +120,18 @@ __global__ void __launch_bounds__(kSmThreads) softmax_temperature_kernel(Softmax
       }
   } else {
     for (int c = tid; c < nfull; c += kSmThreads) {
-      const u32x4_t v = load_chunk<DT>(row, c);
+      const u32x4_t v = *reinterpret_cast<const u32x4_t*>(row + static_cast<int64_t>(c) * 16);
       float p[P];
 #pragma unroll
-      for (int j = 0; j < P; ++j) p[j] = prob(Elem<DT>::at(v, j));
+      for (int j = 0; j < P; ++j) p[j] = sp::prob(Elem<DT>::at(v, j), inv_t, m, inv_s);
 #pragma unroll
       for (int q = 0; q < P / 4; ++q)
         *reinterpret_cast<f32x4_t*>(prow + c * P + 4 * q) =
             f32x4_t{p[4 * q], p[4 * q + 1], p[4 * q + 2], p[4 * q + 3]};
     }
   }
-  for (int e = e_tail + tid; e < d; e += kSmThreads) prow[e] = prob(Elem<DT>::load1(row, e));
+  for (int e = e_tail + tid; e < d; e += kSmThreads)
+    prow[e] = sp::prob(Elem<DT>::load1(row, e), inv_t, m, inv_s);
 }
 
 template <int DT>
@@ -237,9 +143,7 @@ int launch_softmax(const SoftmaxArgs& a, hipStream_t s) {
   // lane; fp32 logits, longer and unaligned rows stream.
   if constexpr (DT == SGL_DTYPE_F32) {
     hipLaunchKernelGGL((softmax_temperature_kernel<DT, 0>), grid, block, 0, s, a);
-    return launch_status();
-  }
-  if (per_lane > kMaxRegChunks || !a.vec)
+  } else if (per_lane > kMaxRegChunks || !a.vec)
     hipLaunchKernelGGL((softmax_temperature_kernel<DT, 0>), grid, block, 0, s, a);
   else if (per_lane <= 8)
     hipLaunchKernelGGL((softmax_temperature_kernel<DT, 8>), grid, block, 0, s, a);

@@ -478,6 +478,31 @@ def test_sampling_probs_matches_c_abi(dev, sb):
 
 
 @pytest.mark.gpu
+def test_sample_from_logits_matches_c_abi(dev, sb):
+    """Sampler::sample's dispatch (engine.cc:310-333: top_k int32 beside
+    top_p, float32 alone; uniform [batch] for the plain draw) through the
+    C++ layer gives the C ABI's draws from logits."""
+    from conftest import capi
+    note("sample from logits")
+    g = _gen(dev, 23)
+    B, V = 6, 151936
+    logits = (torch.randn((B, V), device=dev, generator=g) * 3).to(torch.bfloat16)
+    temps = torch.linspace(0.6, 1.2, B, device=dev)
+    u1 = torch.rand(B, device=dev, generator=g)
+    u = torch.rand((32, B), device=dev, generator=g)
+    k = torch.randint(1, 64, (B,), device=dev, generator=g)
+    tp = torch.rand(B, device=dev, generator=g) * 0.5 + 0.45
+    s, ok = sb.sample_from_logits(logits, temps, u1)
+    assert ok is None and torch.equal(s, capi.sampling_from_logits(logits, u1, "plain", temps)[0])
+    s, ok = sb.sample_from_logits(logits, temps, u, k, tp)
+    r = capi.sampling_from_logits(logits, u, "top_k_top_p", temps, top_k=k.int(), top_p=tp)
+    assert torch.equal(s, r[0]) and torch.equal(ok, r[1])
+    s, ok = sb.sample_from_logits(logits, temps, u, k, None)
+    r = capi.sampling_from_logits(logits, u, "top_k", temps, top_k=k.float())
+    assert torch.equal(s, r[0]) and torch.equal(ok, r[1])
+
+
+@pytest.mark.gpu
 def test_sampling_functions_match_c_abi(dev, sb):
     """The reference's sampling API (include/sglang/engine/sampling.h:7-36) as
     the Sampler calls it (engine.cc:300-345: uniform [32, batch], top_k float32

@@ -321,3 +321,81 @@ def test_softmax_temperature_rejects_bad_arguments(dev):
     st = capi.lib().sgl_softmax_temperature(capi._p(probs), 8, capi._p(x), 16, 0, None, 1.0, 2, 16,
                                             None)
     assert st == -1  # row stride below vocab
+
+
+# ---------------------------------------------------------------- draws from logits
+#
+# sgl_sampling_from_logits computes each probability as sgl_softmax_temperature
+# writes it (same operations, same row statistics), so its samples and
+# success flags must equal those of softmax_temperature followed by the same
+# draw from probabilities, bit for bit.
+
+def _draw_from_probs(probs, u, mode, k, tp):
+    if mode == "plain":
+        return capi.sampling_from_probs(probs, u), None
+    if mode == "top_k":
+        return capi.top_k_sampling_from_probs(probs, u, k.float())
+    if mode == "top_p":
+        return capi.top_p_sampling_from_probs(probs, u, tp)
+    return capi.top_k_top_p_sampling_from_probs(probs, u, k.int(), 0, tp, 0.0)
+
+
+def _logits_case(dev, logits, temps, mode, seed, label):
+    note(f"sampling_from_logits {label} mode={mode} shape={tuple(logits.shape)} dtype={logits.dtype}")
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    B = logits.shape[0]
+    u = torch.rand((B,) if mode == "plain" else (32, B), device=dev, generator=g)
+    k = torch.randint(1, 80, (B,), device=dev, generator=g)
+    tp = torch.rand(B, device=dev, generator=g) * 0.5 + 0.45
+    probs = capi.softmax_temperature(logits, temps)
+    s_ref, ok_ref = _draw_from_probs(probs, u, mode, k, tp)
+    kk = None if mode in ("plain", "top_p") else (k.float() if mode == "top_k" else k.int())
+    s, ok = capi.sampling_from_logits(logits, u, mode, temps, top_k=kk,
+                                      top_p=tp if mode in ("top_p", "top_k_top_p") else None)
+    torch.cuda.synchronize()
+    assert torch.equal(s, s_ref), (label, mode, torch.nonzero(s != s_ref)[:5])
+    if ok_ref is not None:
+        assert torch.equal(ok, ok_ref), (label, mode)
+
+
+@pytest.mark.parametrize("mode", ["plain", "top_k", "top_p", "top_k_top_p"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_sampling_from_logits_equals_softmax_then_draw(dev, dtype, mode):
+    g = torch.Generator(device=dev)
+    g.manual_seed(21)
+    B = 12
+    logits = (torch.randn((B, QWEN3_VOCAB), device=dev, generator=g) * 3).to(dtype)
+    logits[3, 1::5] = float("-inf")
+    temps = torch.linspace(0.4, 1.5, B, device=dev)
+    _logits_case(dev, logits, temps, mode, 7, "qwen3")
+
+
+@pytest.mark.parametrize("vocab,offset,dtype", [
+    (1003, 0, torch.bfloat16),    # partial last chunk, d % 4 != 0
+    (5000, 1, torch.bfloat16),    # unaligned rows
+    (200001, 0, torch.float16),   # rows the softmax kernel streams
+    (4099, 1, torch.float32),     # unaligned fp32 rows
+])
+def test_sampling_from_logits_shapes(dev, vocab, offset, dtype):
+    g = torch.Generator(device=dev)
+    g.manual_seed(vocab)
+    B = 5
+    base = (torch.randn((B, vocab + 13), device=dev, generator=g) * 4).to(dtype)
+    logits = base[:, offset:offset + vocab]
+    temps = torch.tensor([0.5, 0.8, 1.0, 1.1, 2.0], device=dev)
+    for mode in ("plain", "top_k_top_p"):
+        _logits_case(dev, logits, temps, mode, vocab + 1, f"v{vocab}+{offset}")
+
+
+def test_sampling_from_logits_rejects_bad_arguments(dev):
+    x = torch.zeros((2, 64), device=dev, dtype=torch.bfloat16)
+    u = torch.rand(2, device=dev)
+    out = torch.empty(2, dtype=torch.int32, device=dev)
+    lib = capi.lib()
+    assert lib.sgl_sampling_from_logits(capi._p(x), 64, 0, None, 1.0, capi._p(u), 4, None, None, 0,
+                                        None, 0.0, capi._p(out), None, 2, 64, 1, None) == -1
+    assert lib.sgl_sampling_from_logits(capi._p(x), 64, 9, None, 1.0, capi._p(u), 0, None, None, 0,
+                                        None, 0.0, capi._p(out), None, 2, 64, 1, None) == -2
+    assert lib.sgl_sampling_from_logits(capi._p(x), 64, 0, None, 0.0, capi._p(u), 0, None, None, 0,
+                                        None, 0.0, capi._p(out), None, 2, 64, 1, None) == -1
