@@ -40,7 +40,7 @@ const char* sgl_status_string(int status);
 
 /* Library version, to check that the loaded .so matches this header. */
 int sgl_abi_version(void);
-#define SGL_ABI_VERSION 12
+#define SGL_ABI_VERSION 13
 
 /* ------------------------------------------------------------------ */
 /* KV-cache store                                                      */
