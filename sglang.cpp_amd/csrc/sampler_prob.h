@@ -2,10 +2,13 @@
 // kernel (softmax.hip) and the draws that read logits directly
 // (sampling.hip), so both compute every probability with the same
 // operations and get the same bits:
-//   y = x * (1 / t); per lane, a running max m and sum of 2^((y - m) log2e)
-//   over its chunks c = tid + kStatLanes k (elements [P c, P c + P)), then
-//   the elements past the whole chunks one by one; folded over the lanes in a
-//   fixed order; p = 2^((y - m) log2e) * (1 / sum).
+//   y = x * (1 / t); per statistics lane v < kStatLanes, a running max m and
+//   sum of 2^((y - m) log2e) over its chunks c = v + kStatLanes k
+//   (elements [P c, P c + P)), then the elements past the whole chunks one
+//   by one; folded in a fixed order (a butterfly within each group of 64
+//   lanes, then the 16 group values in order); p = 2^((y - m) log2e) *
+//   (1 / sum). A 1024-thread workgroup runs one lane per thread; a 512-thread
+//   workgroup runs lanes t and t + 512 on thread t.
 // Floating-point contraction is off in these functions: a fused multiply-add
 // chosen differently in the two kernels would change low bits.
 #pragma once
@@ -16,7 +19,7 @@ namespace sgl {
 namespace sp {
 
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr int kStatLanes = 512;  // lanes that compute a row's statistics
+constexpr int kStatLanes = 1024;  // lanes that compute a row's statistics
 constexpr int kStatWaves = kStatLanes / kWave;
 
 template <int DT>
@@ -89,10 +92,9 @@ __device__ __forceinline__ float lane_sum_at(float mx, float s, float m) {
   return mx == -INFINITY ? 0.f : s * __builtin_amdgcn_exp2f((mx - m) * kLog2e);
 }
 
-// Fixed-order reductions over the waves of a workgroup (only the first
-// kStatWaves hold statistics; the others contribute -inf / 0, which leaves
-// the folds' bits unchanged): wave reduction, then every wave folds the
-// wave values in wave order.
+// Fixed-order reductions over the kStatWaves groups of 64 statistics lanes:
+// a butterfly within each group, then every wave folds the group values in
+// order. One value per thread (1024 threads: group = wave) ...
 template <int kWaves>
 __device__ __forceinline__ float block_max(float x, float* sh) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -122,16 +124,58 @@ __device__ __forceinline__ float block_sum(float x, float* sh) {
   return s;
 }
 
-// A lane's statistics over a row read from memory (the streaming order of
-// the softmax kernel): chunks c = lane + kStatLanes k below nfull (aligned
-// rows), then elements from nfull * P one by one. lane >= kStatLanes: none.
+// ... or two per thread (512 threads: x0 for lane t = group w, x1 for lane
+// t + 512 = group w + 8), the same butterflies and the same fold.
+template <int kWaves>
+__device__ __forceinline__ float block_max2(float x0, float x1, float* sh) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    x0 = fmaxf(x0, __shfl_xor(x0, o, kWave));
+    x1 = fmaxf(x1, __shfl_xor(x1, o, kWave));
+  }
+  __syncthreads();
+  if (lane == 0) {
+    sh[wave] = x0;
+    sh[kWaves + wave] = x1;
+  }
+  __syncthreads();
+  float m = sh[0];
+#pragma unroll
+  for (int w = 1; w < 2 * kWaves; ++w) m = fmaxf(m, sh[w]);
+  return m;
+}
+
+template <int kWaves>
+__device__ __forceinline__ float block_sum2(float x0, float x1, float* sh) {
+#pragma clang fp contract(off)
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    x0 += __shfl_xor(x0, o, kWave);
+    x1 += __shfl_xor(x1, o, kWave);
+  }
+  __syncthreads();
+  if (lane == 0) {
+    sh[wave] = x0;
+    sh[kWaves + wave] = x1;
+  }
+  __syncthreads();
+  float s = 0.f;
+#pragma unroll
+  for (int w = 0; w < 2 * kWaves; ++w) s += sh[w];
+  return s;
+}
+
+// Statistics lane `lane`'s max and sum over a row read from memory: chunks
+// c = lane + kStatLanes k below nfull (aligned rows), then the elements from
+// nfull * P one by one.
 template <int DT>
 __device__ __forceinline__ void lane_stats(const char* row, int d, bool vec, int lane, float inv_t,
                                            float& mx, float& s) {
   constexpr int P = Elem<DT>::kPer;
   mx = -INFINITY;
   s = 0.f;
-  if (lane >= kStatLanes) return;
   const int nfull = vec ? d / P : 0;
   auto chunk = [&](int c) {
     return *reinterpret_cast<const u32x4_t*>(row + static_cast<int64_t>(c) * 16);

@@ -479,7 +479,7 @@ __device__ __forceinline__ void sample_row(const SampleArgs& a, const Src& row, 
 
 // SRC < 0: rows of fp32 probabilities; else logits of element type SRC,
 // whose row max and sum are computed first exactly as the softmax kernel
-// computes them (its 512 statistics lanes; the other waves add nothing).
+// computes them (one statistics lane per thread).
 template <int SRC>
 __global__ void __launch_bounds__(kThreads) sampling_kernel(SampleArgs a) {
   __shared__ Shared sh;
@@ -487,7 +487,7 @@ __global__ void __launch_bounds__(kThreads) sampling_kernel(SampleArgs a) {
   if constexpr (SRC < 0) {
     sample_row(a, ProbRow{a.probs + static_cast<int64_t>(row_id) * a.d}, sh);
   } else {
-    static_assert(kThreads >= sp::kStatLanes, "the statistics lanes are threads of the workgroup");
+    static_assert(kThreads == sp::kStatLanes, "one statistics lane per thread");
     constexpr int B = 16 / sp::Elem<SRC>::kPer;
     const char* x = static_cast<const char*>(a.logits) + static_cast<int64_t>(row_id) * a.x_st * B;
     const float t = a.temps ? a.temps[row_id] : a.temp;

@@ -30,9 +30,9 @@ namespace {
 using sp::Elem;
 
 // 512 threads (two waves per SIMD, up to 256 VGPRs each): a 16-bit row of
-// 151,936 logits is 38 16-byte chunks (152 VGPRs) per lane. The lanes are
-// the statistics lanes of sampler_prob.h.
-constexpr int kSmThreads = sp::kStatLanes;
+// 151,936 logits is 38 16-byte chunks (152 VGPRs) per lane. Thread t runs
+// the statistics lanes t and t + 512 of sampler_prob.h.
+constexpr int kSmThreads = sp::kStatLanes / 2;
 constexpr int kSmWaves = kSmThreads / kWave;
 constexpr int kMaxRegChunks = 40;  // 16-byte chunks a lane holds (160 VGPRs)
 // Word 3 of a raw buffer resource on gfx950 (32-bit data format, no
@@ -48,15 +48,16 @@ struct SoftmaxArgs {
   bool vec;            // 16-byte aligned rows (base and stride of both)
 };
 
-// NC > 0 (16-byte aligned rows): the lane's whole chunks c = tid + T k,
+// NC > 0 (16-byte aligned rows): the thread's whole chunks c = tid + T k,
 // k < NC, stay in registers (buffer loads: one lane offset, the chunk step
 // as the scalar offset, reads past the row return 0); NC == 0: the row is
 // read again for the output. Either way the statistics follow
-// sp::lane_stats' order (whole chunks in k order, then the elements past
-// them one by one), so they are the same bits on both paths.
+// sp::lane_stats' order for lanes tid and tid + T (whole chunks in order,
+// then the elements past them one by one), so they are the same bits on
+// both paths and in the draws from logits.
 template <int DT, int NC>
 __global__ void __launch_bounds__(kSmThreads) softmax_temperature_kernel(SoftmaxArgs a) {
-  __shared__ float red[kSmWaves];
+  __shared__ float red[2 * kSmWaves];
   constexpr int P = Elem<DT>::kPer;
   constexpr int B = 16 / P;  // bytes per element
   const int r = blockIdx.x;
@@ -69,7 +70,9 @@ __global__ void __launch_bounds__(kSmThreads) softmax_temperature_kernel(Softmax
   const float t = a.temps ? a.temps[r] : a.temp;
   const float inv_t = 1.0f / t;
 
-  float mx, s;
+  // Statistics lanes t (mx0, s0) and t + 512 (mx1, s1): held chunk j is
+  // chunk t + 512 j, i.e. lane t + 512 (j % 2)'s chunk j / 2.
+  float mx0, s0, mx1, s1;
   u32x4_t held[NC > 0 ? NC : 1];
   __amdgpu_buffer_rsrc_t prs;
   if constexpr (NC > 0) {
@@ -80,24 +83,31 @@ __global__ void __launch_bounds__(kSmThreads) softmax_temperature_kernel(Softmax
       held[k] = __builtin_bit_cast(
           u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rs, tid * 16, k * kSmThreads * 16, 0));
     prs = __builtin_amdgcn_make_buffer_rsrc(prow, 0, d * 4, kRawBufferWord3);
-    mx = -INFINITY;
-    s = 0.f;
+    mx0 = mx1 = -INFINITY;
+    s0 = s1 = 0.f;
 #pragma unroll
     for (int k = 0; k < NC; ++k)
       if (tid + k * kSmThreads < nfull) {
         float y[P];
         sp::scaled<DT>(held[k], inv_t, y);
-        sp::online_update(y, mx, s);
+        if (k % 2 == 0) sp::online_update(y, mx0, s0);
+        else sp::online_update(y, mx1, s1);
       }
-    for (int e = e_tail + tid; e < d; e += kSmThreads) {
+    for (int e = e_tail + tid; e < d; e += sp::kStatLanes) {
       const float y[1] = {sp::scaled1(Elem<DT>::load1(row, e), inv_t)};
-      sp::online_update(y, mx, s);
+      sp::online_update(y, mx0, s0);
+    }
+    for (int e = e_tail + tid + kSmThreads; e < d; e += sp::kStatLanes) {
+      const float y[1] = {sp::scaled1(Elem<DT>::load1(row, e), inv_t)};
+      sp::online_update(y, mx1, s1);
     }
   } else {
-    sp::lane_stats<DT>(row, d, a.vec, tid, inv_t, mx, s);
+    sp::lane_stats<DT>(row, d, a.vec, tid, inv_t, mx0, s0);
+    sp::lane_stats<DT>(row, d, a.vec, tid + kSmThreads, inv_t, mx1, s1);
   }
-  const float m = sp::block_max<kSmWaves>(mx, red);
-  const float inv_s = 1.0f / sp::block_sum<kSmWaves>(sp::lane_sum_at(mx, s, m), red);
+  const float m = sp::block_max2<kSmWaves>(mx0, mx1, red);
+  const float inv_s = 1.0f / sp::block_sum2<kSmWaves>(sp::lane_sum_at(mx0, s0, m),
+                                                      sp::lane_sum_at(mx1, s1, m), red);
 
   // The probabilities.
   if constexpr (NC > 0) {
