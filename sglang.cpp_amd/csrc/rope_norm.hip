@@ -288,22 +288,27 @@ __global__ void __launch_bounds__(256) fused_qknorm_rope_store_kernel(
   const bool is_v = r >= hq + hkv;
   const bool is_q = r < hq;
   const uint16_t* w = is_q ? qw : kw;
+  // Addresses are a workgroup-uniform 64-bit row base (the token is uniform)
+  // plus a 32-bit lane offset, so each access is one scalar-base
+  // instruction and no per-lane 64-bit address is held.
+  const uint32_t lane_off = static_cast<uint32_t>(r * D + lane_in_row * 8);
   u32x4_t raw[NT];
   int64_t slot[NT], pos[NT];
-  uint16_t* src[NT];
+  uint16_t* rowb[NT];
 #pragma unroll
   for (int k = 0; k < NT; ++k) {
     const int64_t t = min(tb * NT + k, num_tokens - 1);
-    src[k] = qkv + t * qkv_st + static_cast<int64_t>(r) * D + lane_in_row * 8;
-    raw[k] = ldg128(src[k]);
+    rowb[k] = qkv + t * qkv_st;
+    raw[k] = ldg128(rowb[k] + lane_off);
     slot[k] = out_loc[t];
     pos[k] = positions[t];
   }
+  const uint32_t head_off = static_cast<uint32_t>(lane_in_row * 8);
   if (is_v) {  // v row: raw copy into the cache
-    const int h = r - hq - hkv;
+    const uint32_t h_off = static_cast<uint32_t>((r - hq - hkv) * D) + head_off;
 #pragma unroll
     for (int k = 0; k < NT; ++k)
-      if (tb * NT + k < num_tokens) stg128(v_cache + (slot[k] * hkv + h) * D + lane_in_row * 8, raw[k]);
+      if (tb * NT + k < num_tokens) stg128(v_cache + slot[k] * hkv * D + h_off, raw[k]);
     return;
   }
   float wf[8];
@@ -354,11 +359,8 @@ __global__ void __launch_bounds__(256) fused_qknorm_rope_store_kernel(
     for (int i = 0; i < 8; ++i) x[i] = rope_one(x[i], p[i], c[i], sn[i]);
     const u32x4_t packed = pack8(x);
     if (tb * NT + k < num_tokens) {
-      if (is_q || k_back) stg128(src[k], packed);
-      if (!is_q) {
-        const int h = r - hq;
-        stg128(k_cache + (slot[k] * hkv + h) * D + lane_in_row * 8, packed);
-      }
+      if (is_q || k_back) stg128(rowb[k] + lane_off, packed);
+      if (!is_q) stg128(k_cache + slot[k] * hkv * D + (static_cast<uint32_t>((r - hq) * D) + head_off), packed);
     }
   }
 }
