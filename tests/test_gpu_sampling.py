@@ -399,3 +399,45 @@ def test_sampling_from_logits_rejects_bad_arguments(dev):
                                         None, 0.0, capi._p(out), None, 2, 64, 1, None) == -2
     assert lib.sgl_sampling_from_logits(capi._p(x), 64, 0, None, 0.0, capi._p(u), 0, None, None, 0,
                                         None, 0.0, capi._p(out), None, 2, 64, 1, None) == -1
+
+
+def test_sampler_entry_points_replay_in_a_graph(dev):
+    """softmax_temperature and the draw from logits captured once in a HIP
+    graph; each replay, with new logits and uniforms written in place and
+    eager work between replays, equals the eager calls on the same inputs."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(99)
+    B, V = 16, QWEN3_VOCAB
+    logits = torch.empty((B, V), device=dev, dtype=torch.bfloat16)
+    temps = torch.linspace(0.5, 1.3, B, device=dev)
+    u = torch.empty((32, B), device=dev)
+    k = torch.full((B,), 40, dtype=torch.int32, device=dev)
+    tp = torch.full((B,), 0.85, device=dev)
+    probs = torch.empty((B, V), device=dev)
+
+    def fill(i):
+        logits.copy_((torch.randn((B, V), device=dev, generator=g) * (2 + i)).to(torch.bfloat16))
+        u.copy_(torch.rand((32, B), device=dev, generator=g))
+
+    fill(0)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):  # warm-up outside the capture
+        capi.softmax_temperature(logits, temps, out=probs)
+        capi.sampling_from_logits(logits, u, "top_k_top_p", temps, top_k=k, top_p=tp)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        capi.softmax_temperature(logits, temps, out=probs)
+        s_g, ok_g = capi.sampling_from_logits(logits, u, "top_k_top_p", temps, top_k=k, top_p=tp)
+    for i in range(4):
+        note(f"graph replay {i}")
+        fill(i + 1)
+        graph.replay()
+        torch.cuda.synchronize()
+        p_eager = capi.softmax_temperature(logits, temps)
+        s_e, ok_e = capi.sampling_from_logits(logits, u, "top_k_top_p", temps, top_k=k, top_p=tp)
+        torch.cuda.synchronize()
+        assert torch.equal(probs, p_eager)
+        assert torch.equal(s_g, s_e) and torch.equal(ok_g, ok_e)
+    del graph
