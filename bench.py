@@ -64,6 +64,9 @@ def parse():
     ap.add_argument("--ceilings-only", action="store_true",
                     help="only measure the practical ceilings of this GPU (stream read, MFMA "
                          "issue on random and constant bf16 operands, empty launch) and print them")
+    ap.add_argument("--replay-host-only", action="store_true",
+                    help="only measure the host cost of prepare_metadata + prepare_for_replay "
+                         "per serving step (configurations 4 and 5)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB (steps times): "
                          "the known-size reference for rocprofv3 FETCH_SIZE / WRITE_SIZE")
@@ -158,6 +161,37 @@ def load_traffic(key):
 
 # ------------------------------------------------------------------ workloads
 
+# The MI355X's last-level (Infinity) cache holds 256 MB: a workload whose
+# buffers fit in it and are re-run back to back is partly served from that
+# cache, not HBM. HBM-bound workloads below this size are therefore timed
+# over several independent buffer sets used in turn, enough that the bytes
+# touched between two uses of one set exceed ROTATE_BYTES; the figure on one
+# set (cache-resident) is reported beside it.
+ROTATE_BYTES = 512 << 20
+
+
+def rotation_sets(set_bytes):
+    """Buffer sets so that the other sets touch >= ROTATE_BYTES between two
+    uses of one set."""
+    return max(1, -(-ROTATE_BYTES // max(1, int(set_bytes))) + 1)
+
+
+def rotating(steps):
+    """One step function that runs the given steps in turn (under graph
+    capture each captured call keeps the set it was captured on)."""
+    if len(steps) == 1:
+        return steps[0]
+    state = {"i": 0}
+
+    def step():
+        i = state["i"]
+        state["i"] = (i + 1) % len(steps)
+        steps[i]()
+
+    return step
+
+
+
 def setup_decode(torch, capi, wl, w, dev, seed=0):
     b, s = w.batch, w.shape
     g = torch.Generator(device=dev)
@@ -182,41 +216,40 @@ def setup_decode(torch, capi, wl, w, dev, seed=0):
     return step, nbytes, flops, dict(q=q, kc=kc, vc=vc, plan=plan)
 
 
-def setup_prefill(torch, capi, wl, w, dev, seed=0):
+def setup_prefill(torch, capi, wl, w, dev, seed=0, sets=1):
     b, s = w.batch, w.shape
     g = torch.Generator(device=dev)
     g.manual_seed(seed)
     hq, hkv, D = s.num_qo_heads, s.num_kv_heads, s.head_dim
     rows = int(b.qo_indptr[-1])
-    kc = torch.randn((b.num_slots, hkv, D), device=dev, generator=g).to(torch.bfloat16)
-    vc = torch.randn((b.num_slots, hkv, D), device=dev, generator=g).to(torch.bfloat16)
-    qkv = torch.randn((rows, s.qkv_width), device=dev, generator=g).to(torch.bfloat16)
-    q = qkv[:, :hq * D].view(-1, hq, D)
-    o = torch.empty((rows, hq, D), device=dev, dtype=torch.bfloat16)
     idx = torch.from_numpy(b.indices).to(dev)
     qop = torch.from_numpy(b.qo_indptr).to(dev)
     kvp = torch.from_numpy(b.kv_indptr).to(dev)
     scale = 1.0 / math.sqrt(D)
     max_qo = int(b.qo_lens.max())
 
-    def step():
-        capi.paged_prefill(q, kc, vc, idx, qop, kvp, max_qo, o, scale)
+    def one_set():
+        kc = torch.randn((b.num_slots, hkv, D), device=dev, generator=g).to(torch.bfloat16)
+        vc = torch.randn((b.num_slots, hkv, D), device=dev, generator=g).to(torch.bfloat16)
+        qkv = torch.randn((rows, s.qkv_width), device=dev, generator=g).to(torch.bfloat16)
+        q = qkv[:, :hq * D].view(-1, hq, D)
+        o = torch.empty((rows, hq, D), device=dev, dtype=torch.bfloat16)
+
+        def step():
+            capi.paged_prefill(q, kc, vc, idx, qop, kvp, max_qo, o, scale)
+        return step
 
     nbytes = wl.attention_bytes(s, b.qo_lens, b.kv_lens, b.page_size)
     flops = wl.attention_flops(s, b.qo_lens, b.kv_lens, causal=True)
-    return step, nbytes, flops
+    return rotating([one_set() for _ in range(sets)]), nbytes, flops
 
 
-def setup_fused(torch, capi, wl, w, dev, seed=0):
+def setup_fused(torch, capi, wl, w, dev, seed=0, sets=1):
     b, s = w.batch, w.shape
     g = torch.Generator(device=dev)
     g.manual_seed(seed)
     hq, hkv, D = s.num_qo_heads, s.num_kv_heads, s.head_dim
     T = int(b.qo_indptr[-1])
-    qkv = torch.randn((T, s.qkv_width), device=dev, generator=g).to(torch.bfloat16)
-    slots = T
-    kc = torch.empty((slots, hkv, D), device=dev, dtype=torch.bfloat16)
-    vc = torch.empty_like(kc)
     qw = (torch.rand(D, device=dev, generator=g) + 0.5).to(torch.bfloat16)
     kw = (torch.rand(D, device=dev, generator=g) + 0.5).to(torch.bfloat16)
     cos, sin = capi.rope_cos_sin_cache(w.extra["max_pos"], D, w.extra["theta"], dev)
@@ -226,13 +259,19 @@ def setup_fused(torch, capi, wl, w, dev, seed=0):
     # The pass is in place; repeated steps re-normalise already-normalised
     # rows, which costs the same bytes and keeps values finite.
 
-    def step():
-        # The pass as the attention layer runs it: k goes to the pool only
-        # (the algorithmic byte count has no k write-back into qkv).
-        capi.fused_qknorm_rope_store(qkv, kc, vc, qw, kw, cos, sin, pos, loc, hq, hkv, D, eps,
-                                     write_k_back=False)
+    def one_set():
+        qkv = torch.randn((T, s.qkv_width), device=dev, generator=g).to(torch.bfloat16)
+        kc = torch.empty((T, hkv, D), device=dev, dtype=torch.bfloat16)
+        vc = torch.empty_like(kc)
 
-    return step, wl.fused_store_bytes(s, T)
+        def step():
+            # The pass as the attention layer runs it: k goes to the pool only
+            # (the algorithmic byte count has no k write-back into qkv).
+            capi.fused_qknorm_rope_store(qkv, kc, vc, qw, kw, cos, sin, pos, loc, hq, hkv, D,
+                                         eps, write_k_back=False)
+        return step
+
+    return rotating([one_set() for _ in range(sets)]), wl.fused_store_bytes(s, T)
 
 
 def setup_mixed(torch, wl, w, dev, layers, seed=0):
@@ -313,6 +352,64 @@ def setup_mixed(torch, wl, w, dev, layers, seed=0):
     pre_flops = wl.attention_flops(s, qo[pre], kvl[pre], causal=True) * layers
     pre_bytes = wl.attention_bytes(s, qo[pre], kvl[pre], b.page_size) * layers
     return graph.replay, dec_bytes, pre_flops, pre_bytes, (graph, cache, backend, batch, alt, qkv)
+
+
+def measure_replay_host(torch, wl, dev, iters=200):
+    """Host cost of one serving step's metadata on the graph-replay path:
+    prepare_metadata (the scheduler's per-step call, scheduler.cc:338) plus
+    prepare_for_replay (GraphRunner::replay, engine.cc:732-743), CPU wall
+    clock per step, at configuration 4's decode batch (256 requests, one
+    captured batch size) and configuration 5's mixed step (64 decode rows +
+    a 2048-token chunk). Each step's calls are timed alone (the device
+    synchronised before them); reported as the median and 90th percentile
+    over `iters` steps, plus each call's median."""
+    import __graft_entry__ as entry
+    sb = entry.load_package().backend.load()
+    out = {}
+    for name, w in (("cfg4", wl.cfg4_decode_large()), ("cfg5", wl.cfg5_mixed(layers=1))):
+        b, sh = w.batch, w.shape
+        cache = sb.MHAKVCache(sh.num_kv_heads, 1, sh.head_dim, b.num_pages + 1, b.page_size,
+                              dev.index or 0)
+        backend = sb.HipAttnBackend(cache, sh.num_qo_heads, sh.num_kv_heads, sh.head_dim)
+        backend.set_page_table(torch.from_numpy(b.page_table).to(dev))
+        max_seq = int(b.page_table.shape[1])
+        decode = name == "cfg4"
+        if decode:
+            backend.init_capture_graph(max_seq, [b.batch_size])
+        else:
+            qo = b.qo_lens
+            backend.init_mixed_capture_graph(max_seq, int((qo == 1).sum()), int((qo > 1).sum()),
+                                             int(qo[qo > 1].max()))
+        pos = torch.from_numpy(b.positions).to(dev)
+        loc = torch.from_numpy(b.out_loc).to(dev)
+
+        def batch_of(shift):
+            reqs = [sb.Req(int(b.table_idx[i]), int(b.cached_lens[i]) - shift,
+                           int(b.device_lens[i]) - shift) for i in range(b.batch_size)]
+            return sb.Batch(not decode, reqs, pos, loc)
+
+        cap = batch_of(0)
+        backend.prepare_for_capture(cap)
+        t_meta, t_rep, t_all = [], [], []
+        for i in range(iters + 20):
+            nb = batch_of(i % 2)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            backend.prepare_metadata(nb)
+            t1 = time.perf_counter()
+            backend.prepare_for_replay(nb)
+            t2 = time.perf_counter()
+            if i >= 20:
+                t_meta.append(t1 - t0)
+                t_rep.append(t2 - t1)
+                t_all.append(t2 - t0)
+        torch.cuda.synchronize()
+        us = lambda v, q=50: round(float(np.percentile(np.asarray(v) * 1e6, q)), 1)
+        out[name] = {"step_us_median": us(t_all), "step_us_p90": us(t_all, 90),
+                     "prepare_metadata_us": us(t_meta), "prepare_for_replay_us": us(t_rep),
+                     "requests": int(b.batch_size), "iters": iters}
+        del backend, cache
+    return out
 
 
 # ------------------------------------------------------------------ CPU baseline
@@ -477,7 +574,7 @@ def roofline_mfma(flops, kernel_ms, traffic_key):
 RESID_TOKENS, RESID_HIDDEN, RESID_INTER = 8192, 4096, 12288  # Qwen3-8B, one 8192-token chunk
 
 
-def setup_resid(torch, capi, name, dev, seed=0):
+def setup_resid(torch, capi, name, dev, seed=0, sets=1):
     """Residual-path kernels at the Qwen3-8B shape (qwen3.cc:24-31 and
     utils.cc:49 call them once per layer). Algorithmic bytes: fused add +
     RMSNorm reads x and residual and writes both (8 T d) plus the weight;
@@ -487,30 +584,37 @@ def setup_resid(torch, capi, name, dev, seed=0):
     T = RESID_TOKENS
     if name == "resid_norm":
         d = RESID_HIDDEN
-        x = torch.randn((T, d), device=dev, generator=g).to(torch.bfloat16)
-        r = torch.randn((T, d), device=dev, generator=g).to(torch.bfloat16)
         w = (torch.rand(d, device=dev, generator=g) + 0.5).to(torch.bfloat16)
 
-        def step():
-            # in place on x and r; repeated steps keep values finite (x is
-            # renormalised each time, r grows by at most ~|x| per step)
-            capi.fused_add_rmsnorm(x, r, w, 1e-6)
+        def one_set():
+            x = torch.randn((T, d), device=dev, generator=g).to(torch.bfloat16)
+            r = torch.randn((T, d), device=dev, generator=g).to(torch.bfloat16)
 
-        return step, 8 * T * d + 2 * d, {"tokens": T, "hidden": d}
+            def step():
+                # in place on x and r; repeated steps keep values finite (x is
+                # renormalised each time, r grows by at most ~|x| per step)
+                capi.fused_add_rmsnorm(x, r, w, 1e-6)
+            return step
+
+        return (rotating([one_set() for _ in range(sets)]), 8 * T * d + 2 * d,
+                {"tokens": T, "hidden": d})
     d = RESID_INTER
-    inp = torch.randn((T, 2 * d), device=dev, generator=g).to(torch.bfloat16)
-    out = torch.empty((T, d), device=dev, dtype=torch.bfloat16)
 
-    def step():
-        capi.silu_and_mul(out, inp)
+    def one_set():
+        inp = torch.randn((T, 2 * d), device=dev, generator=g).to(torch.bfloat16)
+        out = torch.empty((T, d), device=dev, dtype=torch.bfloat16)
 
-    return step, 6 * T * d, {"tokens": T, "intermediate": d}
+        def step():
+            capi.silu_and_mul(out, inp)
+        return step
+
+    return rotating([one_set() for _ in range(sets)]), 6 * T * d, {"tokens": T, "intermediate": d}
 
 
 SAMPLING_BATCH, QWEN3_VOCAB = 256, 151936
 
 
-def setup_sampling(torch, capi, dev, seed=0):
+def setup_sampling(torch, capi, dev, seed=0, sets=1):
     """Top-k + top-p draw as the reference's Sampler::sample runs it
     (engine.cc:300-345): probs = softmax(logits / T) fp32 [256, 151936],
     uniform [32, 256], per-row top_k int32 and top_p. Algorithmic bytes: one
@@ -518,19 +622,22 @@ def setup_sampling(torch, capi, dev, seed=0):
     g = torch.Generator(device=dev)
     g.manual_seed(seed)
     B, V = SAMPLING_BATCH, QWEN3_VOCAB
-    logits = torch.randn((B, V), device=dev, generator=g) * 3
     temp = torch.linspace(0.6, 1.2, B, device=dev).view(B, 1)
-    probs = torch.softmax(logits / temp, -1).contiguous()
-    del logits
     u = torch.rand((32, B), device=dev, generator=g)
     k = torch.full((B,), 50, dtype=torch.int32, device=dev)
     tp = torch.full((B,), 0.9, dtype=torch.float32, device=dev)
 
-    def step():
-        capi.top_k_top_p_sampling_from_probs(probs, u, k, 0, tp, 0.0)
+    def one_set():
+        logits = torch.randn((B, V), device=dev, generator=g) * 3
+        probs = torch.softmax(logits / temp, -1).contiguous()
+        del logits
 
-    return step, B * V * 4 + 32 * B * 4 + B * 5, {"batch": B, "vocab": V, "top_k": 50,
-                                                  "top_p": 0.9}
+        def step():
+            capi.top_k_top_p_sampling_from_probs(probs, u, k, 0, tp, 0.0)
+        return step
+
+    return rotating([one_set() for _ in range(sets)]), B * V * 4 + 32 * B * 4 + B * 5, {
+        "batch": B, "vocab": V, "top_k": 50, "top_p": 0.9}
 
 
 # ------------------------------------------------------------------ ceilings
@@ -551,6 +658,8 @@ def load_probes():
     lib.sgl_probe_page_read.restype = i32
     lib.sgl_probe_decode_read.argtypes = [vp, vp, vp, i32, i32, i32, i32, i32, vp, vp]
     lib.sgl_probe_decode_read.restype = i32
+    lib.sgl_probe_stream_copy.argtypes = [vp, vp, i64, i32, i32, vp]
+    lib.sgl_probe_stream_copy.restype = i32
     for f in (lib.sgl_probe_stream_read, lib.sgl_probe_mfma_bf16, lib.sgl_probe_empty):
         f.restype = i32
     return lib
@@ -665,6 +774,39 @@ def measure_ceilings(torch, dev, min_warm_s=0.5, sweep=None):
             dbest[key] = round(gbs, 1)
     out["decode_read_pattern"] = {"GB/s": dbest, "bytes": nbytes, "page_slots": 16,
                                   "slot_bytes": 2048}
+    # read + write streams: a copy of 1 GiB into another 1 GiB, the same in
+    # place, and a 2 GiB fill (bytes counted: everything read plus written)
+    half = nbytes // 2
+    a_, b_ = buf[:half], buf[half:]
+    for key, src_, dst_, n_, counted, vars_ in (
+            ("stream_copy", a_, b_, half, 2 * half, (0, 1, 2, 3, 4, 5, 6, 7)),
+            ("stream_copy_inplace", a_, a_, half, 2 * half, (0, 1, 2, 3, 4, 5, 6, 7)),
+            ("stream_write", None, buf, nbytes, nbytes, (8, 10, 12, 14))):
+        cbest = (0.0, 0, 0)
+        for variant, cgrid in [(v, gr) for v in vars_ for gr in (1024, 2048, 4096, 8192)]:
+            def goc():
+                _probe_ok(lib.sgl_probe_stream_copy(
+                    None if src_ is None else src_.data_ptr(), dst_.data_ptr(), n_, cgrid,
+                    variant, sp), "sgl_probe_stream_copy")
+            for _ in range(3):
+                goc()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(s)
+            for _ in range(10):
+                goc()
+            e1.record(s)
+            torch.cuda.synchronize()
+            gbs = counted / (e0.elapsed_time(e1) / 10 * 1e-3) / 1e9
+            if sweep is not None:
+                sweep.append({"probe": key, "variant": variant, "grid": cgrid,
+                              "GB/s": round(gbs, 1)})
+            if gbs > cbest[0]:
+                cbest = (gbs, cgrid, variant)
+        out[key] = {"GB/s": round(cbest[0], 1), "frac_of_published": round(cbest[0] / HBM_PEAK_GBS, 4),
+                    "grid": cbest[1], "nt_loads": bool(cbest[2] & 1),
+                    "nt_stores": bool(cbest[2] & 2), "in_flight": 16 if cbest[2] & 4 else 8,
+                    "bytes": counted}
     del buf
     out["stream_read"] = {"GB/s": round(best[0], 1), "frac_of_published": round(best[0] / HBM_PEAK_GBS, 4),
                           "grid": best[1], "loads_in_flight": 4 << ((best[2] >> 1) & 3),
@@ -713,21 +855,31 @@ def measure_ceilings(torch, dev, min_warm_s=0.5, sweep=None):
     return out
 
 
+# HBM-bound workloads that write a third or more of their bytes: held
+# against the streaming copy's ceiling (read and write together), the
+# others against the streaming read's.
+WRITE_HEAVY = ("cfg3", "resid_norm", "resid_act", "sampler_softmax")
+
+
 def ceiling_fracs(extra, ceil):
     """Each kernel's achieved rate over the practical ceiling of its bound."""
     sr = ceil["stream_read"]["GB/s"]
+    cr = ceil.get("stream_copy", {}).get("GB/s", sr)
     mr = ceil["mfma_random"]["TFLOP/s"]
     fr = {}
     for name, rec in extra.items():
         rl = rec.get("roofline") if isinstance(rec, dict) else None
         if not rl:
             continue
-        c = sr if rl["bound"] == "hbm" else mr
+        if rl["bound"] == "hbm":
+            c = cr if name in WRITE_HEAVY else sr
+        else:
+            c = mr
         fr[name] = round(rl["achieved"] / c, 4)
     return fr
 
 
-def setup_sampler_softmax(torch, capi, dev, seed=0):
+def setup_sampler_softmax(torch, capi, dev, seed=0, sets=1):
     """The probabilities of Sampler::sample (engine.cc:306-308) for the
     sampling workload's batch: bf16 logits [256, 151936] (the LM head's
     output), per-row temperatures. Algorithmic bytes: one read of the
@@ -737,21 +889,25 @@ def setup_sampler_softmax(torch, capi, dev, seed=0):
     g = torch.Generator(device=dev)
     g.manual_seed(seed)
     B, V = SAMPLING_BATCH, QWEN3_VOCAB
-    logits = (torch.randn((B, V), device=dev, generator=g) * 3).to(torch.bfloat16)
     temps = torch.linspace(0.6, 1.2, B, device=dev)
-    out = torch.empty((B, V), device=dev)
 
-    def step():
-        capi.softmax_temperature(logits, temps, out=out)
+    def one_set():
+        logits = (torch.randn((B, V), device=dev, generator=g) * 3).to(torch.bfloat16)
+        out = torch.empty((B, V), device=dev)
 
-    def torch_step():
-        torch.softmax(logits.to(torch.float32) / temps.view(B, 1), -1)
+        def step():
+            capi.softmax_temperature(logits, temps, out=out)
 
-    return step, torch_step, B * V * (2 + 4) + 4 * B, {"batch": B, "vocab": V,
-                                                         "logits": "bf16"}
+        def torch_step():
+            torch.softmax(logits.to(torch.float32) / temps.view(B, 1), -1)
+        return step, torch_step
+
+    pairs = [one_set() for _ in range(sets)]
+    return (rotating([p[0] for p in pairs]), rotating([p[1] for p in pairs]),
+            B * V * (2 + 4) + 4 * B, {"batch": B, "vocab": V, "logits": "bf16"})
 
 
-def setup_sampler_step(torch, capi, dev, seed=0):
+def setup_sampler_step(torch, capi, dev, seed=0, sets=1):
     """The whole Sampler step as engine.cc:306-333 runs it for the sampling
     workload's rows: bf16 logits [256, 151936], per-row temperatures,
     top-k 50 + top-p 0.9, uniform [32, 256]. Returns the fused launch
@@ -762,32 +918,56 @@ def setup_sampler_step(torch, capi, dev, seed=0):
     g = torch.Generator(device=dev)
     g.manual_seed(seed)
     B, V = SAMPLING_BATCH, QWEN3_VOCAB
-    logits = (torch.randn((B, V), device=dev, generator=g) * 3).to(torch.bfloat16)
     temps = torch.linspace(0.6, 1.2, B, device=dev)
     u = torch.rand((32, B), device=dev, generator=g)
     k = torch.full((B,), 50, dtype=torch.int32, device=dev)
     tp = torch.full((B,), 0.9, dtype=torch.float32, device=dev)
     probs = torch.empty((B, V), device=dev)
 
-    def fused():
-        capi.sampling_from_logits(logits, u, "top_k_top_p", temps, top_k=k, top_p=tp)
+    def one_set():
+        logits = (torch.randn((B, V), device=dev, generator=g) * 3).to(torch.bfloat16)
 
-    def two():
-        capi.softmax_temperature(logits, temps, out=probs)
-        capi.top_k_top_p_sampling_from_probs(probs, u, k, 0, tp, 0.0)
+        def fused():
+            capi.sampling_from_logits(logits, u, "top_k_top_p", temps, top_k=k, top_p=tp)
 
-    def torch_probs():
-        p = torch.softmax(logits.to(torch.float32) / temps.view(B, 1), -1).contiguous()
-        capi.top_k_top_p_sampling_from_probs(p, u, k, 0, tp, 0.0)
+        def two():
+            capi.softmax_temperature(logits, temps, out=probs)
+            capi.top_k_top_p_sampling_from_probs(probs, u, k, 0, tp, 0.0)
 
-    return fused, two, torch_probs, B * V * 2 + 4 * B + 32 * B * 4, {
-        "batch": B, "vocab": V, "logits": "bf16", "top_k": 50, "top_p": 0.9}
+        def torch_probs():
+            p = torch.softmax(logits.to(torch.float32) / temps.view(B, 1), -1).contiguous()
+            capi.top_k_top_p_sampling_from_probs(p, u, k, 0, tp, 0.0)
+        return fused, two, torch_probs
+
+    trip = [one_set() for _ in range(sets)]
+    return (rotating([t[0] for t in trip]), rotating([t[1] for t in trip]),
+            rotating([t[2] for t in trip]), B * V * 2 + 4 * B + 32 * B * 4, {
+                "batch": B, "vocab": V, "logits": "bf16", "top_k": 50, "top_p": 0.9})
+
+
+def _resident(rec_rot, ev_1, nbytes=None, flops=None, sets=1):
+    """The one-set (cache-resident) figure beside a rotated-buffer record."""
+    out = {"kernel_ms": ev_1}
+    if nbytes:
+        out["GB/s"] = nbytes / (ev_1 * 1e-3) / 1e9
+        out["hbm_frac"] = round(out["GB/s"] / HBM_PEAK_GBS, 4)
+    if flops:
+        out["TFLOP/s"] = flops / (ev_1 * 1e-3) / 1e12
+        out["mfma_frac"] = round(out["TFLOP/s"] / BF16_PEAK_TFLOPS, 4)
+    rec_rot["buffer_sets"] = sets
+    rec_rot["rotated_bytes"] = ROTATE_BYTES
+    rec_rot["cache_resident"] = out
+    return rec_rot
 
 
 def run_workload(name, torch, capi, wl, dev, steps, warmup, cfg5_layers, min_warm_s=0.0):
     timer = Timer(torch, min_warm_s)
     if name == "sampler_step":
         fused, two, torch_probs, nbytes, shape = setup_sampler_step(torch, capi, dev)
+        _, ev1 = timer.run_graph(fused, steps, warmup)
+        del fused, two, torch_probs
+        sets = rotation_sets(nbytes)
+        fused, two, torch_probs, nbytes, shape = setup_sampler_step(torch, capi, dev, sets=sets)
         ewall, eev = timer.run(fused, steps, warmup)
         wall, ev = timer.run_graph(fused, steps, warmup)
         _, two_ev = timer.run_graph(two, steps, warmup)
@@ -799,9 +979,14 @@ def run_workload(name, torch, capi, wl, dev, steps, warmup, cfg5_layers, min_war
                "two_launch_ms": two_ev, "torch_probs_then_draw_ms": tp_ev,
                "speedup_vs_torch_probs_then_draw": tp_ev / ev,
                "roofline": roofline_hbm(nbytes, ev, None)}
-        return None, rec
+        return None, _resident(rec, ev1, nbytes, sets=sets)
     if name == "sampler_softmax":
         step, torch_step, nbytes, shape = setup_sampler_softmax(torch, capi, dev)
+        _, ev1 = timer.run_graph(step, steps, warmup)
+        del step, torch_step
+        torch.cuda.empty_cache()
+        sets = rotation_sets(nbytes)
+        step, torch_step, nbytes, shape = setup_sampler_softmax(torch, capi, dev, sets=sets)
         ewall, eev = timer.run(step, steps, warmup)
         wall, ev = timer.run_graph(step, steps, warmup)
         _, tev = timer.run_graph(torch_step, steps, warmup)
@@ -811,23 +996,33 @@ def run_workload(name, torch, capi, wl, dev, steps, warmup, cfg5_layers, min_war
                "GB/s": nbytes / (wall * 1e-3) / 1e9,
                "torch_path_ms": tev, "speedup_vs_torch_path": tev / ev,
                "roofline": roofline_hbm(nbytes, ev, "softmax_temperature_sampler")}
-        return None, rec
+        return None, _resident(rec, ev1, nbytes, sets=sets)
     if name == "sampling":
         step, nbytes, shape = setup_sampling(torch, capi, dev)
+        _, ev1 = timer.run(step, steps, warmup)
+        del step
+        torch.cuda.empty_cache()
+        sets = rotation_sets(nbytes)
+        step, nbytes, shape = setup_sampling(torch, capi, dev, sets=sets)
         wall, ev = timer.run(step, steps, warmup)
         rec = {"workload": f"sampling_top_k_top_p_b{SAMPLING_BATCH}_v{QWEN3_VOCAB}", **shape,
                "ms_per_step": wall, "kernel_ms": ev, "bytes": nbytes,
                "GB/s": nbytes / (wall * 1e-3) / 1e9,
                "roofline": roofline_hbm(nbytes, ev, "sampling_top_k_top_p")}
-        return None, rec
+        return None, _resident(rec, ev1, nbytes, sets=sets)
     if name in ("resid_norm", "resid_act"):
         step, nbytes, shape = setup_resid(torch, capi, name, dev)
+        _, ev1 = timer.run(step, steps, warmup)
+        del step
+        torch.cuda.empty_cache()
+        sets = rotation_sets(nbytes)
+        step, nbytes, shape = setup_resid(torch, capi, name, dev, sets=sets)
         wall, ev = timer.run(step, steps, warmup)
         kname = "fused_add_rmsnorm" if name == "resid_norm" else "silu_and_mul"
         rec = {"workload": f"{name}_qwen3_8b_t{RESID_TOKENS}_bf16", **shape, "ms_per_step": wall,
                "kernel_ms": ev, "bytes": nbytes, "GB/s": nbytes / (wall * 1e-3) / 1e9,
                "roofline": roofline_hbm(nbytes, ev, f"{kname}_qwen3_8b")}
-        return None, rec
+        return None, _resident(rec, ev1, nbytes, sets=sets)
     # Configurations 1, 2 and 3 are single calls of 10-25 us, within a few us
     # of the host's per-call launch cost from Python: they are timed as a
     # captured graph of the K calls (the eager figures are kept beside them).
@@ -847,27 +1042,42 @@ def run_workload(name, torch, capi, wl, dev, steps, warmup, cfg5_layers, min_war
         w = wl.cfg2_prefill_prefix() if name == "cfg2" else wl.cfg5_prefill_chunk()
         key = "paged_prefill_cfg2" if name == "cfg2" else "paged_prefill_cfg5_chunk"
         step, nbytes, flops = setup_prefill(torch, capi, wl, w, dev)
-        wall, ev = timer.run(step, steps, warmup)
-        eager = {}
         if name == "cfg2":
+            # 21 MB, latency-bound: timed on one set, as a graph of the K calls
+            wall, ev = timer.run(step, steps, warmup)
             eager = {"eager_ms_per_step": wall, "eager_kernel_ms": ev, "timing": "graph"}
             wall, ev = timer.run_graph(step, steps, warmup)
+            sets, ev1 = 1, None
+        else:
+            _, ev1 = timer.run(step, steps, warmup)
+            del step
+            sets = rotation_sets(nbytes)
+            step, nbytes, flops = setup_prefill(torch, capi, wl, w, dev, sets=sets)
+            wall, ev = timer.run(step, steps, warmup)
+            eager = {}
         rec = {"workload": w.name, "ms_per_step": wall, "kernel_ms": ev, **eager, "flops": flops,
                "bytes": nbytes, "TFLOP/s": flops / (wall * 1e-3) / 1e12,
                "GB/s": nbytes / (wall * 1e-3) / 1e9,
                "roofline": roofline_mfma(flops, ev, key),
                "roofline_hbm": roofline_hbm(nbytes, ev, None)}
+        if ev1 is not None:
+            rec = _resident(rec, ev1, nbytes, flops, sets=sets)
         return w, rec
     if name == "cfg3":
         w = wl.cfg3_fused_store()
         step, nbytes = setup_fused(torch, capi, wl, w, dev)
+        _, ev1 = timer.run_graph(step, steps, warmup)
+        del step
+        torch.cuda.empty_cache()
+        sets = rotation_sets(nbytes)
+        step, nbytes = setup_fused(torch, capi, wl, w, dev, sets=sets)
         wall, ev = timer.run(step, steps, warmup)
         eager = {"eager_ms_per_step": wall, "eager_kernel_ms": ev, "timing": "graph"}
         wall, ev = timer.run_graph(step, steps, warmup)
         rec = {"workload": w.name, "ms_per_step": wall, "kernel_ms": ev, **eager, "bytes": nbytes,
                "GB/s": nbytes / (wall * 1e-3) / 1e9,
                "roofline": roofline_hbm(nbytes, ev, "fused_qknorm_rope_store_cfg3")}
-        return w, rec
+        return w, _resident(rec, ev1, nbytes, sets=sets)
     if name == "cfg5":
         w = wl.cfg5_mixed(layers=cfg5_layers)
         step, dec_bytes, pre_flops, pre_bytes, keep = setup_mixed(torch, wl, w, dev, cfg5_layers)
@@ -908,6 +1118,10 @@ def main():
         print(json.dumps({"copy_bytes": n, "steps": args.steps}))
         return
 
+    if args.replay_host_only:
+        print(json.dumps({"replay_host": measure_replay_host(torch, wl, dev)}), flush=True)
+        return
+
     if args.ceilings_only:
         sweep = []
         ceil = measure_ceilings(torch, dev, args.min_warm_seconds, sweep)
@@ -932,6 +1146,12 @@ def main():
             print(f"[bench] {name}: {json.dumps(extra[name])}", file=sys.stderr, flush=True)
 
     if not args.no_extra:
+        try:
+            extra["replay_host"] = measure_replay_host(torch, wl, dev)
+        except Exception as e:  # report, keep the headline line
+            extra["replay_host"] = {"error": repr(e)}
+        print(f"[bench] replay_host: {json.dumps(extra['replay_host'])}", file=sys.stderr,
+              flush=True)
         try:
             ceil = measure_ceilings(torch, dev, args.min_warm_seconds)
             extra["ceilings"] = ceil

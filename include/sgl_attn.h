@@ -283,8 +283,11 @@ int sgl_paged_decode(const sgl_decode_plan_t* plan, const void* q,
  * until the process ends; plans with workspace_bytes above it get
  * SGL_ERR_CAPACITY. Nothing is allocated. Calls on one GPU share the array
  * and must be stream-ordered: calls that overlap on one GPU race. A batch
- * past the plan's capacity gets NaN rows as in sgl_paged_decode (the status
- * word is not readable here; check batches with sgl_decode_plan_check).
+ * past the plan's capacity gets NaN rows and the CAPACITY status word as in
+ * sgl_paged_decode; sgl_decode_status(NULL, ...) reads that word from the
+ * current device's scratch. sgl_decode_plan looks the scratch address up
+ * for the current device, so a call captured into a graph after a plan was
+ * made runs no lookup inside the capture.
  * Replaces: no counterpart in the reference; it exists for callers that
  *           cannot allocate.
  */
@@ -302,6 +305,8 @@ int sgl_paged_decode_noalloc(const sgl_decode_plan_t* plan, const void* q,
 /*
  * Reads the status word a decode call left in its workspace (waits for the
  * stream): SGL_OK, or SGL_ERR_CAPACITY when the batch exceeded its plan.
+ * workspace NULL reads the word of sgl_paged_decode_noalloc's scratch on the
+ * current device.
  * Replaces: no device-side counterpart in the reference (FlashInfer's plan
  *           is host-side); pairs with sgl_paged_decode.
  */

@@ -475,9 +475,11 @@ def decode_workspace(plan: DecodePlan, device: torch.device) -> torch.Tensor:
     return torch.empty(int(plan.workspace_bytes), dtype=torch.uint8, device=device)
 
 
-def decode_status(workspace: torch.Tensor) -> int:
-    """Status word of the last decode call on this workspace (waits for the stream)."""
-    dev = _need_gpu(workspace)
+def decode_status(workspace: Optional[torch.Tensor]) -> int:
+    """Status word of the last decode call on this workspace (waits for the
+    stream); None reads the no-alloc entry point's scratch on the current
+    device."""
+    dev = _need_gpu(workspace) if workspace is not None else _need_gpu()
     st = ctypes.c_int32(-100)
     _check(lib().sgl_decode_status(_p(workspace), ctypes.byref(st), _stream(dev)),
            "sgl_decode_status")

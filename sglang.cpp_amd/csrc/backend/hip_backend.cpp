@@ -436,6 +436,10 @@ torch::Tensor HipAttnBackend::attend(const torch::Tensor& q_in, int layer_id, Ba
 
 void HipAttnBackend::init_capture_graph(int max_seq_len, const std::vector<int>& bs_list) {
   capture_.reset();
+  // Graphs of the previous capture set are retired with it (the caller
+  // destroys them before capturing again), and so are the grown-out
+  // workspaces they may have recorded.
+  retired_workspaces_.clear();
   if (bs_list.empty()) return;
   TORCH_CHECK(max_seq_len > 0, "max_seq_len must be positive");
   auto cap = std::make_unique<CaptureState>();
@@ -543,6 +547,7 @@ void HipAttnBackend::prepare_for_replay(Batch& batch) {
 void HipAttnBackend::init_mixed_capture_graph(int max_seq_len, int max_decode_rows,
                                               int max_prefill_reqs, int max_prefill_qo) {
   mixed_.reset();
+  retired_workspaces_.clear();  // as in init_capture_graph
   TORCH_CHECK(max_seq_len > 0 && max_decode_rows >= 0 && max_prefill_reqs > 0 &&
                   max_prefill_qo > 1 && max_prefill_qo <= max_seq_len,
               "init_mixed_capture_graph: need max_seq_len > 0, max_decode_rows >= 0, "

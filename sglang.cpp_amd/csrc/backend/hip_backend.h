@@ -168,7 +168,9 @@ class HipAttnBackend : public BaseAttnBackend {
   torch::Tensor page_table_;
   torch::Tensor workspace_;
   // Set once the growable workspace has been recorded into a graph: growing
-  // it then keeps the old buffer alive (a graph may still write to it).
+  // it then keeps the old buffer alive (a graph may still write to it) until
+  // the next init_capture_graph / init_mixed_capture_graph, before which the
+  // caller destroys the graphs it captured.
   bool workspace_captured_ = false;
   std::vector<torch::Tensor> retired_workspaces_;
   std::unique_ptr<CaptureState> capture_;

@@ -122,6 +122,17 @@ __device__ __forceinline__ u32x4_t ldg128(const void* p) {
 __device__ __forceinline__ void stg128(void* p, const u32x4_t& v) {
   *reinterpret_cast<u32x4_t*>(p) = v;
 }
+// 16-byte load / store, non-temporal when NT (streams read or written once).
+template <bool NT>
+__device__ __forceinline__ u32x4_t ldg128_nt(const void* p) {
+  if constexpr (NT) return __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+  else return ldg128(p);
+}
+template <bool NT>
+__device__ __forceinline__ void stg128_nt(void* p, const u32x4_t& v) {
+  if constexpr (NT) __builtin_nontemporal_store(v, reinterpret_cast<u32x4_t*>(p));
+  else stg128(p, v);
+}
 
 // Combine each lane with lane ^ 16 / lane ^ 32 through gfx950's
 // v_permlane16_swap / v_permlane32_swap (register to register; a generic

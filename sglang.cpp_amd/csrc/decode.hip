@@ -630,6 +630,55 @@ static int device_cu_count() {
   return cached;
 }
 
+// ------------------------------------------------------------------ no-alloc variant
+//
+// Callers that cannot allocate (code under graph capture, tight serving
+// loops) get the decode with its split workspace in a file-scope device
+// array. Each GPU holds its own copy of the array for the life of the
+// process; its device address is looked up once per device and used for
+// every launch (the array's name is only a host-side stand-in). All calls on
+// one GPU share the array: calls that overlap on one GPU (different streams
+// without ordering) race on it.
+
+namespace {
+constexpr int64_t kScratchBytes = 32ll << 20;
+constexpr int kMaxDevices = 64;
+}  // namespace
+
+static __device__ __align__(256) char scratch[kScratchBytes];
+
+static void* g_scratch_ptr[kMaxDevices];
+static std::mutex g_scratch_mu;
+
+// Device address of `scratch` on the current device, looked up once per
+// device with that device current; nullptr with *status set on failure.
+// sgl_decode_plan makes the lookup for the current device, so a caller that
+// plans before a graph capture never runs it inside the capture.
+static void* scratch_on_current_device(int* status) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    *status = static_cast<int>(e);
+    return nullptr;
+  }
+  if (dev < 0 || dev >= kMaxDevices) {
+    *status = SGL_ERR_UNSUPPORTED;
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr) {
+      *status = e != hipSuccess ? static_cast<int>(e) : SGL_ERR_INVALID_ARG;
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = ptr;
+  }
+  *status = SGL_OK;
+  return g_scratch_ptr[dev];
+}
+
 // LDS of one fused decode + prefill workgroup (the CU's whole LDS).
 constexpr size_t kMixedLds = 160 * 1024;
 
@@ -699,8 +748,18 @@ static int decode_plan_for(const int32_t* kv_indptr_host, int batch_size, int nu
 
 extern "C" int sgl_decode_plan(const int32_t* kv_indptr_host, int batch_size, int num_qo_heads,
                                int num_kv_heads, int head_dim, sgl_decode_plan_t* plan) {
-  return decode_plan_for(kv_indptr_host, batch_size, num_qo_heads, num_kv_heads, head_dim, 0,
-                         kMaxChunkTokens, plan);
+  const int st = decode_plan_for(kv_indptr_host, batch_size, num_qo_heads, num_kv_heads,
+                                 head_dim, 0, kMaxChunkTokens, plan);
+  // Resolve the no-alloc scratch address of the current device now (host
+  // code, before any capture the caller may begin); without a visible
+  // device the lookup is left to the first no-alloc call.
+  int n = 0;
+  if (st == SGL_OK && hipGetDeviceCount(&n) == hipSuccess && n > 0) {
+    int ignored = 0;
+    (void)scratch_on_current_device(&ignored);
+  }
+  (void)hipGetLastError();
+  return st;
 }
 
 extern "C" int sgl_decode_plan_cus(const int32_t* kv_indptr_host, int batch_size,
@@ -749,7 +808,12 @@ extern "C" int sgl_decode_plan_check(const sgl_decode_plan_t* plan,
 }
 
 extern "C" int sgl_decode_status(const void* workspace, int32_t* status, void* stream) {
-  if (!workspace || !status) return SGL_ERR_INVALID_ARG;
+  if (!status) return SGL_ERR_INVALID_ARG;
+  if (!workspace) {  // the no-alloc entry point's scratch on the current device
+    int st = SGL_OK;
+    workspace = scratch_on_current_device(&st);
+    if (!workspace) return st;
+  }
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t e = hipMemcpyAsync(status, workspace, sizeof(int32_t), hipMemcpyDeviceToHost, s);
   if (e == hipSuccess) e = hipStreamSynchronize(s);
@@ -940,53 +1004,6 @@ extern "C" int sgl_paged_mixed(const sgl_decode_plan_t* plan, const void* q,
   if (st != SGL_OK) return st;
   hipLaunchKernelGGL(decode_merge_kernel, dim3(d.hkv, d.batch), dim3(256), 0, s, d);
   return launch_status();
-}
-
-// ------------------------------------------------------------------ no-alloc variant
-//
-// Callers that cannot allocate (code under graph capture, tight serving
-// loops) get the decode with its split workspace in a file-scope device
-// array. Each GPU holds its own copy of the array for the life of the
-// process; its device address is looked up once per device and used for
-// every launch (the array's name is only a host-side stand-in). All calls on
-// one GPU share the array: calls that overlap on one GPU (different streams
-// without ordering) race on it.
-
-namespace {
-constexpr int64_t kScratchBytes = 32ll << 20;
-constexpr int kMaxDevices = 64;
-}  // namespace
-
-static __device__ __align__(256) char scratch[kScratchBytes];
-
-static void* g_scratch_ptr[kMaxDevices];
-static std::mutex g_scratch_mu;
-
-// Device address of `scratch` on the current device (looked up on first
-// use with that device current); nullptr with *status set on failure.
-static void* scratch_on_current_device(int* status) {
-  int dev = 0;
-  hipError_t e = hipGetDevice(&dev);
-  if (e != hipSuccess) {
-    *status = static_cast<int>(e);
-    return nullptr;
-  }
-  if (dev < 0 || dev >= kMaxDevices) {
-    *status = SGL_ERR_UNSUPPORTED;
-    return nullptr;
-  }
-  std::lock_guard<std::mutex> lock(g_scratch_mu);
-  if (!g_scratch_ptr[dev]) {
-    void* ptr = nullptr;
-    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
-    if (e != hipSuccess || ptr == nullptr) {
-      *status = e != hipSuccess ? static_cast<int>(e) : SGL_ERR_INVALID_ARG;
-      return nullptr;
-    }
-    g_scratch_ptr[dev] = ptr;
-  }
-  *status = SGL_OK;
-  return g_scratch_ptr[dev];
 }
 
 extern "C" int sgl_paged_decode_noalloc(const sgl_decode_plan_t* plan, const void* q,

@@ -15,10 +15,14 @@
 //     clock each ran at (cycle counter over the 100 MHz real-time counter):
 //     the matrix-core ceiling prefill is held against, and how far the clock
 //     falls under high-toggle matrix work;
+//   * a streaming copy (read and write in equal parts), an in-place
+//     read-modify-write and a fill, cached or non-temporal: the ceiling of
+//     kernels that write as much as they read (the fused store, the
+//     residual norm, the Sampler's probabilities);
 //   * an empty kernel: the per-launch floor of short calls.
-// The only global writes are a guard store that never fires for the read
-// probe (it keeps the loads live) and one value plus four clock stamps per
-// workgroup for the MFMA probe.
+// Apart from the copy probe's destination, the only global writes are a
+// guard store that never fires for the read probe (it keeps the loads live)
+// and one value plus four clock stamps per workgroup for the MFMA probe.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -60,6 +64,43 @@ __global__ void __launch_bounds__(kThreads) stream_read_kernel(const u32x4_t* __
   for (; i < n16; i += stride) acc ^= src[i];
   const uint32_t x = acc[0] ^ acc[1] ^ acc[2] ^ acc[3];
   if (x == 0x9e3779b9u && (acc[0] + acc[1]) == 0x7f4a7c15u) sink[0] = x;  // never taken in practice
+}
+
+// Streaming copy (or, with dst == src, an in-place read-modify-write; with
+// kWriteOnly, a fill): block-contiguous, each workgroup walks its own
+// contiguous 1/grid of the buffer, kDepth 16-byte loads in flight per lane,
+// then the kDepth stores. Loads and stores each cached or non-temporal.
+template <int kDepth, bool kNtLoad, bool kNtStore, bool kWriteOnly>
+__global__ void __launch_bounds__(kThreads) stream_copy_kernel(const u32x4_t* __restrict__ src,
+                                                               u32x4_t* dst, int64_t n16) {
+  const int64_t per = (n16 + gridDim.x - 1) / gridDim.x;
+  const int64_t b0 = static_cast<int64_t>(blockIdx.x) * per;
+  const int64_t end = min(n16, b0 + per);
+  int64_t i = b0 + threadIdx.x;
+  for (; i + (kDepth - 1) * kThreads < end; i += kDepth * kThreads) {
+    u32x4_t v[kDepth];
+#pragma unroll
+    for (int k = 0; k < kDepth; ++k) {
+      if constexpr (kWriteOnly) {
+        const uint32_t x = static_cast<uint32_t>(i + k * kThreads);
+        v[k] = u32x4_t{x, x ^ 1u, x ^ 2u, x ^ 3u};
+      } else {
+        v[k] = kNtLoad ? __builtin_nontemporal_load(src + i + k * kThreads) : src[i + k * kThreads];
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < kDepth; ++k) {
+      v[k] ^= u32x4_t{1u, 0u, 0u, 0u};
+      if (kNtStore)
+        __builtin_nontemporal_store(v[k], dst + i + k * kThreads);
+      else
+        dst[i + k * kThreads] = v[k];
+    }
+  }
+  for (; i < end; i += kThreads) {
+    u32x4_t v = kWriteOnly ? u32x4_t{0u, 0u, 0u, 0u} : src[i];
+    dst[i] = v ^ u32x4_t{1u, 0u, 0u, 0u};
+  }
 }
 
 // Paged read: workgroup b reads pages order[b * per .. (b + 1) * per) of
@@ -275,6 +316,41 @@ extern "C" int sgl_probe_stream_read(const void* src, int64_t bytes, int grid, i
     else { if (nt) SGL_PROBE_READ(16, true, false); else SGL_PROBE_READ(16, false, false); }
   }
 #undef SGL_PROBE_READ
+  return status_of_launch();
+}
+
+// Streams `bytes` (a multiple of 16, 16-byte aligned) from src to dst with
+// `grid` workgroups of 256 threads; dst == src is an in-place
+// read-modify-write. variant: bit 0 = non-temporal loads, bit 1 =
+// non-temporal stores, bit 2 = 16 rather than 8 accesses in flight per lane,
+// bit 3 = write only (a fill of dst; src unused and may be null).
+extern "C" int sgl_probe_stream_copy(const void* src, void* dst, int64_t bytes, int grid,
+                                     int variant, void* stream) {
+  const bool write_only = variant & 8;
+  if ((!src && !write_only) || !dst || bytes <= 0 || bytes % 16 || grid <= 0 || variant < 0 ||
+      variant > 15 || reinterpret_cast<uintptr_t>(dst) % 16 ||
+      reinterpret_cast<uintptr_t>(src) % 16)
+    return SGL_ERR_INVALID_ARG;
+  const auto* p = static_cast<const u32x4_t*>(src);
+  auto* q = static_cast<u32x4_t*>(dst);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t n = bytes / 16;
+#define SGL_PROBE_COPY(D_, L_, S_, W_) \
+  hipLaunchKernelGGL((stream_copy_kernel<D_, L_, S_, W_>), dim3(grid), dim3(kThreads), 0, s, p, q, n)
+#define SGL_PROBE_COPY_D(L_, S_, W_) \
+  if (variant & 4) SGL_PROBE_COPY(16, L_, S_, W_); else SGL_PROBE_COPY(8, L_, S_, W_);
+  if (write_only) {
+    if (variant & 2) { SGL_PROBE_COPY_D(false, true, true) } else { SGL_PROBE_COPY_D(false, false, true) }
+  } else {
+    switch (variant & 3) {
+      case 0: SGL_PROBE_COPY_D(false, false, false) break;
+      case 1: SGL_PROBE_COPY_D(true, false, false) break;
+      case 2: SGL_PROBE_COPY_D(false, true, false) break;
+      default: SGL_PROBE_COPY_D(true, true, false) break;
+    }
+  }
+#undef SGL_PROBE_COPY_D
+#undef SGL_PROBE_COPY
   return status_of_launch();
 }
 

@@ -63,6 +63,11 @@ struct NormArgs {
 };
 
 constexpr int kRowsPerBlock = 4;  // one wave per row
+// Rows are read once and written once: non-temporal loads and stores.
+// Measured at the Qwen3-8B shape (fused add, T 8192, hidden 4096) on
+// buffers rotated past the 256 MB last-level cache: 4.62 -> 5.38 TB/s; the
+// same rows re-run back to back from the cache lose 6.5 -> 5.6 TB/s.
+constexpr bool kNormNt = true;
 
 // One wave per row. NV > 0: the row (<= 512 NV elements) stays in registers
 // between the sum of squares and the scaling, so HBM sees one read and one
@@ -81,13 +86,13 @@ __global__ void __launch_bounds__(kWave * kRowsPerBlock) rmsnorm_kernel(NormArgs
   auto first = [&](int j, float (&f)[8]) {
     const int64_t e0 = (static_cast<int64_t>(j) * kWave + lane) * 8;
     if (e0 < d) {
-      load8<DT, VEC>(xr, e0, d, f);
+      load8<DT, VEC, kNormNt>(xr, e0, d, f);
       if constexpr (ADD) {
         float r[8];
-        load8<DT, VEC>(rr, e0, d, r);
+        load8<DT, VEC, kNormNt>(rr, e0, d, r);
 #pragma unroll
         for (int i = 0; i < 8; ++i) f[i] += r[i];
-        store8<DT, VEC>(rr, e0, d, f);
+        store8<DT, VEC, kNormNt>(rr, e0, d, f);
       }
     } else {
 #pragma unroll
@@ -101,7 +106,7 @@ __global__ void __launch_bounds__(kWave * kRowsPerBlock) rmsnorm_kernel(NormArgs
     load8<DT, VEC>(a.w, e0, d, w);
 #pragma unroll
     for (int i = 0; i < 8; ++i) f[i] = (f[i] * scale) * w[i];
-    store8<DT, VEC>(outr, e0, d, f);
+    store8<DT, VEC, kNormNt>(outr, e0, d, f);
   };
   float ss = 0.f;
   if constexpr (NV > 0) {

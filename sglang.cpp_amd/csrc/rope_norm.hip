@@ -267,6 +267,13 @@ __global__ void __launch_bounds__(128) rope_generic_kernel(
 // for the scalar token index and one rounding per pair, 24.9 -> 23.3 us for
 // two tokens per thread; four measured slower).
 constexpr int kFusedTokensPerBlock = 2;
+// The qkv rows are read once and the q rows and the K/V pool rows written
+// once: non-temporal loads and stores. Measured at config 3 on buffers
+// rotated past the 256 MB last-level cache (HBM-resident): 4.46 -> 5.20
+// TB/s (1, 3 and 4 tokens per thread: 5.03, 5.13, 5.01); the same buffers
+// re-run back to back from the cache lose 5.5-5.9 -> 5.3 TB/s.
+constexpr bool kFusedNtLoad = true;
+constexpr bool kFusedNtStore = true;
 
 template <int LPR>
 __global__ void __launch_bounds__(256) fused_qknorm_rope_store_kernel(
@@ -299,7 +306,7 @@ __global__ void __launch_bounds__(256) fused_qknorm_rope_store_kernel(
   for (int k = 0; k < NT; ++k) {
     const int64_t t = min(tb * NT + k, num_tokens - 1);
     rowb[k] = qkv + t * qkv_st;
-    raw[k] = ldg128(rowb[k] + lane_off);
+    raw[k] = ldg128_nt<kFusedNtLoad>(rowb[k] + lane_off);
     slot[k] = out_loc[t];
     pos[k] = positions[t];
   }
@@ -308,7 +315,7 @@ __global__ void __launch_bounds__(256) fused_qknorm_rope_store_kernel(
     const uint32_t h_off = static_cast<uint32_t>((r - hq - hkv) * D) + head_off;
 #pragma unroll
     for (int k = 0; k < NT; ++k)
-      if (tb * NT + k < num_tokens) stg128(v_cache + slot[k] * hkv * D + h_off, raw[k]);
+      if (tb * NT + k < num_tokens) stg128_nt<kFusedNtStore>(v_cache + slot[k] * hkv * D + h_off, raw[k]);
     return;
   }
   float wf[8];
@@ -359,8 +366,8 @@ __global__ void __launch_bounds__(256) fused_qknorm_rope_store_kernel(
     for (int i = 0; i < 8; ++i) x[i] = rope_one(x[i], p[i], c[i], sn[i]);
     const u32x4_t packed = pack8(x);
     if (tb * NT + k < num_tokens) {
-      if (is_q || k_back) stg128(rowb[k] + lane_off, packed);
-      if (!is_q) stg128(k_cache + slot[k] * hkv * D + (static_cast<uint32_t>((r - hq) * D) + head_off), packed);
+      if (is_q || k_back) stg128_nt<kFusedNtStore>(rowb[k] + lane_off, packed);
+      if (!is_q) stg128_nt<kFusedNtStore>(k_cache + slot[k] * hkv * D + (static_cast<uint32_t>((r - hq) * D) + head_off), packed);
     }
   }
 }

@@ -109,7 +109,7 @@ def test_probe_library_exports_its_entry_points():
         pytest.skip("libsgl_probes.so not built")
     lib = ctypes.CDLL(str(path))
     for name in ("sgl_probe_stream_read", "sgl_probe_page_read", "sgl_probe_decode_read",
-                 "sgl_probe_mfma_bf16", "sgl_probe_empty"):
+                 "sgl_probe_mfma_bf16", "sgl_probe_empty", "sgl_probe_stream_copy"):
         assert hasattr(lib, name), name
     bench = _bench_module()
     assert bench.load_probes() is not None
@@ -123,5 +123,10 @@ def test_ceiling_fractions_use_the_bound_of_each_kernel():
              "cfg5": {"graph_ms": 21.0}}
     fr = bench.ceiling_fracs(extra, ceil)
     assert fr == {"cfg4": 0.9, "prefill_chunk": 0.5}
+    # a kernel that writes as much as it reads: against the copy ceiling
+    ceil["stream_copy"] = {"GB/s": 5000.0}
+    extra["cfg3"] = {"roofline": {"bound": "hbm", "achieved": 4500.0}}
+    fr = bench.ceiling_fracs(extra, ceil)
+    assert fr == {"cfg4": 0.9, "prefill_chunk": 0.5, "cfg3": 0.9}
     # one MFMA of the probe: 32 x 32 x 16 multiply-adds
     assert bench.MFMA_FLOPS == 32768
