@@ -40,7 +40,7 @@ const char* sgl_status_string(int status);
 
 /* Library version, to check that the loaded .so matches this header. */
 int sgl_abi_version(void);
-#define SGL_ABI_VERSION 13
+#define SGL_ABI_VERSION 14
 
 /* ------------------------------------------------------------------ */
 /* KV-cache store                                                      */
@@ -128,6 +128,22 @@ int sgl_gather_int32_2d(const int32_t* table, int64_t rows, int64_t stride,
                         int64_t cols, const int32_t* req_indices,
                         const int32_t* positions, int32_t* out, int64_t count,
                         void* stream);
+
+/*
+ * Up to SGL_MAX_I32_COPIES device-to-device int32 copies in one launch:
+ * dst[i] = src[i] for i < count of each entry (entries must not overlap).
+ * The graph-replay path refreshes every capture buffer of a step (indptrs,
+ * row maps, indices) with this one call instead of one copy per buffer.
+ * Replaces: the per-buffer copies of FlashInferBackend::prepare_for_replay
+ *           (src/attention/flashinfer_backend.cu:267-352).
+ */
+typedef struct {
+  const int32_t* src;
+  int32_t* dst;
+  int64_t count;
+} sgl_i32_copy_t;
+#define SGL_MAX_I32_COPIES 8
+int sgl_copy_i32(const sgl_i32_copy_t* copies, int num_copies, void* stream);
 
 /* ------------------------------------------------------------------ */
 /* RoPE and q/k RMSNorm                                                */

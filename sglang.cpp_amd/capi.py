@@ -26,7 +26,7 @@ SGL_INDEX_I64 = 1
 SGL_DTYPE_BF16 = 0
 SGL_DTYPE_F16 = 1
 SGL_DTYPE_F32 = 2
-ABI_VERSION = 13
+ABI_VERSION = 14
 FUSED_NO_K_WRITEBACK = 1  # SGL_FUSED_NO_K_WRITEBACK
 
 
@@ -51,6 +51,13 @@ class DecodePlan(ctypes.Structure):
     ]
 
 
+class I32Copy(ctypes.Structure):
+    """sgl_i32_copy_t."""
+    _fields_ = [("src", ctypes.c_void_p), ("dst", ctypes.c_void_p), ("count", ctypes.c_int64)]
+
+
+MAX_I32_COPIES = 8
+
 _lib: Optional[ctypes.CDLL] = None
 
 _vp = ctypes.c_void_p
@@ -67,6 +74,7 @@ _SIGNATURES = {
     "sgl_write_token_pool": ([_vp, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _vp], _i32),
     "sgl_write_page_table": ([_vp, _i64, _i64, _i64, _vp, _i64, _vp, _i32, _i32, _vp], _i32),
     "sgl_gather_int32_2d": ([_vp, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _vp], _i32),
+    "sgl_copy_i32": ([_vp, _i32, _vp], _i32),
     "sgl_rope_cos_sin_cache": ([_vp, _vp, _i64, _i32, _f32, _vp], _i32),
     "sgl_qk_rmsnorm": ([_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                         _f32, _i32, _vp], _i32),
@@ -253,6 +261,23 @@ def write_page_table(page_table: torch.Tensor, page_starts: torch.Tensor,
     _check(lib().sgl_write_page_table(_p(page_table), rows, stride, cols, _p(page_starts),
                                       page_starts.numel(), _p(alloc_info), alloc_info.shape[0],
                                       page_size, _stream(dev)), "sgl_write_page_table")
+
+
+def copy_i32(pairs: Sequence) -> None:
+    """sgl_copy_i32: dst[:n] = src[:n] for each (src, dst, n) in one launch
+    (int32 device tensors, n elements from the start of each)."""
+    if len(pairs) > MAX_I32_COPIES:
+        raise ValueError(f"at most {MAX_I32_COPIES} copies per call")
+    ts = [t for src, dst, _ in pairs for t in (src, dst)]
+    dev = _need_gpu(*ts)
+    arr = (I32Copy * max(1, len(pairs)))()
+    for i, (src, dst, n) in enumerate(pairs):
+        if src.dtype != torch.int32 or dst.dtype != torch.int32:
+            raise ValueError("copy_i32 moves int32 tensors")
+        if not (0 <= n <= min(src.numel(), dst.numel())):
+            raise ValueError("count exceeds a tensor")
+        arr[i] = I32Copy(src.data_ptr(), dst.data_ptr(), n)
+    _check(lib().sgl_copy_i32(arr, len(pairs), _stream(dev)), "sgl_copy_i32")
 
 
 def gather_int32_2d(table: torch.Tensor, req_indices: torch.Tensor,

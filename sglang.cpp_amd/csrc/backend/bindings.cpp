@@ -86,7 +86,14 @@ PYBIND11_MODULE(sgl_backend, m) {
       .def("uses_capture_buffers",
            [](const Batch& b) { return hip_meta(b)->use_capture_buffers; })
       .def("qo_indptr_host", [](const Batch& b) { return hip_meta(b)->qo_indptr_host; })
-      .def("kv_indptr_host", [](const Batch& b) { return hip_meta(b)->kv_indptr_host; });
+      .def("kv_indptr_host", [](const Batch& b) { return hip_meta(b)->kv_indptr_host; })
+      .def("record_metadata_stream",  // HipAttnMetadata::record_stream (scheduler.cc:152-179)
+           [](const Batch& b, int64_t stream_id, int device_index) {
+             // torch.cuda.Stream's (stream_id, device_index) name a HIP stream
+             hip_meta(b)->record_stream(c10::hip::HIPStream(c10::Stream::unpack3(
+                 stream_id, static_cast<c10::DeviceIndex>(device_index), c10::DeviceType::HIP)));
+           },
+           py::arg("stream_id"), py::arg("device_index"));
 
   py::class_<BaseKVCachePool, std::shared_ptr<BaseKVCachePool>>(m, "BaseKVCachePool");
   py::class_<MHAKVCache, BaseKVCachePool, std::shared_ptr<MHAKVCache>>(m, "MHAKVCache")
@@ -122,7 +129,9 @@ PYBIND11_MODULE(sgl_backend, m) {
            py::arg("max_seq_len"), py::arg("max_decode_rows"), py::arg("max_prefill_reqs"),
            py::arg("max_prefill_qo"))
       .def("prepare_for_capture", &HipAttnBackend::prepare_for_capture)
-      .def("prepare_for_replay", &HipAttnBackend::prepare_for_replay);
+      .def("prepare_for_replay", &HipAttnBackend::prepare_for_replay)
+      .def("pad_mixed_batch", &HipAttnBackend::pad_mixed_batch, py::arg("batch"),
+           py::arg("dummy"));
 
   m.def("write_page_table", &write_page_table, py::arg("page_table"),
         py::arg("allocated_pages"), py::arg("allocation_info"), py::arg("page_size"),

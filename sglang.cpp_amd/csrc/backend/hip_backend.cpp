@@ -95,13 +95,12 @@ torch::Tensor HipAttnMetadata::get_last_indices(int bs) const {
   return indptr.slice(0, 1, bs + 1) - 1;
 }
 
-void HipAttnMetadata::record_stream(c10::Stream stream) const {
+void HipAttnMetadata::record_stream(const c10::hip::HIPStream& stream) const {
   for (const torch::Tensor* t : {&indptr, &last_rows, &dec_kv_indptr, &dec_indices, &dec_q_rows,
                                  &dec_table_idx, &pre_qo_indptr, &pre_kv_indptr, &pre_indices,
                                  &pre_q_start, &pre_table_idx}) {
     if (t->defined() && t->is_cuda() && t->numel() > 0)
-      c10::hip::HIPCachingAllocator::recordStream(t->storage().data_ptr(),
-                                                  c10::hip::HIPStream(stream));
+      c10::hip::HIPCachingAllocator::recordStream(t->storage().data_ptr(), stream);
   }
 }
 
@@ -165,53 +164,58 @@ torch::Tensor& HipAttnBackend::workspace(int64_t bytes) {
   return workspace_;
 }
 
-torch::Tensor HipAttnBackend::to_device(const std::vector<int32_t>& host, HipAttnMetadata& meta) {
-  const int64_t n = static_cast<int64_t>(host.size());
-  auto pinned = torch::empty({n}, kI32.pinned_memory(true));
-  if (n > 0) std::memcpy(pinned.data_ptr<int32_t>(), host.data(), sizeof(int32_t) * n);
-  meta.host_staging.push_back(pinned);  // alive until the async copy has run
-  return pinned.to(kv_cache_->device(), /*non_blocking=*/true);
-}
-
 std::shared_ptr<HipAttnMetadata> HipAttnBackend::metadata_of(Batch& batch) const {
   auto meta = std::dynamic_pointer_cast<HipAttnMetadata>(batch.attn_metadata);
   TORCH_CHECK(meta, "HipAttnBackend requires HipAttnMetadata (call prepare_metadata first)");
   return meta;
 }
 
-// Decode rows for the requests `reqs` of the batch (indices into padded_reqs),
-// their queries at rows q_rows.
-void HipAttnBackend::build_decode_rows(HipAttnMetadata& meta, const std::vector<int>& reqs,
-                                       const std::vector<int32_t>& q_rows, const Batch& batch,
-                                       int decode_cus) {
-  const int n = static_cast<int>(reqs.size());
-  std::vector<int32_t> kv_indptr(n + 1, 0), table_idx(n);
-  for (int i = 0; i < n; ++i) {
-    const auto& req = batch.padded_reqs[reqs[i]];
-    kv_indptr[i + 1] = kv_indptr[i] + req->device_len();
-    table_idx[i] = req->table_idx;
+namespace {
+
+// Fields of one upload start at multiples of 64 int32 (256 bytes).
+constexpr int64_t kFieldAlign = 64;
+int64_t align_field(int64_t n) { return (n + kFieldAlign - 1) / kFieldAlign * kFieldAlign; }
+
+// One step's host int32 metadata, gathered so that it reaches the device in
+// a single pinned copy; the device tensor continues past the uploaded
+// fields with room the kernels fill (the index arrays).
+class PackedUpload {
+ public:
+  // Appends v and returns its offset; pad = false lets the next field
+  // follow it directly (two fields then read as one array).
+  int64_t add(const std::vector<int32_t>& v, bool pad = true) {
+    const int64_t off = static_cast<int64_t>(host_.size());
+    host_.insert(host_.end(), v.begin(), v.end());
+    if (pad) host_.resize(align_field(static_cast<int64_t>(host_.size())), 0);
+    return off;
   }
-  meta.num_decode = n;
-  meta.dec_kv_indptr = to_device(kv_indptr, meta);
-  meta.dec_table_idx = to_device(table_idx, meta);
-  meta.dec_q_rows = to_device(q_rows, meta);
-  meta.dec_indices = torch::empty({std::max(kv_indptr[n], 1)}, kI32.device(kv_cache_->device()));
-  check_sgl(sgl_build_decode_indices(page_table_.data_ptr<int32_t>(), page_table_.size(0),
-                                     page_table_.stride(0), page_table_.size(1),
-                                     meta.dec_table_idx.data_ptr<int32_t>(),
-                                     meta.dec_kv_indptr.data_ptr<int32_t>(),
-                                     meta.dec_indices.data_ptr<int32_t>(), n,
-                                     current_stream(kv_cache_->device())),
-            "sgl_build_decode_indices");
-  if (decode_cus > 0)
-    check_sgl(sgl_decode_plan_cus(kv_indptr.data(), n, num_qo_heads_, num_kv_heads_, head_dim_,
-                                  decode_cus, &meta.dec_plan),
-              "sgl_decode_plan_cus");
-  else
-    check_sgl(sgl_decode_plan(kv_indptr.data(), n, num_qo_heads_, num_kv_heads_, head_dim_,
-                              &meta.dec_plan),
-              "sgl_decode_plan");
-  workspace(meta.dec_plan.workspace_bytes);
+  int64_t size() const { return static_cast<int64_t>(host_.size()); }
+  // [uploaded fields | device_only entries] on dev; the pinned source stays
+  // alive in `staging` until the copy has run (the pinned allocator also
+  // records the copy's stream).
+  torch::Tensor send(int64_t device_only, const torch::Device& dev,
+                     std::vector<torch::Tensor>& staging) {
+    const int64_t n = size();
+    auto out = torch::empty({std::max<int64_t>(n + device_only, 1)}, kI32.device(dev));
+    if (n > 0) {
+      auto pinned = torch::empty({n}, kI32.pinned_memory(true));
+      std::memcpy(pinned.data_ptr<int32_t>(), host_.data(), sizeof(int32_t) * n);
+      out.slice(0, 0, n).copy_(pinned, /*non_blocking=*/true);
+      staging.push_back(std::move(pinned));
+    }
+    return out;
+  }
+
+ private:
+  std::vector<int32_t> host_;
+};
+
+}  // namespace
+
+torch::Tensor HipAttnBackend::to_device(const std::vector<int32_t>& host, HipAttnMetadata& meta) {
+  PackedUpload up;
+  up.add(host, false);
+  return up.send(0, kv_cache_->device(), meta.host_staging).slice(0, 0, host.size());
 }
 
 void HipAttnBackend::prepare_metadata(Batch& batch) {
@@ -219,103 +223,144 @@ void HipAttnBackend::prepare_metadata(Batch& batch) {
   auto meta = std::make_shared<HipAttnMetadata>();
   meta->is_prefill = batch.is_prefill();
   const int bs = batch.padded_size();
-  for (const auto& req : batch.padded_reqs) {
-    meta->seq_lens.push_back(req->device_len());
-    meta->cached_lens.push_back(req->cached_len);
+  meta->seq_lens.resize(bs);
+  meta->cached_lens.resize(bs);
+  meta->kv_indptr_host.assign(bs + 1, 0);
+  for (int i = 0; i < bs; ++i) {
+    const auto& req = batch.padded_reqs[i];
+    meta->seq_lens[i] = req->device_len();
+    meta->cached_lens[i] = req->cached_len;
+    meta->kv_indptr_host[i + 1] = meta->kv_indptr_host[i] + req->device_len();
   }
-  meta->kv_indptr_host.assign(1, 0);
-  for (const auto& req : batch.padded_reqs)
-    meta->kv_indptr_host.push_back(meta->kv_indptr_host.back() + req->device_len());
 
+  // Which requests go to which kernel. Decode batches (flashinfer_backend.cu:
+  // 408-464): every request, query row i. Prefill batches (:466-519):
+  // qo_len = max(1, extend), kv_len = device_len, and with no cache hit
+  // anywhere qo_indptr = kv_indptr; one-token requests go to the split-KV
+  // decode kernel, the rest to the causal prefill kernel (each writes its
+  // own rows of o).
+  std::vector<int> dec, pre;
   if (batch.is_decode()) {
-    // Reference: decode branch of prepare_metadata (flashinfer_backend.cu:408-464).
-    std::vector<int> all(bs);
-    std::vector<int32_t> rows(bs);
-    for (int i = 0; i < bs; ++i) all[i] = rows[i] = i;
-    build_decode_rows(*meta, all, rows, batch);
+    dec.resize(bs);
+    for (int i = 0; i < bs; ++i) dec[i] = i;
     meta->qo_indptr_host.resize(bs + 1);
     for (int i = 0; i <= bs; ++i) meta->qo_indptr_host[i] = i;
-    meta->indptr = meta->dec_kv_indptr;
-    batch.attn_metadata = meta;
-    return;
-  }
-
-  // Prefill branch (flashinfer_backend.cu:466-519): qo_len = max(1, extend),
-  // kv_len = device_len; with no cache hit anywhere qo_indptr = kv_indptr.
-  std::vector<int32_t> qo_lens(bs);
-  bool all_no_cache_hit = true;
-  for (int i = 0; i < bs; ++i) {
-    qo_lens[i] = std::max(1, batch.padded_reqs[i]->extend_len());
-    all_no_cache_hit = all_no_cache_hit && batch.padded_reqs[i]->cached_len == 0;
-  }
-  if (all_no_cache_hit) {
-    meta->qo_indptr_host = meta->kv_indptr_host;
   } else {
-    meta->qo_indptr_host.assign(1, 0);
+    bool all_no_cache_hit = true;
+    for (int i = 0; i < bs; ++i) all_no_cache_hit = all_no_cache_hit && batch.padded_reqs[i]->cached_len == 0;
+    if (all_no_cache_hit) {
+      meta->qo_indptr_host = meta->kv_indptr_host;
+    } else {
+      meta->qo_indptr_host.assign(bs + 1, 0);
+      for (int i = 0; i < bs; ++i)
+        meta->qo_indptr_host[i + 1] =
+            meta->qo_indptr_host[i] + std::max(1, batch.padded_reqs[i]->extend_len());
+    }
     for (int i = 0; i < bs; ++i)
-      meta->qo_indptr_host.push_back(meta->qo_indptr_host.back() + qo_lens[i]);
+      (meta->qo_indptr_host[i + 1] - meta->qo_indptr_host[i] == 1 ? dec : pre).push_back(i);
   }
-  meta->indptr = to_device(meta->qo_indptr_host, *meta);
+  const int nd = static_cast<int>(dec.size()), np = static_cast<int>(pre.size());
 
-  // Route: one-token requests to the split-KV decode kernel, the rest to the
-  // causal prefill kernel; each writes its own rows of o.
-  std::vector<int> dec, pre;
-  for (int i = 0; i < bs; ++i) {
-    const int q_len = meta->qo_indptr_host[i + 1] - meta->qo_indptr_host[i];
-    (q_len == 1 ? dec : pre).push_back(i);
-  }
-  if (!dec.empty()) {
-    // Both kinds of rows: one launch with the decode rows on the CU share
-    // their K/V bytes need next to the prefill's flops.
-    if (!pre.empty() && fused_mixed_ && num_kv_heads_ <= 8 && 8 % num_kv_heads_ == 0) {
-      int64_t dec_tokens = 0;
-      for (int i : dec) dec_tokens += batch.padded_reqs[i]->device_len();
-      double flops = 0.0;
-      for (int i : pre) {
-        const double qo = meta->qo_indptr_host[i + 1] - meta->qo_indptr_host[i];
-        const double kv = batch.padded_reqs[i]->device_len();
-        flops += qo * (kv - qo) + qo * (qo + 1) / 2;
-      }
-      flops *= 4.0 * head_dim_ * num_qo_heads_;
-      const int h = sgl_mixed_decode_cus(dec_tokens, num_kv_heads_, head_dim_, flops);
-      if (h < device_cus_) {
-        meta->fused = true;
-        meta->dec_cus = h;
-      }
+  // Both kinds of rows: one launch with the decode rows on the CU share
+  // their K/V bytes need next to the prefill's flops.
+  if (nd > 0 && np > 0 && fused_mixed_ && num_kv_heads_ <= 8 && 8 % num_kv_heads_ == 0) {
+    int64_t dec_tokens = 0;
+    for (int i : dec) dec_tokens += batch.padded_reqs[i]->device_len();
+    double flops = 0.0;
+    for (int i : pre) {
+      const double qo = meta->qo_indptr_host[i + 1] - meta->qo_indptr_host[i];
+      const double kv = batch.padded_reqs[i]->device_len();
+      flops += qo * (kv - qo) + qo * (qo + 1) / 2;
     }
-    std::vector<int32_t> rows;
-    for (int i : dec) rows.push_back(meta->qo_indptr_host[i]);
-    build_decode_rows(*meta, dec, rows, batch, meta->dec_cus);
-  }
-  if (!pre.empty()) {
-    const int n = static_cast<int>(pre.size());
-    std::vector<int32_t> qo_indptr(n + 1, 0), kv_indptr(n + 1, 0), q_start(n), table_idx(n);
-    int max_qo = 0;
-    for (int i = 0; i < n; ++i) {
-      const int r = pre[i];
-      const int q_len = meta->qo_indptr_host[r + 1] - meta->qo_indptr_host[r];
-      qo_indptr[i + 1] = qo_indptr[i] + q_len;
-      kv_indptr[i + 1] = kv_indptr[i] + batch.padded_reqs[r]->device_len();
-      q_start[i] = meta->qo_indptr_host[r];
-      table_idx[i] = batch.padded_reqs[r]->table_idx;
-      max_qo = std::max(max_qo, q_len);
+    flops *= 4.0 * head_dim_ * num_qo_heads_;
+    const int h = sgl_mixed_decode_cus(dec_tokens, num_kv_heads_, head_dim_, flops);
+    if (h < device_cus_) {
+      meta->fused = true;
+      meta->dec_cus = h;
     }
-    meta->num_prefill = n;
+  }
+
+  // Host fields of both kinds of rows, then one upload.
+  std::vector<int32_t> dec_ip(nd + 1, 0), dec_rows(nd), pre_qo(np + 1, 0), pre_ip(np + 1, 0),
+      pre_start(np), table(nd + np);
+  for (int i = 0; i < nd; ++i) {
+    const auto& req = batch.padded_reqs[dec[i]];
+    dec_ip[i + 1] = dec_ip[i] + req->device_len();
+    dec_rows[i] = meta->qo_indptr_host[dec[i]];
+    table[i] = req->table_idx;
+  }
+  int max_qo = 0;
+  for (int i = 0; i < np; ++i) {
+    const int r = pre[i];
+    const auto& req = batch.padded_reqs[r];
+    const int q_len = meta->qo_indptr_host[r + 1] - meta->qo_indptr_host[r];
+    pre_qo[i + 1] = pre_qo[i] + q_len;
+    pre_ip[i + 1] = pre_ip[i] + req->device_len();
+    pre_start[i] = meta->qo_indptr_host[r];
+    table[nd + i] = req->table_idx;
+    max_qo = std::max(max_qo, q_len);
+  }
+  // The index arrays: decode rows' indices, then (from a 256-byte boundary)
+  // the prefill rows'. One gather fills both: its kv_indptr runs over the
+  // decode rows and continues at the prefill base, so the last decode row's
+  // gather also fills the padding gap (page-table values, never read).
+  const int64_t dec_total = dec_ip[nd], pre_total = pre_ip[np];
+  const int64_t pre_base = nd > 0 ? align_field(std::max<int64_t>(dec_total, 1)) : 0;
+  TORCH_CHECK(pre_base + pre_total <= 0x7fffffff, "batch KV tokens exceed int32 offsets");
+  PackedUpload up;
+  const int64_t o_qo = batch.is_prefill() ? up.add(meta->qo_indptr_host) : -1;
+  const int64_t o_dip = up.add(dec_ip), o_drows = up.add(dec_rows);
+  const int64_t o_pqo = up.add(pre_qo), o_pip = up.add(pre_ip), o_pstart = up.add(pre_start);
+  const int64_t o_table = up.add(table);
+  int64_t o_gather_ip = o_dip;  // decode rows only
+  if (np > 0 && nd == 0) o_gather_ip = o_pip;
+  if (np > 0 && nd > 0) {
+    std::vector<int32_t> both(nd + np + 1);
+    for (int i = 0; i < nd; ++i) both[i] = dec_ip[i];
+    for (int i = 0; i <= np; ++i) both[nd + i] = static_cast<int32_t>(pre_base + pre_ip[i]);
+    o_gather_ip = up.add(both);
+  }
+  const int64_t o_ind = up.size();
+  const int64_t ind_len = pre_base + (np > 0 ? std::max<int64_t>(pre_total, 1) : 0);
+  auto dev = up.send(std::max<int64_t>(ind_len, 1), kv_cache_->device(), meta->host_staging);
+  auto field = [&](int64_t off, int64_t n) { return dev.slice(0, off, off + n); };
+  if (nd + np > 0)
+    check_sgl(sgl_build_decode_indices(page_table_.data_ptr<int32_t>(), page_table_.size(0),
+                                       page_table_.stride(0), page_table_.size(1),
+                                       dev.data_ptr<int32_t>() + o_table,
+                                       dev.data_ptr<int32_t>() + o_gather_ip,
+                                       dev.data_ptr<int32_t>() + o_ind, nd + np,
+                                       current_stream(kv_cache_->device())),
+              "sgl_build_decode_indices");
+
+  if (nd > 0 || batch.is_decode()) {
+    meta->num_decode = nd;
+    meta->dec_kv_indptr = field(o_dip, nd + 1);
+    meta->dec_q_rows = field(o_drows, nd);
+    meta->dec_table_idx = field(o_table, nd);
+    meta->dec_indices = field(o_ind, std::max<int64_t>(dec_total, 1));
+    if (meta->fused)
+      check_sgl(sgl_decode_plan_cus(dec_ip.data(), nd, num_qo_heads_, num_kv_heads_, head_dim_,
+                                    meta->dec_cus, &meta->dec_plan),
+                "sgl_decode_plan_cus");
+    else
+      check_sgl(sgl_decode_plan(dec_ip.data(), nd, num_qo_heads_, num_kv_heads_, head_dim_,
+                                &meta->dec_plan),
+                "sgl_decode_plan");
+    // The split workspace grows in forward, on the stream that uses it: a
+    // scheduler that prepares step n + 1 on its own stream while step n's
+    // forward runs must not free the buffer that forward is using.
+  }
+  if (np > 0) {
+    meta->num_prefill = np;
     meta->max_qo_len = max_qo;
-    meta->pre_qo_indptr = to_device(qo_indptr, *meta);
-    meta->pre_kv_indptr = to_device(kv_indptr, *meta);
-    meta->pre_q_start = to_device(q_start, *meta);
-    meta->pre_table_idx = to_device(table_idx, *meta);
-    meta->pre_indices = torch::empty({std::max(kv_indptr[n], 1)}, kI32.device(kv_cache_->device()));
-    // Device gather replaces the reference's torch::cat of page-table slices.
-    check_sgl(sgl_build_prefill_indices(page_table_.data_ptr<int32_t>(), page_table_.size(0),
-                                        page_table_.stride(0), page_table_.size(1),
-                                        meta->pre_table_idx.data_ptr<int32_t>(),
-                                        meta->pre_kv_indptr.data_ptr<int32_t>(),
-                                        meta->pre_indices.data_ptr<int32_t>(), n,
-                                        current_stream(kv_cache_->device())),
-              "sgl_build_prefill_indices");
+    meta->pre_qo_indptr = field(o_pqo, np + 1);
+    meta->pre_kv_indptr = field(o_pip, np + 1);
+    meta->pre_q_start = field(o_pstart, np);
+    meta->pre_table_idx = field(o_table + nd, np);
+    meta->pre_indices = field(o_ind + pre_base, std::max<int64_t>(pre_total, 1));
   }
+  meta->indptr = batch.is_prefill() ? field(o_qo, bs + 1) : meta->dec_kv_indptr;
   batch.attn_metadata = meta;
 }
 
@@ -524,12 +569,15 @@ void HipAttnBackend::prepare_for_replay(Batch& batch) {
   }
   check_sgl(sgl_decode_plan_check(&cap->dec_plan, meta->kv_indptr_host.data(), bs),
             "sgl_decode_plan_check");
-  const int64_t total = meta->kv_indptr_host[bs];
-  cap->dec_kv_indptr.copy_(meta->dec_kv_indptr, /*non_blocking=*/true);
-  if (total > 0)
-    cap->dec_indices.slice(0, 0, total).copy_(meta->dec_indices.slice(0, 0, total),
-                                              /*non_blocking=*/true);
+  // kv_indptr and indices into the capture buffers: one launch on the
+  // engine stream, after the previous replay's reads of them.
+  const sgl_i32_copy_t copies[2] = {
+      {meta->dec_kv_indptr.data_ptr<int32_t>(), cap->dec_kv_indptr.data_ptr<int32_t>(), bs + 1},
+      {meta->dec_indices.data_ptr<int32_t>(), cap->dec_indices.data_ptr<int32_t>(),
+       meta->kv_indptr_host[bs]}};
+  check_sgl(sgl_copy_i32(copies, 2, current_stream(kv_cache_->device())), "sgl_copy_i32");
   cap->kv_indptr_host = meta->kv_indptr_host;
+  cap->host_staging = meta->host_staging;  // the source's pending H2D copy stays alive
   batch.attn_metadata = cap;
 }
 
@@ -595,6 +643,30 @@ void HipAttnBackend::init_mixed_capture_graph(int max_seq_len, int max_decode_ro
   mixed_ = std::move(m);
 }
 
+bool HipAttnBackend::pad_mixed_batch(Batch& batch, const std::shared_ptr<Req>& dummy) const {
+  TORCH_CHECK(batch.is_prefill(), "pad_mixed_batch pads prefill-phase (mixed) batches");
+  TORCH_CHECK(dummy && dummy->cached_len == 0 && dummy->device_len() == 1,
+              "the dummy request has cached_len 0 and device_len 1");
+  if (!mixed_) return false;
+  // Query rows as prepare_metadata counts them: qo_len = max(1, extend),
+  // or device_len when no request has a cache hit.
+  const int bs = batch.padded_size();
+  bool all_no_cache_hit = true;
+  for (const auto& r : batch.padded_reqs) all_no_cache_hit = all_no_cache_hit && r->cached_len == 0;
+  int n_dec = 0;
+  for (const auto& r : batch.padded_reqs)
+    n_dec += (all_no_cache_hit ? r->device_len() : std::max(1, r->extend_len())) == 1;
+  const int n_pre = bs - n_dec;
+  int best = -1;
+  for (const auto& kv : mixed_->metadata)
+    if (kv.first.second == n_pre && kv.first.first >= n_dec &&
+        (best < 0 || kv.first.first < best))
+      best = kv.first.first;
+  if (best < 0) return false;
+  batch.padded_reqs.insert(batch.padded_reqs.end(), static_cast<size_t>(best - n_dec), dummy);
+  return true;
+}
+
 void HipAttnBackend::check_mixed_capacity(const HipAttnMetadata& m) const {
   TORCH_CHECK(m.num_decode <= mixed_->max_dec, "mixed step has ", m.num_decode,
               " decode rows; capture capacity is ", mixed_->max_dec);
@@ -607,25 +679,31 @@ void HipAttnBackend::check_mixed_capacity(const HipAttnMetadata& m) const {
                 "request longer than the captured max_seq_len");
 }
 
-// Device-to-device copy of a batch's metadata contents into capture buffers.
+// A batch's metadata contents into capture buffers: every field in one
+// device launch (sgl_copy_i32) on the current stream.
 void HipAttnBackend::copy_contents(HipAttnMetadata& dst, const HipAttnMetadata& src) {
   const int bs = static_cast<int>(src.qo_indptr_host.size()) - 1;
-  dst.indptr.slice(0, 0, bs + 1).copy_(src.indptr.slice(0, 0, bs + 1), true);
+  std::vector<sgl_i32_copy_t> c;
+  auto add = [&](const torch::Tensor& from, torch::Tensor& to, int64_t n) {
+    if (n > 0) c.push_back({from.data_ptr<int32_t>(), to.data_ptr<int32_t>(), n});
+  };
+  add(src.indptr, dst.indptr, bs + 1);
   if (src.num_decode > 0) {
     const int n = src.num_decode;
-    dst.dec_kv_indptr.slice(0, 0, n + 1).copy_(src.dec_kv_indptr.slice(0, 0, n + 1), true);
-    dst.dec_q_rows.slice(0, 0, n).copy_(src.dec_q_rows.slice(0, 0, n), true);
-    const int64_t total = src.dec_indices.numel();
-    dst.dec_indices.slice(0, 0, total).copy_(src.dec_indices, true);
+    add(src.dec_kv_indptr, dst.dec_kv_indptr, n + 1);
+    add(src.dec_q_rows, dst.dec_q_rows, n);
+    add(src.dec_indices, dst.dec_indices, src.dec_indices.numel());
   }
   if (src.num_prefill > 0) {
     const int n = src.num_prefill;
-    dst.pre_qo_indptr.slice(0, 0, n + 1).copy_(src.pre_qo_indptr.slice(0, 0, n + 1), true);
-    dst.pre_kv_indptr.slice(0, 0, n + 1).copy_(src.pre_kv_indptr.slice(0, 0, n + 1), true);
-    dst.pre_q_start.slice(0, 0, n).copy_(src.pre_q_start.slice(0, 0, n), true);
-    const int64_t total = src.pre_indices.numel();
-    dst.pre_indices.slice(0, 0, total).copy_(src.pre_indices, true);
+    add(src.pre_qo_indptr, dst.pre_qo_indptr, n + 1);
+    add(src.pre_kv_indptr, dst.pre_kv_indptr, n + 1);
+    add(src.pre_q_start, dst.pre_q_start, n);
+    add(src.pre_indices, dst.pre_indices, src.pre_indices.numel());
   }
+  check_sgl(sgl_copy_i32(c.data(), static_cast<int>(c.size()),
+                         current_stream(src.indptr.device())),
+            "sgl_copy_i32");
   dst.seq_lens = src.seq_lens;
   dst.cached_lens = src.cached_lens;
   dst.qo_indptr_host = src.qo_indptr_host;

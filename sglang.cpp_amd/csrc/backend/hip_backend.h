@@ -10,6 +10,7 @@
 #pragma once
 
 #include <c10/core/Stream.h>
+#include <c10/hip/HIPStream.h>
 #include <hip/hip_runtime.h>
 #include <torch/torch.h>
 
@@ -78,8 +79,8 @@ struct HipAttnMetadata : public BaseAttnMetadata {
 
   torch::Tensor get_last_indices(int bs) const override;
   // Marks the device tensors as used on `stream` (the scheduler prepares
-  // metadata on its own stream; scheduler.cc:171-179 does this by downcast).
-  void record_stream(c10::Stream stream) const;
+  // metadata on its own stream; scheduler.cc:152-179 does this by downcast).
+  void record_stream(const c10::hip::HIPStream& stream) const;
 };
 
 class HipAttnBackend : public BaseAttnBackend {
@@ -110,6 +111,17 @@ class HipAttnBackend : public BaseAttnBackend {
   void prepare_for_capture(Batch& batch) override;
   void prepare_for_replay(Batch& batch) override;
 
+  // GraphRunner::pad_batch (src/engine/engine.cc:628-645) for mixed steps:
+  // appends copies of `dummy` (the reference's dummy_req_: table_idx the page
+  // table's spare row, whose columns all hold the spare slot; cached_len 0,
+  // device_len 1, hence one query row over the spare slot) until the
+  // batch's decode rows reach the smallest captured mixed step with the same
+  // number of prefill requests. The caller extends positions / out_loc with
+  // one token per dummy (position 0, the spare slot), as the reference's
+  // prepare_batch does over padded_reqs. Returns false, batch unchanged, when
+  // no captured step fits.
+  bool pad_mixed_batch(Batch& batch, const std::shared_ptr<Req>& dummy) const;
+
   // Attention over the pool only (K/V of the new tokens already stored, e.g.
   // by the fused norm + RoPE + store pass). q: [T, Hq, D] view; returns
   // [T, Hq * D].
@@ -133,14 +145,11 @@ class HipAttnBackend : public BaseAttnBackend {
   std::shared_ptr<HipAttnMetadata> metadata_of(Batch& batch) const;
   torch::Tensor& workspace(int64_t bytes);
   torch::Tensor to_device(const std::vector<int32_t>& host, HipAttnMetadata& meta);
-  void build_decode_rows(HipAttnMetadata& meta, const std::vector<int>& reqs,
-                         const std::vector<int32_t>& q_rows, const Batch& batch,
-                         int decode_cus = 0);
 
   void prepare_mixed_for_capture(Batch& batch);
   void prepare_mixed_for_replay(Batch& batch);
   void check_mixed_capacity(const HipAttnMetadata& m) const;
-  static void copy_contents(HipAttnMetadata& dst, const HipAttnMetadata& src);
+  void copy_contents(HipAttnMetadata& dst, const HipAttnMetadata& src);
 
   struct MixedCapture {
     int max_seq_len = 0, max_dec = 0, max_pre = 0, max_qo = 0;

@@ -67,6 +67,31 @@ __global__ void __launch_bounds__(256) gather_int32_2d_kernel(
   out[i] = (r >= 0 && r < rows && p >= 0 && p < cols) ? table[r * stride + p] : 0;
 }
 
+// Several int32 copies in one launch (the capture buffers of a replayed
+// step); every workgroup strides over each entry in turn, 16 bytes per lane
+// where source and destination allow it.
+struct CopyArgs {
+  sgl_i32_copy_t c[SGL_MAX_I32_COPIES];
+  int n;
+};
+
+__global__ void __launch_bounds__(256) copy_i32_kernel(CopyArgs a) {
+  const int64_t tid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int j = 0; j < a.n; ++j) {
+    const int32_t* src = a.c[j].src;
+    int32_t* dst = a.c[j].dst;
+    const int64_t n = a.c[j].count;
+    const bool vec = ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) & 15) == 0;
+    int64_t head = 0;
+    if (vec) {
+      head = n / 4 * 4;
+      for (int64_t i = tid * 4; i < head; i += stride * 4) stg128(dst + i, ldg128(src + i));
+    }
+    for (int64_t i = head + tid; i < n; i += stride) dst[i] = src[i];
+  }
+}
+
 // Page allocation -> token-granular page table. Allocation a = (row,
 // first_page, last_page) takes page starts [pre[a], pre[a+1]) of the batch's
 // allocated pages, pre the exclusive prefix sum of last - first. Each block
@@ -200,6 +225,25 @@ extern "C" int sgl_write_page_table(int32_t* page_table, int64_t rows, int64_t s
   hipLaunchKernelGGL(sgl::write_page_table_kernel, dim3(static_cast<uint32_t>(blocks)),
                      dim3(256), 0, static_cast<hipStream_t>(stream), page_table, rows, stride,
                      cols, page_starts, num_pages, alloc_info, num_allocs, page_size);
+  return sgl::launch_status();
+}
+
+extern "C" int sgl_copy_i32(const sgl_i32_copy_t* copies, int num_copies, void* stream) {
+  if (num_copies < 0 || num_copies > SGL_MAX_I32_COPIES || (num_copies > 0 && !copies))
+    return SGL_ERR_INVALID_ARG;
+  sgl::CopyArgs a{};
+  int64_t most = 0;
+  for (int j = 0; j < num_copies; ++j) {
+    const sgl_i32_copy_t& c = copies[j];
+    if (c.count < 0 || (c.count > 0 && (!c.src || !c.dst))) return SGL_ERR_INVALID_ARG;
+    if (c.count == 0) continue;
+    a.c[a.n++] = c;
+    most = std::max(most, c.count);
+  }
+  if (a.n == 0) return SGL_OK;
+  const int64_t blocks = std::min<int64_t>(1024, (most + 1023) / 1024);
+  hipLaunchKernelGGL(sgl::copy_i32_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), a);
   return sgl::launch_status();
 }
 

@@ -70,6 +70,16 @@ def test_argument_checks_reject_before_launch():
                                            1, 128, ctypes.c_float(1e-6), 0, None) == -4
     assert lib.sgl_paged_prefill(16, 0, 0, 16, 16, 0, 0, 16, 16, 16, None, 2, 4, 16, 8, 64,
                                  ctypes.c_float(0.1), 16, 0, 0, None) == -2  # head_dim 64
+    # batched int32 copies: too many entries, a null pointer with work, nothing to do
+    copies = (capi.I32Copy * 9)()
+    assert lib.sgl_copy_i32(copies, 9, None) == -1
+    copies[0] = capi.I32Copy(None, 16, 5)
+    assert lib.sgl_copy_i32(copies, 1, None) == -1
+    copies[0] = capi.I32Copy(16, 16, -1)
+    assert lib.sgl_copy_i32(copies, 1, None) == -1
+    copies[0] = capi.I32Copy(None, None, 0)
+    assert lib.sgl_copy_i32(copies, 1, None) == 0
+    assert lib.sgl_copy_i32(None, 0, None) == 0
 
 
 def ws_bytes(units, hq):
