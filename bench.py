@@ -507,15 +507,30 @@ def cpu_baseline_fused(torch, wl, w):
     pos = torch.from_numpy(b.positions.astype(np.int64))
     loc = torch.from_numpy(b.out_loc.astype(np.int64))
     eps = w.extra["eps"]
-    med, runs = tc.median_time(lambda: tc.fused_qknorm_rope_store(qkv, kc, vc, qw, kw, cos, sin,
-                                                                   pos, loc, hq, hkv, eps))
+
+    def once():
+        tc.fused_qknorm_rope_store(qkv, kc, vc, qw, kw, cos, sin, pos, loc, hq, hkv, eps)
+
+    # One pass takes tens of milliseconds, where scheduler noise is large:
+    # each timed run repeats the pass until it lasts about half a second.
+    once()
+    t0 = time.perf_counter()
+    once()
+    reps = max(1, int(0.5 / max(time.perf_counter() - t0, 1e-3)))
+
+    def timed():
+        for _ in range(reps):
+            once()
+
+    med, runs = tc.median_time(timed, runs=7)
+    med, runs = med / reps, [t / reps for t in runs]
     nbytes = wl.fused_store_bytes(s, T)
     return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": threads,
             "kind": "port", "cpu_model": tc.host_info()["cpu_model"], "median_s": round(med, 4),
             "runs_s": [round(t, 4) for t in runs],
             "sample": f"LibTorch-CPU fused qk-norm + RoPE + KV store (oracle/torch_cpu.py), all "
-                      f"{T} tokens of {w.name}, median of 5 runs after 1 warm-up, "
-                      f"{threads} threads"}
+                      f"{T} tokens of {w.name}, {reps} passes per timed run, median of 7 runs "
+                      f"after 1 warm-up, {threads} threads"}
 
 
 def cpu_baseline_mixed(torch, wl, w):
