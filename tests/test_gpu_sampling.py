@@ -291,6 +291,19 @@ def test_softmax_temperature_qwen3_vocab(oracle, dev, dtype):
     assert bool((got[2, ::7] == 0).all())
 
 
+@pytest.mark.parametrize("mode", ["plain", "top_k", "top_p", "top_k_top_p"])
+def test_sampling_from_logits_flat_rows(dev, mode):
+    """Nearly flat rows (every probability below the copy threshold): every
+    round sweeps the row again, and copies above the pivot overflow."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(33)
+    B = 6
+    logits = (torch.randn((B, QWEN3_VOCAB), device=dev, generator=g) * 0.05).to(torch.bfloat16)
+    logits[1, :5] = 6.0  # one row with a few dominant entries
+    temps = torch.ones(B, device=dev)
+    _logits_case(dev, logits, temps, mode, 34, "flat")
+
+
 @pytest.mark.parametrize("vocab,offset,dtype", [
     (1003, 0, torch.bfloat16),     # partial last chunk
     (8, 0, torch.float16),         # one chunk
@@ -376,6 +389,9 @@ def test_sampling_from_logits_equals_softmax_then_draw(dev, dtype, mode):
     (5000, 1, torch.bfloat16),    # unaligned rows
     (200001, 0, torch.float16),   # rows the softmax kernel streams
     (4099, 1, torch.float32),     # unaligned fp32 rows
+    (32000, 0, torch.bfloat16),   # a 32K vocabulary
+    (65536, 0, torch.float16),    # 64 blocks exactly
+    (QWEN3_VOCAB + 8, 0, torch.bfloat16),  # just past the Qwen3 vocabulary
 ])
 def test_sampling_from_logits_shapes(dev, vocab, offset, dtype):
     g = torch.Generator(device=dev)
