@@ -64,6 +64,9 @@ def parse():
     ap.add_argument("--ceilings-only", action="store_true",
                     help="only measure the practical ceilings of this GPU (stream read, MFMA "
                          "issue on random and constant bf16 operands, empty launch) and print them")
+    ap.add_argument("--no-resident-leg", action="store_true",
+                    help="time rotated (HBM-resident) buffer sets only, without the one-set "
+                         "cache-resident leg (profiler runs)")
     ap.add_argument("--replay-host-only", action="store_true",
                     help="only measure the host cost of prepare_metadata + prepare_for_replay "
                          "per serving step (configurations 4 and 5)")
@@ -960,8 +963,21 @@ def setup_sampler_step(torch, capi, dev, seed=0, sets=1):
                 "batch": B, "vocab": V, "logits": "bf16", "top_k": 50, "top_p": 0.9})
 
 
+# Whether rotated workloads also time their one-set (cache-resident) leg;
+# off for profiler runs, whose summaries then hold the rotated launches only.
+RESIDENT_LEG = True
+
+
+def _resident_leg(run, step, steps, warmup):
+    return run(step, steps, warmup)[1] if RESIDENT_LEG else None
+
+
 def _resident(rec_rot, ev_1, nbytes=None, flops=None, sets=1):
     """The one-set (cache-resident) figure beside a rotated-buffer record."""
+    rec_rot["buffer_sets"] = sets
+    rec_rot["rotated_bytes"] = ROTATE_BYTES
+    if ev_1 is None:
+        return rec_rot
     out = {"kernel_ms": ev_1}
     if nbytes:
         out["GB/s"] = nbytes / (ev_1 * 1e-3) / 1e9
@@ -969,8 +985,6 @@ def _resident(rec_rot, ev_1, nbytes=None, flops=None, sets=1):
     if flops:
         out["TFLOP/s"] = flops / (ev_1 * 1e-3) / 1e12
         out["mfma_frac"] = round(out["TFLOP/s"] / BF16_PEAK_TFLOPS, 4)
-    rec_rot["buffer_sets"] = sets
-    rec_rot["rotated_bytes"] = ROTATE_BYTES
     rec_rot["cache_resident"] = out
     return rec_rot
 
@@ -979,7 +993,7 @@ def run_workload(name, torch, capi, wl, dev, steps, warmup, cfg5_layers, min_war
     timer = Timer(torch, min_warm_s)
     if name == "sampler_step":
         fused, two, torch_probs, nbytes, shape = setup_sampler_step(torch, capi, dev)
-        _, ev1 = timer.run_graph(fused, steps, warmup)
+        ev1 = _resident_leg(timer.run_graph, fused, steps, warmup)
         del fused, two, torch_probs
         sets = rotation_sets(nbytes)
         fused, two, torch_probs, nbytes, shape = setup_sampler_step(torch, capi, dev, sets=sets)
@@ -993,11 +1007,11 @@ def run_workload(name, torch, capi, wl, dev, steps, warmup, cfg5_layers, min_war
                "GB/s": nbytes / (wall * 1e-3) / 1e9,
                "two_launch_ms": two_ev, "torch_probs_then_draw_ms": tp_ev,
                "speedup_vs_torch_probs_then_draw": tp_ev / ev,
-               "roofline": roofline_hbm(nbytes, ev, None)}
+               "roofline": roofline_hbm(nbytes, ev, "sampler_step_top_k_top_p")}
         return None, _resident(rec, ev1, nbytes, sets=sets)
     if name == "sampler_softmax":
         step, torch_step, nbytes, shape = setup_sampler_softmax(torch, capi, dev)
-        _, ev1 = timer.run_graph(step, steps, warmup)
+        ev1 = _resident_leg(timer.run_graph, step, steps, warmup)
         del step, torch_step
         torch.cuda.empty_cache()
         sets = rotation_sets(nbytes)
@@ -1014,7 +1028,7 @@ def run_workload(name, torch, capi, wl, dev, steps, warmup, cfg5_layers, min_war
         return None, _resident(rec, ev1, nbytes, sets=sets)
     if name == "sampling":
         step, nbytes, shape = setup_sampling(torch, capi, dev)
-        _, ev1 = timer.run(step, steps, warmup)
+        ev1 = _resident_leg(timer.run, step, steps, warmup)
         del step
         torch.cuda.empty_cache()
         sets = rotation_sets(nbytes)
@@ -1027,7 +1041,7 @@ def run_workload(name, torch, capi, wl, dev, steps, warmup, cfg5_layers, min_war
         return None, _resident(rec, ev1, nbytes, sets=sets)
     if name in ("resid_norm", "resid_act"):
         step, nbytes, shape = setup_resid(torch, capi, name, dev)
-        _, ev1 = timer.run(step, steps, warmup)
+        ev1 = _resident_leg(timer.run, step, steps, warmup)
         del step
         torch.cuda.empty_cache()
         sets = rotation_sets(nbytes)
@@ -1064,7 +1078,7 @@ def run_workload(name, torch, capi, wl, dev, steps, warmup, cfg5_layers, min_war
             wall, ev = timer.run_graph(step, steps, warmup)
             sets, ev1 = 1, None
         else:
-            _, ev1 = timer.run(step, steps, warmup)
+            ev1 = _resident_leg(timer.run, step, steps, warmup)
             del step
             sets = rotation_sets(nbytes)
             step, nbytes, flops = setup_prefill(torch, capi, wl, w, dev, sets=sets)
@@ -1075,13 +1089,13 @@ def run_workload(name, torch, capi, wl, dev, steps, warmup, cfg5_layers, min_war
                "GB/s": nbytes / (wall * 1e-3) / 1e9,
                "roofline": roofline_mfma(flops, ev, key),
                "roofline_hbm": roofline_hbm(nbytes, ev, None)}
-        if ev1 is not None:
+        if name != "cfg2":
             rec = _resident(rec, ev1, nbytes, flops, sets=sets)
         return w, rec
     if name == "cfg3":
         w = wl.cfg3_fused_store()
         step, nbytes = setup_fused(torch, capi, wl, w, dev)
-        _, ev1 = timer.run_graph(step, steps, warmup)
+        ev1 = _resident_leg(timer.run_graph, step, steps, warmup)
         del step
         torch.cuda.empty_cache()
         sets = rotation_sets(nbytes)
@@ -1108,6 +1122,8 @@ def run_workload(name, torch, capi, wl, dev, steps, warmup, cfg5_layers, min_war
 
 def main():
     args = parse()
+    global RESIDENT_LEG
+    RESIDENT_LEG = not args.no_resident_leg
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the attention hot "
               "path is single-GPU in this build — run with --gpus 1.", file=sys.stderr)

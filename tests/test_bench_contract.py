@@ -67,13 +67,13 @@ def test_traffic_keys_have_profiles():
     keys = ["paged_decode_cfg1", "paged_decode_cfg4", "paged_prefill_cfg2",
             "paged_prefill_cfg5_chunk", "fused_qknorm_rope_store_cfg3",
             "fused_add_rmsnorm_qwen3_8b", "silu_and_mul_qwen3_8b", "sampling_top_k_top_p",
-            "softmax_temperature_sampler"]
+            "softmax_temperature_sampler", "sampler_step_top_k_top_p"]
     for k in keys:
         assert k in traffic and traffic[k] > 0, k
         assert (REPO / "profiles" / f"{k}.md").exists(), k
     # every key bench.py names literally is one of them
     for k in ("paged_prefill_cfg2", "paged_prefill_cfg5_chunk", "fused_qknorm_rope_store_cfg3",
-              "sampling_top_k_top_p", "softmax_temperature_sampler"):
+              "sampling_top_k_top_p", "softmax_temperature_sampler", "sampler_step_top_k_top_p"):
         assert f'"{k}"' in src, k
 
 
