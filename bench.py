@@ -873,10 +873,10 @@ def measure_ceilings(torch, dev, min_warm_s=0.5, sweep=None):
     return out
 
 
-# HBM-bound workloads that write a third or more of their bytes: held
-# against the streaming copy's ceiling (read and write together), the
-# others against the streaming read's.
-WRITE_HEAVY = ("cfg3", "resid_norm", "resid_act", "sampler_softmax")
+# HBM-bound workloads that write half or more of their bytes: held against
+# the streaming copy's ceiling (read and write together), the others
+# against the streaming read's.
+WRITE_HEAVY = ("cfg3", "resid_norm", "sampler_softmax")
 
 
 def ceiling_fracs(extra, ceil):
