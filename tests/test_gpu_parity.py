@@ -736,6 +736,42 @@ def test_prefill_wide_ragged(oracle, dev, hq, hkv, qo, prefix):
 
 
 
+def check_prefill_rows(oracle, batch, q, kc, vc, o, scale, r, toks, what):
+    """Sampled query tokens of request r: token i of its chunk sees the kv
+    prefix [0, kv - qo + i] (the causal definition), one oracle decode
+    over that prefix per token, every head."""
+    qo0, kv0 = int(batch.qo_indptr[r]), int(batch.kv_indptr[r])
+    qo_len = int(batch.qo_indptr[r + 1]) - qo0
+    kv_len = int(batch.kv_indptr[r + 1]) - kv0
+    toks = np.asarray(toks)
+    vis = kv_len - qo_len + toks + 1
+    ip = np.concatenate([[0], np.cumsum(vis)]).astype(np.int32)
+    idx = np.concatenate([batch.indices[kv0:kv0 + n] for n in vis]).astype(np.int32)
+    ref = oracle.decode(u16(q[qo0 + toks]).copy(), u16(kc), u16(vc), idx, ip, scale)
+    assert_attn_close(o[qo0 + toks].float().cpu().numpy(), ref, what=what)
+
+
+@pytest.mark.parametrize("qo,prefix,page", [
+    (2048, 4096, 16),  # configuration 5's chunk
+    (2048, 0, 1),      # no prefix: the pairs' light tiles see few kv tiles
+    (1040, 300, 16),   # an odd tile count: the middle tile's second group is empty
+    (1024, 30000, 16), # a long prefix: pairs of nearly equal tiles
+])
+def test_prefill_paired_launch_sampled(oracle, dev, qo, prefix, page):
+    """The paired launch (32q/4kv, one request, at most one workgroup per
+    CU) at full size: sampled tokens of every pair position (every 16-token
+    tile's first and last token, every third tile, plus random ones)
+    against the oracle, and no row left unwritten."""
+    note(f"prefill paired launch qo={qo} prefix={prefix} page={page}")
+    rng = np.random.default_rng(qo + prefix)
+    b = wl.make_paged_batch(rng, [prefix], [prefix + qo], page_size=page)
+    q, kc, vc, o, scale = run_prefill(dev, b, 32, 4, 128, 40)
+    assert not torch.isnan(o.float()).any()
+    edges = np.unique(np.concatenate([np.arange(0, qo, 16), np.arange(15, qo, 16)]))
+    sample = np.unique(np.concatenate([edges[::3], rng.choice(qo, 64, replace=False)]))
+    check_prefill_rows(oracle, b, q, kc, vc, o, scale, 0, sample, f"paired {qo}/{prefix}")
+
+
 @pytest.mark.parametrize("seed", [0, 1, 2, 3, 4, 5])
 def test_prefill_random_batches(oracle, dev, seed):
     """Seeded random ragged batches (lengths, prefixes, head groups, page
