@@ -290,10 +290,12 @@ def test_backend_decode_graph_capture_replay(oracle, dev, sb):
 
     scale = 1 / math.sqrt(D)
     pt = full.page_table
-    for it in range(4):
+    for it in range(5):
         lens = rng.integers(1, max_seq + 1, bs)
         if it == 3:
             lens[:] = max_seq
+        if it == 4:
+            lens[:] = 1  # every request at its first token
         loc = np.array([pt[i, lens[i] - 1] for i in range(bs)], np.int32)
         q = _randn((bs, hq * D), dev, g)
         k = _randn((bs, hkv * D), dev, g)
