@@ -547,11 +547,15 @@ __global__ void __launch_bounds__(kSmallWaves * kWave) paged_decode_small_kernel
 }
 
 // Folds the partials of every split request: one workgroup per (kv head,
-// request) handles its G heads; each thread owns 4 consecutive d of one head
-// and folds the request's pieces (any number of them) with log-sum-exp
-// weights, 16-byte loads, several in flight. Requests reaching
+// request), each thread owning 4 consecutive d of one of the G heads. The
+// pieces are folded kFoldPieces at a time, every load of a group issued at
+// once (a request of up to kFoldPieces pieces is one memory round trip
+// after kv_indptr), with a log2-sum-exp reference point that is moved, and
+// the folded sum rescaled, only when a group raises it. Requests reaching
 // past the plan's token capacity get NaN rows and the CAPACITY status.
-__global__ void __launch_bounds__(256) decode_merge_kernel(DecodeArgs a) {
+constexpr int kFoldPieces = 4;
+
+__global__ void __launch_bounds__(kMaxGroup * (kD / 4)) decode_merge_kernel(DecodeArgs a) {
   const int h = blockIdx.x;
   const int r = blockIdx.y;
   const int rb = a.kv_indptr[r];
@@ -574,30 +578,44 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(DecodeArgs a) {
   const int u0 = rb / W;
   const int u1 = (re - 1) / W;
   if (u0 == u1) return;  // whole request, written by the decode kernel
+  const int s0 = 2 * u0 + (rb > u0 * W ? 1 : 0);  // slot of the first piece
+  const int np = u1 - u0 + 1;
   for (int e = threadIdx.x; e < G * (kD / 4); e += blockDim.x) {
     const int g = e / (kD / 4);
     const int d4 = (e - g * (kD / 4)) * 4;
     const int head = h * G + g;
-    const int s0 = 2 * u0 + (rb > u0 * W ? 1 : 0);  // slot of the first piece
-    // Two passes with independent loads (no rescale chain between pieces):
-    // the largest log2-sum-exp, then the weighted sum.
     float m = -INFINITY;
-#pragma unroll 8
-    for (int u = u0; u <= u1; ++u) {
-      const int slot = u == u0 ? s0 : 2 * u;
-      m = fmaxf(m, a.part_lse[static_cast<int64_t>(slot) * a.hq + head]);
-    }
     float den = 0.f;
     f32x4_t accm = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 8
-    for (int u = u0; u <= u1; ++u) {
-      const int slot = u == u0 ? s0 : 2 * u;
-      const int64_t pidx = static_cast<int64_t>(slot) * a.hq + head;
-      const float lse = a.part_lse[pidx];
-      const f32x4_t v = *reinterpret_cast<const f32x4_t*>(a.part_o + pidx * kD + d4);
-      const float wgt = lse == -INFINITY ? 0.f : exp2f(lse - m);
-      den += wgt;
-      accm += v * wgt;
+#pragma unroll 2
+    for (int c = 0; c < np; c += kFoldPieces) {
+      float lse[kFoldPieces];
+      f32x4_t v[kFoldPieces];
+#pragma unroll
+      for (int k = 0; k < kFoldPieces; ++k) {
+        const int p = c + k;
+        const int slot = p == 0 ? s0 : 2 * (u0 + min(p, np - 1));
+        const int64_t pidx = static_cast<int64_t>(slot) * a.hq + head;
+        lse[k] = a.part_lse[pidx];
+        v[k] = *reinterpret_cast<const f32x4_t*>(a.part_o + pidx * kD + d4);
+      }
+      float mc = m;
+#pragma unroll
+      for (int k = 0; k < kFoldPieces; ++k)
+        if (c + k < np) mc = fmaxf(mc, lse[k]);
+      if (mc > m) {  // rescale what is folded so far to the new reference
+        const float sc = m == -INFINITY ? 0.f : exp2f(m - mc);
+        den *= sc;
+        accm *= sc;
+        m = mc;
+      }
+#pragma unroll
+      for (int k = 0; k < kFoldPieces; ++k) {
+        if (c + k >= np) break;
+        const float wgt = lse[k] == -INFINITY ? 0.f : exp2f(lse[k] - m);
+        den += wgt;
+        accm += v[k] * wgt;
+      }
     }
     const float inv = den > 0.f ? 1.0f / den : 0.f;
     uint16_t* op = a.o + static_cast<int64_t>(qrow) * a.o_st +
@@ -877,6 +895,9 @@ int decode_args(const sgl_decode_plan_t* plan, const void* q, int64_t q_stride_t
   return SGL_OK;
 }
 
+// Merge workgroup size: one thread per 4 d of each of the G heads, in whole waves.
+int merge_threads(int group) { return (group * (kD / 4) + kWave - 1) / kWave * kWave; }
+
 // Points the kernel arguments at a workspace of the plan's layout.
 void bind_workspace(DecodeArgs& a, const sgl_decode_plan_t* plan, void* workspace) {
   const WorkspaceLayout w = workspace_layout(plan->num_units, plan->num_qo_heads);
@@ -903,7 +924,7 @@ int launch_decode(const DecodeArgs& a, const sgl_decode_plan_t* plan, hipStream_
   if (st != SGL_OK) return st;
   // Always launched: besides folding split requests it is what reports a
   // batch that exceeds the plan.
-  hipLaunchKernelGGL(decode_merge_kernel, dim3(a.hkv, a.batch), dim3(256), 0, s, a);
+  hipLaunchKernelGGL(decode_merge_kernel, dim3(a.hkv, a.batch), dim3(merge_threads(a.group)), 0, s, a);
   return launch_status();
 }
 
@@ -1002,7 +1023,7 @@ extern "C" int sgl_paged_mixed(const sgl_decode_plan_t* plan, const void* q,
   }
   st = launch_status();
   if (st != SGL_OK) return st;
-  hipLaunchKernelGGL(decode_merge_kernel, dim3(d.hkv, d.batch), dim3(256), 0, s, d);
+  hipLaunchKernelGGL(decode_merge_kernel, dim3(d.hkv, d.batch), dim3(merge_threads(d.group)), 0, s, d);
   return launch_status();
 }
 
