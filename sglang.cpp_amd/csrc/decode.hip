@@ -36,6 +36,7 @@
 #include <math.h>
 
 #include <mutex>
+#include <type_traits>
 
 #include "common.h"
 #include "prefill_impl.h"
@@ -89,6 +90,16 @@ __device__ __forceinline__ int unit_tokens(const DecodeArgs& a, int total) {
 struct WaveLds {
   uint16_t q[16 * kQPitch];  // Q rows of the wave's G heads (zero rows past G)
 };
+
+// Per-wave LDS of the decode role that loads K as whole rows: Q, and the
+// 16-token x 16-chunk K tile of the step being transposed (chunk c of token
+// t at 16 t + (c ^ t), which keeps both the row writes and the column reads
+// free of bank conflicts).
+struct RowKWaveLds : WaveLds {
+  u32x4_t kt[256];
+};
+template <bool kRows>
+using UnitWaveLds = std::conditional_t<kRows, RowKWaveLds, WaveLds>;
 
 // Workspace carve-up shared by the plan and the launch: a 256-byte header
 // (int32 status word at offset 0), then the partial outputs and their
@@ -191,16 +202,18 @@ struct HeadState {
 //
 // K and V of step t + 1 are in flight during step t; the Q rows are loaded
 // first and the first step's K/V rows issued before Q is waited for.
-template <bool kState, bool kBarrier = !kState>
+template <bool kState, bool kBarrier = !kState, bool kRows = false>
 __device__ __forceinline__ void decode_head(const DecodeArgs& a, WaveLds& L, const int32_t* sidx,
                                             int pslot, bool whole, int h, int len, int qrow,
-                                            int lane, HeadState* st = nullptr) {
+                                            int lane, HeadState* st = nullptr,
+                                            u32x4_t* kt = nullptr) {
   const int n = lane & 15;
   const int j = lane >> 4;
   const int G = a.group;
   const bool head_ok = n < G;
   const char* klane = reinterpret_cast<const char*>(a.kc + static_cast<int64_t>(h) * a.kv_sh + 8 * j);
   const char* vlane = reinterpret_cast<const char*>(a.vc + static_cast<int64_t>(h) * a.kv_sh + 8 * n);
+  const char* krow = reinterpret_cast<const char*>(a.kc + static_cast<int64_t>(h) * a.kv_sh + 8 * n);
   const uint32_t ss_bytes = static_cast<uint32_t>(a.kv_ss * 2);
 
   // Q rows of this kv head's G query heads (16 rows x 16 chunks), for LDS.
@@ -217,7 +230,24 @@ __device__ __forceinline__ void decode_head(const DecodeArgs& a, WaveLds& L, con
   // K and V rows of the first step in flight, K issued first as inside the
   // loop (the loop-head wait counts merge both paths).
   u32x4_t kr[4], vr[4];
-  load_k_step(klane, ss_bytes, sidx[min(n, len - 1)], kr);
+  // kRows: K is loaded as V is (lane (n, j): token 4 j + e, chunk n, whole
+  // rows per instruction) and turned into the operand layout (token n,
+  // chunk 4 s + j) through the wave's LDS tile at the top of each step.
+  auto transpose_k = [&]() {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int tr = 4 * j + e;
+      kt[16 * tr + (n ^ tr)] = kr[e];
+    }
+    wave_lds_sync();
+#pragma unroll
+    for (int s4 = 0; s4 < 4; ++s4) kr[s4] = kt[16 * n + ((4 * s4 + j) ^ n)];
+    wave_lds_sync();
+  };
+  if constexpr (kRows)
+    load_v_step(krow, ss_bytes, sidx, 0, len, j, kr);
+  else
+    load_k_step(klane, ss_bytes, sidx[min(n, len - 1)], kr);
   __builtin_amdgcn_sched_barrier(0);
   load_v_step(vlane, ss_bytes, sidx, 0, len, j, vr);
   __builtin_amdgcn_sched_barrier(0);
@@ -285,10 +315,18 @@ __device__ __forceinline__ void decode_head(const DecodeArgs& a, WaveLds& L, con
     // burst than as per-head pieces spread over time.
     if constexpr (kBarrier) __builtin_amdgcn_s_barrier();
     const int tn = t + kStep;
-    const int kslot_next = sidx[min(tn + n, len - 1)];
-    const f32x4_t sacc = qk(kr);
-    __builtin_amdgcn_sched_barrier(0);
-    load_k_step(klane, ss_bytes, kslot_next, kr);  // K of the next step
+    f32x4_t sacc;
+    if constexpr (kRows) {
+      transpose_k();
+      sacc = qk(kr);
+      __builtin_amdgcn_sched_barrier(0);
+      load_v_step(krow, ss_bytes, sidx, tn, len, j, kr);  // K of the next step
+    } else {
+      const int kslot_next = sidx[min(tn + n, len - 1)];
+      sacc = qk(kr);
+      __builtin_amdgcn_sched_barrier(0);
+      load_k_step(klane, ss_bytes, kslot_next, kr);  // K of the next step
+    }
     __builtin_amdgcn_sched_barrier(0);
     softmax_pv(sacc, vr, t);
     __builtin_amdgcn_sched_barrier(0);
@@ -345,8 +383,11 @@ __device__ __forceinline__ void zero_row(const DecodeArgs& a, int qrow, int t, i
 }
 
 // LDS bytes of one unit: the per-wave Q copies, then the unit's slot indices.
+// kRows: the per-wave K tile of whole-row K loads too.
+template <bool kRows>
 __device__ __host__ inline size_t unit_lds_bytes(int hkv, int chunk) {
-  return static_cast<size_t>(hkv) * sizeof(WaveLds) + static_cast<size_t>(chunk) * sizeof(int32_t);
+  return static_cast<size_t>(hkv) * sizeof(UnitWaveLds<kRows>) +
+         static_cast<size_t>(chunk) * sizeof(int32_t);
 }
 
 // Persistent, token-balanced schedule: unit u takes the tokens
@@ -355,7 +396,12 @@ __device__ __host__ inline size_t unit_lds_bytes(int hkv, int chunk) {
 // The workgroup (index blk) holds UPW units, unit blk UPW + g on waves
 // [g hkv, (g + 1) hkv) with LDS region g (unit_lds_bytes each); units past
 // num_units idle. kBarrier: the units' waves keep in step (UPW = 1 only).
-template <int UPW, bool kBarrier>
+// kRows: K rows are loaded whole and transposed through LDS (the decode
+// role of the fused decode + prefill launch, where the decode has only part
+// of the CUs and its per-CU stream rate sets the step: +1.5% on config 5's
+// step; with the whole device the HBM bandwidth is the limit and the
+// transpose costs 1% on config 4).
+template <int UPW, bool kBarrier, bool kRows = false>
 __device__ __forceinline__ void decode_units(const DecodeArgs& a, char* smem, int blk) {
   static_assert(UPW == 1 || !kBarrier, "a per-step barrier needs one unit per workgroup");
   const int lane = threadIdx.x & 63;
@@ -374,8 +420,8 @@ __device__ __forceinline__ void decode_units(const DecodeArgs& a, char* smem, in
   // overflows; every launch starts from a clear status.
   if (u == 0 && gt == 0) *a.status = SGL_OK;
   const bool active = u < a.num_units && tok0 < tok1;
-  char* base = smem + g * unit_lds_bytes(a.hkv, a.chunk);
-  int32_t* sidx = reinterpret_cast<int32_t*>(base + a.hkv * sizeof(WaveLds));
+  char* base = smem + g * unit_lds_bytes<kRows>(a.hkv, a.chunk);
+  int32_t* sidx = reinterpret_cast<int32_t*>(base + a.hkv * sizeof(UnitWaveLds<kRows>));
   int r = 0;
   if (active) {
     // First i in [0, batch] with kv_indptr[i] >= tok0 (uniform binary search).
@@ -396,7 +442,7 @@ __device__ __forceinline__ void decode_units(const DecodeArgs& a, char* smem, in
       for (int rr = 0; rr < a.batch; ++rr) zero_row(a, a.q_indptr ? a.q_indptr[rr] : rr, gt, gn);
     return;
   }
-  WaveLds& L = reinterpret_cast<WaveLds*>(base)[wave];
+  UnitWaveLds<kRows>& L = reinterpret_cast<UnitWaveLds<kRows>*>(base)[wave];
 
   for (; r < a.batch; ++r) {
     const int rb = a.kv_indptr[r];
@@ -414,8 +460,10 @@ __device__ __forceinline__ void decode_units(const DecodeArgs& a, char* smem, in
     if (s1 <= s0) continue;
     const bool whole = rb >= tok0 && re <= tok1;
     const int pslot = 2 * u + (rb > tok0 ? 1 : 0);
-    decode_head<false, kBarrier>(a, L, sidx + (s0 - tok0), pslot, whole, wave, s1 - s0, qrow,
-                                 lane);
+    u32x4_t* kt = nullptr;
+    if constexpr (kRows) kt = L.kt;
+    decode_head<false, kBarrier, kRows>(a, L, sidx + (s0 - tok0), pslot, whole, wave, s1 - s0,
+                                        qrow, lane, nullptr, kt);
   }
 }
 
@@ -443,7 +491,7 @@ __global__ void __launch_bounds__(512, 1) mixed_attention_kernel(DecodeArgs d, p
                                                                   int dec_blocks) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   if (static_cast<int>(blockIdx.x) < dec_blocks)
-    decode_units<UPW, false>(d, smem, blockIdx.x);
+    decode_units<UPW, false, true>(d, smem, blockIdx.x);
   else
     pf::prefill_item<8, false, 1>(p, smem, static_cast<int>(blockIdx.x) - dec_blocks,
                                   static_cast<int>(gridDim.x) - dec_blocks);
@@ -705,7 +753,8 @@ constexpr size_t kMixedLds = 160 * 1024;
 static int mixed_max_unit(int num_kv_heads) {
   const size_t per_unit = kMixedLds / (8 / num_kv_heads);
   const int64_t w = (static_cast<int64_t>(per_unit) -
-                     static_cast<int64_t>(num_kv_heads) * static_cast<int64_t>(sizeof(WaveLds))) /
+                     static_cast<int64_t>(num_kv_heads) *
+                         static_cast<int64_t>(sizeof(UnitWaveLds<true>))) /
                     static_cast<int64_t>(sizeof(int32_t)) / kStep * kStep;
   return static_cast<int>(w < kMaxChunkTokens ? w : kMaxChunkTokens);
 }
@@ -917,8 +966,7 @@ int launch_decode(const DecodeArgs& a, const sgl_decode_plan_t* plan, hipStream_
   }
   const dim3 grid(plan->num_units);
   const dim3 block(a.hkv * kWave);
-  const size_t lds = static_cast<size_t>(a.hkv) * sizeof(WaveLds) +
-                     static_cast<size_t>(plan->kv_chunk_size) * sizeof(int32_t);
+  const size_t lds = unit_lds_bytes<false>(a.hkv, plan->kv_chunk_size);
   hipLaunchKernelGGL(paged_decode_kernel, grid, block, lds, s, a);
   int st = launch_status();
   if (st != SGL_OK) return st;
@@ -1008,7 +1056,7 @@ extern "C" int sgl_paged_mixed(const sgl_decode_plan_t* plan, const void* q,
   const int64_t dec_blocks = ((plan->num_units + upw - 1) / upw + 7) / 8 * 8;
   if (items + dec_blocks > 0x7fffffff) return SGL_ERR_INVALID_ARG;
   p.tiles_per_req = static_cast<int>(tiles);
-  size_t lds = static_cast<size_t>(upw) * unit_lds_bytes(num_kv_heads, plan->kv_chunk_size);
+  size_t lds = static_cast<size_t>(upw) * unit_lds_bytes<true>(num_kv_heads, plan->kv_chunk_size);
   if (lds < static_cast<size_t>(pf::prefill_lds_bytes<8, 1>()))
     lds = pf::prefill_lds_bytes<8, 1>();
   if (lds > kMixedLds) return SGL_ERR_INVALID_ARG;  // excluded by `fits`
