@@ -182,11 +182,13 @@ def test_decode_plan_cus_host():
     for cus, hq, hkv in ((160, 32, 4), (64, 32, 8), (8, 16, 1), (8, 16, 2), (32, 8, 1)):
         plan = capi.decode_plan_cus(ip, hq, hkv, 128, cus)
         # The fused launch stages each unit's slot indices (4 bytes a token)
-        # and each kv head's Q rows (16 x 136 bf16) in LDS for 8 / hkv units
-        # per workgroup: all of it within the CU's 160 KiB.
-        assert (8 // hkv) * (hkv * 16 * 136 * 2 + 4 * plan.kv_chunk_size) <= 160 * 1024
+        # and per kv head the Q rows (16 x 136 bf16) and a 4 KiB K tile in
+        # LDS for 8 / hkv units per workgroup: all of it within the CU's
+        # 160 KiB.
+        wave = 16 * 136 * 2 + 4096
+        assert (8 // hkv) * (hkv * wave + 4 * plan.kv_chunk_size) <= 160 * 1024
         # The longest unit that fits bounds the count from below.
-        w_max = min(8192, ((160 * 1024 // (8 // hkv) - hkv * 4352) // 4) // 16 * 16)
+        w_max = min(8192, ((160 * 1024 // (8 // hkv) - hkv * wave) // 4) // 16 * 16)
         target = max(cus * (8 // hkv), -(-int(kv.sum()) // w_max))
         assert target * 0.9 <= plan.num_units <= target
         assert plan.max_total_tokens == plan.num_units * plan.kv_chunk_size >= int(kv.sum())
