@@ -16,18 +16,21 @@
 //   * One wave per kv head: each K/V byte is read from HBM once and feeds all
 //     G query heads of that kv head (GQA sharing).
 //   * 16-token steps on the matrix cores: S^T = K . Q^T on
-//     v_mfma_f32_16x16x32_bf16 (K straight from HBM into VGPRs, Q^T from a
-//     per-wave LDS copy), O^T += V^T . P^T on v_mfma_f32_16x16x16bf16_1k fed
-//     from the S^T accumulators; the online softmax is lane-local plus two
-//     lane exchanges.
+//     v_mfma_f32_16x16x32_bf16 (Q^T from a per-wave LDS copy; K straight
+//     from HBM into the operand registers, or, where a CU's own stream rate
+//     sets the time, loaded as whole rows and transposed through a per-wave
+//     LDS tile), O^T += V^T . P^T on v_mfma_f32_16x16x16bf16_1k fed from the
+//     S^T accumulators; the online softmax is lane-local plus two lane
+//     exchanges.
 //   * K and V of step t+1 are issued before the products of step t.
 // A request that spans units is written as fp32 partials (normalised output
 // plus log2-sum-exp) into two slots per unit -- slot 2u for the piece of the
 // request running into unit u from before it, slot 2u+1 for the piece of the
 // request that starts inside u and runs past it -- and folded by a second,
-// short kernel. Merging inside the decode launch would need an agent-scope
-// release per workgroup, which on this multi-XCD part is an L2 write-back per
-// workgroup; the kernel boundary is cheaper.
+// short kernel. Merging inside the decode launch would need the pieces
+// written coherently across the XCDs' L2s (agent-scope releases, which write
+// back the L2, or write-through stores): both measured slower than the
+// kernel boundary.
 //
 // A batch whose tokens exceed the plan's capacity (num_units * W_max) is not
 // processed silently wrong: the merge kernel writes NaN to the rows of every
