@@ -5,14 +5,15 @@
 // widening copy, an elementwise pass and a softmax that reads its input
 // again for the max, the sum and the output.
 //
-// Here one 512-thread workgroup takes one row: y_i = float(x_i) * (1 / t),
+// Here one workgroup takes one row: y_i = float(x_i) * (1 / t),
 // m = max_i y_i, s = sum_i 2^((y_i - m) log2 e), p_i = 2^((y_i - m) log2 e)
 // * (1 / s), the max and the sum taken together (online) as the row streams
-// in. For 16-bit logits rows of up to kMaxRegChunks * 4096 elements
-// (Qwen3's 151,936 included) the raw row stays in registers for the output
-// phase, so HBM sees one read of the logits and one write of the
-// probabilities; fp32 logits and longer rows read the row again for the
-// output (mostly from the last-level cache).
+// in. For aligned 16-bit logits rows of up to kMaxRegChunks * 8192 elements
+// (Qwen3's 151,936 included) a 1024-thread workgroup keeps the raw row in
+// registers for the output phase, so HBM sees one read of the logits and one
+// write of the probabilities; fp32 logits, longer and unaligned rows go to a
+// 512-thread workgroup that reads the row again for the output (mostly from
+// the last-level cache).
 //
 // Accuracy against the exact softmax of float(x) / t (float64): y carries
 // half an ulp of |y| from the reciprocal-multiply (about 6e-8 |y|), the exp2
@@ -29,12 +30,15 @@ namespace {
 
 using sp::Elem;
 
-// 512 threads (two waves per SIMD, up to 256 VGPRs each): a 16-bit row of
-// 151,936 logits is 38 16-byte chunks (152 VGPRs) per lane. Thread t runs
-// the statistics lanes t and t + 512 of sampler_prob.h.
+// Streaming rows: 512 threads, thread t runs the statistics lanes t and
+// t + 512 of sampler_prob.h.
 constexpr int kSmThreads = sp::kStatLanes / 2;
 constexpr int kSmWaves = kSmThreads / kWave;
-constexpr int kMaxRegChunks = 40;  // 16-byte chunks a lane holds (160 VGPRs)
+// Register-held rows: 1024 threads (four waves per SIMD, up to 128 VGPRs
+// each), at most kMaxRegChunks 16-byte chunks (80 VGPRs) per lane. Measured
+// against 512 threads holding twice the chunks (two waves per SIMD): 53.8 ->
+// 50.9 us on HBM-resident Qwen3 rows, 42.9 -> 40.1 us cache-resident.
+constexpr int kMaxRegChunks = 20;
 // Word 3 of a raw buffer resource on gfx950 (32-bit data format, no
 // swizzle, unit stride): plain byte-addressed loads with a range check.
 constexpr int kRawBufferWord3 = 0x00020000;
@@ -48,15 +52,11 @@ struct SoftmaxArgs {
   bool vec;            // 16-byte aligned rows (base and stride of both)
 };
 
-// NC > 0 (16-byte aligned rows): the thread's whole chunks c = tid + T k,
-// k < NC, stay in registers (buffer loads: one lane offset, the chunk step
-// as the scalar offset, reads past the row return 0); NC == 0: the row is
-// read again for the output. Either way the statistics follow
-// sp::lane_stats' order for lanes tid and tid + T (whole chunks in order,
-// then the elements past them one by one), so they are the same bits on
-// both paths and in the draws from logits.
-template <int DT, int NC>
-__global__ void __launch_bounds__(kSmThreads) softmax_temperature_kernel(SoftmaxArgs a) {
+// The row read twice (statistics, then output) in sp::lane_stats' order for
+// lanes tid and tid + 512, so the statistics are the same bits as the
+// register-held kernel's and the draws from logits'.
+template <int DT>
+__global__ void __launch_bounds__(kSmThreads) softmax_temperature_stream(SoftmaxArgs a) {
   __shared__ float red[2 * kSmWaves];
   constexpr int P = Elem<DT>::kPer;
   constexpr int B = 16 / P;  // bytes per element
@@ -70,101 +70,116 @@ __global__ void __launch_bounds__(kSmThreads) softmax_temperature_kernel(Softmax
   const float t = a.temps ? a.temps[r] : a.temp;
   const float inv_t = 1.0f / t;
 
-  // Statistics lanes t (mx0, s0) and t + 512 (mx1, s1): held chunk j is
-  // chunk t + 512 j, i.e. lane t + 512 (j % 2)'s chunk j / 2.
   float mx0, s0, mx1, s1;
-  u32x4_t held[NC > 0 ? NC : 1];
-  __amdgpu_buffer_rsrc_t prs;
-  if constexpr (NC > 0) {
-    const __amdgpu_buffer_rsrc_t rs =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(row), 0, d * B, kRawBufferWord3);
-#pragma unroll
-    for (int k = 0; k < NC; ++k)
-      held[k] = __builtin_bit_cast(
-          u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rs, tid * 16, k * kSmThreads * 16, 0));
-    prs = __builtin_amdgcn_make_buffer_rsrc(prow, 0, d * 4, kRawBufferWord3);
-    mx0 = mx1 = -INFINITY;
-    s0 = s1 = 0.f;
-#pragma unroll
-    for (int k = 0; k < NC; ++k)
-      if (tid + k * kSmThreads < nfull) {
-        float y[P];
-        sp::scaled<DT>(held[k], inv_t, y);
-        if (k % 2 == 0) sp::online_update(y, mx0, s0);
-        else sp::online_update(y, mx1, s1);
-      }
-    for (int e = e_tail + tid; e < d; e += sp::kStatLanes) {
-      const float y[1] = {sp::scaled1(Elem<DT>::load1(row, e), inv_t)};
-      sp::online_update(y, mx0, s0);
-    }
-    for (int e = e_tail + tid + kSmThreads; e < d; e += sp::kStatLanes) {
-      const float y[1] = {sp::scaled1(Elem<DT>::load1(row, e), inv_t)};
-      sp::online_update(y, mx1, s1);
-    }
-  } else {
-    sp::lane_stats<DT>(row, d, a.vec, tid, inv_t, mx0, s0);
-    sp::lane_stats<DT>(row, d, a.vec, tid + kSmThreads, inv_t, mx1, s1);
-  }
+  sp::lane_stats<DT>(row, d, a.vec, tid, inv_t, mx0, s0);
+  sp::lane_stats<DT>(row, d, a.vec, tid + kSmThreads, inv_t, mx1, s1);
   const float m = sp::block_max2<kSmWaves>(mx0, mx1, red);
   const float inv_s = 1.0f / sp::block_sum2<kSmWaves>(sp::lane_sum_at(mx0, s0, m),
                                                       sp::lane_sum_at(mx1, s1, m), red);
 
   // The probabilities.
-  if constexpr (NC > 0) {
-    // Recompute y from the packed row: without this barrier the compiler
-    // keeps the fp32 values of the statistics pass alive instead (twice the
-    // registers).
+  for (int c = tid; c < nfull; c += kSmThreads) {
+    const u32x4_t v = *reinterpret_cast<const u32x4_t*>(row + static_cast<int64_t>(c) * 16);
+    float p[P];
 #pragma unroll
-    for (int k = 0; k < NC; ++k) asm volatile("" : "+v"(held[k]));
+    for (int j = 0; j < P; ++j) p[j] = sp::prob(Elem<DT>::at(v, j), inv_t, m, inv_s);
 #pragma unroll
-    for (int k = 0; k < NC; ++k)
-      if (tid + k * kSmThreads < nfull) {
-        float p[P];
-#pragma unroll
-        for (int j = 0; j < P; ++j) p[j] = sp::prob(Elem<DT>::at(held[k], j), inv_t, m, inv_s);
-#pragma unroll
-        for (int q = 0; q < P / 4; ++q)
-          __builtin_amdgcn_raw_buffer_store_b128(
-              __builtin_bit_cast(u32x4_t, f32x4_t{p[4 * q], p[4 * q + 1], p[4 * q + 2], p[4 * q + 3]}),
-              prs, tid * (4 * P) + 16 * q, k * kSmThreads * 4 * P, 0);
-      }
-  } else {
-    for (int c = tid; c < nfull; c += kSmThreads) {
-      const u32x4_t v = *reinterpret_cast<const u32x4_t*>(row + static_cast<int64_t>(c) * 16);
-      float p[P];
-#pragma unroll
-      for (int j = 0; j < P; ++j) p[j] = sp::prob(Elem<DT>::at(v, j), inv_t, m, inv_s);
-#pragma unroll
-      for (int q = 0; q < P / 4; ++q)
-        *reinterpret_cast<f32x4_t*>(prow + c * P + 4 * q) =
-            f32x4_t{p[4 * q], p[4 * q + 1], p[4 * q + 2], p[4 * q + 3]};
-    }
+    for (int q = 0; q < P / 4; ++q)
+      *reinterpret_cast<f32x4_t*>(prow + c * P + 4 * q) =
+          f32x4_t{p[4 * q], p[4 * q + 1], p[4 * q + 2], p[4 * q + 3]};
   }
   for (int e = e_tail + tid; e < d; e += kSmThreads)
+    prow[e] = sp::prob(Elem<DT>::load1(row, e), inv_t, m, inv_s);
+}
+
+// Register-held rows (aligned 16-bit logits): thread t is the statistics
+// lane t and holds its chunks c = t + 1024 k, k < NC (a row of 151,936
+// logits is 19 chunks, 76 VGPRs, per lane), loaded with buffer loads (one
+// lane offset, the chunk step as the scalar offset, reads past the row
+// return 0). Same statistics order, so the same bits, as the streaming
+// kernel and the draws from logits.
+template <int DT, int NC>
+__global__ void __launch_bounds__(sp::kStatLanes) softmax_temperature_held(SoftmaxArgs a) {
+  __shared__ float red[sp::kStatWaves];
+  constexpr int T = sp::kStatLanes;
+  constexpr int P = Elem<DT>::kPer;
+  constexpr int B = 16 / P;  // bytes per element
+  const int r = blockIdx.x;
+  const char* row = static_cast<const char*>(a.logits) + static_cast<int64_t>(r) * a.x_st * B;
+  float* prow = a.probs + static_cast<int64_t>(r) * a.p_st;
+  const int d = static_cast<int>(a.d);
+  const int nfull = d / P;          // aligned rows only
+  const int e_tail = nfull * P;
+  const int tid = threadIdx.x;
+  const float t = a.temps ? a.temps[r] : a.temp;
+  const float inv_t = 1.0f / t;
+
+  u32x4_t held[NC];
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(row), 0, d * B, kRawBufferWord3);
+#pragma unroll
+  for (int k = 0; k < NC; ++k)
+    held[k] = __builtin_bit_cast(
+        u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rs, tid * 16, k * T * 16, 0));
+  const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(prow, 0, d * 4, kRawBufferWord3);
+  float mx = -INFINITY, sm = 0.f;
+#pragma unroll
+  for (int k = 0; k < NC; ++k)
+    if (tid + k * T < nfull) {
+      float y[P];
+      sp::scaled<DT>(held[k], inv_t, y);
+      sp::online_update(y, mx, sm);
+    }
+  for (int e = e_tail + tid; e < d; e += T) {
+    const float y[1] = {sp::scaled1(Elem<DT>::load1(row, e), inv_t)};
+    sp::online_update(y, mx, sm);
+  }
+  const float m = sp::block_max<sp::kStatWaves>(mx, red);
+  const float inv_s = 1.0f / sp::block_sum<sp::kStatWaves>(sp::lane_sum_at(mx, sm, m), red);
+
+  // The probabilities, recomputed from the packed row: without this barrier
+  // the compiler keeps the fp32 values of the statistics pass alive instead
+  // (twice the registers).
+#pragma unroll
+  for (int k = 0; k < NC; ++k) asm volatile("" : "+v"(held[k]));
+#pragma unroll
+  for (int k = 0; k < NC; ++k)
+    if (tid + k * T < nfull) {
+      float p[P];
+#pragma unroll
+      for (int j = 0; j < P; ++j) p[j] = sp::prob(Elem<DT>::at(held[k], j), inv_t, m, inv_s);
+#pragma unroll
+      for (int q = 0; q < P / 4; ++q)
+        __builtin_amdgcn_raw_buffer_store_b128(
+            __builtin_bit_cast(u32x4_t, f32x4_t{p[4 * q], p[4 * q + 1], p[4 * q + 2], p[4 * q + 3]}),
+            prs, tid * (4 * P) + 16 * q, k * T * 4 * P, 0);
+    }
+  for (int e = e_tail + tid; e < d; e += T)
     prow[e] = sp::prob(Elem<DT>::load1(row, e), inv_t, m, inv_s);
 }
 
 template <int DT>
 int launch_softmax(const SoftmaxArgs& a, hipStream_t s) {
   constexpr int P = Elem<DT>::kPer;
-  const int64_t per_lane = (a.d / P + kSmThreads - 1) / kSmThreads;  // whole chunks per lane
-  const dim3 grid(static_cast<uint32_t>(a.batch)), block(kSmThreads);
-  // Registers hold aligned 16-bit rows of up to kMaxRegChunks chunks per
-  // lane; fp32 logits, longer and unaligned rows stream.
+  const int64_t per_lane = (a.d / P + sp::kStatLanes - 1) / sp::kStatLanes;  // chunks per lane
+  const dim3 grid(static_cast<uint32_t>(a.batch));
+  const dim3 held(sp::kStatLanes);
   if constexpr (DT == SGL_DTYPE_F32) {
-    hipLaunchKernelGGL((softmax_temperature_kernel<DT, 0>), grid, block, 0, s, a);
-  } else if (per_lane > kMaxRegChunks || !a.vec)
-    hipLaunchKernelGGL((softmax_temperature_kernel<DT, 0>), grid, block, 0, s, a);
+    hipLaunchKernelGGL((softmax_temperature_stream<DT>), grid, dim3(kSmThreads), 0, s, a);
+    return launch_status();
+  }
+  if (!a.vec || per_lane > kMaxRegChunks)
+    hipLaunchKernelGGL((softmax_temperature_stream<DT>), grid, dim3(kSmThreads), 0, s, a);
+  else if (per_lane <= 4)
+    hipLaunchKernelGGL((softmax_temperature_held<DT, 4>), grid, held, 0, s, a);
   else if (per_lane <= 8)
-    hipLaunchKernelGGL((softmax_temperature_kernel<DT, 8>), grid, block, 0, s, a);
+    hipLaunchKernelGGL((softmax_temperature_held<DT, 8>), grid, held, 0, s, a);
+  else if (per_lane <= 12)
+    hipLaunchKernelGGL((softmax_temperature_held<DT, 12>), grid, held, 0, s, a);
   else if (per_lane <= 16)
-    hipLaunchKernelGGL((softmax_temperature_kernel<DT, 16>), grid, block, 0, s, a);
-  else if (per_lane <= 24)
-    hipLaunchKernelGGL((softmax_temperature_kernel<DT, 24>), grid, block, 0, s, a);
-  else if (per_lane <= 32)
-    hipLaunchKernelGGL((softmax_temperature_kernel<DT, 32>), grid, block, 0, s, a);
+    hipLaunchKernelGGL((softmax_temperature_held<DT, 16>), grid, held, 0, s, a);
   else
-    hipLaunchKernelGGL((softmax_temperature_kernel<DT, kMaxRegChunks>), grid, block, 0, s, a);
+    hipLaunchKernelGGL((softmax_temperature_held<DT, kMaxRegChunks>), grid, held, 0, s, a);
   return launch_status();
 }
 
