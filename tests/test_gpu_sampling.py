@@ -311,6 +311,11 @@ def test_sampling_from_logits_flat_rows(dev, mode):
     (5001, 1, torch.float32),      # unaligned fp32 rows
     (200000, 0, torch.bfloat16),   # longer than the registers hold: streamed
     (65536, 0, torch.float16),     # register path, fewer chunks per lane
+    (163840, 0, torch.bfloat16),   # exactly the 20 chunks a lane holds
+    (163848, 0, torch.bfloat16),   # one chunk past them: streamed
+    (32768, 0, torch.bfloat16),    # 4 chunks a lane
+    (90000, 0, torch.float16),     # 11 chunks a lane, partial last chunk round
+    (131080, 0, torch.bfloat16),   # 17 chunks a lane, one lane holding the 17th
 ])
 def test_softmax_temperature_shapes(oracle, dev, vocab, offset, dtype):
     g = torch.Generator(device=dev)
