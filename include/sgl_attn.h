@@ -40,7 +40,7 @@ const char* sgl_status_string(int status);
 
 /* Library version, to check that the loaded .so matches this header. */
 int sgl_abi_version(void);
-#define SGL_ABI_VERSION 14
+#define SGL_ABI_VERSION 15
 
 /* ------------------------------------------------------------------ */
 /* KV-cache store                                                      */
@@ -228,7 +228,8 @@ typedef struct {
   int32_t num_kv_heads;
   int32_t head_dim;
   int64_t max_total_tokens; /* capacity: num_units * kv_chunk_size tokens per call */
-  int64_t workspace_bytes;  /* 256-byte header (status word) + fp32 partials, two per unit */
+  int64_t workspace_bytes;  /* 256-byte header (status word) + fp32 partials, two per unit,
+                               + one int32 per unit */
 } sgl_decode_plan_t;
 
 /*
@@ -274,7 +275,9 @@ int sgl_decode_plan_check(const sgl_decode_plan_t* plan, const int32_t* kv_indpt
  * when the device kv_indptr[batch] exceeds plan->max_total_tokens the rows
  * of every request reaching past the capacity are written as NaN and the
  * word is set to SGL_ERR_CAPACITY (read it with sgl_decode_status). Two
- * kernels run on the stream (decode, then merge), or one for small batches
+ * kernels run on the stream (decode, then merge: one workgroup per (kv
+ * head, request), or per (kv head, unit) when the batch has more requests
+ * than the plan has units), or one for small batches
  * (plans at the 64-token minimum unit with batch_size x Hkv workgroups at
  * most the CU count). Calls that share one workspace must be stream-ordered.
  * Replaces: BatchDecodeWithPagedKVCacheDispatched call in

@@ -26,7 +26,7 @@ SGL_INDEX_I64 = 1
 SGL_DTYPE_BF16 = 0
 SGL_DTYPE_F16 = 1
 SGL_DTYPE_F32 = 2
-ABI_VERSION = 14
+ABI_VERSION = 15
 FUSED_NO_K_WRITEBACK = 1  # SGL_FUSED_NO_K_WRITEBACK
 
 

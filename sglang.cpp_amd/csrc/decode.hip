@@ -73,6 +73,7 @@ struct DecodeArgs {
   float* part_o;     // [2 num_units, hq, D]
   float* part_lse;   // [2 num_units, hq]
   int32_t* status;   // workspace status word
+  int32_t* unit_req; // [num_units]: the request running into unit u from before, or -1
   int chunk;         // W_max: largest unit (LDS staging capacity)
   int chunk_min;     // W_min: smallest unit
   int batch;
@@ -106,9 +107,10 @@ using UnitWaveLds = std::conditional_t<kRows, RowKWaveLds, WaveLds>;
 
 // Workspace carve-up shared by the plan and the launch: a 256-byte header
 // (int32 status word at offset 0), then the partial outputs and their
-// log2-sum-exp, two slots per unit.
+// log2-sum-exp, two slots per unit, then per unit the request that runs into
+// it from an earlier unit (-1 if none).
 struct WorkspaceLayout {
-  int64_t part_o_off, part_lse_off, total;
+  int64_t part_o_off, part_lse_off, unit_req_off, total;
 };
 
 inline WorkspaceLayout workspace_layout(int num_units, int hq) {
@@ -117,7 +119,8 @@ inline WorkspaceLayout workspace_layout(int num_units, int hq) {
   auto align = [](int64_t x) { return (x + 255) / 256 * 256; };
   w.part_o_off = 256;
   w.part_lse_off = w.part_o_off + align(npart * kD * 4);
-  w.total = w.part_lse_off + align(npart * 4);
+  w.unit_req_off = w.part_lse_off + align(npart * 4);
+  w.total = w.unit_req_off + align(static_cast<int64_t>(num_units) * 4);
   return w;
 }
 
@@ -435,8 +438,11 @@ __device__ __forceinline__ void decode_units(const DecodeArgs& a, char* smem, in
     }
     // Request lo - 1 runs across tok0 when its end kv_indptr[lo] lies past tok0.
     r = (lo > 0 && a.kv_indptr[lo] > tok0) ? lo - 1 : lo;
+    if (gt == 0) a.unit_req[u] = r < a.batch && a.kv_indptr[r] < tok0 ? r : -1;
     // Stage the unit's slot indices (shared by every kv head) in LDS.
     for (int e = gt; e < tok1 - tok0; e += gn) sidx[e] = a.indices[tok0 + e];
+  } else if (u < a.num_units && gt == 0) {
+    a.unit_req[u] = -1;
   }
   __syncthreads();
   if (!active) {
@@ -616,14 +622,11 @@ __global__ void __launch_bounds__(kSmallWaves * kWave) paged_decode_small_kernel
 // past the plan's token capacity get NaN rows and the CAPACITY status.
 constexpr int kFoldPieces = 4;
 
-__global__ void __launch_bounds__(kMaxGroup * (kD / 4)) decode_merge_kernel(DecodeArgs a) {
-  const int h = blockIdx.x;
-  const int r = blockIdx.y;
+__device__ __forceinline__ void merge_request(const DecodeArgs& a, int h, int r, int W) {
   const int rb = a.kv_indptr[r];
   const int re = a.kv_indptr[r + 1];
   const int G = a.group;
   const int qrow = a.q_indptr ? a.q_indptr[r] : r;
-  const int W = unit_tokens(a, a.kv_indptr[a.batch]);
   if (static_cast<int64_t>(re) > static_cast<int64_t>(a.num_units) * W) {
     for (int e = threadIdx.x; e < G * (kD / 4); e += blockDim.x) {
       const int g = e / (kD / 4);
@@ -685,6 +688,38 @@ __global__ void __launch_bounds__(kMaxGroup * (kD / 4)) decode_merge_kernel(Deco
                       pack_bf16x2(accm[2] * inv, accm[3] * inv)};
     *reinterpret_cast<u32x2_t*>(op) = packed;
   }
+}
+
+// One workgroup per (kv head, request): every request's fold or NaN rows.
+__global__ void __launch_bounds__(kMaxGroup * (kD / 4)) decode_merge_kernel(DecodeArgs a) {
+  merge_request(a, blockIdx.x, blockIdx.y, unit_tokens(a, a.kv_indptr[a.batch]));
+}
+
+// One workgroup per (kv head, unit), for batches of more requests than
+// units: the unit where a split request ends folds it (that request is the
+// one running into the unit from before, recorded by the decode), and the
+// extra row y = num_units writes the NaN rows of requests past the capacity.
+__global__ void __launch_bounds__(kMaxGroup * (kD / 4)) decode_merge_units_kernel(DecodeArgs a) {
+  const int h = blockIdx.x;
+  const int u = blockIdx.y;
+  const int total = a.kv_indptr[a.batch];
+  const int W = unit_tokens(a, total);
+  const int64_t cover = static_cast<int64_t>(a.num_units) * W;
+  if (u == a.num_units) {
+    if (total <= cover) return;
+    int lo = 0, hi = a.batch;  // first request with kv_indptr[r + 1] > cover
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (a.kv_indptr[mid + 1] <= cover) lo = mid + 1; else hi = mid;
+    }
+    for (int r = lo; r < a.batch; ++r) merge_request(a, h, r, W);
+    return;
+  }
+  const int r = a.unit_req[u];
+  if (r < 0) return;
+  const int re = a.kv_indptr[r + 1];
+  if (static_cast<int64_t>(re) > cover || (re - 1) / W != u) return;
+  merge_request(a, h, r, W);
 }
 
 }  // namespace
@@ -960,6 +995,17 @@ int decode_args(const sgl_decode_plan_t* plan, const void* q, int64_t q_stride_t
 // Merge workgroup size: one thread per 4 d of each of the G heads, in whole waves.
 int merge_threads(int group) { return (group * (kD / 4) + kWave - 1) / kWave * kWave; }
 
+// The merge launch: per request, or per unit when the batch has more
+// requests than the plan has units (fewer workgroups that only exit).
+void launch_merge(const DecodeArgs& a, hipStream_t s) {
+  if (a.batch > a.num_units + 1)
+    hipLaunchKernelGGL(decode_merge_units_kernel, dim3(a.hkv, a.num_units + 1),
+                       dim3(merge_threads(a.group)), 0, s, a);
+  else
+    hipLaunchKernelGGL(decode_merge_kernel, dim3(a.hkv, a.batch), dim3(merge_threads(a.group)), 0,
+                       s, a);
+}
+
 // Points the kernel arguments at a workspace of the plan's layout.
 void bind_workspace(DecodeArgs& a, const sgl_decode_plan_t* plan, void* workspace) {
   const WorkspaceLayout w = workspace_layout(plan->num_units, plan->num_qo_heads);
@@ -967,6 +1013,7 @@ void bind_workspace(DecodeArgs& a, const sgl_decode_plan_t* plan, void* workspac
   a.status = reinterpret_cast<int32_t*>(base);
   a.part_o = reinterpret_cast<float*>(base + w.part_o_off);
   a.part_lse = reinterpret_cast<float*>(base + w.part_lse_off);
+  a.unit_req = reinterpret_cast<int32_t*>(base + w.unit_req_off);
 }
 
 // Decode launch + merge launch on one stream (or the small-batch kernel alone).
@@ -985,7 +1032,7 @@ int launch_decode(const DecodeArgs& a, const sgl_decode_plan_t* plan, hipStream_
   if (st != SGL_OK) return st;
   // Always launched: besides folding split requests it is what reports a
   // batch that exceeds the plan.
-  hipLaunchKernelGGL(decode_merge_kernel, dim3(a.hkv, a.batch), dim3(merge_threads(a.group)), 0, s, a);
+  launch_merge(a, s);
   return launch_status();
 }
 
@@ -1084,7 +1131,7 @@ extern "C" int sgl_paged_mixed(const sgl_decode_plan_t* plan, const void* q,
   }
   st = launch_status();
   if (st != SGL_OK) return st;
-  hipLaunchKernelGGL(decode_merge_kernel, dim3(d.hkv, d.batch), dim3(merge_threads(d.group)), 0, s, d);
+  launch_merge(d, s);
   return launch_status();
 }
 

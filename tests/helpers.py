@@ -61,10 +61,12 @@ def assert_bf16_close(got: np.ndarray, ref: np.ndarray, atol=1e-6, what: str = "
 
 def decode_ws_bytes(units: int, hq: int) -> int:
     """Decode workspace layout: a 256-byte header (status word), then fp32
-    partial outputs [2 units, hq, 128] and log2-sum-exp [2 units, hq], each
-    padded to 256 bytes."""
+    partial outputs [2 units, hq, 128], log2-sum-exp [2 units, hq] and the
+    int32 request running into each unit [units], each padded to 256
+    bytes."""
     npart = 2 * units * hq
-    return 256 + -(-npart * 512 // 256) * 256 + -(-npart * 4 // 256) * 256
+    pad = lambda x: -(-x // 256) * 256
+    return 256 + pad(npart * 512) + pad(npart * 4) + pad(units * 4)
 
 
 def forced_plan(capi, kv_indptr, hq, hkv, unit):

@@ -83,9 +83,11 @@ def test_argument_checks_reject_before_launch():
 
 
 def ws_bytes(units, hq):
-    """Workspace layout: 256-byte header, then fp32 partial o and lse, two slots per unit."""
+    """Workspace layout: 256-byte header, then fp32 partial o and lse (two
+    slots per unit) and one int32 per unit."""
     npart = 2 * units * hq
-    return 256 + -(-npart * 512 // 256) * 256 + -(-npart * 4 // 256) * 256
+    pad = lambda x: -(-x // 256) * 256
+    return 256 + pad(npart * 512) + pad(npart * 4) + pad(units * 4)
 
 
 def test_decode_plan_host_logic():

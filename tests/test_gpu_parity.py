@@ -515,6 +515,48 @@ def test_decode_plan_exceeded_reports_capacity(oracle, dev):
     assert_attn_close(o.float().cpu().numpy(), ref, what="fitting batch after overflow")
 
 
+def test_decode_plan_exceeded_more_requests_than_units(oracle, dev):
+    """The capacity contract when the batch has more requests than the plan
+    has units (the merge then runs one workgroup per unit): a plan for 40
+    requests of 10 tokens (7 units of 64) reused for 40 longer requests;
+    requests past the capacity are NaN, split requests within it fold
+    correctly, the status is CAPACITY, and the next fitting call clears it."""
+    note("decode plan exceeded, 40 requests on 7 units")
+    rng = np.random.default_rng(41)
+    plan = capi.decode_plan(np.arange(0, 401, 10, dtype=np.int32), 16, 8, 128)
+    assert plan.num_units + 1 < 40 and plan.kv_chunk_size == 64
+    cap = plan.max_total_tokens
+    lens = [int(x) for x in rng.integers(5, 36, 40)]
+    b = wl.make_paged_batch(rng, [x - 1 for x in lens], lens, page_size=16, decode=True)
+    assert b.kv_indptr[-1] > cap
+    kc, vc = _pool(dev, b.num_slots, 8, 128, 42)
+    g = gen(dev, 43)
+    q = randn_bf16((40, 16, 128), dev, g)
+    o = torch.zeros((40, 16, 128), device=dev, dtype=torch.bfloat16)
+    ws = capi.decode_workspace(plan, dev)
+    idx = torch.from_numpy(b.indices).to(dev)
+    kvp = torch.from_numpy(b.kv_indptr).to(dev)
+    capi.paged_decode(plan, q, kc, vc, idx, kvp, o, ws)
+    assert capi.decode_status(ws) == -3
+    scale = 1 / math.sqrt(128)
+    ref = oracle.decode(u16(q).copy(), u16(kc), u16(vc), b.indices, b.kv_indptr, scale)
+    got = o.float().cpu().numpy()
+    split = 0
+    for r in range(40):
+        rb, re = int(b.kv_indptr[r]), int(b.kv_indptr[r + 1])
+        if re > cap:
+            assert np.isnan(got[r]).all(), f"request {r} past capacity must be NaN"
+        else:
+            split += (re - 1) // 64 != rb // 64
+            assert_attn_close(got[r], ref[r], what=f"request {r} within capacity")
+    assert split > 0
+    fit = np.concatenate([[0], np.cumsum([min(x, 10) for x in lens])]).astype(np.int32)
+    capi.paged_decode(plan, q, kc, vc, idx, torch.from_numpy(fit).to(dev), o, ws)
+    assert capi.decode_status(ws) == 0
+    ref = oracle.decode(u16(q).copy(), u16(kc), u16(vc), b.indices, fit, scale)
+    assert_attn_close(o.float().cpu().numpy(), ref, what="fitting batch after overflow")
+
+
 def test_decode_page_permutation_invariance(dev):
     """Moving every KV row to another slot (and the table with it) leaves o bitwise unchanged."""
     note("decode page-permutation invariance")
