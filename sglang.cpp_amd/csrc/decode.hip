@@ -23,6 +23,12 @@
 //     S^T accumulators; the online softmax is lane-local plus two lane
 //     exchanges.
 //   * K and V of step t+1 are issued before the products of step t.
+//   * The decode-only launch keeps each wave's finished pieces (output rows,
+//     or split partials) in an LDS ring and writes them when its unit is
+//     done (or the ring is full), and stages its first requests' kv_indptr
+//     and row entries in LDS: stores interleaved with the unit's read
+//     stream cost far more than their bytes (config 4 shape, same tokens:
+//     -1.4% at 256 requests, -7% at 2,048).
 // A request that spans units is written as fp32 partials (normalised output
 // plus log2-sum-exp) into two slots per unit -- slot 2u for the piece of the
 // request running into unit u from before it, slot 2u+1 for the piece of the
@@ -78,6 +84,7 @@ struct DecodeArgs {
   int chunk_min;     // W_min: smallest unit
   int batch;
   int num_units;     // workgroups of the decode launch
+  int out_bytes;     // decode-only launch: bytes of each wave's LDS output ring (0: write directly)
 };
 
 // Unit size for this launch: the batch's tokens spread evenly over the
@@ -212,7 +219,7 @@ template <bool kState, bool kBarrier = !kState, bool kRows = false>
 __device__ __forceinline__ void decode_head(const DecodeArgs& a, WaveLds& L, const int32_t* sidx,
                                             int pslot, bool whole, int h, int len, int qrow,
                                             int lane, HeadState* st = nullptr,
-                                            u32x4_t* kt = nullptr) {
+                                            u32x4_t* kt = nullptr, char* oslot = nullptr) {
   const int n = lane & 15;
   const int j = lane >> 4;
   const int G = a.group;
@@ -351,6 +358,34 @@ __device__ __forceinline__ void decode_head(const DecodeArgs& a, WaveLds& L, con
   const float inv = l > 0.f ? 1.0f / l : 0.f;
   const int head = h * G + n;
   // Lane holds O[head n][d = 32 j + 8 i + nb] in acc[nb][i].
+  if (oslot) {
+    // Into the wave's LDS output record (head n's row at 16 + 256 n for a
+    // whole request's bf16 output, at 16 + 512 n for a partial's fp32, its
+    // log2-sum-exp at 16 + 512 G + 4 n); written to memory when the unit is
+    // done.
+    char* row = oslot + 16 + (whole ? 256 : 512) * n;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (whole) {
+        float v[8];
+#pragma unroll
+        for (int nb = 0; nb < 8; ++nb) v[nb] = acc[nb][i] * inv;
+        *reinterpret_cast<u32x4_t*>(row + 2 * (32 * j + 8 * i)) = pack8(v);
+      } else {
+        f32x4_t v0, v1;
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb) {
+          v0[nb] = acc[nb][i] * inv;
+          v1[nb] = acc[nb + 4][i] * inv;
+        }
+        *reinterpret_cast<f32x4_t*>(row + 4 * (32 * j + 8 * i)) = v0;
+        *reinterpret_cast<f32x4_t*>(row + 4 * (32 * j + 8 * i + 4)) = v1;
+      }
+    }
+    if (!whole && j == 0)
+      *reinterpret_cast<float*>(oslot + 16 + 512 * G + 4 * n) = l > 0.f ? m + log2f(l) : -INFINITY;
+    return;
+  }
   if (whole) {
     uint16_t* op = a.o + static_cast<int64_t>(qrow) * a.o_st + static_cast<int64_t>(head) * a.o_sh;
 #pragma unroll
@@ -388,12 +423,71 @@ __device__ __forceinline__ void zero_row(const DecodeArgs& a, int qrow, int t, i
   }
 }
 
-// LDS bytes of one unit: the per-wave Q copies, then the unit's slot indices.
-// kRows: the per-wave K tile of whole-row K loads too.
+// Requests whose kv_indptr / row entries a unit stages in LDS (the walk
+// over further requests reads them from memory).
+constexpr int kReqStage = 256;
+constexpr size_t kMaxOutRing = 32 * 1024;  // output ring bytes per wave of the decode-only launch
+
+// Request entries a unit stages: the decode-only launch's (kv_indptr[r0 ..
+// r0 + kReqStage], rows[r0 .. r0 + kReqStage)); the fused launch's decode
+// role, whose units hold one or two pieces, stages none (staging there cost
+// its launch 4%).
+template <bool kRows>
+__device__ __host__ constexpr int req_stage() { return kRows ? 0 : kReqStage; }
+
+// LDS bytes of one unit: the per-wave Q copies, the staged request entries,
+// then the unit's slot indices. kRows: the per-wave K tile of whole-row K
+// loads too.
 template <bool kRows>
 __device__ __host__ inline size_t unit_lds_bytes(int hkv, int chunk) {
   return static_cast<size_t>(hkv) * sizeof(UnitWaveLds<kRows>) +
+         static_cast<size_t>(kRows ? 0 : 2 * kReqStage + 1) * sizeof(int32_t) +
          static_cast<size_t>(chunk) * sizeof(int32_t);
+}
+
+// Offset of the decode-only launch's output rings in a unit's LDS.
+__device__ __host__ inline size_t out_ring_offset(int hkv, int chunk) {
+  return (unit_lds_bytes<false>(hkv, chunk) + 15) / 16 * 16;
+}
+
+// Bytes of one output record: a 16-byte header (whole, row, partial slot,
+// record bytes), then the G rows (bf16 for a whole request, fp32 and the
+// log2-sum-exp for a partial).
+__device__ __host__ inline int out_record_bytes(int group, bool whole) {
+  return whole ? 16 + 256 * group : (16 + 512 * group + 4 * group + 15) / 16 * 16;
+}
+
+// Writes the records of a wave's output ring ([0, used) bytes) to memory,
+// kv head h.
+__device__ __forceinline__ void flush_ring(const DecodeArgs& a, const char* ring, int used, int h,
+                                           int lane) {
+  const int G = a.group;
+  wave_lds_sync();
+  for (int at = 0; at < used;) {
+    const char* sl = ring + at;
+    const int* hdr = reinterpret_cast<const int*>(sl);
+    const int whole = __builtin_amdgcn_readfirstlane(hdr[0]);
+    const int qrow = __builtin_amdgcn_readfirstlane(hdr[1]);
+    const int pslot = __builtin_amdgcn_readfirstlane(hdr[2]);
+    at += __builtin_amdgcn_readfirstlane(hdr[3]);
+    if (whole) {
+      for (int e = lane; e < G * 16; e += kWave) {
+        const int g = e >> 4, c = e & 15;
+        stg128(a.o + static_cast<int64_t>(qrow) * a.o_st + static_cast<int64_t>(h * G + g) * a.o_sh +
+                   c * 8,
+               *reinterpret_cast<const u32x4_t*>(sl + 16 + 256 * g + 16 * c));
+      }
+    } else {
+      const int64_t p0 = static_cast<int64_t>(pslot) * a.hq + h * G;
+      for (int e = lane; e < G * 32; e += kWave) {
+        const int g = e >> 5, c = e & 31;
+        *reinterpret_cast<f32x4_t*>(a.part_o + (p0 + g) * kD + 4 * c) =
+            *reinterpret_cast<const f32x4_t*>(sl + 16 + 512 * g + 16 * c);
+      }
+      if (lane < G) a.part_lse[p0 + lane] = *reinterpret_cast<const float*>(sl + 16 + 512 * G + 4 * lane);
+    }
+  }
+  wave_lds_sync();
 }
 
 // Persistent, token-balanced schedule: unit u takes the tokens
@@ -427,7 +521,9 @@ __device__ __forceinline__ void decode_units(const DecodeArgs& a, char* smem, in
   if (u == 0 && gt == 0) *a.status = SGL_OK;
   const bool active = u < a.num_units && tok0 < tok1;
   char* base = smem + g * unit_lds_bytes<kRows>(a.hkv, a.chunk);
-  int32_t* sidx = reinterpret_cast<int32_t*>(base + a.hkv * sizeof(UnitWaveLds<kRows>));
+  int32_t* rq_kv = reinterpret_cast<int32_t*>(base + a.hkv * sizeof(UnitWaveLds<kRows>));
+  int32_t* rq_row = rq_kv + (kRows ? 0 : kReqStage + 1);
+  int32_t* sidx = rq_row + req_stage<kRows>();
   int r = 0;
   if (active) {
     // First i in [0, batch] with kv_indptr[i] >= tok0 (uniform binary search).
@@ -439,8 +535,17 @@ __device__ __forceinline__ void decode_units(const DecodeArgs& a, char* smem, in
     // Request lo - 1 runs across tok0 when its end kv_indptr[lo] lies past tok0.
     r = (lo > 0 && a.kv_indptr[lo] > tok0) ? lo - 1 : lo;
     if (gt == 0) a.unit_req[u] = r < a.batch && a.kv_indptr[r] < tok0 ? r : -1;
-    // Stage the unit's slot indices (shared by every kv head) in LDS.
+    // Stage the unit's slot indices (shared by every kv head) and the
+    // entries of its first requests in LDS: the walk over requests then
+    // reads no memory at a request boundary.
     for (int e = gt; e < tok1 - tok0; e += gn) sidx[e] = a.indices[tok0 + e];
+    if constexpr (!kRows) {
+      const int nst = min(kReqStage, a.batch - r);
+      for (int e = gt; e <= nst; e += gn) {
+        rq_kv[e] = a.kv_indptr[r + e];
+        if (e < nst) rq_row[e] = a.q_indptr ? a.q_indptr[r + e] : r + e;
+      }
+    }
   } else if (u < a.num_units && gt == 0) {
     a.unit_req[u] = -1;
   }
@@ -452,14 +557,31 @@ __device__ __forceinline__ void decode_units(const DecodeArgs& a, char* smem, in
     return;
   }
   UnitWaveLds<kRows>& L = reinterpret_cast<UnitWaveLds<kRows>*>(base)[wave];
+  // Decode-only launch: finished pieces go to the wave's LDS output ring and
+  // reach memory when the unit is done (or the ring is full): stores
+  // interleaved with the unit's read stream cost far more than their bytes.
+  const bool defer = UPW == 1 && kBarrier && !kRows && a.out_bytes > 0;
+  char* ring = smem + out_ring_offset(a.hkv, a.chunk) + static_cast<size_t>(wave) * a.out_bytes;
+  int used = 0;
+  const int r0 = r;
+  const int nst = min(req_stage<kRows>(), a.batch - r0);  // staged requests [r0, r0 + nst)
 
   for (; r < a.batch; ++r) {
-    const int rb = a.kv_indptr[r];
-    const int re = a.kv_indptr[r + 1];
+    int rb, re, qrow;
+    if constexpr (kRows) {
+      rb = a.kv_indptr[r];
+      re = a.kv_indptr[r + 1];
+      qrow = a.q_indptr ? a.q_indptr[r] : r;
+    } else {
+      const int k = r - r0;
+      const bool staged = k < nst;
+      rb = __builtin_amdgcn_readfirstlane(staged ? rq_kv[k] : a.kv_indptr[r]);
+      re = __builtin_amdgcn_readfirstlane(staged ? rq_kv[k + 1] : a.kv_indptr[r + 1]);
+      qrow = __builtin_amdgcn_readfirstlane(staged ? rq_row[k] : (a.q_indptr ? a.q_indptr[r] : r));
+    }
     // Requests starting at or past tok1 belong to later units, except empty
     // requests at the very end of the stream, which the last unit owns.
     if (rb >= tok1 && !(last_unit && rb == total)) break;
-    const int qrow = a.q_indptr ? a.q_indptr[r] : r;
     if (re == rb) {  // empty request: zero output row
       zero_row(a, qrow, gt, gn);
       continue;
@@ -471,9 +593,27 @@ __device__ __forceinline__ void decode_units(const DecodeArgs& a, char* smem, in
     const int pslot = 2 * u + (rb > tok0 ? 1 : 0);
     u32x4_t* kt = nullptr;
     if constexpr (kRows) kt = L.kt;
+    char* oslot = nullptr;
+    if (defer) {
+      const int rec = out_record_bytes(a.group, whole);
+      if (used + rec > a.out_bytes) {
+        flush_ring(a, ring, used, wave, lane);
+        used = 0;
+      }
+      oslot = ring + used;
+      if (lane == 0) {
+        int* hdr = reinterpret_cast<int*>(oslot);
+        hdr[0] = whole;
+        hdr[1] = qrow;
+        hdr[2] = pslot;
+        hdr[3] = rec;
+      }
+      used += rec;
+    }
     decode_head<false, kBarrier, kRows>(a, L, sidx + (s0 - tok0), pslot, whole, wave, s1 - s0,
-                                        qrow, lane, nullptr, kt);
+                                        qrow, lane, nullptr, kt, oslot);
   }
+  if (defer) flush_ring(a, ring, used, wave, lane);
 }
 
 // One unit per workgroup (one wave per kv head), about 8 waves per CU.
@@ -801,8 +941,7 @@ constexpr size_t kMixedLds = 160 * 1024;
 static int mixed_max_unit(int num_kv_heads) {
   const size_t per_unit = kMixedLds / (8 / num_kv_heads);
   const int64_t w = (static_cast<int64_t>(per_unit) -
-                     static_cast<int64_t>(num_kv_heads) *
-                         static_cast<int64_t>(sizeof(UnitWaveLds<true>))) /
+                     static_cast<int64_t>(unit_lds_bytes<true>(num_kv_heads, 0))) /
                     static_cast<int64_t>(sizeof(int32_t)) / kStep * kStep;
   return static_cast<int>(w < kMaxChunkTokens ? w : kMaxChunkTokens);
 }
@@ -989,6 +1128,7 @@ int decode_args(const sgl_decode_plan_t* plan, const void* q, int64_t q_stride_t
   a.chunk_min = plan->min_chunk_size;
   a.batch = batch_size;
   a.num_units = plan->num_units;
+  a.out_bytes = 0;
   return SGL_OK;
 }
 
@@ -1026,8 +1166,18 @@ int launch_decode(const DecodeArgs& a, const sgl_decode_plan_t* plan, hipStream_
   }
   const dim3 grid(plan->num_units);
   const dim3 block(a.hkv * kWave);
-  const size_t lds = unit_lds_bytes<false>(a.hkv, plan->kv_chunk_size);
-  hipLaunchKernelGGL(paged_decode_kernel, grid, block, lds, s, a);
+  // Output rings in what LDS the plan's units per CU leave free (at least
+  // one partial record per wave, else the pieces are written directly).
+  DecodeArgs da = a;
+  const int upc = a.hkv < 8 ? 8 / a.hkv : 1;
+  const size_t off = out_ring_offset(a.hkv, plan->kv_chunk_size);
+  const size_t budget = 160 * 1024 / upc;
+  size_t ring = budget > off ? (budget - off) / a.hkv / 16 * 16 : 0;
+  if (ring > kMaxOutRing) ring = kMaxOutRing;
+  da.out_bytes = ring >= static_cast<size_t>(out_record_bytes(a.group, false)) ? static_cast<int>(ring) : 0;
+  const size_t lds = da.out_bytes > 0 ? off + static_cast<size_t>(a.hkv) * da.out_bytes
+                                      : unit_lds_bytes<false>(a.hkv, plan->kv_chunk_size);
+  hipLaunchKernelGGL(paged_decode_kernel, grid, block, lds, s, da);
   int st = launch_status();
   if (st != SGL_OK) return st;
   // Always launched: besides folding split requests it is what reports a

@@ -725,8 +725,9 @@ def test_paged_mixed_random(oracle, dev, seed):
 @pytest.mark.parametrize("hq,hkv", [(8, 1), (16, 2)])
 def test_paged_mixed_long_units(oracle, dev, hq, hkv):
     """Long decode rows on few CUs at 1 and 2 kv heads: 8 or 4 units share a
-    fused workgroup's LDS, so the plan caps the unit length (4032 and 8064
-    tokens) rather than exceed it; results against the oracle."""
+    fused workgroup's LDS, so the plan caps the unit length (at most 4032
+    and 8064 tokens, less what the per-wave K tiles take) rather than exceed
+    it; results against the oracle."""
     note(f"paged mixed long units hq={hq} hkv={hkv}")
     rng = np.random.default_rng(35 + hkv)
     kv_dec = [int(x) for x in rng.integers(30000, 45000, 7)]
