@@ -25,8 +25,7 @@
 //   * K and V of step t+1 are issued before the products of step t.
 //   * The decode-only launch keeps each wave's finished pieces (output rows,
 //     or split partials) in an LDS ring and writes them when its unit is
-//     done (or the ring is full), and stages its first requests' kv_indptr
-//     and row entries in LDS: stores interleaved with the unit's read
+//     done (or the ring is full): stores interleaved with the unit's read
 //     stream cost far more than their bytes (config 4 shape, same tokens:
 //     -1.4% at 256 requests, -7% at 2,048).
 // A request that spans units is written as fp32 partials (normalised output
@@ -423,25 +422,13 @@ __device__ __forceinline__ void zero_row(const DecodeArgs& a, int qrow, int t, i
   }
 }
 
-// Requests whose kv_indptr / row entries a unit stages in LDS (the walk
-// over further requests reads them from memory).
-constexpr int kReqStage = 256;
 constexpr size_t kMaxOutRing = 32 * 1024;  // output ring bytes per wave of the decode-only launch
 
-// Request entries a unit stages: the decode-only launch's (kv_indptr[r0 ..
-// r0 + kReqStage], rows[r0 .. r0 + kReqStage)); the fused launch's decode
-// role, whose units hold one or two pieces, stages none (staging there cost
-// its launch 4%).
-template <bool kRows>
-__device__ __host__ constexpr int req_stage() { return kRows ? 0 : kReqStage; }
-
-// LDS bytes of one unit: the per-wave Q copies, the staged request entries,
-// then the unit's slot indices. kRows: the per-wave K tile of whole-row K
-// loads too.
+// LDS bytes of one unit: the per-wave Q copies, then the unit's slot
+// indices. kRows: the per-wave K tile of whole-row K loads too.
 template <bool kRows>
 __device__ __host__ inline size_t unit_lds_bytes(int hkv, int chunk) {
   return static_cast<size_t>(hkv) * sizeof(UnitWaveLds<kRows>) +
-         static_cast<size_t>(kRows ? 0 : 2 * kReqStage + 1) * sizeof(int32_t) +
          static_cast<size_t>(chunk) * sizeof(int32_t);
 }
 
@@ -521,9 +508,7 @@ __device__ __forceinline__ void decode_units(const DecodeArgs& a, char* smem, in
   if (u == 0 && gt == 0) *a.status = SGL_OK;
   const bool active = u < a.num_units && tok0 < tok1;
   char* base = smem + g * unit_lds_bytes<kRows>(a.hkv, a.chunk);
-  int32_t* rq_kv = reinterpret_cast<int32_t*>(base + a.hkv * sizeof(UnitWaveLds<kRows>));
-  int32_t* rq_row = rq_kv + (kRows ? 0 : kReqStage + 1);
-  int32_t* sidx = rq_row + req_stage<kRows>();
+  int32_t* sidx = reinterpret_cast<int32_t*>(base + a.hkv * sizeof(UnitWaveLds<kRows>));
   int r = 0;
   if (active) {
     // First i in [0, batch] with kv_indptr[i] >= tok0 (uniform binary search).
@@ -535,17 +520,8 @@ __device__ __forceinline__ void decode_units(const DecodeArgs& a, char* smem, in
     // Request lo - 1 runs across tok0 when its end kv_indptr[lo] lies past tok0.
     r = (lo > 0 && a.kv_indptr[lo] > tok0) ? lo - 1 : lo;
     if (gt == 0) a.unit_req[u] = r < a.batch && a.kv_indptr[r] < tok0 ? r : -1;
-    // Stage the unit's slot indices (shared by every kv head) and the
-    // entries of its first requests in LDS: the walk over requests then
-    // reads no memory at a request boundary.
+    // Stage the unit's slot indices (shared by every kv head) in LDS.
     for (int e = gt; e < tok1 - tok0; e += gn) sidx[e] = a.indices[tok0 + e];
-    if constexpr (!kRows) {
-      const int nst = min(kReqStage, a.batch - r);
-      for (int e = gt; e <= nst; e += gn) {
-        rq_kv[e] = a.kv_indptr[r + e];
-        if (e < nst) rq_row[e] = a.q_indptr ? a.q_indptr[r + e] : r + e;
-      }
-    }
   } else if (u < a.num_units && gt == 0) {
     a.unit_req[u] = -1;
   }
@@ -563,25 +539,14 @@ __device__ __forceinline__ void decode_units(const DecodeArgs& a, char* smem, in
   const bool defer = UPW == 1 && kBarrier && !kRows && a.out_bytes > 0;
   char* ring = smem + out_ring_offset(a.hkv, a.chunk) + static_cast<size_t>(wave) * a.out_bytes;
   int used = 0;
-  const int r0 = r;
-  const int nst = min(req_stage<kRows>(), a.batch - r0);  // staged requests [r0, r0 + nst)
 
   for (; r < a.batch; ++r) {
-    int rb, re, qrow;
-    if constexpr (kRows) {
-      rb = a.kv_indptr[r];
-      re = a.kv_indptr[r + 1];
-      qrow = a.q_indptr ? a.q_indptr[r] : r;
-    } else {
-      const int k = r - r0;
-      const bool staged = k < nst;
-      rb = __builtin_amdgcn_readfirstlane(staged ? rq_kv[k] : a.kv_indptr[r]);
-      re = __builtin_amdgcn_readfirstlane(staged ? rq_kv[k + 1] : a.kv_indptr[r + 1]);
-      qrow = __builtin_amdgcn_readfirstlane(staged ? rq_row[k] : (a.q_indptr ? a.q_indptr[r] : r));
-    }
+    const int rb = a.kv_indptr[r];
+    const int re = a.kv_indptr[r + 1];
     // Requests starting at or past tok1 belong to later units, except empty
     // requests at the very end of the stream, which the last unit owns.
     if (rb >= tok1 && !(last_unit && rb == total)) break;
+    const int qrow = a.q_indptr ? a.q_indptr[r] : r;
     if (re == rb) {  // empty request: zero output row
       zero_row(a, qrow, gt, gn);
       continue;
