@@ -1,16 +1,20 @@
 // The Sampler's probabilities from logits, shared by the temperature-softmax
 // kernel (softmax.hip) and the draws that read logits directly
 // (sampling.hip), so both compute every probability with the same
-// operations and get the same bits:
-//   y = x * (1 / t); per statistics lane v < kStatLanes, a running max m and
-//   sum of 2^((y - m) log2e) over its chunks c = v + kStatLanes k
+// operations and get the same bits. With a = log2(e) / t (one division per
+// row) the exponent of a raw logit x is x a - M a, M the row's largest raw
+// logit, formed by one fused multiply-add with the row constant nb = -(M a):
+//   per statistics lane v < kStatLanes, a running max mx of its raw logits
+//   and sum of 2^(x a - mx a) over its chunks c = v + kStatLanes k
 //   (elements [P c, P c + P)), then the elements past the whole chunks one
-//   by one; folded in a fixed order (a butterfly within each group of 64
-//   lanes, then the 16 group values in order); p = 2^((y - m) log2e) *
-//   (1 / sum). A 1024-thread workgroup runs one lane per thread; a 512-thread
-//   workgroup runs lanes t and t + 512 on thread t.
-// Floating-point contraction is off in these functions: a fused multiply-add
-// chosen differently in the two kernels would change low bits.
+//   by one; the lanes folded in a fixed order (a butterfly within each group
+//   of 64 lanes, then the 16 group values in order) into M and
+//   s = sum 2^(x a - M a); p = 2^(fma(x, a, nb)) * (1 / s).
+// A temperature that is not positive gives a = NaN, so that row's
+// probabilities are NaN (and its draws the last index).
+// Floating-point contraction is off in these functions: the one fused
+// multiply-add is explicit, and another one chosen differently in the two
+// kernels would change low bits.
 #pragma once
 
 #include "common.h"
@@ -53,43 +57,58 @@ struct Elem<SGL_DTYPE_F32> {
   __device__ static float load1(const void* p, int64_t i) { return static_cast<const float*>(p)[i]; }
 };
 
-// Running (max, sum of 2^((y - max) log2e)) of a lane, updated by N values.
-template <int N>
-__device__ __forceinline__ void online_update(const float (&y)[N], float& mx, float& s) {
+// The exp2 scale of a raw logit: log2(e) / t, NaN unless t > 0.
+__device__ __forceinline__ float exp2_scale(float t) {
 #pragma clang fp contract(off)
-  float cm = y[0];
+  return t > 0.f ? kLog2e / t : __builtin_nanf("");
+}
+
+// The row constant of the exponent fma(x, a, nb) given the row max M.
+__device__ __forceinline__ float exp2_offset(float m, float a) {
+#pragma clang fp contract(off)
+  return -(m * a);
+}
+
+// A lane's running state: max mx of its raw logits, nb = exp2_offset(mx, a)
+// and the sum s of 2^(fma(x, a, nb)). Starts at (-inf, 0, 0).
+struct LaneStats {
+  float mx = -INFINITY, nb = 0.f, s = 0.f;
+};
+
+// LaneStats updated by N raw logits.
+template <int N>
+__device__ __forceinline__ void online_update(const float (&x)[N], float a, LaneStats& st) {
+#pragma clang fp contract(off)
+  float cm = x[0];
 #pragma unroll
-  for (int j = 1; j < N; ++j) cm = fmaxf(cm, y[j]);
-  if (cm > mx) {
-    s *= __builtin_amdgcn_exp2f((mx - cm) * kLog2e);  // 0 while mx = -inf
-    mx = cm;
+  for (int j = 1; j < N; ++j) cm = fmaxf(cm, x[j]);
+  if (cm > st.mx) {
+    const float nb = exp2_offset(cm, a);
+    st.s *= __builtin_amdgcn_exp2f(__builtin_fmaf(st.mx, a, nb));  // 0 while mx = -inf
+    st.mx = cm;
+    st.nb = nb;
   }
 #pragma unroll
-  for (int j = 0; j < N; ++j) s += __builtin_amdgcn_exp2f((y[j] - mx) * kLog2e);
+  for (int j = 0; j < N; ++j) st.s += __builtin_amdgcn_exp2f(__builtin_fmaf(x[j], a, st.nb));
 }
 
 template <int DT>
-__device__ __forceinline__ void scaled(const u32x4_t& v, float inv_t, float (&y)[Elem<DT>::kPer]) {
-#pragma clang fp contract(off)
+__device__ __forceinline__ void unpack(const u32x4_t& v, float (&x)[Elem<DT>::kPer]) {
 #pragma unroll
-  for (int j = 0; j < Elem<DT>::kPer; ++j) y[j] = Elem<DT>::at(v, j) * inv_t;
+  for (int j = 0; j < Elem<DT>::kPer; ++j) x[j] = Elem<DT>::at(v, j);
 }
 
-__device__ __forceinline__ float scaled1(float x, float inv_t) {
+// The probability of raw logit x given a, nb = exp2_offset(M, a) and 1 / s.
+__device__ __forceinline__ float prob(float x, float a, float nb, float inv_s) {
 #pragma clang fp contract(off)
-  return x * inv_t;
+  return __builtin_amdgcn_exp2f(__builtin_fmaf(x, a, nb)) * inv_s;
 }
 
-// The probability of logit x given the row's max m and 1 / sum.
-__device__ __forceinline__ float prob(float x, float inv_t, float m, float inv_s) {
+// A lane's sum relative to the row max M (a lane with no element adds 0).
+__device__ __forceinline__ float lane_sum_at(const LaneStats& st, float m, float a) {
 #pragma clang fp contract(off)
-  return __builtin_amdgcn_exp2f((x * inv_t - m) * kLog2e) * inv_s;
-}
-
-// A lane's sum relative to the row max (a lane with no element adds 0).
-__device__ __forceinline__ float lane_sum_at(float mx, float s, float m) {
-#pragma clang fp contract(off)
-  return mx == -INFINITY ? 0.f : s * __builtin_amdgcn_exp2f((mx - m) * kLog2e);
+  return st.mx == -INFINITY ? 0.f
+                            : st.s * __builtin_amdgcn_exp2f(__builtin_fmaf(st.mx, a, exp2_offset(m, a)));
 }
 
 // Fixed-order reductions over the kStatWaves groups of 64 statistics lanes:
@@ -167,15 +186,13 @@ __device__ __forceinline__ float block_sum2(float x0, float x1, float* sh) {
   return s;
 }
 
-// Statistics lane `lane`'s max and sum over a row read from memory: chunks
+// Statistics lane `lane`'s state over a row read from memory: chunks
 // c = lane + kStatLanes k below nfull (aligned rows), then the elements from
 // nfull * P one by one.
 template <int DT>
-__device__ __forceinline__ void lane_stats(const char* row, int d, bool vec, int lane, float inv_t,
-                                           float& mx, float& s) {
+__device__ __forceinline__ LaneStats lane_stats(const char* row, int d, bool vec, int lane, float a) {
   constexpr int P = Elem<DT>::kPer;
-  mx = -INFINITY;
-  s = 0.f;
+  LaneStats st;
   const int nfull = vec ? d / P : 0;
   auto chunk = [&](int c) {
     return *reinterpret_cast<const u32x4_t*>(row + static_cast<int64_t>(c) * 16);
@@ -190,20 +207,21 @@ __device__ __forceinline__ void lane_stats(const char* row, int d, bool vec, int
     for (int k = 0; k < kAhead; ++k) v[k] = chunk(c + k * kStatLanes);
 #pragma unroll
     for (int k = 0; k < kAhead; ++k) {
-      float y[P];
-      scaled<DT>(v[k], inv_t, y);
-      online_update(y, mx, s);
+      float x[P];
+      unpack<DT>(v[k], x);
+      online_update(x, a, st);
     }
   }
   for (; c < nfull; c += kStatLanes) {
-    float y[P];
-    scaled<DT>(chunk(c), inv_t, y);
-    online_update(y, mx, s);
+    float x[P];
+    unpack<DT>(chunk(c), x);
+    online_update(x, a, st);
   }
   for (int e = nfull * P + lane; e < d; e += kStatLanes) {
-    const float y[1] = {scaled1(Elem<DT>::load1(row, e), inv_t)};
-    online_update(y, mx, s);
+    const float x[1] = {Elem<DT>::load1(row, e)};
+    online_update(x, a, st);
   }
+  return st;
 }
 
 }  // namespace sp

@@ -20,21 +20,28 @@
 // and has no effect.
 //
 // MI355X layout: one 1024-thread workgroup (16 waves) per row. The row is
-// cut into blocks of 1024 probabilities, four coalesced 16-byte loads per
-// lane of a wave; waves take blocks round-robin, two blocks in flight. A
-// sweep with a threshold leaves in LDS the mass above it of every block
-// (one wave reduction per block) and the row's mass and count above it. A
-// draw is wave 0's alone: each lane sums a run of block masses, a DPP wave
-// scan finds the lane whose run crosses u, that lane walks to the crossing
-// block, and the wave scans the block's probabilities in row order to the
-// first crossing index. A rejection round is one sweep: the sweep that
-// counts the probabilities above the new pivot also gives the next draw its
-// block masses. A vocabulary row (Qwen3: 151,936 x 4 B) comes from HBM on
-// the first sweep. That sweep also copies into LDS every probability above
-// 1/31,360 (at most 31,360 of them in a normalised row), so rounds whose
+// cut into blocks of 512 probabilities, eight consecutive ones per lane
+// (two 16-byte loads of fp32 probabilities, or one of 16-bit logits); waves
+// take blocks round-robin, two blocks in flight. A sweep with a threshold
+// leaves in LDS the mass above it of every block (one wave reduction per
+// block) and the row's mass and count above it. A draw is wave 0's alone:
+// each lane sums a run of block masses, a DPP wave scan finds the lane
+// whose run crosses u, that lane walks to the crossing block, and the wave
+// scans the block's probabilities in row order to the first crossing
+// index. A rejection round is one sweep: the sweep that counts the
+// probabilities above the new pivot also gives the next draw its block
+// masses. A vocabulary row (Qwen3: 151,936 x 4 B) comes from HBM on the
+// first sweep. That sweep also copies into LDS every probability above
+// 1/30,464 (at most 30,464 of them in a normalised row), so rounds whose
 // pivot clears that threshold sweep the copies instead of the row; when it
 // does not, the next sweep of the row copies what exceeds its pivot, space
 // allowing. Only the crossing block of a draw is read from the row then.
+//
+// Draws from 16-bit logits (rows of up to 163,840, 16-byte aligned, length
+// a multiple of 8) read the row from HBM once: thread t keeps its 16-byte
+// chunks t + 1024 k in registers, which are exactly lane t % 64's share of
+// blocks t / 64 + 16 k, computes the row statistics from them, and every
+// sweep of the row recomputes the probabilities from the registers.
 #include <math.h>
 
 #include "common.h"
@@ -46,18 +53,24 @@ namespace {
 constexpr int kThreads = 1024;
 constexpr int kWaves = kThreads / kWave;
 constexpr int kVec = 4;
-constexpr int kSub = 4;                       // 16-byte loads per lane per block
-constexpr int kSpan = kWave * kVec;           // probabilities per wave load (1 KiB)
-constexpr int kBlock = kSpan * kSub;          // probabilities per block
-constexpr int kMaxBlocks = 2048;              // rows up to 2M probabilities
+constexpr int kSub = 2;                       // 16-byte loads per lane per block
+constexpr int kPerLane = kVec * kSub;         // consecutive probabilities per lane
+constexpr int kBlock = kWave * kPerLane;      // probabilities per block (512)
+constexpr int kMaxBlocks = 4096;              // rows up to 2M probabilities
 // Candidate mode (rows of at most kCandBlocks blocks, 1M probabilities): a
 // sweep of the row also copies the probabilities above a threshold into
 // LDS, grouped by block, and later rounds whose pivot is at or above that
 // threshold sweep those copies instead of the row. The copies share one LDS
 // pool with the block masses, which then need only kCandBlocks entries.
-constexpr int kCandBlocks = 1024;              // one (start, count) word per block
+constexpr int kCandBlocks = 2048;              // one (start, count) word per block
 constexpr int kPool = 36864;                   // 144 KiB
-constexpr int kCandCap = kPool - kCandBlocks;  // 35,840 copies
+constexpr int kCandCap = kPool - kCandBlocks;  // 34,816 copies
+// Draws from 16-bit logits hold rows of up to kMaxHeldChunks 16-byte chunks a
+// lane (163,840 logits, 80 VGPRs) in registers.
+constexpr int kMaxHeldChunks = 20;
+// Word 3 of a raw buffer resource on gfx950 (32-bit data format, no
+// swizzle, unit stride): byte-addressed loads with a range check.
+constexpr int kRawBufferWord3 = 0x00020000;
 static_assert(kPool >= kMaxBlocks, "block masses of the longest rows fit the pool");
 static_assert(kCandCap < 65536 && kBlock < 65536, "segment words hold two 16-bit fields");
 
@@ -96,7 +109,7 @@ struct ProbRow {
 template <int DT>
 struct LogitRow {
   const char* x;
-  float inv_t, m, inv_s;
+  float sc, nb, inv_s;  // sampler_prob.h's row constants
   // Four consecutive elements from e (e % 4 == 0 on a 16-byte aligned row).
   __device__ f32x4_t load4(int64_t e) const {
     u32x4_t v;
@@ -108,11 +121,11 @@ struct LogitRow {
     }
     f32x4_t r;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) r[j] = sp::prob(sp::Elem<DT>::at(v, j), inv_t, m, inv_s);
+    for (int j = 0; j < 4; ++j) r[j] = sp::prob(sp::Elem<DT>::at(v, j), sc, nb, inv_s);
     return r;
   }
   __device__ float load1(int64_t e) const {
-    return sp::prob(sp::Elem<DT>::load1(x, e), inv_t, m, inv_s);
+    return sp::prob(sp::Elem<DT>::load1(x, e), sc, nb, inv_s);
   }
 };
 
@@ -168,9 +181,9 @@ __device__ __forceinline__ T read_lane(T x, int l) {
   return __builtin_bit_cast(T, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), l));
 }
 
-// One block of a row: lane l holds probabilities kSpan s + kVec l + j
-// (s < kSub, j < kVec) of the block; bounds-checked when the block is the
-// row's last or the row is not 16-byte aligned.
+// One block of a row: lane l holds probabilities kPerLane l + kVec s + j
+// (s < kSub, j < kVec) of the block, in row order; bounds-checked when the
+// block is the row's last or the row is not 16-byte aligned.
 struct BlockVals {
   f32x4_t v[kSub];
 };
@@ -178,29 +191,28 @@ struct BlockVals {
 template <class Src>
 __device__ __forceinline__ void load_block(const Src& row, int b, int d, bool full, BlockVals& bv) {
   const int lane = threadIdx.x & 63;
-  const int e0 = b * kBlock + kVec * lane;
+  const int e0 = b * kBlock + kPerLane * lane;
   if (full) {
 #pragma unroll
-    for (int s = 0; s < kSub; ++s) bv.v[s] = row.load4(e0 + kSpan * s);
+    for (int s = 0; s < kSub; ++s) bv.v[s] = row.load4(e0 + kVec * s);
   } else {
 #pragma unroll
     for (int s = 0; s < kSub; ++s)
 #pragma unroll
       for (int j = 0; j < kVec; ++j) {
-        const int e = e0 + kSpan * s + j;
+        const int e = e0 + kVec * s + j;
         bv.v[s][j] = e < d ? row.load1(e) : 0.f;
       }
   }
 }
 
-// Row totals from the per-wave mass wm (wave-uniform) and per-lane counts
-// wn: wave sums, then wave 0 adds the 16 wave totals in a fixed DPP order.
-__device__ __forceinline__ void finish_totals(float wm, float wn, Shared& sh) {
+// Row totals from the per-wave mass wm and count wn (both wave-uniform):
+// wave 0 adds the 16 wave totals in a fixed DPP order.
+__device__ __forceinline__ void finish_totals(float wm, int wn, Shared& sh) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  wn = wave_sum_f(wn);
   if (lane == 0) {
     sh.wave_f[wave] = wm;
-    sh.wave_n[wave] = wn;
+    sh.wave_n[wave] = static_cast<float>(wn);
   }
   __syncthreads();
   if (wave == 0) {
@@ -214,45 +226,60 @@ __device__ __forceinline__ void finish_totals(float wm, float wn, Shared& sh) {
   __syncthreads();
 }
 
+// The lanes below this one whose bit is set in mask.
+__device__ __forceinline__ int lanes_below(uint64_t mask) {
+  return __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
+                                   __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0u));
+}
+
 // Mass and count above thr of one block (mass wave-reduced into pool[b],
-// count per lane); kCompact: also the copies above cthr, each lane's after
-// those of lower lanes (a fixed order).
+// count wave-wide from the comparison masks); kCompact: also the copies
+// above cthr, placed element-major (element j of every lane, lanes in
+// order, then element j + 1), a fixed order that needs one lane count per
+// element that has any copy.
 template <bool kCompact>
 __device__ __forceinline__ void sweep_block(const BlockVals& bv, int b, float thr, float cthr,
-                                            float& wm, float& wn, Shared& sh) {
+                                            float& wm, int& wn, Shared& sh) {
   const int lane = threadIdx.x & 63;
-  float m = 0.f, n = 0.f;
+  float m = 0.f;
 #pragma unroll
   for (int s = 0; s < kSub; ++s)
 #pragma unroll
     for (int j = 0; j < kVec; ++j) {
       const float x = bv.v[s][j];
-      m += x > thr ? x : 0.f;
-      n += x > thr ? 1.f : 0.f;
+      const bool above = x > thr;
+      m += above ? x : 0.f;
+      wn += __builtin_popcountll(__ballot(above));
     }
-  wn += n;
   m = wave_sum_f(m);
   wm += m;
   if (lane == 0) sh.pool[b] = m;
   if constexpr (kCompact) {
-    float c = 0.f;
+    uint64_t mk[kPerLane];
+    int tot = 0;
 #pragma unroll
     for (int s = 0; s < kSub; ++s)
 #pragma unroll
-      for (int j = 0; j < kVec; ++j) c += bv.v[s][j] > cthr ? 1.f : 0.f;
-    const float incl = wave_scan(c);
-    const int tot = static_cast<int>(read_lane(incl, 63));
+      for (int j = 0; j < kVec; ++j) {
+        mk[kVec * s + j] = __ballot(bv.v[s][j] > cthr);
+        tot += __builtin_popcountll(mk[kVec * s + j]);
+      }
     int base = 0;
     if (tot > 0) {
       if (lane == 0) base = atomicAdd(&sh.ncand, tot);
       base = read_lane(base, 0);
       if (base + tot <= kCandCap) {
-        int pos = kCandBlocks + base + static_cast<int>(incl - c);
+        int pos = kCandBlocks + base;
 #pragma unroll
         for (int s = 0; s < kSub; ++s)
 #pragma unroll
-          for (int j = 0; j < kVec; ++j)
-            if (bv.v[s][j] > cthr) sh.pool[pos++] = bv.v[s][j];
+          for (int j = 0; j < kVec; ++j) {
+            const uint64_t mj = mk[kVec * s + j];
+            if (mj != 0) {
+              if (bv.v[s][j] > cthr) sh.pool[pos + lanes_below(mj)] = bv.v[s][j];
+              pos += __builtin_popcountll(mj);
+            }
+          }
       }
     }
     if (lane == 0) sh.seg[b] = static_cast<uint32_t>(base) | static_cast<uint32_t>(tot) << 16;
@@ -266,10 +293,11 @@ __device__ __forceinline__ void sweep_block(const BlockVals& bv, int b, float th
 template <bool kCompact, class Src>
 __device__ __forceinline__ void sweep(const Src& row, int d, bool vec, float thr, float cthr,
                                       Shared& sh) {
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int nblk = (d + kBlock - 1) / kBlock;
   const int nfull = vec ? d / kBlock : 0;  // blocks loaded without bounds checks
-  float wm = 0.f, wn = 0.f;
+  float wm = 0.f;
+  int wn = 0;
   __syncthreads();  // the previous readers of sh are done
   int b = wave;
   for (; b + kWaves < nfull; b += 2 * kWaves) {
@@ -312,98 +340,122 @@ __device__ __forceinline__ void sweep_cand(int d, float thr, Shared& sh) {
     // wave-uniform partial of the four blocks, in group order
     wm += read_lane(m, 0) + read_lane(m, 16) + read_lane(m, 32) + read_lane(m, 48);
   }
-  finish_totals(wm, wn, sh);
+  finish_totals(wm, static_cast<int>(wave_sum_f(wn)), sh);
 }
 
-// The inverse-CDF draw over the probabilities above thr with target u,
-// from the block masses of the last sweep with the same threshold, by wave
-// 0 alone (one barrier): lane l sums its run of block masses, a wave scan
-// finds the first lane whose run crosses u, that lane walks its run to the
-// crossing block, and the wave scans that block. Leaves the index in
-// sh.sampled and its probability in sh.sampled_p.
+// The inverse-CDF draw over the probabilities above thr with target u, from
+// the block masses of the last sweep with the same threshold, in two steps.
+// find_block (one wave): lane l sums its run of block masses, a wave scan
+// finds the first lane whose run crosses u, and that lane walks its run to
+// the crossing block; returns it (nblk when no run crosses) and the mass
+// before it (wave-uniform).
+__device__ __forceinline__ void find_block(int nblk, float u, const Shared& sh, int& bs,
+                                           float& base) {
+  const int lane = threadIdx.x & 63;
+  const int per = (nblk + kWave - 1) / kWave;
+  const int b0 = min(nblk, lane * per), b1 = min(nblk, b0 + per);
+  float own = 0.f;
+  for (int b = b0; b < b1; ++b) own += sh.pool[b];
+  const float incl = wave_scan(own);
+  const uint64_t cross = __ballot(incl > u);
+  bs = nblk;
+  base = 0.f;
+  if (cross) {
+    const int L = __builtin_ctzll(cross);
+    float run = incl - own;
+    int b = b1 - 1;
+    if (lane == L) {
+      for (int c = b0; c < b1; ++c) {
+        if (run + sh.pool[c] > u) {
+          b = c;
+          break;
+        }
+        run += sh.pool[c];
+      }
+    }
+    bs = read_lane(b, L);
+    base = read_lane(run, L);
+  }
+}
+
+// scan_block (one wave): lane l holds the block's probabilities
+// [kPerLane l, kPerLane l + kPerLane) in p, element e0 + i of the row, valid
+// where below d; the first one above thr whose running mass from base
+// exceeds u (lowest lane first: lanes run in row order), else (rounding
+// inside the block missed u) the block's last one above thr. Returns false
+// when the block has none above thr.
+__device__ __forceinline__ bool scan_block(const float (&p)[kPerLane], int e0, int d, float thr,
+                                           float base, float u, Shared& sh) {
+  const int lane = threadIdx.x & 63;
+  int first = d, last_valid = -1;
+  float first_p = 0.f, last_p = 0.f;
+  float local = 0.f;
+#pragma unroll
+  for (int i = 0; i < kPerLane; ++i) local += p[i] > thr ? p[i] : 0.f;
+  const float cincl = wave_scan(local);
+  float cdf = base + (cincl - local);
+#pragma unroll
+  for (int i = 0; i < kPerLane; ++i) {
+    const bool valid = p[i] > thr && e0 + i < d;
+    cdf += valid ? p[i] : 0.f;
+    if (valid) {
+      last_valid = e0 + i;
+      last_p = p[i];
+    }
+    if (valid && cdf > u && first == d) {
+      first = e0 + i;
+      first_p = p[i];
+    }
+  }
+  const uint64_t has_first = __ballot(first < d);
+  const uint64_t has_last = __ballot(last_valid >= 0);
+  if (has_first) {
+    if (lane == __builtin_ctzll(has_first)) {
+      sh.sampled = first;
+      sh.sampled_p = first_p;
+    }
+    return true;
+  }
+  if (has_last) {
+    if (lane == 63 - __builtin_clzll(has_last)) {
+      sh.sampled = last_valid;
+      sh.sampled_p = last_p;
+    }
+    return true;
+  }
+  return false;
+}
+
+// The draw by wave 0 alone (one barrier), the crossing block read from the
+// row: leaves the index in sh.sampled and its probability in sh.sampled_p
+// (d - 1 when no probability above thr is found).
 template <class Src>
 __device__ __forceinline__ void draw(const Src& row, int d, bool vec, float thr, float u,
                                      Shared& sh) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int nblk = (d + kBlock - 1) / kBlock;
   if (wave == 0) {
-    const int per = (nblk + kWave - 1) / kWave;
-    const int b0 = min(nblk, lane * per), b1 = min(nblk, b0 + per);
-    float own = 0.f;
-    for (int b = b0; b < b1; ++b) own += sh.pool[b];
-    const float incl = wave_scan(own);
-    const uint64_t cross = __ballot(incl > u);
-    int bs = nblk;
-    float base = 0.f;
-    if (cross) {
-      const int L = __builtin_ctzll(cross);
-      float run = incl - own;
-      int b = b1 - 1;
-      if (lane == L) {
-        for (int c = b0; c < b1; ++c) {
-          if (run + sh.pool[c] > u) {
-            b = c;
-            break;
-          }
-          run += sh.pool[c];
-        }
-      }
-      bs = read_lane(b, L);
-      base = read_lane(run, L);  // mass before block bs
-    }
-    int first = d, last_valid = -1;
-    float first_p = 0.f, last_p = 0.f;
+    int bs;
+    float base;
+    find_block(nblk, u, sh, bs, base);
+    bool found = false;
     if (bs < nblk) {
-      // Lane l scans the block's probabilities [16 l, 16 l + 16) in row order.
-      constexpr int kPer = kBlock / kWave;
-      const int e0 = bs * kBlock + kPer * lane;
-      float p[kPer];
-      if (vec && e0 + kPer <= d) {
+      const int e0 = bs * kBlock + kPerLane * lane;
+      float p[kPerLane];
+      if (vec && e0 + kPerLane <= d) {
 #pragma unroll
-        for (int s = 0; s < kPer / 4; ++s) {
+        for (int s = 0; s < kPerLane / 4; ++s) {
           const f32x4_t v = row.load4(e0 + 4 * s);
 #pragma unroll
           for (int j = 0; j < 4; ++j) p[4 * s + j] = v[j];
         }
       } else {
 #pragma unroll
-        for (int i = 0; i < kPer; ++i) p[i] = e0 + i < d ? row.load1(e0 + i) : 0.f;
+        for (int i = 0; i < kPerLane; ++i) p[i] = e0 + i < d ? row.load1(e0 + i) : 0.f;
       }
-      float local = 0.f;
-#pragma unroll
-      for (int i = 0; i < kPer; ++i) local += p[i] > thr ? p[i] : 0.f;
-      const float cincl = wave_scan(local);
-      float cdf = base + (cincl - local);
-#pragma unroll
-      for (int i = 0; i < kPer; ++i) {
-        const bool valid = p[i] > thr && e0 + i < d;
-        cdf += valid ? p[i] : 0.f;
-        if (valid) {
-          last_valid = e0 + i;
-          last_p = p[i];
-        }
-        if (valid && cdf > u && first == d) {
-          first = e0 + i;
-          first_p = p[i];
-        }
-      }
+      found = scan_block(p, e0, d, thr, base, u, sh);
     }
-    // The first crossing (lowest lane: lanes run in row order), else
-    // (rounding inside the block missed u) the block's last candidate,
-    // else d - 1.
-    const uint64_t has_first = __ballot(first < d);
-    const uint64_t has_last = __ballot(last_valid >= 0);
-    if (has_first) {
-      if (lane == __builtin_ctzll(has_first)) {
-        sh.sampled = first;
-        sh.sampled_p = first_p;
-      }
-    } else if (has_last) {
-      if (lane == 63 - __builtin_clzll(has_last)) {
-        sh.sampled = last_valid;
-        sh.sampled_p = last_p;
-      }
-    } else if (lane == 0) {
+    if (!found && lane == 0) {
       sh.sampled = d - 1;
       sh.sampled_p = row.load1(d - 1);
     }
@@ -411,8 +463,82 @@ __device__ __forceinline__ void draw(const Src& row, int d, bool vec, float thr,
   __syncthreads();
 }
 
+// Sweeps of a row read from memory (fp32 probabilities or logits).
 template <class Src>
-__device__ __forceinline__ void sample_row(const SampleArgs& a, const Src& row, Shared& sh) {
+struct StreamSweep {
+  const Src& row;
+  int d;
+  bool vec;
+  template <bool kCompact>
+  __device__ __forceinline__ void run(float thr, float cthr, Shared& sh) const {
+    sweep<kCompact>(row, d, vec, thr, cthr, sh);
+  }
+  __device__ __forceinline__ void pick(float thr, float u, Shared& sh) const {
+    draw(row, d, vec, thr, u, sh);
+  }
+};
+
+// Sweeps of a 16-bit logits row held in registers (aligned rows, d % 8 == 0):
+// thread t holds chunk c = t + 1024 k (elements [8 c, 8 c + 8)) in held[k],
+// which is lane t % 64's share of block t / 64 + 16 k -- the block a wave
+// takes in sweep() and in the same per-lane order, so the masses, counts and
+// copies are the bits the sweep of the fp32 probabilities gives.
+template <int DT, int NC>
+struct HeldSweep {
+  const u32x4_t (&held)[NC];
+  const LogitRow<DT>& row;
+  int d;
+  float sc, nb, inv_s;
+  // The draw reads its crossing block from the row (scanning it from the
+  // registers of the wave that holds it, after one more barrier, measured
+  // no faster).
+  __device__ __forceinline__ void pick(float thr, float u, Shared& sh) const {
+    draw(row, d, true, thr, u, sh);
+  }
+  template <bool kCompact>
+  __device__ __forceinline__ void run(float thr, float cthr, Shared& sh) const {
+    // Wave-uniform, in a scalar register (block indices and LDS addresses
+    // then cost no VGPRs).
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nblk = (d + kBlock - 1) / kBlock;
+    const int nchunk = d / kPerLane;
+    float wm = 0.f;
+    int wn = 0;
+    __syncthreads();  // the previous readers of sh are done
+#pragma unroll
+    for (int k = 0; k < NC; ++k) {
+      const int b = wave + kWaves * k;
+      if (b < nblk) {
+        // An opaque copy: the probabilities are the same every sweep, and
+        // hoisted out of the rounds they would take 8 NC VGPRs instead of
+        // the packed row's 4 NC.
+        u32x4_t h = held[k];
+        asm volatile("" : "+v"(h));
+        BlockVals bv;
+#pragma unroll
+        for (int s = 0; s < kSub; ++s)
+#pragma unroll
+          for (int j = 0; j < kVec; ++j)
+            bv.v[s][j] = sp::prob(sp::Elem<DT>::at(h, kVec * s + j), sc, nb, inv_s);
+        if (kThreads * (k + 1) > nchunk) {  // the row's last chunks: some lanes hold none
+          const bool in = static_cast<int>(threadIdx.x) + kThreads * k < nchunk;
+#pragma unroll
+          for (int s = 0; s < kSub; ++s)
+#pragma unroll
+            for (int j = 0; j < kVec; ++j) bv.v[s][j] = in ? bv.v[s][j] : 0.f;
+        }
+        sweep_block<kCompact>(bv, b, thr, cthr, wm, wn, sh);
+      }
+      // One block's values live at a time (the row itself takes 4 NC VGPRs).
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    finish_totals(wm, wn, sh);
+  }
+};
+
+template <class Src, class Sweep>
+__device__ __forceinline__ void sample_row(const SampleArgs& a, const Src& row, const Sweep& rs,
+                                           Shared& sh) {
   const int row_id = blockIdx.x;
   const bool cand_ok = a.mode != 0 && (a.d + kBlock - 1) / kBlock <= kCandBlocks;
   // The first sweep already copies the probabilities above cand_thr: at
@@ -423,13 +549,13 @@ __device__ __forceinline__ void sample_row(const SampleArgs& a, const Src& row, 
   float u = a.uniform[row_id];
   if (cand_ok) {
     if (threadIdx.x == 0) sh.ncand = 0;
-    sweep<true>(row, a.d, a.vec, 0.f, cand_thr, sh);
+    rs.template run<true>(0.f, cand_thr, sh);
     cand = sh.ncand <= kCandCap;
   } else {
-    sweep<false>(row, a.d, a.vec, 0.f, 0.f, sh);
+    rs.template run<false>(0.f, 0.f, sh);
   }
   if (a.mode == 0) {
-    draw(row, a.d, a.vec, 0.f, u, sh);
+    rs.pick(0.f, u, sh);
     if (threadIdx.x == 0) a.out[row_id] = sh.sampled;
     return;
   }
@@ -444,7 +570,7 @@ __device__ __forceinline__ void sample_row(const SampleArgs& a, const Src& row, 
     // The next round's uniform is loaded while this round runs.
     const float u_next =
         r + 1 < a.rounds ? a.uniform[static_cast<int64_t>(r + 1) * a.batch + row_id] : 0.f;
-    draw(row, a.d, a.vec, pivot, u * q, sh);
+    rs.pick(pivot, u * q, sh);
     sampled = sh.sampled;
     const float ps = sh.sampled_p;
     if (ps > pivot) {
@@ -456,11 +582,11 @@ __device__ __forceinline__ void sample_row(const SampleArgs& a, const Src& row, 
         sweep_cand(a.d, pivot, sh);
       } else if (!cand && cand_ok) {
         if (threadIdx.x == 0) sh.ncand = 0;
-        sweep<true>(row, a.d, a.vec, pivot, pivot, sh);
+        rs.template run<true>(pivot, pivot, sh);
         cand = sh.ncand <= kCandCap;
         cand_thr = pivot;
       } else {
-        sweep<false>(row, a.d, a.vec, pivot, 0.f, sh);
+        rs.template run<false>(pivot, 0.f, sh);
       }
     }
     q = sh.total;
@@ -485,19 +611,77 @@ __global__ void __launch_bounds__(kThreads) sampling_kernel(SampleArgs a) {
   __shared__ Shared sh;
   const int row_id = blockIdx.x;
   if constexpr (SRC < 0) {
-    sample_row(a, ProbRow{a.probs + static_cast<int64_t>(row_id) * a.d}, sh);
+    const ProbRow row{a.probs + static_cast<int64_t>(row_id) * a.d};
+    sample_row(a, row, StreamSweep<ProbRow>{row, a.d, a.vec}, sh);
   } else {
     static_assert(kThreads == sp::kStatLanes, "one statistics lane per thread");
     constexpr int B = 16 / sp::Elem<SRC>::kPer;
     const char* x = static_cast<const char*>(a.logits) + static_cast<int64_t>(row_id) * a.x_st * B;
     const float t = a.temps ? a.temps[row_id] : a.temp;
-    const float inv_t = 1.0f / t;
-    float mx, s;
-    sp::lane_stats<SRC>(x, a.d, a.stats_vec, threadIdx.x, inv_t, mx, s);
-    const float m = sp::block_max<kWaves>(mx, sh.wave_f);
-    const float inv_s = 1.0f / sp::block_sum<kWaves>(sp::lane_sum_at(mx, s, m), sh.wave_f);
-    sample_row(a, LogitRow<SRC>{x, inv_t, m, inv_s}, sh);
+    const float sc = sp::exp2_scale(t);
+    const sp::LaneStats st = sp::lane_stats<SRC>(x, a.d, a.stats_vec, threadIdx.x, sc);
+    const float m = sp::block_max<kWaves>(st.mx, sh.wave_f);
+    const float inv_s = 1.0f / sp::block_sum<kWaves>(sp::lane_sum_at(st, m, sc), sh.wave_f);
+    const LogitRow<SRC> row{x, sc, sp::exp2_offset(m, sc), inv_s};
+    sample_row(a, row, StreamSweep<LogitRow<SRC>>{row, a.d, a.vec}, sh);
   }
+}
+
+// Draws from 16-bit logits rows of at most NC chunks a lane, aligned and
+// d % 8 == 0: the row is read from memory once, into registers, in the
+// statistics order of sp::lane_stats (the same bits); every later sweep of
+// the row recomputes its probabilities from the registers. Only a draw's
+// crossing block is read from memory again.
+template <int SRC, int NC>
+__global__ void __launch_bounds__(kThreads) sampling_held_kernel(SampleArgs a) {
+  __shared__ Shared sh;
+  static_assert(kThreads == sp::kStatLanes && sp::Elem<SRC>::kPer == kPerLane,
+                "a statistics chunk is a lane's share of a block");
+  const int row_id = blockIdx.x;
+  const int tid = threadIdx.x;
+  const char* x = static_cast<const char*>(a.logits) + static_cast<int64_t>(row_id) * a.x_st * 2;
+  const float t = a.temps ? a.temps[row_id] : a.temp;
+  const float sc = sp::exp2_scale(t);
+  const int nchunk = a.d / kPerLane;
+  u32x4_t held[NC];
+  const __amdgpu_buffer_rsrc_t rsrc =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(x), 0, a.d * 2, kRawBufferWord3);
+#pragma unroll
+  for (int k = 0; k < NC; ++k)
+    held[k] = __builtin_bit_cast(
+        u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rsrc, tid * 16, k * kThreads * 16, 0));
+  sp::LaneStats st;
+#pragma unroll
+  for (int k = 0; k < NC; ++k)
+    if (tid + k * kThreads < nchunk) {
+      float xs[kPerLane];
+      sp::unpack<SRC>(held[k], xs);
+      sp::online_update(xs, sc, st);
+    }
+  const float m = sp::block_max<kWaves>(st.mx, sh.wave_f);
+  const float inv_s = 1.0f / sp::block_sum<kWaves>(sp::lane_sum_at(st, m, sc), sh.wave_f);
+  const float nb = sp::exp2_offset(m, sc);
+  // Keeps the packed row, not the statistics pass's fp32 values, live.
+#pragma unroll
+  for (int k = 0; k < NC; ++k) asm volatile("" : "+v"(held[k]));
+  const LogitRow<SRC> row{x, sc, nb, inv_s};
+  sample_row(a, row, HeldSweep<SRC, NC>{held, row, a.d, sc, nb, inv_s}, sh);
+}
+
+template <int SRC>
+void launch_held(const SampleArgs& a, int per_lane, dim3 grid, dim3 block, hipStream_t s) {
+  if (per_lane <= 4)
+    hipLaunchKernelGGL((sampling_held_kernel<SRC, 4>), grid, block, 0, s, a);
+  else if (per_lane <= 8)
+    hipLaunchKernelGGL((sampling_held_kernel<SRC, 8>), grid, block, 0, s, a);
+  else if (per_lane <= 12)
+    hipLaunchKernelGGL((sampling_held_kernel<SRC, 12>), grid, block, 0, s, a);
+  else if (per_lane <= 16)
+    hipLaunchKernelGGL((sampling_held_kernel<SRC, 16>), grid, block, 0, s, a);
+  else if (per_lane <= 19)  // Qwen3's 151,936 logits
+    hipLaunchKernelGGL((sampling_held_kernel<SRC, 19>), grid, block, 0, s, a);
+  else
+    hipLaunchKernelGGL((sampling_held_kernel<SRC, kMaxHeldChunks>), grid, block, 0, s, a);
 }
 
 int launch_sampling(const SampleArgs& a, void* stream) {
@@ -510,7 +694,14 @@ int launch_sampling(const SampleArgs& a, void* stream) {
   if (a.probs) {
     hipLaunchKernelGGL(sampling_kernel<-1>, grid, block, 0, s, a);
   } else if (a.logits) {
-    if (a.logit_dtype == SGL_DTYPE_BF16)
+    const int per_lane = (a.d / kPerLane + kThreads - 1) / kThreads;
+    const bool held = a.logit_dtype != SGL_DTYPE_F32 && a.vec && a.d % kPerLane == 0 &&
+                      per_lane <= kMaxHeldChunks;
+    if (held && a.logit_dtype == SGL_DTYPE_BF16)
+      launch_held<SGL_DTYPE_BF16>(a, per_lane, grid, block, s);
+    else if (held)
+      launch_held<SGL_DTYPE_F16>(a, per_lane, grid, block, s);
+    else if (a.logit_dtype == SGL_DTYPE_BF16)
       hipLaunchKernelGGL(sampling_kernel<SGL_DTYPE_BF16>, grid, block, 0, s, a);
     else if (a.logit_dtype == SGL_DTYPE_F16)
       hipLaunchKernelGGL(sampling_kernel<SGL_DTYPE_F16>, grid, block, 0, s, a);

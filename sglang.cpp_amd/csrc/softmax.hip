@@ -5,8 +5,8 @@
 // widening copy, an elementwise pass and a softmax that reads its input
 // again for the max, the sum and the output.
 //
-// Here one workgroup takes one row: y_i = float(x_i) * (1 / t),
-// m = max_i y_i, s = sum_i 2^((y_i - m) log2 e), p_i = 2^((y_i - m) log2 e)
+// Here one workgroup takes one row: with a = log2(e) / t and M the row's
+// largest logit, s = sum_i 2^(x_i a - M a) and p_i = 2^(fma(x_i, a, -(M a)))
 // * (1 / s), the max and the sum taken together (online) as the row streams
 // in. For aligned 16-bit logits rows of up to kMaxRegChunks * 8192 elements
 // (Qwen3's 151,936 included) a 1024-thread workgroup keeps the raw row in
@@ -15,11 +15,13 @@
 // 512-thread workgroup that reads the row again for the output (mostly from
 // the last-level cache).
 //
-// Accuracy against the exact softmax of float(x) / t (float64): y carries
-// half an ulp of |y| from the reciprocal-multiply (about 6e-8 |y|), the exp2
-// argument a few ulp of |y - m|, so a probability is within ~1e-5 relative
-// for logits up to ~100 in magnitude; the fp32 sum adds below ~1e-5 for rows
-// of this length.
+// Accuracy against the exact softmax of float(x) / t (float64): the exp2
+// argument x a - M a carries the rounding of a (half an ulp, times |x a|)
+// and of M a (half an ulp of |M a|), and one more rounding in the fma, so a
+// probability is within ~1e-5 relative for scaled logits |x / t| up to
+// ~100; the fp32 sum adds below ~1e-5 for rows of this length. (The
+// exponent as one fma of the raw logit is two vector operations per element
+// fewer than scaling, subtracting and multiplying by log2 e.)
 #include <math.h>
 
 #include "common.h"
@@ -68,28 +70,28 @@ __global__ void __launch_bounds__(kSmThreads) softmax_temperature_stream(Softmax
   const int e_tail = nfull * P;         // first element taken one by one
   const int tid = threadIdx.x;
   const float t = a.temps ? a.temps[r] : a.temp;
-  const float inv_t = 1.0f / t;
+  const float sc = sp::exp2_scale(t);
 
-  float mx0, s0, mx1, s1;
-  sp::lane_stats<DT>(row, d, a.vec, tid, inv_t, mx0, s0);
-  sp::lane_stats<DT>(row, d, a.vec, tid + kSmThreads, inv_t, mx1, s1);
-  const float m = sp::block_max2<kSmWaves>(mx0, mx1, red);
-  const float inv_s = 1.0f / sp::block_sum2<kSmWaves>(sp::lane_sum_at(mx0, s0, m),
-                                                      sp::lane_sum_at(mx1, s1, m), red);
+  const sp::LaneStats st0 = sp::lane_stats<DT>(row, d, a.vec, tid, sc);
+  const sp::LaneStats st1 = sp::lane_stats<DT>(row, d, a.vec, tid + kSmThreads, sc);
+  const float m = sp::block_max2<kSmWaves>(st0.mx, st1.mx, red);
+  const float inv_s = 1.0f / sp::block_sum2<kSmWaves>(sp::lane_sum_at(st0, m, sc),
+                                                      sp::lane_sum_at(st1, m, sc), red);
+  const float nb = sp::exp2_offset(m, sc);
 
   // The probabilities.
   for (int c = tid; c < nfull; c += kSmThreads) {
     const u32x4_t v = *reinterpret_cast<const u32x4_t*>(row + static_cast<int64_t>(c) * 16);
     float p[P];
 #pragma unroll
-    for (int j = 0; j < P; ++j) p[j] = sp::prob(Elem<DT>::at(v, j), inv_t, m, inv_s);
+    for (int j = 0; j < P; ++j) p[j] = sp::prob(Elem<DT>::at(v, j), sc, nb, inv_s);
 #pragma unroll
     for (int q = 0; q < P / 4; ++q)
       *reinterpret_cast<f32x4_t*>(prow + c * P + 4 * q) =
           f32x4_t{p[4 * q], p[4 * q + 1], p[4 * q + 2], p[4 * q + 3]};
   }
   for (int e = e_tail + tid; e < d; e += kSmThreads)
-    prow[e] = sp::prob(Elem<DT>::load1(row, e), inv_t, m, inv_s);
+    prow[e] = sp::prob(Elem<DT>::load1(row, e), sc, nb, inv_s);
 }
 
 // Register-held rows (aligned 16-bit logits): thread t is the statistics
@@ -112,7 +114,7 @@ __global__ void __launch_bounds__(sp::kStatLanes) softmax_temperature_held(Softm
   const int e_tail = nfull * P;
   const int tid = threadIdx.x;
   const float t = a.temps ? a.temps[r] : a.temp;
-  const float inv_t = 1.0f / t;
+  const float sc = sp::exp2_scale(t);
 
   u32x4_t held[NC];
   const __amdgpu_buffer_rsrc_t rs =
@@ -122,20 +124,21 @@ __global__ void __launch_bounds__(sp::kStatLanes) softmax_temperature_held(Softm
     held[k] = __builtin_bit_cast(
         u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rs, tid * 16, k * T * 16, 0));
   const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(prow, 0, d * 4, kRawBufferWord3);
-  float mx = -INFINITY, sm = 0.f;
+  sp::LaneStats st;
 #pragma unroll
   for (int k = 0; k < NC; ++k)
     if (tid + k * T < nfull) {
-      float y[P];
-      sp::scaled<DT>(held[k], inv_t, y);
-      sp::online_update(y, mx, sm);
+      float x[P];
+      sp::unpack<DT>(held[k], x);
+      sp::online_update(x, sc, st);
     }
   for (int e = e_tail + tid; e < d; e += T) {
-    const float y[1] = {sp::scaled1(Elem<DT>::load1(row, e), inv_t)};
-    sp::online_update(y, mx, sm);
+    const float x[1] = {Elem<DT>::load1(row, e)};
+    sp::online_update(x, sc, st);
   }
-  const float m = sp::block_max<sp::kStatWaves>(mx, red);
-  const float inv_s = 1.0f / sp::block_sum<sp::kStatWaves>(sp::lane_sum_at(mx, sm, m), red);
+  const float m = sp::block_max<sp::kStatWaves>(st.mx, red);
+  const float inv_s = 1.0f / sp::block_sum<sp::kStatWaves>(sp::lane_sum_at(st, m, sc), red);
+  const float nb = sp::exp2_offset(m, sc);
 
   // The probabilities, recomputed from the packed row: without this barrier
   // the compiler keeps the fp32 values of the statistics pass alive instead
@@ -147,7 +150,7 @@ __global__ void __launch_bounds__(sp::kStatLanes) softmax_temperature_held(Softm
     if (tid + k * T < nfull) {
       float p[P];
 #pragma unroll
-      for (int j = 0; j < P; ++j) p[j] = sp::prob(Elem<DT>::at(held[k], j), inv_t, m, inv_s);
+      for (int j = 0; j < P; ++j) p[j] = sp::prob(Elem<DT>::at(held[k], j), sc, nb, inv_s);
 #pragma unroll
       for (int q = 0; q < P / 4; ++q)
         __builtin_amdgcn_raw_buffer_store_b128(
@@ -155,7 +158,7 @@ __global__ void __launch_bounds__(sp::kStatLanes) softmax_temperature_held(Softm
             prs, tid * (4 * P) + 16 * q, k * T * 4 * P, 0);
     }
   for (int e = e_tail + tid; e < d; e += T)
-    prow[e] = sp::prob(Elem<DT>::load1(row, e), inv_t, m, inv_s);
+    prow[e] = sp::prob(Elem<DT>::load1(row, e), sc, nb, inv_s);
 }
 
 template <int DT>

@@ -17,7 +17,7 @@ decision boundary at some round up to its end: the target u * q within
 SUM_TOL of a CDF step, or the mass above the pivot within SUM_TOL of top_p.
 Every other row must give the oracle's sample and success flag exactly.
 SUM_TOL = 2e-5 bounds the kernel's fp32 fixed-order sums of up to 151,936
-probabilities of total mass <= 1 (block sums of 1024, then a sum over
+probabilities of total mass <= 1 (block sums of 512, then a sum over
 blocks: well under 1e-5), plus the same error carried into u * q.
 """
 import sys
@@ -151,7 +151,7 @@ def run_all(oracle, dev, p, u, k, tp, exact):
 
 @pytest.mark.parametrize("batch,d", [(64, QWEN3_VOCAB), (5, 1001), (3, 4096),
                                      (4, 150001),    # odd length: bounds-checked loads
-                                     (2, 1 << 21)])  # longest rows (2,048 blocks, no LDS copies)
+                                     (2, 1 << 21)])  # longest rows (4,096 blocks, no LDS copies)
 def test_sampling_dyadic_bit_exact(oracle, dev, batch, d):
     note(f"sampling dyadic batch={batch} d={d}")
     rng = np.random.default_rng(60 + d % 97)
@@ -397,6 +397,11 @@ def test_sampling_from_logits_equals_softmax_then_draw(dev, dtype, mode):
     (32000, 0, torch.bfloat16),   # a 32K vocabulary
     (65536, 0, torch.float16),    # 64 blocks exactly
     (QWEN3_VOCAB + 8, 0, torch.bfloat16),  # just past the Qwen3 vocabulary
+    (90000, 0, torch.bfloat16),   # register-held rows, 11 chunks a lane
+    (120008, 0, torch.float16),   # register-held, partial last block
+    (163840, 0, torch.float16),   # the longest register-held rows (20 chunks)
+    (163848, 0, torch.bfloat16),  # one chunk past them: streamed
+    (40004, 0, torch.bfloat16),   # aligned, d % 8 != 0: streamed
 ])
 def test_sampling_from_logits_shapes(dev, vocab, offset, dtype):
     g = torch.Generator(device=dev)
