@@ -450,10 +450,11 @@ int sgl_gelu_and_mul(void* out, const void* input, int64_t tokens, int64_t d,
  * for r < batch; t_r = temperatures[r] (fp32 [batch]) or, when temperatures
  * is NULL, the scalar temperature (> 0). logits_dtype: SGL_DTYPE_BF16,
  * SGL_DTYPE_F16 or SGL_DTYPE_F32; row strides in elements (>= vocab). One
- * 512-thread workgroup per row; 16-bit rows of up to 163,840 elements
- * are read from HBM once. Exponentials as 2^(x log2e / t - max log2e)
- * (relative error of a probability below ~1e-5 against the exact softmax
- * of float(x) / t).
+ * workgroup per row; aligned 16-bit rows of up to 163,840 elements are
+ * held in registers and read from HBM once. Exponentials as
+ * 2^(fma(x, a, -max a)) with a = log2e / t (relative error of a probability
+ * below ~1e-5 against the exact softmax of float(x) / t). A row whose
+ * temperature is not positive gets NaN probabilities.
  * Replaces: the probabilities of Sampler::sample, logits.to(kFloat32) /
  *           temperatures then torch::softmax (src/engine/engine.cc:306-308).
  */
