@@ -326,6 +326,25 @@ def test_softmax_temperature_shapes(oracle, dev, vocab, offset, dtype):
     _softmax_case(oracle, dev, logits, None, 0.9, label=f"v{vocab}+{offset}")
 
 
+def test_nonpositive_temperature_rows(dev):
+    """A per-row temperature that is not positive gives that row NaN
+    probabilities (the other rows are untouched), and the draws from logits
+    still equal softmax then draw on every row."""
+    note("softmax_temperature and draws with temperatures 0 and -1")
+    g = torch.Generator(device=dev)
+    g.manual_seed(71)
+    B = 4
+    logits = (torch.randn((B, QWEN3_VOCAB), device=dev, generator=g) * 3).to(torch.bfloat16)
+    temps = torch.tensor([1.0, 0.0, -1.0, 0.7], device=dev)
+    probs = capi.softmax_temperature(logits, temps)
+    torch.cuda.synchronize()
+    assert bool(torch.isnan(probs[1]).all()) and bool(torch.isnan(probs[2]).all())
+    ref = torch.softmax(logits[[0, 3]].float() / temps[[0, 3]].view(2, 1), -1)
+    assert torch.allclose(probs[[0, 3]], ref, rtol=SOFTMAX_RTOL, atol=SOFTMAX_ATOL)
+    for mode in ("plain", "top_k_top_p"):
+        _logits_case(dev, logits, temps, mode, 72, "nonpositive-t")
+
+
 def test_softmax_temperature_rejects_bad_arguments(dev):
     x = torch.zeros((2, 16), device=dev, dtype=torch.bfloat16)
     with pytest.raises(ValueError):
