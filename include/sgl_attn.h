@@ -471,7 +471,7 @@ int sgl_softmax_temperature(float* probs, int64_t probs_stride_row, const void* 
  * fp32 [batch_size]. deterministic is accepted for the reference's
  * signature; sums here always run in a fixed order. Rows of up to 2^21
  * probabilities (SGL_ERR_UNSUPPORTED beyond). One 1024-thread workgroup
- * per row, about 148 KiB of LDS; nothing is allocated.
+ * per row, about 153 KiB of LDS; nothing is allocated.
  * Replaces: flashinfer_sample_from_probs (src/engine/sampling.cu:65-84).
  */
 int sgl_sampling_from_probs(const float* probs, const float* uniform, int32_t* out,
