@@ -433,6 +433,30 @@ def test_sampling_from_logits_shapes(dev, vocab, offset, dtype):
         _logits_case(dev, logits, temps, mode, vocab + 1, f"v{vocab}+{offset}")
 
 
+def test_sampling_from_logits_seeded_shapes(dev):
+    """Seeded random shapes (vocabulary 8 to 200,000, aligned or offset
+    rows, bf16 / fp16 / fp32, random temperatures and rounds): each lands on
+    the register-held or the streamed path by its own length and alignment,
+    and every draw equals softmax then draw."""
+    rng = np.random.default_rng(2024)
+    dtypes = [torch.bfloat16, torch.float16, torch.float32]
+    for i in range(10):
+        vocab = int(rng.choice([int(rng.integers(8, 4096)), int(rng.integers(4096, 200001))]))
+        if i % 3 == 0:
+            vocab = vocab // 8 * 8 or 8  # multiples of 8 reach the held path
+        offset = int(rng.integers(0, 2)) if i % 2 else 0
+        dtype = dtypes[i % 3]
+        B = int(rng.integers(1, 6))
+        g = torch.Generator(device=dev)
+        g.manual_seed(100 + i)
+        base = (torch.randn((B, vocab + 8), device=dev, generator=g) *
+                float(rng.uniform(0.5, 6))).to(dtype)
+        logits = base[:, offset:offset + vocab]
+        temps = torch.from_numpy(rng.uniform(0.3, 2.0, B).astype(np.float32)).to(dev)
+        mode = ["plain", "top_k", "top_p", "top_k_top_p"][i % 4]
+        _logits_case(dev, logits, temps, mode, 200 + i, f"seeded{i}-v{vocab}+{offset}")
+
+
 def test_sampling_from_logits_rejects_bad_arguments(dev):
     x = torch.zeros((2, 64), device=dev, dtype=torch.bfloat16)
     u = torch.rand(2, device=dev)
